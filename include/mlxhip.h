@@ -1,0 +1,341 @@
+/*
+ * mlxhip.h — C ABI of mlx-hip, an MI355X (gfx950) compute backend for the
+ * oxidizedMLX tensor runtime.
+ *
+ * ABI version: 1
+ *
+ * Conventions follow the reference's own C ABI (crates/mlx-sys/csrc/mlxrs.h:1-12):
+ *   - opaque handles, created and freed exactly once; free(NULL) is a no-op;
+ *   - functions returning a handle return NULL on failure;
+ *   - functions returning int return MLXHIP_OK (0) on success, otherwise one
+ *     of mlxhip_status_t, which maps 1:1 onto the reference's MlxError
+ *     variants (crates/mlx-core/src/lib.rs:31-50);
+ *   - the message of the last failure on the calling thread is available
+ *     from mlxhip_last_error().
+ * Every entry point is thread-safe. Pointers named "device" are HIP device
+ * addresses (from mlxhip_buffer_ptr or any other HIP allocation on the same
+ * device); everything else is host memory. No torch or HIP types appear in
+ * any signature: streams are passed as `void*` holding a hipStream_t
+ * (NULL = the device's null stream).
+ */
+#ifndef MLXHIP_H
+#define MLXHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLXHIP_ABI_VERSION 1
+
+/* ── Status codes (MlxError, crates/mlx-core/src/lib.rs:31-50) ───────────── */
+typedef enum {
+    MLXHIP_OK = 0,
+    MLXHIP_ERR_NULL_PTR = 1,            /* MlxError::NullPtr */
+    MLXHIP_ERR_FFI_FAILED = 2,          /* MlxError::FfiFailed (HIP runtime error) */
+    MLXHIP_ERR_SHAPE_MISMATCH = 3,      /* MlxError::ShapeMismatch */
+    MLXHIP_ERR_INVALID_ARGUMENT = 4,    /* MlxError::InvalidArgument */
+    MLXHIP_ERR_BACKEND_UNAVAILABLE = 5, /* MlxError::BackendUnavailable (no GPU) */
+    MLXHIP_ERR_IO = 6                   /* MlxError::IoError */
+} mlxhip_status_t;
+
+/* ── Element types (DType, crates/mlx-core/src/types.rs:4-11; same codes as
+ *    mlx_dtype_t in crates/mlx-sys/csrc/mlxrs.h:40-46) ───────────────────── */
+typedef enum {
+    MLXHIP_DTYPE_F32 = 0,
+    MLXHIP_DTYPE_F16 = 1,
+    MLXHIP_DTYPE_BF16 = 2,
+    MLXHIP_DTYPE_I32 = 3,
+    MLXHIP_DTYPE_I64 = 4
+} mlxhip_dtype_t;
+
+/* ── Op kinds: OpKind (crates/mlx-core/src/graph.rs:33-168), same order ──── */
+typedef enum {
+    MLXHIP_OP_CONSTANT = 0,
+    MLXHIP_OP_PARAMETER = 1,
+    MLXHIP_OP_ADD = 2,
+    MLXHIP_OP_SUB = 3,
+    MLXHIP_OP_MUL = 4,
+    MLXHIP_OP_DIV = 5,
+    MLXHIP_OP_NEG = 6,
+    MLXHIP_OP_EXP = 7,
+    MLXHIP_OP_LOG = 8,
+    MLXHIP_OP_SUM = 9,                    /* axis, has_axis */
+    MLXHIP_OP_MEAN = 10,                  /* axis, has_axis */
+    MLXHIP_OP_MAX = 11,                   /* axis, has_axis */
+    MLXHIP_OP_MATMUL = 12,
+    MLXHIP_OP_RESHAPE = 13,               /* shape = new_shape */
+    MLXHIP_OP_TRANSPOSE = 14,             /* axes (NULL = reverse) */
+    MLXHIP_OP_SOFTMAX = 15,               /* axis */
+    MLXHIP_OP_SILU = 16,
+    MLXHIP_OP_GELU = 17,
+    MLXHIP_OP_LAYER_NORM = 18,            /* eps */
+    MLXHIP_OP_RMS_NORM = 19,              /* eps */
+    MLXHIP_OP_ROPE = 20,                  /* rotary_dim, pos_offset, theta */
+    MLXHIP_OP_BROADCAST = 21,             /* shape = target_shape */
+    MLXHIP_OP_EMBEDDING = 22,
+    MLXHIP_OP_SCALED_MASKED_SOFTMAX = 23, /* scale, causal */
+    MLXHIP_OP_ATTENTION = 24,             /* scale, causal */
+    MLXHIP_OP_LAYER_NORM_VJP = 25,        /* eps */
+    MLXHIP_OP_RMS_NORM_VJP = 26,          /* eps */
+    MLXHIP_OP_SOFTMAX_VJP = 27,           /* axis */
+    MLXHIP_OP_SILU_VJP = 28,
+    MLXHIP_OP_GELU_VJP = 29,
+    MLXHIP_OP_SQRT = 30,
+    MLXHIP_OP_ROPE_MLX = 31,              /* OpKind::RoPE: base, offset, traditional */
+    MLXHIP_OP_NARROW = 32,                /* axis, start, length */
+    MLXHIP_OP_CONCATENATE = 33,           /* axis */
+    MLXHIP_OP_COUNT_ = 34
+} mlxhip_op_kind_t;
+
+/* One OpKind value with its parameters. Fields an op does not use are
+ * ignored. Mirrors the enum payloads of graph.rs:33-168. */
+typedef struct {
+    int32_t kind;           /* mlxhip_op_kind_t */
+    int32_t axis;           /* Sum/Mean/Max (if has_axis), Softmax, SoftmaxVjp, Narrow, Concatenate */
+    int32_t has_axis;       /* Sum/Mean/Max: 0 means `axis: None` */
+    int32_t causal;         /* ScaledMaskedSoftmax, Attention (0/1) */
+    float eps;              /* LayerNorm, RmsNorm and their VJPs */
+    float scale;            /* ScaledMaskedSoftmax, Attention */
+    float theta;            /* Rope */
+    float base;             /* RoPE */
+    const int64_t* shape;   /* Reshape new_shape, Broadcast target_shape */
+    size_t shape_len;
+    const int64_t* axes;    /* Transpose permutation; NULL means `axes: None` */
+    size_t axes_len;
+    int64_t start;          /* Narrow */
+    int64_t length;         /* Narrow */
+    uint64_t rotary_dim;    /* Rope */
+    uint64_t pos_offset;    /* Rope */
+    uint64_t offset;        /* RoPE */
+    int32_t traditional;    /* RoPE */
+    int32_t reserved_;
+} mlxhip_op_t;
+
+/* NodeInput (crates/mlx-core/src/backend.rs:16-20): row-major contiguous f32
+ * data of `len` elements with its logical shape and dtype. */
+typedef struct {
+    const float* data;
+    size_t len;
+    const int64_t* shape;
+    size_t ndim;
+    int32_t dtype;          /* mlxhip_dtype_t (logical tag; data is always f32) */
+} mlxhip_input_t;
+
+/* TensorMeta (crates/mlx-core/src/graph.rs:18-21). */
+typedef struct {
+    const int64_t* shape;
+    size_t ndim;
+    int32_t dtype;          /* mlxhip_dtype_t */
+} mlxhip_meta_t;
+
+/* ── Library, device and error state ─────────────────────────────────────── */
+
+/* Returns MLXHIP_ABI_VERSION of the loaded library. */
+int mlxhip_abi_version(void);
+
+/* Message of the last failure on this thread ("" if none). The pointer stays
+ * valid until the next failing call on the same thread. */
+const char* mlxhip_last_error(void);
+
+/* Status code (mlxhip_status_t) of the last failure on this thread; lets
+ * callers of the handle/id-returning functions recover the MlxError variant. */
+int mlxhip_last_status(void);
+
+/* Number of visible HIP devices (0 when no GPU; never fails). */
+int mlxhip_device_count(void);
+
+/* Selects the device used by later calls on this thread and initialises it
+ * (replaces Metal context creation, crates/mlx-metal/src/context.rs:25).
+ * Returns MLXHIP_ERR_BACKEND_UNAVAILABLE when no GPU is present. */
+int mlxhip_init(int device);
+
+/* Blocks until all work on `stream` (NULL = every stream of the device) ends. */
+int mlxhip_synchronize(void* stream);
+
+/* ── Backend::eval_node, host-vector contract ────────────────────────────── */
+
+/* Backend::eval_node (crates/mlx-core/src/backend.rs:27-35): evaluates one
+ * op on materialised host inputs and writes numel(out_meta) f32 values to
+ * out_host. `out_len` must equal that count (else MLXHIP_ERR_SHAPE_MISMATCH).
+ * Constant/Parameter return MLXHIP_ERR_INVALID_ARGUMENT as in
+ * crates/mlx-core/src/cpu_kernels.rs:21-23; ops without a HIP kernel return
+ * MLXHIP_ERR_INVALID_ARGUMENT ("unsupported op") as in
+ * crates/mlx-metal/src/backend.rs:511-514. Inputs are copied to HBM, the
+ * kernel runs there, and the result is copied back before returning. */
+int mlxhip_eval_node(const mlxhip_op_t* op,
+                     const mlxhip_input_t* inputs, size_t n_inputs,
+                     const mlxhip_meta_t* out_meta,
+                     float* out_host, size_t out_len);
+
+/* ── Device-resident buffers (the "Unified Buffer" the reference planned,
+ *    docs/ARCHITECTURE_TDD.md:89-99; replaces UnifiedBuffer,
+ *    crates/mlx-metal/src/unified.rs:136-239) ────────────────────────────── */
+
+typedef struct mlxhip_buffer_t mlxhip_buffer_t;
+
+/* Allocates `bytes` of HBM on the current device. bytes == 0 yields a valid
+ * empty buffer (crates/mlx-metal/src/unified.rs:318-324). */
+mlxhip_buffer_t* mlxhip_buffer_alloc(size_t bytes);
+void mlxhip_buffer_free(mlxhip_buffer_t* buf);
+void* mlxhip_buffer_ptr(const mlxhip_buffer_t* buf);    /* device address */
+size_t mlxhip_buffer_size(const mlxhip_buffer_t* buf);  /* bytes */
+/* Synchronous host <-> device copies of `bytes` at byte `offset`. */
+int mlxhip_buffer_upload(mlxhip_buffer_t* buf, size_t offset, const void* host, size_t bytes);
+int mlxhip_buffer_download(const mlxhip_buffer_t* buf, size_t offset, void* host, size_t bytes);
+
+/* Backend::eval_node with device-resident operands: as mlxhip_eval_node but
+ * every input's `data` is a device address and the result is written to the
+ * device address `out` (numel(out_meta) f32 values). Runs on `stream`,
+ * asynchronously; no host copies. */
+int mlxhip_eval_node_dev(const mlxhip_op_t* op,
+                         const mlxhip_input_t* inputs, size_t n_inputs,
+                         const mlxhip_meta_t* out_meta,
+                         float* out, void* stream);
+
+/* ── Stream: lazy graph + scheduler with HBM-resident buffers ────────────────
+ * Restates Stream (crates/mlx-core/src/backend.rs:37-185) and Graph
+ * (crates/mlx-core/src/graph.rs:170-305) with this backend bound: CSE of
+ * non-source ops, memoisation, eval_count/cache_len, and buffers that stay in
+ * HBM until the stream is freed. Only get_buffer copies to the host. */
+
+typedef struct mlxhip_stream_t mlxhip_stream_t;
+
+mlxhip_stream_t* mlxhip_stream_new(void);
+void mlxhip_stream_free(mlxhip_stream_t* s);
+/* Stream::add_constant (backend.rs:59-71). Returns the node id (never 0), or
+ * 0 on failure. */
+uint64_t mlxhip_stream_add_constant(mlxhip_stream_t* s, const float* data, size_t len,
+                                    const mlxhip_meta_t* meta);
+/* Stream::add_op (backend.rs:74-82). Returns the node id, or 0 on failure. */
+uint64_t mlxhip_stream_add_op(mlxhip_stream_t* s, const mlxhip_op_t* op,
+                              const uint64_t* inputs, size_t n_inputs,
+                              const mlxhip_meta_t* meta);
+/* Stream::eval (backend.rs:85-159). */
+int mlxhip_stream_eval(mlxhip_stream_t* s, uint64_t node);
+/* Stream::get_buffer (backend.rs:162-164): copies the node's f32 data to
+ * `out` (len must equal its numel). MLXHIP_ERR_INVALID_ARGUMENT if the node
+ * is not materialised. */
+int mlxhip_stream_get_buffer(mlxhip_stream_t* s, uint64_t node, float* out, size_t len);
+/* Stream::eval_count (backend.rs:177-179): number of backend node
+ * evaluations (a fused group counts each node it covers). */
+uint64_t mlxhip_stream_eval_count(const mlxhip_stream_t* s);
+/* Stream::cache_len (backend.rs:182-184). */
+size_t mlxhip_stream_cache_len(const mlxhip_stream_t* s);
+/* Number of kernel launches issued by eval so far (fusion makes this smaller
+ * than eval_count). No reference counterpart; telemetry in the spirit of
+ * BufferTelemetry, crates/mlx-metal/src/instrument.rs:2-29. */
+uint64_t mlxhip_stream_launch_count(const mlxhip_stream_t* s);
+/* Enables (1, default) or disables (0) look-ahead fusion of single-consumer
+ * elementwise chains and of Transpose into MatMul operand layouts. */
+int mlxhip_stream_set_fusion(mlxhip_stream_t* s, int enabled);
+
+/* ── Direct kernel entry points (device pointers, asynchronous on `stream`) ─ */
+
+/* Batched GEMM, row-major: for each b < batch,
+ *   C_b[M,N] = op(A_b) · op(B_b), f32 accumulate,
+ * op(A) = A [M,K] (trans_a = 0, row pitch lda) or A^T with A stored [K,M]
+ * (trans_a = 1); op(B) = B [K,N] (trans_b = 0, row pitch ldb) or B^T with B
+ * stored [N,K] (trans_b = 1). A_b = a + b*stride_a elements (likewise B, C).
+ * ab_dtype: F32 (f32 MFMA), BF16 or F16 (16-bit MFMA); both operands share it.
+ * c_dtype: F32, or BF16/F16 (round-to-nearest-even of the f32 accumulator).
+ * Replaces matmul (crates/mlx-core/src/cpu_kernels.rs:197-230) and the Metal
+ * tiled_gemm_f32 (crates/mlx-metal/src/kernels/gemm.metal:32-77), adding the
+ * batched and transposed-operand forms that autograd's MatMul VJP
+ * (crates/mlx-autograd/src/vjp.rs:71-80) and Linear (crates/mlx-nn/src/linear.rs:34-43)
+ * express through Transpose nodes. */
+int mlxhip_gemm(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t trans_b,
+                int64_t m, int64_t n, int64_t k, int64_t batch,
+                const void* a, int64_t lda, int64_t stride_a,
+                const void* b, int64_t ldb, int64_t stride_b,
+                void* c, int64_t ldc, int64_t stride_c,
+                void* stream);
+
+/* Row-wise softmax over the last axis of a [rows, cols] f32 matrix
+ * (softmax, crates/mlx-core/src/cpu_kernels.rs:276-315, axis = -1). */
+int mlxhip_softmax_rows(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
+/* Row softmax of x*scale with the causal fill -1e9 for col > row
+ * (scaled_masked_softmax, cpu_kernels.rs:671-712); causal is 0/1. */
+int mlxhip_scaled_masked_softmax_rows(const float* x, float* y, int64_t rows, int64_t cols,
+                                      float scale, int32_t causal, void* stream);
+/* LayerNorm without affine over the last axis (layer_norm, cpu_kernels.rs:338-363). */
+int mlxhip_layernorm_rows(const float* x, float* y, int64_t rows, int64_t cols,
+                          float eps, void* stream);
+/* RMSNorm without weight over the last axis (rms_norm, cpu_kernels.rs:647-669). */
+int mlxhip_rmsnorm_rows(const float* x, float* y, int64_t rows, int64_t cols,
+                        float eps, void* stream);
+/* SoftmaxVjp, last axis: dx = s*(dy - sum(dy*s)) (softmax_vjp, cpu_kernels.rs:515-553). */
+int mlxhip_softmax_vjp_rows(const float* dy, const float* s, float* dx,
+                            int64_t rows, int64_t cols, void* stream);
+/* LayerNormVjp (layer_norm_vjp, cpu_kernels.rs:403-454). */
+int mlxhip_layernorm_vjp_rows(const float* dy, const float* x, float* dx,
+                              int64_t rows, int64_t cols, float eps, void* stream);
+/* RmsNormVjp (rms_norm_vjp, cpu_kernels.rs:462-510). */
+int mlxhip_rmsnorm_vjp_rows(const float* dy, const float* x, float* dx,
+                            int64_t rows, int64_t cols, float eps, void* stream);
+
+/* Fused elementwise chain. acc starts as inputs[0][i]; each instruction
+ * updates it in order; out[i] = acc. Every input is read once and out is
+ * written once, whatever the chain length. Each instruction's arithmetic is
+ * the f32 operation of the matching OpKind (cpu_kernels.rs:24-35,51-67,
+ * 85-88,104-106, 558-606), rounded to f32 after every step exactly as the
+ * unfused graph would (no contraction into FMA). */
+typedef enum {
+    MLXHIP_EW_ADD = 0,    /* acc = acc + in[operand] */
+    MLXHIP_EW_SUB = 1,    /* acc = acc - in[operand] */
+    MLXHIP_EW_RSUB = 2,   /* acc = in[operand] - acc */
+    MLXHIP_EW_MUL = 3,    /* acc = acc * in[operand] */
+    MLXHIP_EW_DIV = 4,    /* acc = acc / in[operand] */
+    MLXHIP_EW_RDIV = 5,   /* acc = in[operand] / acc */
+    MLXHIP_EW_NEG = 6,    /* acc = -acc */
+    MLXHIP_EW_EXP = 7,
+    MLXHIP_EW_LOG = 8,
+    MLXHIP_EW_SQRT = 9,
+    MLXHIP_EW_SILU = 10,
+    MLXHIP_EW_GELU = 11,
+    MLXHIP_EW_SILU_VJP = 12, /* acc = in[operand] * silu'(acc)  (dy = in[operand]) */
+    MLXHIP_EW_GELU_VJP = 13, /* acc = in[operand] * gelu'(acc) */
+    MLXHIP_EW_COUNT_ = 14
+} mlxhip_ew_op_t;
+
+typedef struct {
+    int32_t op;       /* mlxhip_ew_op_t */
+    int32_t operand;  /* input index for binary ops; ignored by unary ops */
+} mlxhip_ew_instr_t;
+
+#define MLXHIP_EW_MAX_INSTR 16
+#define MLXHIP_EW_MAX_INPUTS 8
+
+int mlxhip_ew_chain(const mlxhip_ew_instr_t* prog, size_t n_instr,
+                    const float* const* inputs, size_t n_inputs,
+                    float* out, int64_t numel, void* stream);
+
+/* 2-D transpose y[cols, rows] = x[rows, cols]^T of 4-byte elements
+ * (transpose, cpu_kernels.rs:232-274, axes = None on rank 2). Bit-exact. */
+int mlxhip_transpose2d(const float* x, float* y, int64_t rows, int64_t cols, void* stream);
+
+/* Element type conversion of n elements: f32 -> bf16/f16 round to nearest
+ * even, bf16/f16 -> f32 exact, same-type copy. */
+int mlxhip_cast(const void* x, int32_t src_dtype, void* y, int32_t dst_dtype,
+                int64_t n, void* stream);
+
+/* ── Timing (HIP events, for benchmarks) ─────────────────────────────────── */
+
+typedef struct mlxhip_event_t mlxhip_event_t;
+mlxhip_event_t* mlxhip_event_create(void);
+void mlxhip_event_destroy(mlxhip_event_t* e);
+int mlxhip_event_record(mlxhip_event_t* e, void* stream);
+/* Milliseconds between two recorded events (waits for `end`). */
+int mlxhip_event_elapsed_ms(const mlxhip_event_t* start, const mlxhip_event_t* end, float* ms);
+
+/* Creates / destroys a HIP stream at the default priority. */
+void* mlxhip_stream_create_hip(void);
+void mlxhip_stream_destroy_hip(void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLXHIP_H */

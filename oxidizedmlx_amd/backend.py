@@ -1,0 +1,264 @@
+"""Python face of libmlxhip.so: HipBackend, HipStream, device buffers, the
+direct kernel entry points and HIP-event timing.
+
+``HipBackend().eval_node(op, inputs, meta)`` is the reference's
+``Backend::eval_node`` (crates/mlx-core/src/backend.rs:27-35) with the
+host-vector contract; ``HipStream`` is ``Stream`` (backend.rs:37-185) bound to
+this backend with HBM-resident buffers (``hip_stream()`` is the drop-in for
+``cpu_stream()`` / ``metal_stream()``). Everything goes through the C ABI;
+without the built library or without a GPU the calls raise
+``BackendUnavailable`` -- there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Sequence
+
+import numpy as np
+
+from . import abi
+from .opkind import NodeInput, Op, TensorMeta, inputs_to_c
+
+_inited = False
+
+
+def lib() -> C.CDLL:
+    return abi.load_library()
+
+
+def init(device: int = 0) -> None:
+    """Loads the library and selects/initialises ``device``."""
+    global _inited
+    L = lib()
+    abi.check(L.mlxhip_init(device), L)
+    _inited = True
+
+
+def device_count() -> int:
+    return lib().mlxhip_device_count()
+
+
+def synchronize(stream: int | None = None) -> None:
+    abi.check(lib().mlxhip_synchronize(stream))
+
+
+class HipBackend:
+    """Backend::eval_node with host inputs (copies in, runs in HBM, copies out)."""
+
+    def eval_node(self, op: Op, inputs: Sequence[NodeInput], out_meta: TensorMeta) -> np.ndarray:
+        L = lib()
+        cop, k1 = op.to_c()
+        arr, k2 = inputs_to_c(inputs)
+        cm, k3 = out_meta.to_c()
+        n = out_meta.numel()
+        out = np.empty(max(n, 1), dtype=np.float32)
+        abi.check(L.mlxhip_eval_node(C.byref(cop), arr, len(inputs), C.byref(cm), out.ctypes.data, n), L)
+        del k1, k2, k3
+        return out[:n]
+
+
+class HipStream:
+    """Stream bound to mlx-hip: lazy graph, CSE, memoised HBM-resident buffers."""
+
+    def __init__(self, fusion: bool = True):
+        L = lib()
+        self._L = L
+        self._s = L.mlxhip_stream_new()
+        if not self._s:
+            raise abi.error_for(L.mlxhip_last_status(), L.mlxhip_last_error().decode())
+        self.metas: dict[int, TensorMeta] = {}
+        if not fusion:
+            self.set_fusion(False)
+
+    def close(self) -> None:
+        if getattr(self, "_s", None):
+            self._L.mlxhip_stream_free(self._s)
+            self._s = None
+
+    def __del__(self):
+        self.close()
+
+    def set_fusion(self, enabled: bool) -> None:
+        abi.check(self._L.mlxhip_stream_set_fusion(self._s, 1 if enabled else 0), self._L)
+
+    def add_constant(self, data, m: TensorMeta) -> int:
+        d = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
+        cm, keep = m.to_c()
+        nid = self._L.mlxhip_stream_add_constant(self._s, d.ctypes.data, d.size, C.byref(cm))
+        if nid == 0:
+            abi.check(self._L.mlxhip_last_status() or abi.ERR_FFI_FAILED, self._L)
+        self.metas[nid] = m
+        return nid
+
+    def add_op(self, op: Op, inputs: Sequence[int], m: TensorMeta) -> int:
+        cop, k1 = op.to_c()
+        cm, k2 = m.to_c()
+        ids = (C.c_uint64 * max(1, len(inputs)))(*inputs)
+        nid = self._L.mlxhip_stream_add_op(self._s, C.byref(cop), ids, len(inputs), C.byref(cm))
+        if nid == 0:
+            abi.check(self._L.mlxhip_last_status() or abi.ERR_FFI_FAILED, self._L)
+        self.metas[nid] = m
+        return nid
+
+    def eval(self, nid: int) -> None:
+        abi.check(self._L.mlxhip_stream_eval(self._s, nid), self._L)
+
+    def get_buffer(self, nid: int) -> np.ndarray:
+        n = self.metas[nid].numel()
+        out = np.empty(max(n, 1), dtype=np.float32)
+        abi.check(self._L.mlxhip_stream_get_buffer(self._s, nid, out.ctypes.data, n), self._L)
+        return out[:n]
+
+    def eval_count(self) -> int:
+        return self._L.mlxhip_stream_eval_count(self._s)
+
+    def cache_len(self) -> int:
+        return self._L.mlxhip_stream_cache_len(self._s)
+
+    def launch_count(self) -> int:
+        return self._L.mlxhip_stream_launch_count(self._s)
+
+
+
+
+def hip_stream(fusion: bool = True) -> HipStream:
+    """The drop-in for ``cpu_stream()`` / ``metal_stream()``."""
+    return HipStream(fusion=fusion)
+
+
+class DeviceBuffer:
+    """HBM buffer owned by Python (freed when collected)."""
+
+    def __init__(self, nbytes: int):
+        L = lib()
+        self._L = L
+        self.nbytes = int(nbytes)
+        self._b = L.mlxhip_buffer_alloc(self.nbytes)
+        if not self._b:
+            raise abi.error_for(abi.ERR_FFI_FAILED, L.mlxhip_last_error().decode())
+        self.ptr = L.mlxhip_buffer_ptr(self._b) or 0
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        abi.check(self._L.mlxhip_buffer_upload(self._b, offset, a.ctypes.data, a.nbytes), self._L)
+
+    def download(self, dtype=np.float32, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        abi.check(self._L.mlxhip_buffer_download(self._b, offset, out.ctypes.data, out.nbytes), self._L)
+        return out
+
+    def free(self) -> None:
+        if getattr(self, "_b", None):
+            self._L.mlxhip_buffer_free(self._b)
+            self._b = None
+            self.ptr = 0
+
+    def __del__(self):
+        self.free()
+
+
+def _p(x) -> int:
+    return x.ptr if isinstance(x, DeviceBuffer) else int(x or 0)
+
+
+def gemm(ab_dtype: int, c_dtype: int, trans_a: bool, trans_b: bool, m: int, n: int, k: int,
+         a, lda: int, b, ldb: int, c, ldc: int, batch: int = 1, stride_a: int = 0,
+         stride_b: int = 0, stride_c: int = 0, stream: int | None = None) -> None:
+    L = lib()
+    abi.check(L.mlxhip_gemm(ab_dtype, c_dtype, int(trans_a), int(trans_b), m, n, k, batch,
+                            _p(a), lda, stride_a, _p(b), ldb, stride_b, _p(c), ldc, stride_c,
+                            stream), L)
+
+
+def softmax_rows(x, y, rows: int, cols: int, stream=None) -> None:
+    abi.check(lib().mlxhip_softmax_rows(_p(x), _p(y), rows, cols, stream))
+
+
+def scaled_masked_softmax_rows(x, y, rows, cols, scale, causal, stream=None) -> None:
+    abi.check(lib().mlxhip_scaled_masked_softmax_rows(_p(x), _p(y), rows, cols, scale,
+                                                      int(causal), stream))
+
+
+def layernorm_rows(x, y, rows: int, cols: int, eps: float, stream=None) -> None:
+    abi.check(lib().mlxhip_layernorm_rows(_p(x), _p(y), rows, cols, eps, stream))
+
+
+def rmsnorm_rows(x, y, rows: int, cols: int, eps: float, stream=None) -> None:
+    abi.check(lib().mlxhip_rmsnorm_rows(_p(x), _p(y), rows, cols, eps, stream))
+
+
+def softmax_vjp_rows(dy, s, dx, rows, cols, stream=None) -> None:
+    abi.check(lib().mlxhip_softmax_vjp_rows(_p(dy), _p(s), _p(dx), rows, cols, stream))
+
+
+def layernorm_vjp_rows(dy, x, dx, rows, cols, eps, stream=None) -> None:
+    abi.check(lib().mlxhip_layernorm_vjp_rows(_p(dy), _p(x), _p(dx), rows, cols, eps, stream))
+
+
+def rmsnorm_vjp_rows(dy, x, dx, rows, cols, eps, stream=None) -> None:
+    abi.check(lib().mlxhip_rmsnorm_vjp_rows(_p(dy), _p(x), _p(dx), rows, cols, eps, stream))
+
+
+EW = {"add": 0, "sub": 1, "rsub": 2, "mul": 3, "div": 4, "rdiv": 5, "neg": 6, "exp": 7,
+      "log": 8, "sqrt": 9, "silu": 10, "gelu": 11, "silu_vjp": 12, "gelu_vjp": 13}
+
+
+def ew_chain(prog: Sequence[tuple], inputs: Sequence, out, numel: int, stream=None) -> None:
+    """prog: sequence of (op_name, operand_index); acc starts as inputs[0]."""
+    ins = (abi.mlxhip_ew_instr_t * max(1, len(prog)))()
+    for i, (op, operand) in enumerate(prog):
+        ins[i].op = EW[op] if isinstance(op, str) else int(op)
+        ins[i].operand = int(operand)
+    ptrs = (C.c_void_p * max(1, len(inputs)))(*[_p(x) for x in inputs])
+    abi.check(lib().mlxhip_ew_chain(ins, len(prog), ptrs, len(inputs), _p(out), numel, stream))
+
+
+def transpose2d(x, y, rows: int, cols: int, stream=None) -> None:
+    abi.check(lib().mlxhip_transpose2d(_p(x), _p(y), rows, cols, stream))
+
+
+def cast(x, src: int, y, dst: int, n: int, stream=None) -> None:
+    abi.check(lib().mlxhip_cast(_p(x), src, _p(y), dst, n, stream))
+
+
+class Event:
+    def __init__(self):
+        L = lib()
+        self._L = L
+        self._e = L.mlxhip_event_create()
+        if not self._e:
+            raise abi.error_for(abi.ERR_FFI_FAILED, L.mlxhip_last_error().decode())
+
+    def record(self, stream=None) -> None:
+        abi.check(self._L.mlxhip_event_record(self._e, stream), self._L)
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float(0)
+        abi.check(self._L.mlxhip_event_elapsed_ms(self._e, end._e, C.byref(ms)), self._L)
+        return ms.value
+
+    def __del__(self):
+        if getattr(self, "_e", None):
+            self._L.mlxhip_event_destroy(self._e)
+            self._e = None
+
+
+def create_stream() -> int:
+    s = lib().mlxhip_stream_create_hip()
+    if not s:
+        raise abi.error_for(abi.ERR_FFI_FAILED, lib().mlxhip_last_error().decode())
+    return s
+
+
+def destroy_stream(s: int) -> None:
+    lib().mlxhip_stream_destroy_hip(s)

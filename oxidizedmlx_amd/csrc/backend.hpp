@@ -1,0 +1,50 @@
+// backend.hpp — HipBackend: the reference's Backend::eval_node
+// (crates/mlx-core/src/backend.rs:27-35) over HBM-resident operands, plus the
+// device-memory pool the host-vector contract and the Stream use.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+#include "../../include/mlxhip.h"
+
+namespace mlxhip {
+
+// Caching pool of device allocations on the current device. release() may
+// only be called once no queued GPU work still uses the block (the callers
+// synchronise their stream first).
+void* pool_alloc(size_t bytes);
+void pool_release(void* p);
+
+// Temporary device buffers of one node evaluation, handed back to the pool
+// by the owner after its stream has been synchronised.
+struct Scratch {
+    std::vector<void*> blocks;
+    float* get(size_t n_floats);
+    void* get_bytes(size_t bytes);
+    void release_all();
+    ~Scratch() { release_all(); }
+};
+
+inline int64_t numel_of(const int64_t* shape, size_t ndim) {
+    int64_t n = 1;
+    for (size_t i = 0; i < ndim; ++i) n *= shape[i];
+    return n;
+}
+
+// Backend::eval_node on device memory: inputs[i].data are device addresses,
+// `out` receives numel(out_meta) floats. Asynchronous on `s`; temporaries go
+// to `scratch`. `trans_hint` (optional) lets the Stream pass MatMul operands
+// whose Transpose node was folded: trans_hint[i] = 1 means inputs[i] holds
+// the untransposed source, so the GEMM reads it transposed.
+int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* inputs, size_t n_inputs,
+                     const mlxhip_meta_t& out_meta, float* out, hipStream_t s, Scratch& scratch,
+                     const int* trans_hint = nullptr);
+
+// Per-thread HIP stream used by the synchronous host-vector entry points.
+hipStream_t thread_stream();
+
+}  // namespace mlxhip

@@ -1,0 +1,53 @@
+// common.hpp — shared host-side plumbing of the mlx-hip library: status codes,
+// per-thread error messages, HIP error mapping, device initialisation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/mlxhip.h"
+
+namespace mlxhip {
+
+// Per-thread message of the last failure (mlxhip_last_error).
+std::string& last_error();
+
+// Records a failure and returns its status code.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Maps a HIP runtime error onto MlxError::FfiFailed with the call site.
+int hip_fail(hipError_t e, const char* what);
+
+#define MLXHIP_HIP(call)                                              \
+    do {                                                              \
+        hipError_t e_ = (call);                                       \
+        if (e_ != hipSuccess) return ::mlxhip::hip_fail(e_, #call);   \
+    } while (0)
+
+#define MLXHIP_TRY(expr)              \
+    do {                              \
+        int rc_ = (expr);             \
+        if (rc_ != MLXHIP_OK) return rc_; \
+    } while (0)
+
+// Makes sure the calling thread has an initialised device (device 0 unless
+// mlxhip_init chose another). Returns MLXHIP_ERR_BACKEND_UNAVAILABLE without
+// a GPU.
+int ensure_device();
+
+// Checks the launch that was just issued.
+inline int launch_check(const char* kernel) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, kernel);
+    return MLXHIP_OK;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace mlxhip

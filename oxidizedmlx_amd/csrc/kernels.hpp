@@ -1,0 +1,70 @@
+// kernels.hpp — internal launch functions of the HIP kernels. Every function
+// enqueues work on stream `s`, validates its sizes on the host first, and
+// returns an mlxhip_status_t.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/mlxhip.h"
+
+namespace mlxhip {
+
+// ── rows.hip ──────────────────────────────────────────────────────────────
+enum RowOp {
+    ROW_SOFTMAX = 0,
+    ROW_SCALED_MASKED_SOFTMAX = 1,
+    ROW_LAYERNORM = 2,
+    ROW_RMSNORM = 3,
+    ROW_SOFTMAX_VJP = 4,    // a = dy, b = softmax output
+    ROW_LAYERNORM_VJP = 5,  // a = dy, b = x
+    ROW_RMSNORM_VJP = 6,    // a = dy, b = x
+};
+int row_op(int op, const float* a, const float* b, float* y, int64_t rows, int64_t cols, float p,
+           int causal, hipStream_t s);
+// Softmax (vjp=false) or SoftmaxVjp along a non-last axis of [outer, dim, inner].
+int fibre_softmax(bool vjp, const float* a, const float* b, float* y, int64_t outer, int64_t dim,
+                  int64_t inner, hipStream_t s);
+
+// ── elementwise.hip ───────────────────────────────────────────────────────
+int ew_chain(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs,
+             int n_inputs, float* out, int64_t numel, hipStream_t s);
+// General N-D permutation (rank <= 8): y[new] = x[old], out shape = shape[perm].
+int permute(const float* x, float* y, const int64_t* shape, const int64_t* perm, int ndim,
+            hipStream_t s);
+int transpose2d(const float* x, float* y, int64_t rows, int64_t cols, hipStream_t s);
+// NumPy right-aligned broadcast (rank <= 8).
+int broadcast(const float* x, float* y, const int64_t* in_shape, int in_ndim,
+              const int64_t* out_shape, int out_ndim, hipStream_t s);
+// Sum/Mean/Max along an axis of [outer, dim, inner]: sequential fold per
+// output element in the reference's order (bit-identical to the CPU).
+// kind: 0 sum, 1 mean, 2 max.
+int reduce_axis(int kind, const float* x, float* y, int64_t outer, int64_t dim, int64_t inner,
+                hipStream_t s);
+// Reduction of all n elements to y[0]. kind as above.
+int reduce_all(int kind, const float* x, float* y, int64_t n, hipStream_t s);
+int cast(const void* x, int src, void* y, int dst, int64_t n, hipStream_t s);
+// f32 -> bf16/f16 (RNE) of a strided 2-D block [rows, cols] with row pitch
+// ld_src into a packed [rows, cols] destination.
+int embedding(const float* w, const float* idx, float* y, int64_t n_idx, int64_t num_emb,
+              int64_t dim, hipStream_t s);
+// Copy of [outer, length, inner] slices starting at `start` of a [outer, dim, inner] tensor.
+int narrow(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner, int64_t start,
+           int64_t length, hipStream_t s);
+// Copies src [outer, d, inner] into dst [outer, total, inner] at offset `at` along the axis.
+int concat_part(const float* x, float* y, int64_t outer, int64_t d, int64_t inner, int64_t total,
+                int64_t at, hipStream_t s);
+int rope_interleaved(const float* x, float* y, int64_t tokens, int64_t head_dim,
+                     int64_t rotary_dim, int64_t pos_offset, float theta, int64_t len,
+                     hipStream_t s);
+int rope_mlx(const float* x, float* y, int64_t n_rows, int64_t head_dim, int64_t offset,
+             float base, int traditional, hipStream_t s);
+int fill(float* y, float v, int64_t n, hipStream_t s);
+
+// ── gemm.hip ──────────────────────────────────────────────────────────────
+int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
+         int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
+         int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s);
+
+}  // namespace mlxhip

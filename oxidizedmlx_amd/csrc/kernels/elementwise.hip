@@ -1,0 +1,586 @@
+// elementwise.hip — HBM-streaming kernels: the fused elementwise chain,
+// transposes/permutations, broadcast, reductions, type casts and the gather /
+// slice / rotary kernels the graph needs.
+//
+// Elementwise semantics follow crates/mlx-core/src/cpu_kernels.rs:
+//   Add/Sub/Mul/Div :24-27,114-128   Neg/Exp/Log :28-39   Sqrt :85-88
+//   Silu :51-54 with sigmoid :104-106   Gelu (tanh approx.) :55-67
+//   SiluVjp :558-576   GeluVjp :582-606
+// Contraction is off in this file, so x*w+b rounds twice exactly like the
+// reference's two graph nodes; transcendental functions are the device
+// libm's (ocml), not glibc's, so they can differ by an ulp or so.
+//
+// Streaming kernels move float4 (dwordx4) per lane, several per thread per
+// grid-stride step so each wave keeps multiple 1 KiB loads in flight.
+#include "../common.hpp"
+#include "../kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace mlxhip {
+namespace {
+
+constexpr int BLOCK = 256;
+
+__device__ inline float sigmoidf_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ inline float gelu_ref(float x) {
+    const float k = sqrtf(2.0f / 3.14159265358979323846f);
+    return 0.5f * x * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+}
+
+__device__ inline float silu_vjp_ref(float dy, float x) {
+    const float sig = sigmoidf_ref(x);
+    return dy * sig * (1.0f + x * (1.0f - sig));
+}
+
+__device__ inline float gelu_vjp_ref(float dy, float x) {
+    const float a = sqrtf(2.0f / 3.14159265358979323846f);
+    const float b = 0.044715f;
+    const float inner = a * (x + b * x * x * x);
+    const float t = tanhf(inner);
+    const float sech2 = 1.0f - t * t;
+    const float dg = 0.5f * (1.0f + t) + 0.5f * x * sech2 * a * (1.0f + 3.0f * b * x * x);
+    return dy * dg;
+}
+
+__device__ inline float apply(int op, float acc, float in) {
+    switch (op) {
+        case MLXHIP_EW_ADD: return acc + in;
+        case MLXHIP_EW_SUB: return acc - in;
+        case MLXHIP_EW_RSUB: return in - acc;
+        case MLXHIP_EW_MUL: return acc * in;
+        case MLXHIP_EW_DIV: return acc / in;
+        case MLXHIP_EW_RDIV: return in / acc;
+        case MLXHIP_EW_NEG: return -acc;
+        case MLXHIP_EW_EXP: return expf(acc);
+        case MLXHIP_EW_LOG: return logf(acc);
+        case MLXHIP_EW_SQRT: return sqrtf(acc);
+        case MLXHIP_EW_SILU: return acc * sigmoidf_ref(acc);
+        case MLXHIP_EW_GELU: return gelu_ref(acc);
+        case MLXHIP_EW_SILU_VJP: return silu_vjp_ref(in, acc);
+        case MLXHIP_EW_GELU_VJP: return gelu_vjp_ref(in, acc);
+        default: return acc;
+    }
+}
+
+__host__ __device__ inline bool ew_binary(int op) {
+    return op == MLXHIP_EW_ADD || op == MLXHIP_EW_SUB || op == MLXHIP_EW_RSUB ||
+           op == MLXHIP_EW_MUL || op == MLXHIP_EW_DIV || op == MLXHIP_EW_RDIV ||
+           op == MLXHIP_EW_SILU_VJP || op == MLXHIP_EW_GELU_VJP;
+}
+
+// The whole program travels in kernel arguments, so every instruction field
+// is wave-uniform (scalar registers) and the interpreter loop costs no VGPRs.
+struct EwProg {
+    const float* in[MLXHIP_EW_MAX_INPUTS];
+    int op[MLXHIP_EW_MAX_INSTR];
+    int operand[MLXHIP_EW_MAX_INSTR];
+    int n_instr;
+};
+
+template <int U>
+__global__ __launch_bounds__(BLOCK) void ew_chain_vec_kernel(EwProg prog, float* __restrict__ out,
+                                                             int64_t n_vec) {
+    const int64_t stride = (int64_t)gridDim.x * BLOCK * U;
+    for (int64_t base = (int64_t)blockIdx.x * BLOCK * U + threadIdx.x; base < n_vec;
+         base += stride) {
+        float4 acc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = base + (int64_t)u * BLOCK;
+            acc[u] = i < n_vec ? reinterpret_cast<const float4*>(prog.in[0])[i]
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        for (int k = 0; k < prog.n_instr; ++k) {
+            const int op = prog.op[k];
+            if (ew_binary(op)) {
+                const float4* src = reinterpret_cast<const float4*>(prog.in[prog.operand[k]]);
+                float4 b[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int64_t i = base + (int64_t)u * BLOCK;
+                    b[u] = i < n_vec ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    acc[u].x = apply(op, acc[u].x, b[u].x);
+                    acc[u].y = apply(op, acc[u].y, b[u].y);
+                    acc[u].z = apply(op, acc[u].z, b[u].z);
+                    acc[u].w = apply(op, acc[u].w, b[u].w);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    acc[u].x = apply(op, acc[u].x, 0.f);
+                    acc[u].y = apply(op, acc[u].y, 0.f);
+                    acc[u].z = apply(op, acc[u].z, 0.f);
+                    acc[u].w = apply(op, acc[u].w, 0.f);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = base + (int64_t)u * BLOCK;
+            if (i < n_vec) reinterpret_cast<float4*>(out)[i] = acc[u];
+        }
+    }
+}
+
+__global__ __launch_bounds__(BLOCK) void ew_chain_scalar_kernel(EwProg prog, float* __restrict__ out,
+                                                                int64_t begin, int64_t n) {
+    const int64_t i = begin + (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (i >= n) return;
+    float acc = prog.in[0][i];
+    for (int k = 0; k < prog.n_instr; ++k) {
+        const int op = prog.op[k];
+        acc = apply(op, acc, ew_binary(op) ? prog.in[prog.operand[k]][i] : 0.f);
+    }
+    out[i] = acc;
+}
+
+// 2-D transpose through a padded 64x64 LDS tile (the +1 column breaks the
+// bank conflicts of the column-wise read).
+__global__ __launch_bounds__(BLOCK) void transpose2d_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ y, int64_t rows,
+                                                            int64_t cols) {
+    __shared__ float tile[64][65];
+    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+#pragma unroll
+    for (int i = 0; i < 64; i += 4) {
+        const int64_t r = r0 + ty + i, c = c0 + tx;
+        if (r < rows && c < cols) tile[ty + i][tx] = x[r * cols + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 64; i += 4) {
+        const int64_t c = c0 + ty + i, r = r0 + tx;
+        if (r < rows && c < cols) y[c * rows + r] = tile[tx][ty + i];
+    }
+}
+
+constexpr int MAXD = 8;
+struct Dims {
+    int64_t v[MAXD];
+};
+
+__global__ __launch_bounds__(BLOCK) void permute_kernel(const float* __restrict__ x,
+                                                        float* __restrict__ y, Dims new_shape,
+                                                        Dims old_stride_of_new, int ndim,
+                                                        int64_t total) {
+    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (f >= total) return;
+    int64_t rem = f, src = 0;
+    for (int d = ndim - 1; d >= 0; --d) {
+        const int64_t c = rem % new_shape.v[d];
+        rem /= new_shape.v[d];
+        src += c * old_stride_of_new.v[d];
+    }
+    y[f] = x[src];
+}
+
+__global__ __launch_bounds__(BLOCK) void broadcast_kernel(const float* __restrict__ x,
+                                                          float* __restrict__ y, Dims out_shape,
+                                                          Dims in_stride, int out_ndim,
+                                                          int64_t total) {
+    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (f >= total) return;
+    int64_t rem = f, src = 0;
+    for (int d = out_ndim - 1; d >= 0; --d) {
+        const int64_t c = rem % out_shape.v[d];
+        rem /= out_shape.v[d];
+        src += c * in_stride.v[d];
+    }
+    y[f] = x[src];
+}
+
+// One thread per output element; sequential fold in the reference's order
+// (reduce_along_axis, cpu_kernels.rs:166-195; Sum folds from -0.0).
+__global__ __launch_bounds__(BLOCK) void reduce_axis_kernel(int kind, const float* __restrict__ x,
+                                                            float* __restrict__ y, int64_t outer,
+                                                            int64_t dim, int64_t inner) {
+    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (f >= outer * inner) return;
+    const int64_t o = f / inner, i = f % inner;
+    const float* p = x + o * dim * inner + i;
+    float v = kind == 2 ? -INFINITY : -0.0f;
+    for (int64_t d = 0; d < dim; ++d) v = kind == 2 ? fmaxf(v, p[d * inner]) : v + p[d * inner];
+    if (kind == 1) v = v / (float)dim;
+    y[f] = v;
+}
+
+// Sequential fold of all elements on one lane (bit-identical to the CPU fold).
+__global__ void reduce_all_seq_kernel(int kind, const float* __restrict__ x, float* __restrict__ y,
+                                      int64_t n) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    float v = kind == 2 ? -INFINITY : -0.0f;
+    for (int64_t i = 0; i < n; ++i) v = kind == 2 ? fmaxf(v, x[i]) : v + x[i];
+    if (kind == 1) v = v / (float)n;
+    y[0] = v;
+}
+
+// Tree reduction for large inputs: per-block partials, then one block folds them.
+__global__ __launch_bounds__(BLOCK) void reduce_partial_kernel(int kind, const float* __restrict__ x,
+                                                               float* __restrict__ part, int64_t n) {
+    __shared__ float sm[BLOCK];
+    float v = kind == 2 ? -INFINITY : 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n; i += (int64_t)gridDim.x * BLOCK)
+        v = kind == 2 ? fmaxf(v, x[i]) : v + x[i];
+    sm[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = BLOCK / 2; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o)
+            sm[threadIdx.x] = kind == 2 ? fmaxf(sm[threadIdx.x], sm[threadIdx.x + o])
+                                        : sm[threadIdx.x] + sm[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = sm[0];
+}
+
+__global__ __launch_bounds__(BLOCK) void reduce_final_kernel(int kind, const float* __restrict__ part,
+                                                             float* __restrict__ y, int np, int64_t n) {
+    __shared__ float sm[BLOCK];
+    float v = kind == 2 ? -INFINITY : 0.0f;
+    for (int i = threadIdx.x; i < np; i += BLOCK) v = kind == 2 ? fmaxf(v, part[i]) : v + part[i];
+    sm[threadIdx.x] = v;
+    __syncthreads();
+    for (int o = BLOCK / 2; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o)
+            sm[threadIdx.x] = kind == 2 ? fmaxf(sm[threadIdx.x], sm[threadIdx.x + o])
+                                        : sm[threadIdx.x] + sm[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) y[0] = kind == 1 ? sm[0] / (float)n : sm[0];
+}
+
+__device__ inline uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__global__ __launch_bounds__(BLOCK) void cast_kernel(const void* __restrict__ x, int src,
+                                                     void* __restrict__ y, int dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (i >= n) return;
+    float v;
+    if (src == MLXHIP_DTYPE_F32) v = static_cast<const float*>(x)[i];
+    else if (src == MLXHIP_DTYPE_BF16) v = __uint_as_float((uint32_t)static_cast<const uint16_t*>(x)[i] << 16);
+    else v = (float)static_cast<const _Float16*>(x)[i];
+    if (dst == MLXHIP_DTYPE_F32) static_cast<float*>(y)[i] = v;
+    else if (dst == MLXHIP_DTYPE_BF16) static_cast<uint16_t*>(y)[i] = f32_to_bf16_rne(v);
+    else static_cast<_Float16*>(y)[i] = (_Float16)v;
+}
+
+// Rust's `f as i32`: saturating, NaN -> 0.
+__device__ inline int32_t f2i_sat(float f) {
+    if (f != f) return 0;
+    if (f >= 2147483647.0f) return INT32_MAX;
+    if (f <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)f;
+}
+
+__global__ __launch_bounds__(BLOCK) void embedding_kernel(const float* __restrict__ w,
+                                                          const float* __restrict__ idx,
+                                                          float* __restrict__ y, int64_t n_idx,
+                                                          int64_t num_emb, int64_t dim) {
+    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (f >= n_idx * dim) return;
+    const int64_t i = f / dim, d = f % dim;
+    int64_t row = f2i_sat(idx[i]);
+    row = row < 0 ? 0 : (row > num_emb - 1 ? num_emb - 1 : row);
+    y[f] = w[row * dim + d];
+}
+
+__global__ __launch_bounds__(BLOCK) void narrow_kernel(const float* __restrict__ x,
+                                                       float* __restrict__ y, int64_t outer,
+                                                       int64_t dim, int64_t inner, int64_t start,
+                                                       int64_t length) {
+    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (f >= outer * length * inner) return;
+    const int64_t o = f / (length * inner), r = f % (length * inner);
+    y[f] = x[o * dim * inner + start * inner + r];
+}
+
+__global__ __launch_bounds__(BLOCK) void concat_kernel(const float* __restrict__ x,
+                                                       float* __restrict__ y, int64_t outer,
+                                                       int64_t d, int64_t inner, int64_t total,
+                                                       int64_t at) {
+    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (f >= outer * d * inner) return;
+    const int64_t o = f / (d * inner), r = f % (d * inner);
+    y[o * total * inner + at * inner + r] = x[f];
+}
+
+// OpKind::Rope (cpu_rope, cpu_kernels.rs:608-645): interleaved pairs of the
+// first rotary_dim columns; the rest is copied.
+__global__ __launch_bounds__(BLOCK) void rope_interleaved_kernel(const float* __restrict__ x,
+                                                                 float* __restrict__ y,
+                                                                 int64_t tokens, int64_t hd,
+                                                                 int64_t rd, int64_t pos_offset,
+                                                                 float theta, int64_t len) {
+    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (f >= len) return;
+    const int64_t t = f / hd, c = f % hd;
+    if (t >= tokens || c >= rd) {
+        y[f] = x[f];
+        return;
+    }
+    const int64_t i = c / 2;
+    const float inv_freq = powf(theta, -2.0f * (float)i / (float)rd);
+    const float angle = (float)(pos_offset + t) * inv_freq;
+    const float sn = sinf(angle), cs = cosf(angle);
+    const int64_t base = t * hd + i * 2;
+    const float x0 = x[base], x1 = x[base + 1];
+    y[f] = (c % 2 == 0) ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
+}
+
+// OpKind::RoPE (rope, cpu_kernels.rs:896-956).
+__global__ __launch_bounds__(BLOCK) void rope_mlx_kernel(const float* __restrict__ x,
+                                                         float* __restrict__ y, int64_t n_rows,
+                                                         int64_t hd, int64_t offset, float base,
+                                                         int traditional) {
+    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    const int64_t half = hd / 2;
+    if (f >= n_rows * half) return;
+    const int64_t i = f / half, d = f % half;
+    const float pos = (float)(offset + i);
+    const float th = pos * powf(base, -(2.0f * (float)d / (float)hd));
+    const float ct = cosf(th), st = sinf(th);
+    int64_t i0, i1;
+    if (traditional) {
+        i0 = i * hd + 2 * d;
+        i1 = i0 + 1;
+    } else {
+        i0 = i * hd + d;
+        i1 = i * hd + d + half;
+    }
+    const float x0 = x[i0], x1 = x[i1];
+    y[i0] = x0 * ct - x1 * st;
+    y[i1] = x0 * st + x1 * ct;
+}
+
+__global__ __launch_bounds__(BLOCK) void fill_kernel(float* __restrict__ y, float v, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (i < n) y[i] = v;
+}
+
+inline unsigned grid_for(int64_t n) { return (unsigned)ceil_div(n, BLOCK); }
+
+}  // namespace
+
+int ew_chain(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs, int n_inputs,
+             float* out, int64_t numel, hipStream_t s) {
+    if (n_instr < 0 || n_instr > MLXHIP_EW_MAX_INSTR)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: %d instructions (max %d)", n_instr,
+                    MLXHIP_EW_MAX_INSTR);
+    if (n_inputs < 1 || n_inputs > MLXHIP_EW_MAX_INPUTS)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: %d inputs (1..%d)", n_inputs,
+                    MLXHIP_EW_MAX_INPUTS);
+    if (numel < 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: negative size");
+    EwProg p{};
+    bool aligned = reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    for (int i = 0; i < n_inputs; ++i) {
+        if (!inputs[i] && numel) return fail(MLXHIP_ERR_NULL_PTR, "ew_chain: input %d is null", i);
+        p.in[i] = inputs[i];
+        aligned = aligned && reinterpret_cast<uintptr_t>(inputs[i]) % 16 == 0;
+    }
+    for (int k = 0; k < n_instr; ++k) {
+        if (prog[k].op < 0 || prog[k].op >= MLXHIP_EW_COUNT_)
+            return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: bad op %d", prog[k].op);
+        if (ew_binary(prog[k].op) && (prog[k].operand < 0 || prog[k].operand >= n_inputs))
+            return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: operand %d out of range",
+                        prog[k].operand);
+        p.op[k] = prog[k].op;
+        p.operand[k] = ew_binary(prog[k].op) ? prog[k].operand : 0;
+    }
+    p.n_instr = n_instr;
+    if (numel == 0) return MLXHIP_OK;
+    int64_t done = 0;
+    if (aligned) {
+        constexpr int U = 4;
+        const int64_t n_vec = numel / 4;
+        if (n_vec > 0) {
+            int64_t grid = ceil_div(n_vec, (int64_t)BLOCK * U);
+            if (grid > 65536) grid = 65536;
+            hipLaunchKernelGGL((ew_chain_vec_kernel<U>), dim3((unsigned)grid), dim3(BLOCK), 0, s, p,
+                               out, n_vec);
+            MLXHIP_TRY(launch_check("ew_chain_vec_kernel"));
+        }
+        done = n_vec * 4;
+    }
+    if (done < numel) {
+        hipLaunchKernelGGL(ew_chain_scalar_kernel, dim3(grid_for(numel - done)), dim3(BLOCK), 0, s,
+                           p, out, done, numel);
+        MLXHIP_TRY(launch_check("ew_chain_scalar_kernel"));
+    }
+    return MLXHIP_OK;
+}
+
+int transpose2d(const float* x, float* y, int64_t rows, int64_t cols, hipStream_t s) {
+    if (rows == 0 || cols == 0) return MLXHIP_OK;
+    if (ceil_div(rows, 64) > 65535) {
+        const int64_t shape[2] = {rows, cols}, perm[2] = {1, 0};
+        return permute(x, y, shape, perm, 2, s);
+    }
+    dim3 grid((unsigned)ceil_div(cols, 64), (unsigned)ceil_div(rows, 64));
+    hipLaunchKernelGGL(transpose2d_kernel, grid, dim3(BLOCK), 0, s, x, y, rows, cols);
+    return launch_check("transpose2d_kernel");
+}
+
+int permute(const float* x, float* y, const int64_t* shape, const int64_t* perm, int ndim,
+            hipStream_t s) {
+    if (ndim > MAXD) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "permute: rank %d > %d", ndim, MAXD);
+    int64_t total = 1;
+    for (int i = 0; i < ndim; ++i) total *= shape[i];
+    if (total == 0) return MLXHIP_OK;
+    if (ndim == 2 && perm[0] == 1 && perm[1] == 0 && ceil_div(shape[0], 64) <= 65535)
+        return transpose2d(x, y, shape[0], shape[1], s);
+    int64_t old_stride[MAXD];
+    old_stride[ndim - 1] = 1;
+    for (int i = ndim - 2; i >= 0; --i) old_stride[i] = old_stride[i + 1] * shape[i + 1];
+    Dims ns{}, st{};
+    bool seen[MAXD] = {};
+    for (int i = 0; i < ndim; ++i) {
+        // A repeated axis would index past the input: only true permutations run.
+        if (perm[i] < 0 || perm[i] >= ndim || seen[perm[i]])
+            return fail(MLXHIP_ERR_INVALID_ARGUMENT, "transpose: axes must be a permutation of 0..%d", ndim - 1);
+        seen[perm[i]] = true;
+        ns.v[i] = shape[perm[i]];
+        st.v[i] = old_stride[perm[i]];
+    }
+    hipLaunchKernelGGL(permute_kernel, dim3(grid_for(total)), dim3(BLOCK), 0, s, x, y, ns, st, ndim,
+                       total);
+    return launch_check("permute_kernel");
+}
+
+int broadcast(const float* x, float* y, const int64_t* in_shape, int in_ndim,
+              const int64_t* out_shape, int out_ndim, hipStream_t s) {
+    if (out_ndim > MAXD || in_ndim > out_ndim)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "broadcast: ranks %d -> %d", in_ndim, out_ndim);
+    int64_t total = 1;
+    for (int i = 0; i < out_ndim; ++i) total *= out_shape[i];
+    if (total == 0) return MLXHIP_OK;
+    Dims os{}, st{};
+    const int pad = out_ndim - in_ndim;
+    int64_t stride = 1;
+    for (int d = out_ndim - 1; d >= 0; --d) {
+        os.v[d] = out_shape[d];
+        if (d >= pad) {
+            const int64_t idim = in_shape[d - pad];
+            if (idim != 1 && idim != out_shape[d])
+                return fail(MLXHIP_ERR_INVALID_ARGUMENT, "broadcast: dim %lld vs %lld",
+                            (long long)idim, (long long)out_shape[d]);
+            st.v[d] = idim == 1 ? 0 : stride;
+            stride *= idim;
+        } else {
+            st.v[d] = 0;
+        }
+    }
+    hipLaunchKernelGGL(broadcast_kernel, dim3(grid_for(total)), dim3(BLOCK), 0, s, x, y, os, st,
+                       out_ndim, total);
+    return launch_check("broadcast_kernel");
+}
+
+int reduce_axis(int kind, const float* x, float* y, int64_t outer, int64_t dim, int64_t inner,
+                hipStream_t s) {
+    const int64_t n = outer * inner;
+    if (n == 0) return MLXHIP_OK;
+    hipLaunchKernelGGL(reduce_axis_kernel, dim3(grid_for(n)), dim3(BLOCK), 0, s, kind, x, y, outer,
+                       dim, inner);
+    return launch_check("reduce_axis_kernel");
+}
+
+// Scratch for the tree reduction: a per-device partials buffer, grown on
+// demand and kept for the process lifetime.
+static float* partials(int need) {
+    static thread_local float* buf[64] = {};
+    static thread_local int cap[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (cap[dev] < need) {
+        if (buf[dev]) (void)hipFree(buf[dev]);
+        buf[dev] = nullptr;
+        cap[dev] = 0;
+        if (hipMalloc(&buf[dev], sizeof(float) * need) != hipSuccess) return nullptr;
+        cap[dev] = need;
+    }
+    return buf[dev];
+}
+
+int reduce_all(int kind, const float* x, float* y, int64_t n, hipStream_t s) {
+    if (n <= 65536) {
+        hipLaunchKernelGGL(reduce_all_seq_kernel, dim3(1), dim3(64), 0, s, kind, x, y, n);
+        return launch_check("reduce_all_seq_kernel");
+    }
+    const int np = 1024;
+    float* part = partials(np);
+    if (!part) return fail(MLXHIP_ERR_FFI_FAILED, "reduce_all: scratch allocation failed");
+    hipLaunchKernelGGL(reduce_partial_kernel, dim3(np), dim3(BLOCK), 0, s, kind, x, part, n);
+    MLXHIP_TRY(launch_check("reduce_partial_kernel"));
+    hipLaunchKernelGGL(reduce_final_kernel, dim3(1), dim3(BLOCK), 0, s, kind, part, y, np, n);
+    return launch_check("reduce_final_kernel");
+}
+
+int cast(const void* x, int src, void* y, int dst, int64_t n, hipStream_t s) {
+    auto ok = [](int t) { return t == MLXHIP_DTYPE_F32 || t == MLXHIP_DTYPE_BF16 || t == MLXHIP_DTYPE_F16; };
+    if (!ok(src) || !ok(dst)) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "cast: unsupported dtype");
+    if (n == 0) return MLXHIP_OK;
+    hipLaunchKernelGGL(cast_kernel, dim3(grid_for(n)), dim3(BLOCK), 0, s, x, src, y, dst, n);
+    return launch_check("cast_kernel");
+}
+
+int embedding(const float* w, const float* idx, float* y, int64_t n_idx, int64_t num_emb,
+              int64_t dim, hipStream_t s) {
+    if (n_idx * dim == 0) return MLXHIP_OK;
+    if (num_emb <= 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "embedding: empty table");
+    hipLaunchKernelGGL(embedding_kernel, dim3(grid_for(n_idx * dim)), dim3(BLOCK), 0, s, w, idx, y,
+                       n_idx, num_emb, dim);
+    return launch_check("embedding_kernel");
+}
+
+int narrow(const float* x, float* y, int64_t outer, int64_t dim, int64_t inner, int64_t start,
+           int64_t length, hipStream_t s) {
+    const int64_t n = outer * length * inner;
+    if (n == 0) return MLXHIP_OK;
+    hipLaunchKernelGGL(narrow_kernel, dim3(grid_for(n)), dim3(BLOCK), 0, s, x, y, outer, dim, inner,
+                       start, length);
+    return launch_check("narrow_kernel");
+}
+
+int concat_part(const float* x, float* y, int64_t outer, int64_t d, int64_t inner, int64_t total,
+                int64_t at, hipStream_t s) {
+    const int64_t n = outer * d * inner;
+    if (n == 0) return MLXHIP_OK;
+    hipLaunchKernelGGL(concat_kernel, dim3(grid_for(n)), dim3(BLOCK), 0, s, x, y, outer, d, inner,
+                       total, at);
+    return launch_check("concat_kernel");
+}
+
+int rope_interleaved(const float* x, float* y, int64_t tokens, int64_t head_dim,
+                     int64_t rotary_dim, int64_t pos_offset, float theta, int64_t len,
+                     hipStream_t s) {
+    if (len == 0) return MLXHIP_OK;
+    hipLaunchKernelGGL(rope_interleaved_kernel, dim3(grid_for(len)), dim3(BLOCK), 0, s, x, y,
+                       tokens, head_dim, rotary_dim, pos_offset, theta, len);
+    return launch_check("rope_interleaved_kernel");
+}
+
+int rope_mlx(const float* x, float* y, int64_t n_rows, int64_t head_dim, int64_t offset, float base,
+             int traditional, hipStream_t s) {
+    const int64_t n = n_rows * (head_dim / 2);
+    if (n == 0) return MLXHIP_OK;
+    hipLaunchKernelGGL(rope_mlx_kernel, dim3(grid_for(n)), dim3(BLOCK), 0, s, x, y, n_rows, head_dim,
+                       offset, base, traditional);
+    return launch_check("rope_mlx_kernel");
+}
+
+int fill(float* y, float v, int64_t n, hipStream_t s) {
+    if (n == 0) return MLXHIP_OK;
+    hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(BLOCK), 0, s, y, v, n);
+    return launch_check("fill_kernel");
+}
+
+}  // namespace mlxhip

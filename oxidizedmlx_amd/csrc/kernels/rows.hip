@@ -1,0 +1,463 @@
+// rows.hip — row-wise reductions over the last axis of a row-major f32
+// matrix: softmax, scaled-masked softmax, LayerNorm, RMSNorm and the VJPs of
+// softmax / LayerNorm / RMSNorm.
+//
+// Reference semantics (crates/mlx-core/src/cpu_kernels.rs):
+//   softmax               :276-315   m = max; e = exp(x - m); s = sum e; y = e / s
+//   scaled_masked_softmax :671-712   x*scale, -1e9 where causal && col > row, softmax
+//   layer_norm            :338-363   mean; var = mean((x-mean)^2); y = (x-mean)/sqrt(var+eps)
+//   rms_norm              :647-669   y = x / sqrt(mean(x^2) + eps)
+//   softmax_vjp           :515-553   dx = s * (dy - sum(dy*s))
+//   layer_norm_vjp        :403-454
+//   rms_norm_vjp          :462-510
+// The arithmetic per element is the reference's (divide where it divides, no
+// contraction into FMA); only the summation order differs (per-lane partial
+// sums, then a butterfly across the wavefront and across waves).
+//
+// Layout / launch (CDNA4, wave64): a row is owned by WPR wavefronts (64*WPR
+// lanes). Each lane keeps NV vectors of VEC floats of the row in VGPRs, so
+// the row is read from HBM once and written once. Lane t of the row reads
+// vector j at element (j*64*WPR + t)*VEC: consecutive lanes touch consecutive
+// 16-byte words (dwordx4, fully coalesced). A 256-thread workgroup holds
+// 4/WPR rows. Rows longer than 64*WPR*NV*VEC fall back to a streaming
+// kernel that re-reads the row (three passes).
+#include "../common.hpp"
+#include "../kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace mlxhip {
+namespace {
+
+constexpr int WAVE = 64;
+constexpr int BLOCK = 256;
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+// Reduction across the WPR waves that share a row. `slot` is this row's
+// LDS slot array (WPR floats); every lane of the row gets the same value.
+template <int WPR, bool MAX>
+__device__ inline float row_reduce(float v, float* slot, int wave_in_row, int lane) {
+    v = MAX ? wave_max(v) : wave_sum(v);
+    if constexpr (WPR > 1) {
+        __syncthreads();  // previous readers of `slot` are done
+        if (lane == 0) slot[wave_in_row] = v;
+        __syncthreads();
+        float r = slot[0];
+#pragma unroll
+        for (int w = 1; w < WPR; ++w) r = MAX ? fmaxf(r, slot[w]) : r + slot[w];
+        v = r;
+    }
+    return v;
+}
+
+template <int VEC>
+struct Vec;
+template <>
+struct Vec<4> {
+    using T = float4;
+    static __device__ inline void load(const float* p, float* d) {
+        float4 t = *reinterpret_cast<const float4*>(p);
+        d[0] = t.x; d[1] = t.y; d[2] = t.z; d[3] = t.w;
+    }
+    static __device__ inline void store(float* p, const float* d) {
+        *reinterpret_cast<float4*>(p) = make_float4(d[0], d[1], d[2], d[3]);
+    }
+};
+template <>
+struct Vec<1> {
+    static __device__ inline void load(const float* p, float* d) { d[0] = *p; }
+    static __device__ inline void store(float* p, const float* d) { *p = d[0]; }
+};
+
+// a: x (forward) or dy (VJP); b: second operand of a VJP (softmax output s,
+// or the forward input x). p: eps or scale.
+template <int OP, int WPR, int NV, int VEC>
+__global__ __launch_bounds__(BLOCK) void row_kernel(const float* __restrict__ a,
+                                                    const float* __restrict__ b,
+                                                    float* __restrict__ y, int64_t rows,
+                                                    int cols, float p, int causal) {
+    constexpr int ROWS_PER_BLOCK = BLOCK / (WAVE * WPR);
+    constexpr int TPR = WAVE * WPR;  // threads per row
+    constexpr int N = NV * VEC;
+    constexpr bool TWO = (OP == ROW_SOFTMAX_VJP || OP == ROW_LAYERNORM_VJP || OP == ROW_RMSNORM_VJP);
+    __shared__ float red[ROWS_PER_BLOCK][WPR > 1 ? WPR : 1];
+
+    const int tid = threadIdx.x;
+    const int row_in_block = tid / TPR;
+    const int t = tid % TPR;
+    const int lane = tid % WAVE;
+    const int wave_in_row = t / WAVE;
+    const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + row_in_block;
+    // Rows past the end still take part in the block barriers.
+    const bool live = row < rows;
+    float* slot = red[row_in_block];
+
+    const float* ar = a + (live ? row : 0) * (int64_t)cols;
+    const float* br = TWO ? b + (live ? row : 0) * (int64_t)cols : nullptr;
+
+    float v[N];
+    float w[TWO ? N : 1];
+    bool ok[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * TPR + t) * VEC;
+        ok[j] = live && c < cols;
+        if (ok[j]) {
+            Vec<VEC>::load(ar + c, &v[j * VEC]);
+            if constexpr (TWO) Vec<VEC>::load(br + c, &w[j * VEC]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                v[j * VEC + e] = 0.0f;
+                if constexpr (TWO) w[j * VEC + e] = 0.0f;
+            }
+        }
+    }
+    const float d = (float)cols;
+
+    if constexpr (OP == ROW_SOFTMAX || OP == ROW_SCALED_MASKED_SOFTMAX) {
+        if constexpr (OP == ROW_SCALED_MASKED_SOFTMAX) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    const int c = (j * TPR + t) * VEC + e;
+                    float x = v[j * VEC + e] * p;
+                    if (causal && (int64_t)c > row) x = -1e9f;
+                    v[j * VEC + e] = x;
+                }
+        }
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (ok[j])
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) m = fmaxf(m, v[j * VEC + e]);
+        m = row_reduce<WPR, true>(m, slot, wave_in_row, lane);
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                float ex = ok[j] ? expf(v[j * VEC + e] - m) : 0.0f;
+                v[j * VEC + e] = ex;
+                s += ex;
+            }
+        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = v[j] / s;
+    } else if constexpr (OP == ROW_LAYERNORM) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) s += v[j];
+        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+        const float mean = s / d;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (ok[j])
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    float dv = v[j * VEC + e] - mean;
+                    q += dv * dv;
+                }
+        q = row_reduce<WPR, false>(q, slot, wave_in_row, lane);
+        const float var = q / d;
+        const float sd = sqrtf(var + p);
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = (v[j] - mean) / sd;
+    } else if constexpr (OP == ROW_RMSNORM) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) s += v[j] * v[j];
+        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+        const float rms = sqrtf(s / d + p);
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = v[j] / rms;
+    } else if constexpr (OP == ROW_SOFTMAX_VJP) {
+        // v = dy, w = s
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) dot += v[j] * w[j];
+        dot = row_reduce<WPR, false>(dot, slot, wave_in_row, lane);
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = w[j] * (v[j] - dot);
+    } else if constexpr (OP == ROW_LAYERNORM_VJP) {
+        // v = dy, w = x
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) s += w[j];
+        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+        const float mean = s / d;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (ok[j])
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    float dv = w[j * VEC + e] - mean;
+                    q += dv * dv;
+                }
+        q = row_reduce<WPR, false>(q, slot, wave_in_row, lane);
+        const float var = q / d;
+        const float inv_std = 1.0f / sqrtf(var + p);
+        float sdy = 0.0f, sdx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (ok[j])
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    float xh = (w[j * VEC + e] - mean) * inv_std;
+                    w[j * VEC + e] = xh;
+                    sdy += v[j * VEC + e];
+                    sdx += v[j * VEC + e] * xh;
+                }
+        sdy = row_reduce<WPR, false>(sdy, slot, wave_in_row, lane);
+        sdx = row_reduce<WPR, false>(sdx, slot, wave_in_row, lane);
+        const float mdy = sdy / d, mdx = sdx / d;
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = inv_std * (v[j] - mdy - w[j] * mdx);
+    } else if constexpr (OP == ROW_RMSNORM_VJP) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) s += w[j] * w[j];
+        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+        const float inv_rms = 1.0f / sqrtf(s / d + p);
+        float sdy = 0.0f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            w[j] = w[j] * inv_rms;
+            sdy += v[j] * w[j];
+        }
+        sdy = row_reduce<WPR, false>(sdy, slot, wave_in_row, lane);
+        const float m = sdy / d;
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] = inv_rms * (v[j] - w[j] * m);
+    }
+
+    float* yr = y + (live ? row : 0) * (int64_t)cols;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * TPR + t) * VEC;
+        if (ok[j]) Vec<VEC>::store(yr + c, &v[j * VEC]);
+    }
+}
+
+// Streaming fallback for rows longer than the register-resident kernels hold:
+// one 256-thread block per row, the row is read in three passes.
+template <int OP>
+__global__ __launch_bounds__(BLOCK) void row_stream_kernel(const float* __restrict__ a,
+                                                           const float* __restrict__ b,
+                                                           float* __restrict__ y, int64_t rows,
+                                                           int64_t cols, float p, int causal) {
+    __shared__ float red[BLOCK / WAVE];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid % WAVE, wv = tid / WAVE;
+    const float* ar = a + row * cols;
+    const float* br = b ? b + row * cols : nullptr;
+    float* yr = y + row * cols;
+    const float d = (float)cols;
+    auto block_reduce = [&](float v, bool mx) -> float {
+        v = mx ? wave_max(v) : wave_sum(v);
+        __syncthreads();
+        if (lane == 0) red[wv] = v;
+        __syncthreads();
+        float r = red[0];
+        for (int w = 1; w < BLOCK / WAVE; ++w) r = mx ? fmaxf(r, red[w]) : r + red[w];
+        return r;
+    };
+    auto xin = [&](int64_t c) -> float {
+        float x = ar[c];
+        if (OP == ROW_SCALED_MASKED_SOFTMAX) {
+            x = x * p;
+            if (causal && c > row) x = -1e9f;
+        }
+        return x;
+    };
+    if (OP == ROW_SOFTMAX || OP == ROW_SCALED_MASKED_SOFTMAX) {
+        float m = -INFINITY;
+        for (int64_t c = tid; c < cols; c += BLOCK) m = fmaxf(m, xin(c));
+        m = block_reduce(m, true);
+        float s = 0.0f;
+        for (int64_t c = tid; c < cols; c += BLOCK) s += expf(xin(c) - m);
+        s = block_reduce(s, false);
+        for (int64_t c = tid; c < cols; c += BLOCK) yr[c] = expf(xin(c) - m) / s;
+    } else if (OP == ROW_LAYERNORM || OP == ROW_LAYERNORM_VJP) {
+        const float* xr = OP == ROW_LAYERNORM ? ar : br;
+        float s = 0.0f;
+        for (int64_t c = tid; c < cols; c += BLOCK) s += xr[c];
+        const float mean = block_reduce(s, false) / d;
+        float q = 0.0f;
+        for (int64_t c = tid; c < cols; c += BLOCK) {
+            float dv = xr[c] - mean;
+            q += dv * dv;
+        }
+        const float var = block_reduce(q, false) / d;
+        const float sd = sqrtf(var + p);
+        if (OP == ROW_LAYERNORM) {
+            for (int64_t c = tid; c < cols; c += BLOCK) yr[c] = (xr[c] - mean) / sd;
+        } else {
+            const float inv = 1.0f / sd;
+            float sdy = 0.0f, sdx = 0.0f;
+            for (int64_t c = tid; c < cols; c += BLOCK) {
+                sdy += ar[c];
+                sdx += ar[c] * ((xr[c] - mean) * inv);
+            }
+            const float mdy = block_reduce(sdy, false) / d;
+            const float mdx = block_reduce(sdx, false) / d;
+            for (int64_t c = tid; c < cols; c += BLOCK)
+                yr[c] = inv * (ar[c] - mdy - ((xr[c] - mean) * inv) * mdx);
+        }
+    } else if (OP == ROW_RMSNORM || OP == ROW_RMSNORM_VJP) {
+        const float* xr = OP == ROW_RMSNORM ? ar : br;
+        float s = 0.0f;
+        for (int64_t c = tid; c < cols; c += BLOCK) s += xr[c] * xr[c];
+        s = block_reduce(s, false);
+        if (OP == ROW_RMSNORM) {
+            const float rms = sqrtf(s / d + p);
+            for (int64_t c = tid; c < cols; c += BLOCK) yr[c] = xr[c] / rms;
+        } else {
+            const float inv = 1.0f / sqrtf(s / d + p);
+            float sdy = 0.0f;
+            for (int64_t c = tid; c < cols; c += BLOCK) sdy += ar[c] * (xr[c] * inv);
+            const float m = block_reduce(sdy, false) / d;
+            for (int64_t c = tid; c < cols; c += BLOCK) yr[c] = inv * (ar[c] - (xr[c] * inv) * m);
+        }
+    } else if (OP == ROW_SOFTMAX_VJP) {
+        float dot = 0.0f;
+        for (int64_t c = tid; c < cols; c += BLOCK) dot += ar[c] * br[c];
+        dot = block_reduce(dot, false);
+        for (int64_t c = tid; c < cols; c += BLOCK) yr[c] = br[c] * (ar[c] - dot);
+    }
+}
+
+// Softmax / SoftmaxVjp along a non-last axis: one thread per (outer, inner)
+// fibre walking `dim` with stride `inner` (adjacent threads read adjacent
+// addresses). Same arithmetic as cpu_kernels.rs:293-313 / :538-550.
+template <bool VJP>
+__global__ __launch_bounds__(BLOCK) void fibre_softmax_kernel(const float* __restrict__ a,
+                                                              const float* __restrict__ b,
+                                                              float* __restrict__ y,
+                                                              int64_t outer, int64_t dim,
+                                                              int64_t inner) {
+    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+    if (f >= outer * inner) return;
+    const int64_t o = f / inner, i = f % inner;
+    const int64_t base = o * dim * inner + i;
+    if (!VJP) {
+        float m = -INFINITY;
+        for (int64_t d = 0; d < dim; ++d) m = fmaxf(m, a[base + d * inner]);
+        float s = 0.0f;
+        for (int64_t d = 0; d < dim; ++d) s += expf(a[base + d * inner] - m);
+        for (int64_t d = 0; d < dim; ++d) y[base + d * inner] = expf(a[base + d * inner] - m) / s;
+    } else {
+        float dot = 0.0f;
+        for (int64_t d = 0; d < dim; ++d) dot += a[base + d * inner] * b[base + d * inner];
+        for (int64_t d = 0; d < dim; ++d)
+            y[base + d * inner] = b[base + d * inner] * (a[base + d * inner] - dot);
+    }
+}
+
+template <int OP, int WPR, int NV, int VEC>
+int launch_rows(const float* a, const float* b, float* y, int64_t rows, int64_t cols, float p,
+                int causal, hipStream_t s) {
+    constexpr int RPB = BLOCK / (WAVE * WPR);
+    const int64_t grid = ceil_div(rows, RPB);
+    hipLaunchKernelGGL((row_kernel<OP, WPR, NV, VEC>), dim3((unsigned)grid), dim3(BLOCK), 0, s, a,
+                       b, y, rows, (int)cols, p, causal);
+    return launch_check("row_kernel");
+}
+
+template <int OP>
+int dispatch_rows(const float* a, const float* b, float* y, int64_t rows, int64_t cols, float p,
+                  int causal, hipStream_t s, int force_wpr) {
+    const bool two = (OP == ROW_SOFTMAX_VJP || OP == ROW_LAYERNORM_VJP || OP == ROW_RMSNORM_VJP);
+    const bool vec4 = (cols % 4 == 0) && (reinterpret_cast<uintptr_t>(a) % 16 == 0) &&
+                      (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
+                      (!two || reinterpret_cast<uintptr_t>(b) % 16 == 0);
+    if (vec4) {
+        // One wave per row up to 4096 columns (64 lanes x 16 float4), unless a
+        // wider row group is forced for tuning.
+        if (force_wpr <= 1) {
+            if (cols <= 256) return launch_rows<OP, 1, 1, 4>(a, b, y, rows, cols, p, causal, s);
+            if (cols <= 512) return launch_rows<OP, 1, 2, 4>(a, b, y, rows, cols, p, causal, s);
+            if (cols <= 1024) return launch_rows<OP, 1, 4, 4>(a, b, y, rows, cols, p, causal, s);
+            if (cols <= 2048) return launch_rows<OP, 1, 8, 4>(a, b, y, rows, cols, p, causal, s);
+            if (cols <= 4096 && force_wpr == 1)
+                return launch_rows<OP, 1, 16, 4>(a, b, y, rows, cols, p, causal, s);
+        }
+        if (force_wpr == 2 && cols <= 4096)
+            return launch_rows<OP, 2, 8, 4>(a, b, y, rows, cols, p, causal, s);
+        if (cols <= 4096) return launch_rows<OP, 4, 4, 4>(a, b, y, rows, cols, p, causal, s);
+        if (cols <= 8192) return launch_rows<OP, 4, 8, 4>(a, b, y, rows, cols, p, causal, s);
+        if (cols <= 16384) return launch_rows<OP, 4, 16, 4>(a, b, y, rows, cols, p, causal, s);
+    } else {
+        if (cols <= 256) return launch_rows<OP, 4, 1, 1>(a, b, y, rows, cols, p, causal, s);
+        if (cols <= 1024) return launch_rows<OP, 4, 4, 1>(a, b, y, rows, cols, p, causal, s);
+        if (cols <= 4096) return launch_rows<OP, 4, 16, 1>(a, b, y, rows, cols, p, causal, s);
+    }
+    hipLaunchKernelGGL((row_stream_kernel<OP>), dim3((unsigned)rows), dim3(BLOCK), 0, s, a, b, y,
+                       rows, cols, p, causal);
+    return launch_check("row_stream_kernel");
+}
+
+int row_force_wpr() {
+    static int v = [] {
+        const char* e = getenv("MLXHIP_ROW_WPR");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+}  // namespace
+
+int row_op(int op, const float* a, const float* b, float* y, int64_t rows, int64_t cols, float p,
+           int causal, hipStream_t s) {
+    if (rows == 0 || cols == 0) return MLXHIP_OK;
+    if (rows < 0 || cols < 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: negative size");
+    if (rows > (int64_t)INT32_MAX) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: too many rows");
+    if (cols > INT32_MAX) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: row too long");
+    // 0 = auto: one wave per row up to 4096 columns.
+    const int fw = row_force_wpr() ? row_force_wpr() : 1;
+    switch (op) {
+        case ROW_SOFTMAX: return dispatch_rows<ROW_SOFTMAX>(a, b, y, rows, cols, p, causal, s, fw);
+        case ROW_SCALED_MASKED_SOFTMAX:
+            return dispatch_rows<ROW_SCALED_MASKED_SOFTMAX>(a, b, y, rows, cols, p, causal, s, fw);
+        case ROW_LAYERNORM: return dispatch_rows<ROW_LAYERNORM>(a, b, y, rows, cols, p, causal, s, fw);
+        case ROW_RMSNORM: return dispatch_rows<ROW_RMSNORM>(a, b, y, rows, cols, p, causal, s, fw);
+        case ROW_SOFTMAX_VJP:
+            return dispatch_rows<ROW_SOFTMAX_VJP>(a, b, y, rows, cols, p, causal, s, fw);
+        case ROW_LAYERNORM_VJP:
+            return dispatch_rows<ROW_LAYERNORM_VJP>(a, b, y, rows, cols, p, causal, s, fw);
+        case ROW_RMSNORM_VJP:
+            return dispatch_rows<ROW_RMSNORM_VJP>(a, b, y, rows, cols, p, causal, s, fw);
+        default: return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: unknown op %d", op);
+    }
+}
+
+int fibre_softmax(bool vjp, const float* a, const float* b, float* y, int64_t outer, int64_t dim,
+                  int64_t inner, hipStream_t s) {
+    const int64_t n = outer * inner;
+    if (n == 0 || dim == 0) return MLXHIP_OK;
+    const int64_t grid = ceil_div(n, BLOCK);
+    if (vjp)
+        hipLaunchKernelGGL((fibre_softmax_kernel<true>), dim3((unsigned)grid), dim3(BLOCK), 0, s, a,
+                           b, y, outer, dim, inner);
+    else
+        hipLaunchKernelGGL((fibre_softmax_kernel<false>), dim3((unsigned)grid), dim3(BLOCK), 0, s,
+                           a, b, y, outer, dim, inner);
+    return launch_check("fibre_softmax_kernel");
+}
+
+}  // namespace mlxhip

@@ -1,0 +1,492 @@
+// stream.cpp — Stream and Graph bound to HipBackend, with every buffer
+// resident in HBM.
+//
+// Restates Stream (crates/mlx-core/src/backend.rs:37-185) and Graph
+// (crates/mlx-core/src/graph.rs:170-305, CSE rules :495-515):
+//   * add_constant never deduplicates (Constant/Parameter are not CSE
+//     eligible) and materialises the data at once;
+//   * add_op interns with CSE on (op, inputs, meta), Add/Mul inputs ordered
+//     by node id first;
+//   * eval topologically sorts the subgraph of the output and evaluates each
+//     unmaterialised node once; results are memoised until the stream is freed.
+// Differences, all below the Backend seam: buffers live in HBM (host copies
+// only in get_buffer), and with fusion enabled the scheduler looks ahead:
+//   * a chain of elementwise nodes whose intermediates have exactly one
+//     consumer runs as one ew_chain kernel (intermediates are not
+//     materialised; they are recomputed if asked for later);
+//   * a rank-2 Transpose whose only consumer is a MatMul is not
+//     materialised; the GEMM reads its source with the transposed layout.
+// eval_count counts every node a backend call covered, so fused and unfused
+// evaluation report the same count.
+#include <algorithm>
+#include <atomic>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "backend.hpp"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mlxhip {
+namespace {
+
+struct OpVal {
+    mlxhip_op_t op{};
+    std::vector<int64_t> shape, axes;
+    bool has_shape = false, has_axes = false;
+
+    static OpVal from(const mlxhip_op_t& o) {
+        OpVal v;
+        v.op = o;
+        if (o.shape) {
+            v.shape.assign(o.shape, o.shape + o.shape_len);
+            v.has_shape = true;
+        }
+        if (o.axes) {
+            v.axes.assign(o.axes, o.axes + o.axes_len);
+            v.has_axes = true;
+        }
+        return v;
+    }
+    mlxhip_op_t c() const {
+        mlxhip_op_t o = op;
+        o.shape = has_shape ? shape.data() : nullptr;
+        o.shape_len = shape.size();
+        o.axes = has_axes ? axes.data() : nullptr;
+        o.axes_len = axes.size();
+        return o;
+    }
+};
+
+struct MetaVal {
+    std::vector<int64_t> shape;
+    int dtype = MLXHIP_DTYPE_F32;
+    int64_t numel() const { return numel_of(shape.data(), shape.size()); }
+    mlxhip_meta_t c() const { return mlxhip_meta_t{shape.data(), shape.size(), dtype}; }
+};
+
+struct Node {
+    uint64_t id;
+    OpVal op;
+    std::vector<uint64_t> inputs;
+    MetaVal meta;
+};
+
+struct DevBuf {
+    float* ptr = nullptr;
+    size_t len = 0;
+};
+
+bool is_elementwise(int k) {
+    switch (k) {
+        case MLXHIP_OP_ADD: case MLXHIP_OP_SUB: case MLXHIP_OP_MUL: case MLXHIP_OP_DIV:
+        case MLXHIP_OP_NEG: case MLXHIP_OP_EXP: case MLXHIP_OP_LOG: case MLXHIP_OP_SQRT:
+        case MLXHIP_OP_SILU: case MLXHIP_OP_GELU: case MLXHIP_OP_SILU_VJP: case MLXHIP_OP_GELU_VJP:
+            return true;
+        default: return false;
+    }
+}
+
+bool is_binary(int k) {
+    return k == MLXHIP_OP_ADD || k == MLXHIP_OP_SUB || k == MLXHIP_OP_MUL || k == MLXHIP_OP_DIV ||
+           k == MLXHIP_OP_SILU_VJP || k == MLXHIP_OP_GELU_VJP;
+}
+
+int unary_ew(int k) {
+    switch (k) {
+        case MLXHIP_OP_NEG: return MLXHIP_EW_NEG;
+        case MLXHIP_OP_EXP: return MLXHIP_EW_EXP;
+        case MLXHIP_OP_LOG: return MLXHIP_EW_LOG;
+        case MLXHIP_OP_SQRT: return MLXHIP_EW_SQRT;
+        case MLXHIP_OP_SILU: return MLXHIP_EW_SILU;
+        default: return MLXHIP_EW_GELU;
+    }
+}
+
+// Chain instruction when the running value (acc) is input `acc_idx` of a
+// binary node and the other input is the operand.
+int binary_ew(int k, int acc_idx) {
+    switch (k) {
+        case MLXHIP_OP_ADD: return MLXHIP_EW_ADD;
+        case MLXHIP_OP_MUL: return MLXHIP_EW_MUL;
+        case MLXHIP_OP_SUB: return acc_idx == 0 ? MLXHIP_EW_SUB : MLXHIP_EW_RSUB;
+        case MLXHIP_OP_DIV: return acc_idx == 0 ? MLXHIP_EW_DIV : MLXHIP_EW_RDIV;
+        case MLXHIP_OP_SILU_VJP: return MLXHIP_EW_SILU_VJP;  // acc = x (input 1), operand = dy
+        default: return MLXHIP_EW_GELU_VJP;
+    }
+}
+
+void append_bits(std::string& k, const void* p, size_t n) { k.append(static_cast<const char*>(p), n); }
+
+}  // namespace
+}  // namespace mlxhip
+
+using namespace mlxhip;
+
+struct mlxhip_stream_t {
+    std::mutex mu;  // guards everything below; eval runs under it
+    std::unordered_map<uint64_t, Node> nodes;
+    std::unordered_map<std::string, uint64_t> cse;
+    std::unordered_map<uint64_t, uint32_t> consumers;
+    std::unordered_map<uint64_t, DevBuf> buffers;
+    uint64_t next_id = 1;
+    std::atomic<uint64_t> eval_calls{0};
+    std::atomic<uint64_t> launches{0};
+    bool fusion = true;
+    hipStream_t hs = nullptr;
+    int device = 0;
+
+    ~mlxhip_stream_t() {
+        if (hs) (void)hipStreamSynchronize(hs);
+        for (auto& kv : buffers) pool_release(kv.second.ptr);
+        if (hs) (void)hipStreamDestroy(hs);
+    }
+
+    uint64_t add_node(const OpVal& op, std::vector<uint64_t> inputs, const MetaVal& meta, bool cse_ok) {
+        std::string key;
+        if (cse_ok) {
+            if ((op.op.kind == MLXHIP_OP_ADD || op.op.kind == MLXHIP_OP_MUL) && inputs.size() == 2 &&
+                inputs[0] > inputs[1])
+                std::swap(inputs[0], inputs[1]);
+            mlxhip_op_t o = op.op;
+            o.shape = nullptr;
+            o.axes = nullptr;
+            append_bits(key, &o, sizeof o);
+            key.push_back(op.has_shape ? 'S' : 's');
+            append_bits(key, op.shape.data(), op.shape.size() * sizeof(int64_t));
+            key.push_back(op.has_axes ? 'A' : 'a');
+            append_bits(key, op.axes.data(), op.axes.size() * sizeof(int64_t));
+            key.push_back('I');
+            append_bits(key, inputs.data(), inputs.size() * sizeof(uint64_t));
+            key.push_back('M');
+            append_bits(key, &meta.dtype, sizeof meta.dtype);
+            append_bits(key, meta.shape.data(), meta.shape.size() * sizeof(int64_t));
+            auto it = cse.find(key);
+            if (it != cse.end()) return it->second;
+        }
+        const uint64_t id = next_id++;
+        for (uint64_t in : inputs) consumers[in]++;
+        nodes.emplace(id, Node{id, op, std::move(inputs), meta});
+        if (cse_ok) cse.emplace(std::move(key), id);
+        return id;
+    }
+
+    // Depth-first post-order of the subgraph rooted at `out` (graph.rs:268-294),
+    // iterative so deep graphs cannot overflow the native stack.
+    std::vector<uint64_t> topo_sort(uint64_t out) {
+        std::vector<uint64_t> order;
+        std::unordered_set<uint64_t> visited;
+        std::vector<std::pair<uint64_t, size_t>> st;
+        visited.insert(out);
+        st.emplace_back(out, 0);
+        while (!st.empty()) {
+            auto& top = st.back();
+            auto it = nodes.find(top.first);
+            if (it != nodes.end() && top.second < it->second.inputs.size()) {
+                const uint64_t nxt = it->second.inputs[top.second++];
+                if (visited.insert(nxt).second) st.emplace_back(nxt, 0);
+            } else {
+                order.push_back(top.first);
+                st.pop_back();
+            }
+        }
+        return order;
+    }
+
+    mlxhip_input_t input_of(uint64_t id, const float* data) {
+        const Node& n = nodes.at(id);
+        return mlxhip_input_t{data, (size_t)n.meta.numel(), n.meta.shape.data(), n.meta.shape.size(), n.meta.dtype};
+    }
+
+    int alloc_out(uint64_t id, float** out) {
+        const Node& n = nodes.at(id);
+        const size_t len = (size_t)n.meta.numel();
+        float* p = static_cast<float*>(pool_alloc((len ? len : 1) * sizeof(float)));
+        if (!p) return fail(MLXHIP_ERR_FFI_FAILED, "stream: device allocation of %zu floats failed", len);
+        buffers[id] = DevBuf{p, len};
+        *out = p;
+        return MLXHIP_OK;
+    }
+
+    int eval(uint64_t output);
+};
+
+int mlxhip_stream_t::eval(uint64_t output) {
+    if (buffers.count(output)) return MLXHIP_OK;
+    if (!nodes.count(output)) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "missing graph node");
+    const std::vector<uint64_t> order = topo_sort(output);
+    std::unordered_set<uint64_t> in_order(order.begin(), order.end());
+
+    // ── look-ahead planning ──────────────────────────────────────────────
+    std::unordered_set<uint64_t> folded_transpose;                  // not materialised
+    std::unordered_map<uint64_t, std::vector<uint64_t>> chain_of;   // chain end -> nodes
+    std::unordered_map<uint64_t, int> acc_input;                    // node -> index of its acc input
+    std::unordered_set<uint64_t> interior;                          // fused, not materialised
+    if (fusion) {
+        for (uint64_t id : order) {
+            if (buffers.count(id)) continue;
+            const Node& n = nodes.at(id);
+            if (n.op.op.kind == MLXHIP_OP_MATMUL && n.inputs.size() == 2) {
+                for (uint64_t in : n.inputs) {
+                    auto it = nodes.find(in);
+                    if (it == nodes.end() || buffers.count(in)) continue;
+                    const Node& t = it->second;
+                    const bool swap2 = t.op.op.kind == MLXHIP_OP_TRANSPOSE && t.meta.shape.size() == 2 &&
+                                       (!t.op.has_axes || (t.op.axes.size() == 2 && t.op.axes[0] == 1 && t.op.axes[1] == 0));
+                    if (swap2 && consumers[in] == 1 && n.inputs[0] != n.inputs[1] && !t.inputs.empty())
+                        folded_transpose.insert(in);
+                }
+            }
+        }
+        for (uint64_t id : order) {
+            if (buffers.count(id) || folded_transpose.count(id)) continue;
+            const Node& n = nodes.at(id);
+            const int k = n.op.op.kind;
+            if (!is_elementwise(k)) continue;
+            const size_t need = is_binary(k) ? 2 : 1;
+            if (n.inputs.size() < need) continue;  // let eval report the error
+            if (is_binary(k)) {
+                const int64_t l0 = nodes.at(n.inputs[0]).meta.numel(), l1 = nodes.at(n.inputs[1]).meta.numel();
+                if (l0 != l1 || l0 != n.meta.numel()) continue;
+            } else if (nodes.at(n.inputs[0]).meta.numel() != n.meta.numel()) {
+                continue;
+            }
+            // Candidate acc inputs: the running value of the chain.
+            std::vector<int> cand;
+            if (k == MLXHIP_OP_SILU_VJP || k == MLXHIP_OP_GELU_VJP) cand = {1};
+            else if (is_binary(k)) cand = {0, 1};
+            else cand = {0};
+            int chosen = -1;
+            for (int c : cand) {
+                const uint64_t in = n.inputs[c];
+                if (is_binary(k) && n.inputs[0] == n.inputs[1]) break;  // x op x: keep both operands materialised
+                if (!in_order.count(in) || buffers.count(in) || folded_transpose.count(in)) continue;
+                auto ch = chain_of.find(in);
+                if (ch == chain_of.end() || consumers[in] != 1) continue;
+                // Limits of one ew_chain launch: instructions and distinct inputs.
+                if (ch->second.size() + 1 > MLXHIP_EW_MAX_INSTR) continue;
+                std::unordered_set<uint64_t> ins;
+                for (uint64_t m : ch->second) {
+                    const Node& mn = nodes.at(m);
+                    if (m == ch->second.front()) ins.insert(mn.inputs[acc_input[m]]);
+                    if (is_binary(mn.op.op.kind)) ins.insert(mn.inputs[1 - acc_input[m]]);
+                }
+                if (is_binary(k)) ins.insert(n.inputs[1 - c]);
+                if (ins.size() > MLXHIP_EW_MAX_INPUTS) continue;
+                chosen = c;
+                break;
+            }
+            if (chosen >= 0) {
+                const uint64_t prev = n.inputs[chosen];
+                std::vector<uint64_t> ch = std::move(chain_of[prev]);
+                chain_of.erase(prev);
+                interior.insert(prev);
+                ch.push_back(id);
+                acc_input[id] = chosen;
+                chain_of[id] = std::move(ch);
+            } else {
+                acc_input[id] = cand[0];
+                chain_of[id] = {id};
+            }
+        }
+    }
+
+    // ── evaluation ────────────────────────────────────────────────────────
+    Scratch scratch;
+    int rc = MLXHIP_OK;
+    for (uint64_t id : order) {
+        if (buffers.count(id) || folded_transpose.count(id) || interior.count(id)) continue;
+        const Node& n = nodes.at(id);
+        auto ch = chain_of.find(id);
+        if (ch != chain_of.end() && ch->second.size() > 1) {
+            // One fused kernel for the whole chain.
+            const std::vector<uint64_t>& nodes_in_chain = ch->second;
+            std::vector<const float*> ins;
+            std::vector<uint64_t> in_ids;
+            auto slot = [&](uint64_t src) -> int {
+                for (size_t i = 0; i < in_ids.size(); ++i)
+                    if (in_ids[i] == src) return (int)i;
+                in_ids.push_back(src);
+                ins.push_back(buffers.at(src).ptr);
+                return (int)in_ids.size() - 1;
+            };
+            const Node& first = nodes.at(nodes_in_chain.front());
+            const uint64_t base = first.inputs[acc_input[nodes_in_chain.front()]];
+            if (!buffers.count(base)) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "fusion: base not materialised"); break; }
+            slot(base);
+            std::vector<mlxhip_ew_instr_t> prog;
+            for (uint64_t m : nodes_in_chain) {
+                const Node& mn = nodes.at(m);
+                const int k = mn.op.op.kind;
+                if (is_binary(k)) {
+                    const int ai = acc_input[m];
+                    const uint64_t other = mn.inputs[1 - ai];
+                    if (!buffers.count(other)) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "fusion: operand not materialised"); break; }
+                    prog.push_back({binary_ew(k, ai), slot(other)});
+                } else {
+                    prog.push_back({unary_ew(k), 0});
+                }
+            }
+            if (rc != MLXHIP_OK) break;
+            float* out = nullptr;
+            if ((rc = alloc_out(id, &out)) != MLXHIP_OK) break;
+            rc = ew_chain(prog.data(), (int)prog.size(), ins.data(), (int)ins.size(), out, n.meta.numel(), hs);
+            eval_calls += nodes_in_chain.size();
+            launches += 1;
+            if (rc != MLXHIP_OK) {
+                pool_release(out);
+                buffers.erase(id);
+                break;
+            }
+            continue;
+        }
+        // Single node through HipBackend::eval_node.
+        std::vector<mlxhip_input_t> ins;
+        int hint[2] = {0, 0};
+        bool missing = false;
+        for (size_t i = 0; i < n.inputs.size(); ++i) {
+            uint64_t src = n.inputs[i];
+            if (folded_transpose.count(src) && n.op.op.kind == MLXHIP_OP_MATMUL && i < 2) {
+                hint[i] = 1;
+                src = nodes.at(src).inputs[0];
+            }
+            auto b = buffers.find(src);
+            if (b == buffers.end()) { missing = true; break; }
+            ins.push_back(input_of(src, b->second.ptr));
+        }
+        if (missing) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "input node should be evaluated before dependents"); break; }
+        float* out = nullptr;
+        if ((rc = alloc_out(id, &out)) != MLXHIP_OK) break;
+        const mlxhip_op_t op = n.op.c();
+        const mlxhip_meta_t meta = n.meta.c();
+        eval_calls += 1 + (hint[0] + hint[1]);
+        launches += 1;
+        rc = eval_node_device(op, ins.data(), ins.size(), meta, out, hs, scratch, hint);
+        if (rc != MLXHIP_OK) {
+            pool_release(out);
+            buffers.erase(id);
+            break;
+        }
+    }
+    // Scratch may only return to the pool after the kernels using it finish.
+    hipError_t e = hipStreamSynchronize(hs);
+    if (rc == MLXHIP_OK && e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    return rc;
+}
+
+extern "C" {
+
+mlxhip_stream_t* mlxhip_stream_new(void) {
+    if (ensure_device() != MLXHIP_OK) return nullptr;
+    auto* s = new mlxhip_stream_t();
+    (void)hipGetDevice(&s->device);
+    if (hipStreamCreateWithFlags(&s->hs, hipStreamNonBlocking) != hipSuccess) {
+        fail(MLXHIP_ERR_FFI_FAILED, "hipStreamCreate failed");
+        delete s;
+        return nullptr;
+    }
+    return s;
+}
+
+void mlxhip_stream_free(mlxhip_stream_t* s) { delete s; }
+
+static MetaVal meta_from(const mlxhip_meta_t* m) {
+    MetaVal v;
+    if (m->ndim) v.shape.assign(m->shape, m->shape + m->ndim);
+    v.dtype = m->dtype;
+    return v;
+}
+
+uint64_t mlxhip_stream_add_constant(mlxhip_stream_t* s, const float* data, size_t len, const mlxhip_meta_t* meta) {
+    if (!s || !meta || (len && !data)) {
+        fail(MLXHIP_ERR_NULL_PTR, "stream_add_constant: null argument");
+        return 0;
+    }
+    if (meta->ndim && !meta->shape) {
+        fail(MLXHIP_ERR_NULL_PTR, "stream_add_constant: null shape");
+        return 0;
+    }
+    std::lock_guard<std::mutex> g(s->mu);
+    MetaVal mv = meta_from(meta);
+    if ((int64_t)len != mv.numel()) {
+        fail(MLXHIP_ERR_SHAPE_MISMATCH, "stream_add_constant: %zu values for %lld elements", len, (long long)mv.numel());
+        return 0;
+    }
+    mlxhip_op_t op{};
+    op.kind = MLXHIP_OP_CONSTANT;
+    const uint64_t id = s->add_node(OpVal::from(op), {}, mv, false);
+    float* p = static_cast<float*>(pool_alloc((len ? len : 1) * sizeof(float)));
+    if (!p) {
+        fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: device allocation failed");
+        return 0;
+    }
+    if (len && hipMemcpyAsync(p, data, len * sizeof(float), hipMemcpyHostToDevice, s->hs) != hipSuccess) {
+        pool_release(p);
+        fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: upload failed");
+        return 0;
+    }
+    (void)hipStreamSynchronize(s->hs);  // `data` may be freed by the caller right after
+    s->buffers[id] = DevBuf{p, len};
+    return id;
+}
+
+uint64_t mlxhip_stream_add_op(mlxhip_stream_t* s, const mlxhip_op_t* op, const uint64_t* inputs, size_t n_inputs,
+                              const mlxhip_meta_t* meta) {
+    if (!s || !op || !meta || (n_inputs && !inputs) || (meta->ndim && !meta->shape)) {
+        fail(MLXHIP_ERR_NULL_PTR, "stream_add_op: null argument");
+        return 0;
+    }
+    std::lock_guard<std::mutex> g(s->mu);
+    for (size_t i = 0; i < n_inputs; ++i)
+        if (!s->nodes.count(inputs[i])) {
+            fail(MLXHIP_ERR_INVALID_ARGUMENT, "stream_add_op: unknown input node %llu", (unsigned long long)inputs[i]);
+            return 0;
+        }
+    const bool cse_ok = op->kind != MLXHIP_OP_CONSTANT && op->kind != MLXHIP_OP_PARAMETER;
+    return s->add_node(OpVal::from(*op), std::vector<uint64_t>(inputs, inputs + n_inputs), meta_from(meta), cse_ok);
+}
+
+int mlxhip_stream_eval(mlxhip_stream_t* s, uint64_t node) {
+    if (!s) return fail(MLXHIP_ERR_NULL_PTR, "stream_eval: null stream");
+    std::lock_guard<std::mutex> g(s->mu);
+    MLXHIP_HIP(hipSetDevice(s->device));
+    return s->eval(node);
+}
+
+int mlxhip_stream_get_buffer(mlxhip_stream_t* s, uint64_t node, float* out, size_t len) {
+    if (!s || (len && !out)) return fail(MLXHIP_ERR_NULL_PTR, "stream_get_buffer: null argument");
+    std::lock_guard<std::mutex> g(s->mu);
+    auto it = s->buffers.find(node);
+    if (it == s->buffers.end()) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "stream_get_buffer: node not materialised");
+    if (len != it->second.len)
+        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "stream_get_buffer: %zu requested, buffer holds %zu", len, it->second.len);
+    if (!len) return MLXHIP_OK;
+    MLXHIP_HIP(hipSetDevice(s->device));
+    MLXHIP_HIP(hipMemcpyAsync(out, it->second.ptr, len * sizeof(float), hipMemcpyDeviceToHost, s->hs));
+    MLXHIP_HIP(hipStreamSynchronize(s->hs));
+    return MLXHIP_OK;
+}
+
+uint64_t mlxhip_stream_eval_count(const mlxhip_stream_t* s) { return s ? s->eval_calls.load() : 0; }
+
+size_t mlxhip_stream_cache_len(const mlxhip_stream_t* s) {
+    if (!s) return 0;
+    auto* m = const_cast<mlxhip_stream_t*>(s);
+    std::lock_guard<std::mutex> g(m->mu);
+    return m->buffers.size();
+}
+
+uint64_t mlxhip_stream_launch_count(const mlxhip_stream_t* s) { return s ? s->launches.load() : 0; }
+
+int mlxhip_stream_set_fusion(mlxhip_stream_t* s, int enabled) {
+    if (!s) return fail(MLXHIP_ERR_NULL_PTR, "stream_set_fusion: null stream");
+    std::lock_guard<std::mutex> g(s->mu);
+    s->fusion = enabled != 0;
+    return MLXHIP_OK;
+}
+
+}  // extern "C"

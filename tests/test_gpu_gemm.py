@@ -1,0 +1,158 @@
+"""MFMA GEMM through the C ABI vs the CPU oracle's matmul
+(crates/mlx-core/src/cpu_kernels.rs:197-230, i-j-p with a sequential f32 sum).
+
+op(A) / op(B) for the transposed layouts are formed on the host by exact
+transposition before the oracle runs. 16-bit cases give the oracle the same
+RNE-rounded inputs (products of bf16/f16 values are exact in f32).
+
+Tolerance |gpu - cpu| <= atol + rtol*|cpu| with
+  atol = 1e-6 * sqrt(K) * max|A| * max|B|   (summation-order bound)
+  rtol = 1e-5 for f32 output, 1e-2 for bf16/f16 output (one final rounding).
+Large shapes compare sampled rows (all columns) so the oracle finishes in
+seconds; the sample always includes the first and last rows.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import cpu_ref
+from oxidizedmlx_amd import abi
+from oxidizedmlx_amd import backend as hb
+from oxidizedmlx_amd import synth
+from parity import assert_allclose
+
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip", "oracle_lib")]
+
+F32, BF16, F16 = abi.F32, abi.BF16, abi.F16
+
+
+def to_dev(x, dt):
+    if dt == BF16:
+        return hb.DeviceBuffer.from_array(synth.bf16_bits(x))
+    if dt == F16:
+        return hb.DeviceBuffer.from_array(synth.f16_bits(x))
+    return hb.DeviceBuffer.from_array(np.ascontiguousarray(x, np.float32))
+
+
+def from_dev(buf, dt, n):
+    if dt == BF16:
+        return synth.bf16_to_f32(buf.download(np.uint16, n))
+    if dt == F16:
+        return buf.download(np.float16, n).astype(np.float32)
+    return buf.download(np.float32, n)
+
+
+def rounded(x, dt):
+    return synth.round_bf16(x) if dt == BF16 else synth.round_f16(x) if dt == F16 else x
+
+
+def oracle_rows(a, b, rows):
+    """Rows `rows` of a @ b by the oracle's loop (a: [M,K], b: [K,N] f32)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    c = np.zeros((a.shape[0], b.shape[1]), np.float32)
+    for r in rows:
+        cpu_ref.matmul_rows(a, b, c, int(r), 1)
+    return c[rows]
+
+
+def sample_rows(m, count):
+    if m <= count:
+        return np.arange(m)
+    r = np.unique(np.concatenate([[0, m - 1], np.linspace(0, m - 1, count).astype(int)]))
+    return r
+
+
+def check_gemm(m, n, k, ab, cd, ta=False, tb=False, batch=1, seed=1, rows=None, ld_pad=0):
+    """Runs one (batched) GEMM and checks sampled rows of every batch slice."""
+    A = synth.normal(seed, (batch, k, m) if ta else (batch, m, k))
+    B = synth.normal(seed + 1, (batch, n, k) if tb else (batch, k, n))
+    Ar, Br = rounded(A, ab), rounded(B, ab)
+    lda = (m if ta else k) + ld_pad
+    ldb = (k if tb else n) + ld_pad
+    # Padded leading dimensions: copy into wider rows.
+    Ap = np.zeros(A.shape[:2] + (lda,), np.float32)
+    Ap[..., : A.shape[2]] = A
+    Bp = np.zeros(B.shape[:2] + (ldb,), np.float32)
+    Bp[..., : B.shape[2]] = B
+    da, db = to_dev(Ap, ab), to_dev(Bp, ab)
+    dc = hb.DeviceBuffer(batch * m * n * (4 if cd == F32 else 2))
+    hb.gemm(ab, cd, ta, tb, m, n, k, da, lda, db, ldb, dc, n, batch=batch,
+            stride_a=Ap[0].size, stride_b=Bp[0].size, stride_c=m * n)
+    C = from_dev(dc, cd, batch * m * n).reshape(batch, m, n)
+    rows = sample_rows(m, 12) if rows is None else rows
+    rtol = 1e-5 if cd == F32 else 1e-2
+    for bi in range(batch):
+        opA = Ar[bi].T if ta else Ar[bi]
+        opB = Br[bi].T if tb else Br[bi]
+        ref = oracle_rows(opA, opB, rows)
+        atol = 1e-6 * math.sqrt(k) * float(np.abs(opA).max()) * float(np.abs(opB).max()) if k else 0
+        assert_allclose(C[bi][rows], ref, atol, rtol,
+                        f"gemm {m}x{n}x{k} ab={ab} c={cd} ta={ta} tb={tb} batch {bi}")
+    return C
+
+
+def test_f32_512_cfg1():
+    # Config 1: f32 C = A.B, M = N = K = 512, N(0,1); all rows checked.
+    check_gemm(512, 512, 512, F32, F32, rows=np.arange(512), seed=0x5EED0001)
+
+
+@pytest.mark.parametrize("cd", [BF16, F32])
+def test_bf16_4096_headline(cd):
+    check_gemm(4096, 4096, 4096, BF16, cd, seed=11, rows=sample_rows(4096, 10))
+
+
+@pytest.mark.parametrize("ab", [BF16, F16])
+@pytest.mark.parametrize("tb", [False, True])
+def test_batched_cfg3(ab, tb):
+    # Config 3: [32,1024,1024] x [32,1024,1024] with f32 accumulate; tb = transposed-B case.
+    check_gemm(1024, 1024, 1024, ab, F32, tb=tb, batch=32, seed=21, rows=np.array([0, 511, 1023]))
+
+
+@pytest.mark.parametrize("ab", [BF16, F16, F32])
+def test_odd_cfg3(ab):
+    # Config 3 odd shape M=1000, N=777, K=1531 (edge tiles; unaligned rows).
+    check_gemm(1000, 777, 1531, ab, F32, seed=31, rows=sample_rows(1000, 24))
+
+
+@pytest.mark.parametrize("ab", [BF16, F16, F32])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("m,n,k", [(67, 45, 93), (128, 256, 64), (300, 200, 520)])
+def test_all_layouts_full(ab, ta, tb, m, n, k):
+    check_gemm(m, n, k, ab, F32, ta=bool(ta), tb=bool(tb), seed=m + n + k, rows=np.arange(m))
+
+
+@pytest.mark.parametrize("ab,cd", [(BF16, BF16), (F16, F16), (BF16, F32)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_big_tile_layouts(ab, cd, ta, tb):
+    # Large enough for the 256x256 tile path, with edge tiles in both M and N.
+    check_gemm(4000, 3900, 520, ab, cd, ta=bool(ta), tb=bool(tb), seed=41, rows=sample_rows(4000, 8))
+
+
+@pytest.mark.parametrize("ab", [BF16, F32])
+def test_padded_leading_dims(ab):
+    check_gemm(130, 70, 90, ab, F32, ld_pad=8, seed=51, rows=np.arange(130))
+    check_gemm(130, 70, 90, ab, F32, ld_pad=3, seed=52, rows=np.arange(130))
+
+
+def test_edge_sizes():
+    check_gemm(1, 1, 1, F32, F32, rows=np.arange(1))
+    check_gemm(1, 300, 7, BF16, F32, rows=np.arange(1))
+    check_gemm(33, 1, 17, F16, F32, rows=np.arange(33))
+    check_gemm(5, 6, 1, BF16, BF16, rows=np.arange(5))
+    # K = 0: C is all zeros.
+    dc = hb.DeviceBuffer.from_array(np.full(12, 7.0, np.float32))
+    hb.gemm(F32, F32, False, False, 3, 4, 0, 0, 1, 0, 4, dc, 4)
+    np.testing.assert_array_equal(dc.download(np.float32), np.zeros(12, np.float32))
+    # M = 0 / N = 0 are no-ops.
+    hb.gemm(BF16, F32, False, False, 0, 4, 8, 0, 8, 0, 4, 0, 4)
+
+
+def test_gemm_argument_errors():
+    with pytest.raises(abi.InvalidArgument):
+        hb.gemm(abi.I32, F32, False, False, 2, 2, 2, 1, 2, 1, 2, 1, 2)
+    with pytest.raises(abi.InvalidArgument):
+        hb.gemm(F32, F32, False, False, 2, 2, 4, 1, 2, 1, 2, 1, 2)  # lda < K
+    with pytest.raises(abi.NullPtr):
+        hb.gemm(F32, F32, False, False, 2, 2, 2, 0, 2, 0, 2, 0, 2)

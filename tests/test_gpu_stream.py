@@ -1,0 +1,288 @@
+"""HipStream (Stream + Graph bound to mlx-hip, HBM-resident buffers).
+
+Restates the reference's Stream tests (crates/mlx-core/src/backend.rs:202-449)
+and checks the scheduler's look-ahead fusion against the unfused graph and
+the CPU oracle."""
+import threading
+
+import numpy as np
+import pytest
+
+from oracle import cpu_ref
+from oxidizedmlx_amd import abi
+from oxidizedmlx_amd import synth
+from oxidizedmlx_amd.backend import HipBackend, HipStream
+from oxidizedmlx_amd.opkind import NodeInput, OpKind, meta
+from parity import assert_allclose, cpu_stream, gen_data
+
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip", "oracle_lib")]
+
+M2 = meta([2])
+
+
+def test_stream_constant_and_add():
+    s = HipStream()
+    a = s.add_constant([1.0, 2.0, 3.0], meta([3]))
+    s.eval(a)
+    np.testing.assert_array_equal(s.get_buffer(a), [1, 2, 3])
+    a = s.add_constant([1.0, 2.0], M2)
+    b = s.add_constant([3.0, 4.0], M2)
+    c = s.add_op(OpKind.Add, [a, b], M2)
+    s.eval(c)
+    np.testing.assert_array_equal(s.get_buffer(c), [4, 6])
+
+
+@pytest.mark.parametrize("fusion", [False, True])
+def test_memoization_repeated_eval(fusion):
+    s = HipStream(fusion=fusion)
+    a, b = s.add_constant([1.0, 2.0], M2), s.add_constant([3.0, 4.0], M2)
+    c = s.add_op(OpKind.Add, [a, b], M2)
+    s.eval(c)
+    n = s.eval_count()
+    assert n > 0
+    s.eval(c)
+    assert s.eval_count() == n
+
+
+def test_memoization_shared_subgraph():
+    s = HipStream(fusion=False)
+    a, b = s.add_constant([1.0, 2.0], M2), s.add_constant([3.0, 4.0], M2)
+    c = s.add_op(OpKind.Add, [a, b], M2)
+    d = s.add_op(OpKind.Mul, [c, c], M2)
+    s.eval(d)
+    n = s.eval_count()
+    s.eval(d)
+    s.eval(c)
+    assert s.eval_count() == n
+    np.testing.assert_array_equal(s.get_buffer(d), [16, 36])
+
+
+@pytest.mark.parametrize("fusion", [False, True])
+def test_memoization_diamond(fusion):
+    s = HipStream(fusion=fusion)
+    a = s.add_constant([1.0, 2.0], M2)
+    b = s.add_op(OpKind.Add, [a, a], M2)
+    c = s.add_op(OpKind.Mul, [a, a], M2)
+    d = s.add_op(OpKind.Add, [b, c], M2)
+    s.eval(d)
+    assert s.eval_count() == 3
+    s.eval(d)
+    assert s.eval_count() == 3
+    np.testing.assert_array_equal(s.get_buffer(d), [3, 8])
+
+
+def test_cache_len_updates():
+    s = HipStream(fusion=False)
+    assert s.cache_len() == 0
+    a, b = s.add_constant([1.0, 2.0], M2), s.add_constant([3.0, 4.0], M2)
+    assert s.cache_len() == 2
+    c = s.add_op(OpKind.Add, [a, b], M2)
+    s.eval(c)
+    assert s.cache_len() == 3
+
+
+def test_cse_dedupes_ops_not_constants():
+    s = HipStream()
+    a, b = s.add_constant([1.0, 2.0], M2), s.add_constant([1.0, 2.0], M2)
+    assert a != b  # constants are never deduplicated (graph.rs:495-500)
+    assert s.add_op(OpKind.Add, [a, b], M2) == s.add_op(OpKind.Add, [b, a], M2)  # commutation
+    assert s.add_op(OpKind.Sub, [a, b], M2) != s.add_op(OpKind.Sub, [b, a], M2)
+    assert s.add_op(OpKind.Softmax(-1), [a], M2) != s.add_op(OpKind.Softmax(0), [a], M2)
+
+
+def build_chain(s, x, w, b, m):
+    nx, nw, nb = s.add_constant(x, m), s.add_constant(w, m), s.add_constant(b, m)
+    xw = s.add_op(OpKind.Mul, [nx, nw], m)
+    z = s.add_op(OpKind.Add, [xw, nb], m)
+    return s.add_op(OpKind.Silu, [z], m)
+
+
+def test_cfg2_fused_chain_full_size():
+    # Config 2 chain y = SiLU(x*w + b), [4096, 4096], x ~ N(0, 2^2), w, b ~ U(-1, 1).
+    shape = (4096, 4096)
+    x = synth.normal(0x5EED0003, shape, 0.0, 2.0)
+    w = synth.uniform(0x5EED0004, shape, -1.0, 1.0)
+    b = synth.uniform(0x5EED0005, shape, -1.0, 1.0)
+    m = meta(shape)
+    c = cpu_stream()
+    yc = build_chain(c, x, w, b, m)
+    c.eval(yc)
+    ref = c.get_buffer(yc)
+    s = HipStream(fusion=True)
+    y = build_chain(s, x, w, b, m)
+    s.eval(y)
+    assert s.launch_count() == 1 and s.eval_count() == 3
+    assert_allclose(s.get_buffer(y), ref, 1e-6, 1e-6, "SiLU(x*w+b) fused 4096x4096")
+    u = HipStream(fusion=False)
+    yu = build_chain(u, x, w, b, m)
+    u.eval(yu)
+    assert u.launch_count() == 3 and u.eval_count() == 3
+    # Fused and unfused kernels do identical f32 arithmetic in the same order.
+    np.testing.assert_array_equal(u.get_buffer(yu), s.get_buffer(y))
+
+
+def test_fusion_long_chain_and_reversed_operands():
+    n = 10007  # not a multiple of 4: exercises the scalar tail
+    xs = [gen_data(n, 200 + i) for i in range(6)]
+    pos = np.abs(gen_data(n, 300)) + np.float32(0.5)
+
+    def g(s):
+        m = meta([n])
+        c = [s.add_constant(v, m) for v in xs]
+        p = s.add_constant(pos, m)
+        t = s.add_op(OpKind.Mul, [c[0], c[1]], m)
+        t = s.add_op(OpKind.Sub, [c[2], t], m)       # acc on the right: RSUB
+        t = s.add_op(OpKind.Exp, [t], m)
+        t = s.add_op(OpKind.Div, [p, t], m)          # RDIV
+        t = s.add_op(OpKind.Gelu, [t], m)
+        t = s.add_op(OpKind.Add, [c[3], t], m)
+        t = s.add_op(OpKind.Neg, [t], m)
+        t = s.add_op(OpKind.SiluVjp, [c[4], t], m)   # dy = c4, x = t
+        return s.add_op(OpKind.Mul, [t, c[5]], m)
+
+    cs = cpu_stream()
+    out_c = g(cs)
+    cs.eval(out_c)
+    hs = HipStream(fusion=True)
+    out_h = g(hs)
+    hs.eval(out_h)
+    assert hs.launch_count() == 1
+    assert hs.eval_count() == cs.eval_calls == 9
+    assert_allclose(hs.get_buffer(out_h), cs.get_buffer(out_c), 1e-5, 1e-5, "long fused chain")
+
+
+def test_fusion_respects_shared_intermediates():
+    n = 4096
+    x, y = gen_data(n, 1), gen_data(n, 2)
+    s = HipStream(fusion=True)
+    m = meta([n])
+    a, b = s.add_constant(x, m), s.add_constant(y, m)
+    t = s.add_op(OpKind.Mul, [a, b], m)  # consumed twice: must be materialised
+    u = s.add_op(OpKind.Exp, [t], m)
+    v = s.add_op(OpKind.Add, [t, u], m)
+    s.eval(v)
+    np.testing.assert_allclose(s.get_buffer(t), x * y, rtol=0, atol=0)
+    ref = (x * y) + np.exp(x * y)
+    np.testing.assert_allclose(s.get_buffer(v), ref, rtol=1e-6, atol=1e-6)
+
+
+def test_transpose_folded_into_gemm():
+    # Linear: x . W^T (crates/mlx-nn/src/linear.rs:34-43) and autograd's
+    # g . B^T / A^T . g (crates/mlx-autograd/src/vjp.rs:71-80).
+    T, I, O = 96, 80, 72
+    x, W = gen_data(T * I, 5).reshape(T, I), gen_data(O * I, 6).reshape(O, I)
+
+    def g(s):
+        nx = s.add_constant(x, meta([T, I]))
+        nw = s.add_constant(W, meta([O, I]))
+        wt = s.add_op(OpKind.Transpose(None), [nw], meta([I, O]))
+        y = s.add_op(OpKind.MatMul, [nx, wt], meta([T, O]))
+        xt = s.add_op(OpKind.Transpose(None), [nx], meta([I, T]))
+        return s.add_op(OpKind.MatMul, [xt, y], meta([I, O]))
+
+    cs = cpu_stream()
+    oc = g(cs)
+    cs.eval(oc)
+    hs = HipStream(fusion=True)
+    oh = g(hs)
+    hs.eval(oh)
+    assert hs.launch_count() == 2 and hs.eval_count() == 4
+    assert_allclose(hs.get_buffer(oh), cs.get_buffer(oc), 1e-4, 1e-4, "folded transposes")
+
+
+def test_stream_errors_match_reference():
+    s = HipStream()
+    a = s.add_constant(np.ones(6, np.float32), meta([2, 3]))
+    b = s.add_constant(np.ones(8, np.float32), meta([4, 2]))
+    mm = s.add_op(OpKind.MatMul, [a, b], meta([2, 2]))
+    with pytest.raises(abi.ShapeMismatch):
+        s.eval(mm)
+    v = s.add_constant(np.ones(3, np.float32), meta([3]))
+    mm1 = s.add_op(OpKind.MatMul, [v, v], meta([1]))
+    with pytest.raises(abi.InvalidArgument):
+        s.eval(mm1)
+    sm = s.add_op(OpKind.Softmax(5), [a], meta([2, 3]))
+    with pytest.raises(abi.InvalidArgument):
+        s.eval(sm)
+    with pytest.raises(abi.InvalidArgument):
+        s.add_op(OpKind.Add, [a, 12345], meta([2, 3]))
+    # eval_node with Constant is rejected (cpu_kernels.rs:21-23)
+    with pytest.raises(abi.InvalidArgument):
+        HipBackend().eval_node(OpKind.Constant, [], meta([1]))
+
+
+def test_eval_node_host_contract_matches_oracle():
+    x = gen_data(64 * 96, 9)
+    inp = [NodeInput(x, (64, 96))]
+    for op in [OpKind.Softmax(-1), OpKind.LayerNorm(1e-5), OpKind.RmsNorm(1e-5), OpKind.Silu,
+               OpKind.Gelu]:
+        h = HipBackend().eval_node(op, inp, meta([64, 96]))
+        c = cpu_ref.CpuRefBackend().eval_node(op, inp, meta([64, 96]))
+        assert_allclose(h, c, 1e-6, 1e-5, repr(op))
+    # bf16 MatMul: operands rounded to bf16, f32 accumulate (logical dtype tag)
+    a, b = gen_data(33 * 40, 10), gen_data(40 * 21, 11)
+    h = HipBackend().eval_node(OpKind.MatMul, [NodeInput(a, (33, 40), abi.BF16),
+                                               NodeInput(b, (40, 21), abi.BF16)],
+                               meta([33, 21], abi.BF16))
+    c = synth.round_bf16(a).reshape(33, 40).astype(np.float64) @ synth.round_bf16(b).reshape(40, 21)
+    np.testing.assert_allclose(h.reshape(33, 21), c, rtol=1e-4, atol=1e-5)
+
+
+def test_empty_tensors():
+    h = HipBackend().eval_node(OpKind.Add, [NodeInput(np.zeros(0, np.float32), (0,)),
+                                           NodeInput(np.zeros(0, np.float32), (0,))], meta([0]))
+    assert h.size == 0
+
+
+def test_concurrent_streams_deterministic():
+    # crates/mlx-core/tests/concurrency_stress.rs:16-101: threads evaluating the
+    # same graph must get bit-identical results.
+    x = gen_data(256 * 512, 77)
+    results, errors = [None] * 8, []
+
+    def work(i):
+        try:
+            s = HipStream()
+            m = meta([256, 512])
+            n = s.add_constant(x, m)
+            y = s.add_op(OpKind.LayerNorm(1e-5), [n], m)
+            z = s.add_op(OpKind.Silu, [y], m)
+            s.eval(z)
+            results[i] = s.get_buffer(z)
+        except Exception as e:  # noqa: BLE001
+            errors.append(e)
+
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors
+    for r in results[1:]:
+        np.testing.assert_array_equal(r, results[0])
+
+
+def test_shared_stream_from_threads():
+    s = HipStream()
+    m = meta([1024])
+    a = s.add_constant(gen_data(1024, 1), m)
+    b = s.add_constant(gen_data(1024, 2), m)
+    c = s.add_op(OpKind.Mul, [a, b], m)
+    outs, errs = [], []
+
+    def work():
+        try:
+            s.eval(c)
+            outs.append(s.get_buffer(c))
+        except Exception as e:  # noqa: BLE001
+            errs.append(e)
+
+    ts = [threading.Thread(target=work) for _ in range(16)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errs
+    for o in outs:
+        np.testing.assert_array_equal(o, outs[0])
+    assert s.eval_count() == 1
