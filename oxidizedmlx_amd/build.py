@@ -34,6 +34,8 @@ SOURCES = [
     "kernels/gemm_bf16.hip",
     "kernels/gemm_f16.hip",
     "kernels/gemm_f32.hip",
+    "kernels/gemm16_bf16.hip",
+    "kernels/gemm16_f16.hip",
 ]
 
 

@@ -3,6 +3,10 @@
 #include "../common.hpp"
 #include "../kernels.hpp"
 #include "gemm_impl.hpp"
+#include "gemm16_impl.hpp"
+
+#include <cstdlib>
+#include <cstring>
 
 namespace mlxhip {
 namespace {
@@ -17,6 +21,18 @@ __global__ __launch_bounds__(256) void zero_c_kernel(char* c, int64_t ldc, int64
 }
 
 int elem_size(int dt) { return dt == MLXHIP_DTYPE_F32 ? 4 : 2; }
+
+// MLXHIP_GEMM_PATH: unset/"auto" = choose by shape, "general" = always the
+// general kernel, "lds16" = the direct-to-LDS 16-bit kernel whenever the
+// operands allow it. Read on every call so one process (the tests) can
+// cover both kernels.
+int gemm_path() {
+    const char* e = getenv("MLXHIP_GEMM_PATH");
+    if (!e) return 0;
+    if (!strcmp(e, "general")) return 1;
+    if (!strcmp(e, "lds16")) return 2;
+    return 0;
+}
 
 }  // namespace
 
@@ -65,6 +81,32 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
     g.ldc = ldc;
     g.sc = stride_c;
     const int ta = trans_a ? 1 : 0, tb = trans_b ? 1 : 0;
+    // 16-bit operands on 256x256 tiles with direct-to-LDS loads when the
+    // problem fills the chip and the operands meet that kernel's layout
+    // requirements; the general kernel covers everything else.
+    const int path = gemm_path();
+    if (ab_dtype != MLXHIP_DTYPE_F32 && path != 1) {
+        const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256) * batch;
+        gemm16::Args h{};
+        if ((path == 2 || big_tiles >= 200) &&
+            gemm16::supported(ta, tb, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, &h.a_bytes,
+                              &h.b_bytes)) {
+            h.m = m;
+            h.n = n;
+            h.k = k;
+            h.a = a;
+            h.lda = lda;
+            h.sa = stride_a;
+            h.b = b;
+            h.ldb = ldb;
+            h.sb = stride_b;
+            h.c = c;
+            h.ldc = ldc;
+            h.sc = stride_c;
+            return ab_dtype == MLXHIP_DTYPE_BF16 ? gemm16_bf16(c_dtype, ta, tb, h, batch, s)
+                                                 : gemm16_f16(c_dtype, ta, tb, h, batch, s);
+        }
+    }
     switch (ab_dtype) {
         case MLXHIP_DTYPE_F32: return gemm_f32(c_dtype, ta, tb, g, batch, aligned, s);
         case MLXHIP_DTYPE_BF16: return gemm_bf16(c_dtype, ta, tb, g, batch, aligned, s);

@@ -1,0 +1,69 @@
+"""The direct-to-LDS 16-bit GEMM kernel (kernels/gemm16_impl.hpp) and the
+general MFMA kernel, each forced through MLXHIP_GEMM_PATH, against the CPU
+oracle's matmul (crates/mlx-core/src/cpu_kernels.rs:197-230) on the same
+RNE-rounded inputs.
+
+Tolerance as in test_gpu_gemm.py: |gpu - cpu| <= atol + rtol*|cpu| with
+atol = 1e-6 * sqrt(K) * max|A| * max|B| and rtol 1e-5 (f32 C) or 1e-2
+(bf16/f16 C). The shapes exercise what the direct-to-LDS kernel handles
+with its out-of-range buffer loads: M and N edges inside a 256 x 256 tile,
+K not a multiple of the 32-wide K tile, tiles with no valid rows at all,
+and batch strides.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from oxidizedmlx_amd import abi
+from test_gpu_gemm import check_gemm, sample_rows
+
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip", "oracle_lib")]
+
+F32, BF16, F16 = abi.F32, abi.BF16, abi.F16
+
+
+@pytest.fixture
+def gemm_path(request):
+    old = os.environ.get("MLXHIP_GEMM_PATH")
+    os.environ["MLXHIP_GEMM_PATH"] = request.param
+    yield request.param
+    if old is None:
+        del os.environ["MLXHIP_GEMM_PATH"]
+    else:
+        os.environ["MLXHIP_GEMM_PATH"] = old
+
+
+@pytest.mark.parametrize("gemm_path", ["lds16"], indirect=True)
+@pytest.mark.parametrize("ab,cd", [(BF16, F32), (BF16, BF16), (F16, F32), (F16, F16)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 32), (300, 264, 520), (64, 40, 8), (520, 776, 1528)])
+def test_lds16_layouts(gemm_path, ab, cd, ta, tb, m, n, k):
+    check_gemm(m, n, k, ab, cd, ta=bool(ta), tb=bool(tb), seed=m + 3 * n + 7 * k,
+               rows=sample_rows(m, 40))
+
+
+@pytest.mark.parametrize("gemm_path", ["lds16"], indirect=True)
+@pytest.mark.parametrize("tb", [False, True])
+def test_lds16_batched_strided(gemm_path, tb):
+    check_gemm(264, 136, 200, BF16, F32, tb=tb, batch=5, seed=77, rows=sample_rows(264, 16))
+    check_gemm(128, 128, 96, F16, F16, tb=tb, batch=3, seed=78, rows=np.arange(128), ld_pad=8)
+
+
+@pytest.mark.parametrize("gemm_path", ["lds16"], indirect=True)
+def test_lds16_headline_shape(gemm_path):
+    check_gemm(4096, 4096, 4096, BF16, BF16, seed=12, rows=sample_rows(4096, 10))
+
+
+@pytest.mark.parametrize("gemm_path", ["general"], indirect=True)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_general_kernel_headline_shape(gemm_path, ta, tb):
+    check_gemm(4096, 4096, 4096, BF16, BF16, ta=bool(ta), tb=bool(tb), seed=13,
+               rows=sample_rows(4096, 6))
+
+
+@pytest.mark.parametrize("gemm_path", ["lds16"], indirect=True)
+def test_lds16_falls_back_when_unsupported(gemm_path):
+    # K = 1531 is not a multiple of 8: the general kernel must run and agree.
+    check_gemm(1000, 777, 1531, BF16, F32, seed=31, rows=sample_rows(1000, 12))
+    check_gemm(70, 64, 48, F16, F32, ld_pad=3, seed=32, rows=np.arange(70))
