@@ -54,6 +54,7 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define MLXHIP_LDS __attribute__((address_space(3)))
 
 constexpr int TILE = 256;                 // BM = BN
@@ -84,8 +85,16 @@ __device__ inline void wait_vmcnt() {
 }
 
 // All LDS reads of this wave done, then a workgroup barrier. No wait on
-// vector-memory loads: in-flight LDS-bound loads stay in flight.
-__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// vector-memory loads: in-flight LDS-bound loads stay in flight. The wait is
+// the compiler's own s_waitcnt (0xC07F = lgkmcnt(0), vmcnt/expcnt at their
+// maxima), so its wait-count bookkeeping knows every LDS read has completed;
+// the empty asm statements keep memory accesses on their side of the barrier.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 // 16 bytes per lane from buffer offset `voff` into LDS at dst + 16 * lane.
 // Issued as inline assembly on purpose: the compiler cannot tell which LDS
@@ -130,14 +139,17 @@ struct Loader {
         k_stride_bytes = KC ? 2u : (uint32_t)(ld * 2);
     }
 
+    // Load i (0 .. LOADS_PER_OP-1) of the tile starting at k0.
+    __device__ inline void issue_one(__amdgpu_buffer_rsrc_t rsrc, MLXHIP_LDS char* stage_op, int wave,
+                                     int k0, int i) const {
+        const uint32_t v = k0 < lim[i] ? off[i] + (uint32_t)k0 * k_stride_bytes : OOB;
+        lds_load16(rsrc, stage_op + (i * 4 + wave) * 1024, v);
+    }
+
     __device__ inline void issue(__amdgpu_buffer_rsrc_t rsrc, MLXHIP_LDS char* stage_op, int wave,
                                  int k0) const {
-        const uint32_t kofs = (uint32_t)k0 * k_stride_bytes;
 #pragma unroll
-        for (int i = 0; i < LOADS_PER_OP; ++i) {
-            const uint32_t v = k0 < lim[i] ? off[i] + kofs : OOB;
-            lds_load16(rsrc, stage_op + (i * 4 + wave) * 1024, v);
-        }
+        for (int i = 0; i < LOADS_PER_OP; ++i) issue_one(rsrc, stage_op, wave, k0, i);
     }
 };
 
@@ -178,6 +190,31 @@ __device__ inline void mfma(const u32x4& a, const u32x4& b, f32x16& acc) {
                                                      __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
 }
 
+// Number of LDS read instructions for one operand's 4 fragments of a k-step.
+template <bool KC>
+constexpr int reads_per_step() { return KC ? 4 : 8; }
+
+// Read `idx` (0 .. reads_per_step-1) of one operand's fragments for k-step s:
+// KC: fragment idx (ds_read_b128); !KC: half idx % 2 of fragment idx / 2
+// (ds_read_b64_tr_b16, k offsets 0-3 or 4-7).
+template <bool KC>
+__device__ inline void read_one(const MLXHIP_LDS char* op, const FragAddr<KC>& fa, int s, int idx, u32x4* f) {
+    if constexpr (KC) {
+        f[idx] = *(const MLXHIP_LDS u32x4*)(op + fa.base[s] + idx * 2048);
+    } else {
+        const int x = idx >> 1, r = idx & 1;
+        const MLXHIP_LDS char* p = op + fa.base[x] + (16 * s + 4 * r) * 512;
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((MLXHIP_LDS i16x4*)p));
+        if (r == 0) {
+            f[x].x = v.x;
+            f[x].y = v.y;
+        } else {
+            f[x].z = v.x;
+            f[x].w = v.y;
+        }
+    }
+}
+
 // Loads the 4 fragments of one operand for k-step s of the stage at `op`.
 template <bool KC>
 __device__ inline void read_frags(const MLXHIP_LDS char* op, const FragAddr<KC>& fa, int s, u32x4* f) {
@@ -195,48 +232,28 @@ __device__ inline void read_frags(const MLXHIP_LDS char* op, const FragAddr<KC>&
     }
 }
 
-__device__ inline uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
-
-// Stores C[m][n .. n+3] (4 consecutive columns of one row).
+// Two f32 -> two 16-bit outputs packed in one dword (low = first), rounded
+// to nearest even: bf16 by v_cvt_pk_bf16_f32, f16 by v_cvt_f16_f32.
 template <int CT>
-__device__ inline void store4(void* c, int64_t idx, int64_t ncols_left, bool vec_ok, const float* v) {
-    if constexpr (CT == MLXHIP_DTYPE_F32) {
-        float* p = static_cast<float*>(c) + idx;
-        if (vec_ok && ncols_left >= 4) {
-            *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-            for (int e = 0; e < 4; ++e)
-                if (e < ncols_left) p[e] = v[e];
-        }
+__device__ inline uint32_t pack2(float a, float b) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    if constexpr (CT == MLXHIP_DTYPE_BF16) {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
     } else {
-        uint16_t h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            if constexpr (CT == MLXHIP_DTYPE_BF16) h[e] = f32_to_bf16(v[e]);
-            else h[e] = __builtin_bit_cast(uint16_t, (_Float16)v[e]);
-        }
-        uint16_t* p = static_cast<uint16_t*>(c) + idx;
-        if (vec_ok && ncols_left >= 4) {
-            *reinterpret_cast<uint2*>(p) = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
-        } else {
-            for (int e = 0; e < 4; ++e)
-                if (e < ncols_left) p[e] = h[e];
-        }
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
     }
 }
 
-template <int DT, int CT, int TA, int TB, int STAGES>
+template <int DT, int CT, int TA, int TB, int STAGES, bool SPREAD>
 __global__ __attribute__((amdgpu_flat_work_group_size(THREADS, THREADS), amdgpu_waves_per_eu(1, 1)))
 void gemm16_kernel(Args g) {
     constexpr bool KCA = (TA == 0);  // A stored [M][K]
     constexpr bool KCB = (TB == 1);  // B stored [N][K]
     static_assert(STAGES >= 3 && STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
-    __shared__ __attribute__((aligned(1024))) char smem_raw[STAGES * STAGE_BYTES];
+    constexpr int SMEM_BYTES = STAGES * STAGE_BYTES > 4 * 128 * (256 + 16) ? STAGES * STAGE_BYTES : 4 * 128 * (256 + 16);
+    __shared__ __attribute__((aligned(1024))) char smem_raw[SMEM_BYTES];
     MLXHIP_LDS char* smem = (MLXHIP_LDS char*)smem_raw;
 
     const int tid = threadIdx.x;
@@ -286,68 +303,137 @@ void gemm16_kernel(Args g) {
     constexpr int LOADS_PER_TILE = 2 * LOADS_PER_OP;
 
     // Prologue: tiles 0 .. STAGES-1 into stages 0 .. STAGES-1.
+    // With SPREAD, B's loads of tile t+STAGES are issued in the first half of
+    // iteration t+1 instead (one per four MFMAs) and the prologue leaves out
+    // B of tile STAGES-1; the count of loads younger than any tile is unchanged.
 #pragma unroll
     for (int t = 0; t < STAGES; ++t) {
         MLXHIP_LDS char* st = smem + t * STAGE_BYTES;
         la.issue(ra, st, wave, t * BK);
-        lb.issue(rb, st + OP_BYTES, wave, t * BK);
+        if (!SPREAD || t < STAGES - 1) lb.issue(rb, st + OP_BYTES, wave, t * BK);
     }
-    wait_vmcnt<(STAGES - 1) * LOADS_PER_TILE>();
+    if constexpr (SPREAD) wait_vmcnt<(STAGES - 2) * LOADS_PER_TILE + LOADS_PER_OP>();
+    else wait_vmcnt<(STAGES - 1) * LOADS_PER_TILE>();
     lds_barrier();
 
     u32x4 af[2][4], bf[2][4];
     read_frags<KCA>(smem, fa, 0, af[0]);
     read_frags<KCB>(smem + OP_BYTES, fb, 0, bf[0]);
 
+    // Each half-tile issues 16 MFMAs, one per 32-cycle MFMA slot, with the
+    // LDS reads / LDS-bound loads of the next half placed between them; the
+    // scheduling barriers keep that order (the compiler would otherwise sink
+    // each read next to its first use and expose the LDS latency).
+    constexpr int NA = reads_per_step<KCA>(), NB = reads_per_step<KCB>(), NR = NA + NB;
+    constexpr int OPS2 = (SPREAD ? 1 : 2) * LOADS_PER_OP + NR;
+    static_assert(NR <= 16, "one read per MFMA slot in the first half");
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt % STAGES;
         const MLXHIP_LDS char* st = smem + cur * STAGE_BYTES;
-        // k-step 1 fragments of this tile; MFMAs of k-step 0.
-        read_frags<KCA>(st, fa, 1, af[1]);
-        read_frags<KCB>(st + OP_BYTES, fb, 1, bf[1]);
+        // First half: MFMAs of k-step 0, reads of k-step 1 of this tile.
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) mfma<DT>(bf[0][j], af[0][i], acc[i][j]);
+        for (int q = 0; q < 16; ++q) {
+            mfma<DT>(bf[0][q & 3], af[0][q >> 2], acc[q >> 2][q & 3]);
+            if (q < NA) read_one<KCA>(st, fa, 1, q, af[1]);
+            else if (q < NR) read_one<KCB>(st + OP_BYTES, fb, 1, q - NA, bf[1]);
+            if constexpr (SPREAD) {
+                // B of tile kt-1+STAGES into the stage released in iteration kt-1.
+                if ((q & 3) == 3)
+                    lb.issue_one(rb, smem + ((kt + STAGES - 1) % STAGES) * STAGE_BYTES + OP_BYTES, wave,
+                                 (kt - 1 + STAGES) * BK, q >> 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
         // Tile kt+1 has landed for every wave; every wave is done reading
         // this tile's stage, which then receives tile kt+STAGES.
         wait_vmcnt<(STAGES - 2) * LOADS_PER_TILE>();
         lds_barrier();
-        {
-            MLXHIP_LDS char* dst = smem + cur * STAGE_BYTES;
-            const int k0 = (kt + STAGES) * BK;
-            la.issue(ra, dst, wave, k0);
-            lb.issue(rb, dst + OP_BYTES, wave, k0);
-        }
+        MLXHIP_LDS char* dst = smem + cur * STAGE_BYTES;
+        const int k0 = (kt + STAGES) * BK;
         const MLXHIP_LDS char* nx = smem + ((kt + 1) % STAGES) * STAGE_BYTES;
-        read_frags<KCA>(nx, fa, 0, af[0]);
-        read_frags<KCB>(nx + OP_BYTES, fb, 0, bf[0]);
+        // Second half: MFMAs of k-step 1; the k-step 0 reads of tile kt+1
+        // and the loads of tile kt+STAGES.
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int q = 0; q < 16; ++q) {
+            mfma<DT>(bf[1][q & 3], af[1][q >> 2], acc[q >> 2][q & 3]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) mfma<DT>(bf[1][j], af[1][i], acc[i][j]);
+            for (int o = (q * OPS2) / 16; o < ((q + 1) * OPS2) / 16; ++o) {
+                // Reads first: the next tile's first MFMAs consume them.
+                if (o < NA) read_one<KCA>(nx, fa, 0, o, af[0]);
+                else if (o < NR) read_one<KCB>(nx + OP_BYTES, fb, 0, o - NA, bf[0]);
+                else if (o < NR + LOADS_PER_OP) la.issue_one(ra, dst, wave, k0, o - NR);
+                else if (!SPREAD) lb.issue_one(rb, dst + OP_BYTES, wave, k0, o - NR - LOADS_PER_OP);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     wait_vmcnt<0>();
 
-    // Epilogue: acc[i][j][v] = C[m][n] with m = m0 + 128 wm + 32 i + lane % 32,
-    // n = n0 + 128 wn + 32 j + 8 (v / 4) + 4 (lane / 32) + v % 4.
-    void* C = g.c;
-    const int64_t cbase = batch * g.sc;
-    const bool vec_ok = (g.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(C) % 16) == 0 && (g.sc % 4) == 0;
+    // Epilogue through LDS. acc[i][j][v] = C[m][n] with m = 128 wm + 32 i +
+    // lane % 32 and n = 128 wn + 32 j + 8 (v / 4) + 4 (lane / 32) + v % 4
+    // inside the tile. Each wave converts its 128 x 128 quadrant into padded
+    // LDS rows (PITCH = row bytes + 16: 16 consecutive rows fall in distinct
+    // bank groups for the 8/16-byte writes) and reads it back row by row, so
+    // every global store instruction writes whole 256- or 512-byte row
+    // segments instead of 16-byte pieces of 32 rows.
+    wait_vmcnt<0>();
+    lds_barrier();  // every wave is done with the operand stages
+    constexpr int ES = CT == MLXHIP_DTYPE_F32 ? 4 : 2;
+    constexpr int ROW_BYTES = 128 * ES;
+    constexpr int PITCH = ROW_BYTES + 16;
+    constexpr int PASS_ROWS = ES == 2 ? 128 : 64;  // quadrant rows staged per pass
+    constexpr int LANES_PER_ROW = ROW_BYTES / 16;
+    constexpr int ROWS_PER_READ = 64 / LANES_PER_ROW;
+    static_assert(4 * PASS_ROWS * PITCH <= SMEM_BYTES, "epilogue staging fits in LDS");
+    MLXHIP_LDS char* region = smem + wave * PASS_ROWS * PITCH;
+    char* C = static_cast<char*>(g.c) + batch * g.sc * ES;
+    const int64_t row0 = m0 + 128 * wm, col0 = n0 + 128 * wn;
+    const bool vec_ok = (g.ldc * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(C) % 16) == 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int64_t m = m0 + 128 * wm + 32 * i + (lane & 31);
-        if (m >= g.m) continue;
+    for (int pass = 0; pass < 128 / PASS_ROWS; ++pass) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int i = 0; i < PASS_ROWS / 32; ++i) {
+            const int ii = pass * (PASS_ROWS / 32) + i;
+            const int r = 32 * i + (lane & 31);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int64_t n = n0 + 128 * wn + 32 * j + 8 * q + 4 * (lane >> 5);
-                if (n >= g.n) continue;
-                const float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                                    acc[i][j][4 * q + 3]};
-                store4<CT>(C, cbase + m * g.ldc + n, g.n - n, vec_ok, v);
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int c = 32 * j + 8 * q + 4 * (lane >> 5);
+                    MLXHIP_LDS char* p = region + r * PITCH + c * ES;
+                    const f32x16& a = acc[ii][j];
+                    if constexpr (ES == 4) {
+                        *(MLXHIP_LDS f32x4*)p = f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+                    } else {
+                        *(MLXHIP_LDS u32x2*)p =
+                            u32x2{pack2<CT>(a[4 * q], a[4 * q + 1]), pack2<CT>(a[4 * q + 2], a[4 * q + 3])};
+                    }
+                }
+        }
+        // The staged rows are read back by the same wave: LDS accesses of one
+        // wave complete in order, so no barrier is needed.
+#pragma unroll 4
+        for (int rr = 0; rr < PASS_ROWS; rr += ROWS_PER_READ) {
+            const int r = rr + lane / LANES_PER_ROW;
+            const int cb = (lane % LANES_PER_ROW) * 16;  // byte offset inside the row
+            const u32x4 v = *(const MLXHIP_LDS u32x4*)(region + r * PITCH + cb);
+            const int64_t m = row0 + pass * PASS_ROWS + r;
+            const int64_t n = col0 + cb / ES;
+            if (m >= g.m || n >= g.n) continue;
+            char* dst = C + (m * g.ldc + n) * ES;
+            if (vec_ok && n + 16 / ES <= g.n) {
+                *reinterpret_cast<u32x4*>(dst) = v;
+            } else {
+                // Row end or unaligned C: element stores.
+#pragma unroll
+                for (int e = 0; e < 16 / ES; ++e) {
+                    if (n + e >= g.n) break;
+                    const uint32_t w = v[(e * ES) / 4];
+                    if constexpr (ES == 4) reinterpret_cast<uint32_t*>(dst)[e] = w;
+                    else reinterpret_cast<uint16_t*>(dst)[e] = (uint16_t)(w >> (16 * (e & 1)));
+                }
             }
+        }
     }
 }
 
@@ -379,7 +465,7 @@ int launch(const Args& a0, int64_t batch, hipStream_t s) {
     a.tiles_m = (int)ceil_div(a.m, TILE);
     a.tiles_n = (int)ceil_div(a.n, TILE);
     dim3 grid((unsigned)(a.tiles_m * a.tiles_n), (unsigned)batch);
-    hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, 4>), grid, dim3(THREADS), 0, s, a);
+    hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, 4, true>), grid, dim3(THREADS), 0, s, a);
     return launch_check("gemm16_kernel");
 }
 

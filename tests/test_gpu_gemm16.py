@@ -16,7 +16,9 @@ import numpy as np
 import pytest
 
 from oxidizedmlx_amd import abi
-from test_gpu_gemm import check_gemm, sample_rows
+from oxidizedmlx_amd import backend as hb
+from oxidizedmlx_amd import synth
+from test_gpu_gemm import check_gemm, sample_rows, to_dev
 
 pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip", "oracle_lib")]
 
@@ -67,3 +69,30 @@ def test_lds16_falls_back_when_unsupported(gemm_path):
     # K = 1531 is not a multiple of 8: the general kernel must run and agree.
     check_gemm(1000, 777, 1531, BF16, F32, seed=31, rows=sample_rows(1000, 12))
     check_gemm(70, 64, 48, F16, F32, ld_pad=3, seed=32, rows=np.arange(70))
+
+
+@pytest.mark.parametrize("gemm_path", ["lds16", "general"], indirect=True)
+@pytest.mark.parametrize("ab", [BF16, F16])
+def test_output_rounding_bit_exact(gemm_path, ab):
+    # K = 8 with only k = 0 non-zero: C[m, n] = a[m] * b[n], a product of two
+    # 16-bit values and so exact in f32. The 16-bit C must then be that
+    # product rounded to nearest even, bit for bit (bf16: synth.bf16_bits;
+    # f16: numpy's float16 conversion).
+    m, n, k = 300, 264, 8
+    a0 = synth.normal(91, (m,)) * np.float32(3.0)
+    b0 = synth.normal(92, (n,))
+    a0 = synth.round_bf16(a0) if ab == BF16 else synth.round_f16(a0)
+    b0 = synth.round_bf16(b0) if ab == BF16 else synth.round_f16(b0)
+    A = np.zeros((m, k), np.float32)
+    A[:, 0] = a0
+    B = np.zeros((k, n), np.float32)
+    B[0, :] = b0
+    exact = np.outer(a0, b0).astype(np.float32)
+    assert np.array_equal(exact.astype(np.float64), np.outer(a0.astype(np.float64), b0.astype(np.float64)))
+    da, db = to_dev(A, ab), to_dev(B, ab)
+    dc = hb.DeviceBuffer(m * n * 2)
+    hb.gemm(ab, ab, False, False, m, n, k, da, k, db, n, dc, n)
+    got = dc.download(np.uint16, m * n).reshape(m, n)
+    want = synth.bf16_bits(exact) if ab == BF16 else exact.astype(np.float16).view(np.uint16)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0]}: got {got[tuple(bad[0])]:#06x} want {want[tuple(bad[0])]:#06x}"
