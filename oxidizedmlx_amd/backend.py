@@ -171,6 +171,19 @@ def _p(x) -> int:
     return x.ptr if isinstance(x, DeviceBuffer) else int(x or 0)
 
 
+def eval_node_dev(op: Op, inputs: Sequence[tuple], out_meta: TensorMeta, out, stream=None) -> None:
+    """Backend::eval_node on HBM-resident operands (mlxhip_eval_node_dev):
+    ``inputs`` are (device buffer or address, shape) pairs, ``out`` receives
+    numel(out_meta) f32 values; asynchronous on ``stream``."""
+    L = lib()
+    cop, k1 = op.to_c()
+    nodes = [NodeInput(np.empty(0, np.float32), tuple(shape)) for _, shape in inputs]
+    arr, k2 = inputs_to_c(nodes, [_p(buf) for buf, _ in inputs])
+    cm, k3 = out_meta.to_c()
+    abi.check(L.mlxhip_eval_node_dev(C.byref(cop), arr, len(inputs), C.byref(cm), _p(out), stream), L)
+    del k1, k2, k3
+
+
 def gemm(ab_dtype: int, c_dtype: int, trans_a: bool, trans_b: bool, m: int, n: int, k: int,
          a, lda: int, b, ldb: int, c, ldc: int, batch: int = 1, stride_a: int = 0,
          stride_b: int = 0, stride_c: int = 0, stream: int | None = None) -> None:

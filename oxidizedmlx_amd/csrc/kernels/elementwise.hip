@@ -79,52 +79,66 @@ struct EwProg {
     int n_instr;
 };
 
-template <int U>
+__device__ inline float4 apply4(int op, float4 a, float4 b) {
+    return make_float4(apply(op, a.x, b.x), apply(op, a.y, b.y), apply(op, a.z, b.z), apply(op, a.w, b.w));
+}
+
+// NI inputs, U float4 per input per thread per grid-stride step. Every
+// input's vectors are loaded before the program runs, so a thread has all
+// NI * U loads in flight at once instead of one input's per instruction; the
+// operand of each instruction is then picked by uniform (scalar) branches.
+template <int NI, int U, bool NT>
 __global__ __launch_bounds__(BLOCK) void ew_chain_vec_kernel(EwProg prog, float* __restrict__ out,
                                                              int64_t n_vec) {
     const int64_t stride = (int64_t)gridDim.x * BLOCK * U;
     for (int64_t base = (int64_t)blockIdx.x * BLOCK * U + threadIdx.x; base < n_vec;
          base += stride) {
+        float4 in[NI][U];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t idx = base + (int64_t)u * BLOCK;
+                in[i][u] = idx < n_vec ? reinterpret_cast<const float4*>(prog.in[i])[idx]
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         float4 acc[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t i = base + (int64_t)u * BLOCK;
-            acc[u] = i < n_vec ? reinterpret_cast<const float4*>(prog.in[0])[i]
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int u = 0; u < U; ++u) acc[u] = in[0][u];
         for (int k = 0; k < prog.n_instr; ++k) {
             const int op = prog.op[k];
-            if (ew_binary(op)) {
-                const float4* src = reinterpret_cast<const float4*>(prog.in[prog.operand[k]]);
-                float4 b[U];
+            const int o = prog.operand[k];
 #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int64_t i = base + (int64_t)u * BLOCK;
-                    b[u] = i < n_vec ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                }
+            for (int i = 0; i < NI; ++i) {
+                if (i == o) {
 #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    acc[u].x = apply(op, acc[u].x, b[u].x);
-                    acc[u].y = apply(op, acc[u].y, b[u].y);
-                    acc[u].z = apply(op, acc[u].z, b[u].z);
-                    acc[u].w = apply(op, acc[u].w, b[u].w);
-                }
-            } else {
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    acc[u].x = apply(op, acc[u].x, 0.f);
-                    acc[u].y = apply(op, acc[u].y, 0.f);
-                    acc[u].z = apply(op, acc[u].z, 0.f);
-                    acc[u].w = apply(op, acc[u].w, 0.f);
+                    for (int u = 0; u < U; ++u) acc[u] = apply4(op, acc[u], in[i][u]);
                 }
             }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t i = base + (int64_t)u * BLOCK;
-            if (i < n_vec) reinterpret_cast<float4*>(out)[i] = acc[u];
+            const int64_t idx = base + (int64_t)u * BLOCK;
+            if (idx < n_vec) {
+                typedef float f32x4 __attribute__((ext_vector_type(4)));
+                const f32x4 v = {acc[u].x, acc[u].y, acc[u].z, acc[u].w};
+                if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out) + idx);
+                else reinterpret_cast<f32x4*>(out)[idx] = v;
+            }
         }
     }
+}
+
+// One float4 per input per thread: with more per thread, each instruction's
+// uniform dispatch is repeated per component and the chain turns VALU-bound
+// (SiLU(x*w+b) ran at 43% of HBM bandwidth with 4, 92% with 1).
+template <int NI>
+int launch_chain_vec(const EwProg& p, float* out, int64_t n_vec, hipStream_t s) {
+    constexpr int U = 1;
+    int64_t grid = ceil_div(n_vec, (int64_t)BLOCK * U);
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL((ew_chain_vec_kernel<NI, U, false>), dim3((unsigned)grid), dim3(BLOCK), 0, s, p, out, n_vec);
+    return launch_check("ew_chain_vec_kernel");
 }
 
 __global__ __launch_bounds__(BLOCK) void ew_chain_scalar_kernel(EwProg prog, float* __restrict__ out,
@@ -400,14 +414,18 @@ int ew_chain(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inp
     if (numel == 0) return MLXHIP_OK;
     int64_t done = 0;
     if (aligned) {
-        constexpr int U = 4;
         const int64_t n_vec = numel / 4;
         if (n_vec > 0) {
-            int64_t grid = ceil_div(n_vec, (int64_t)BLOCK * U);
-            if (grid > 65536) grid = 65536;
-            hipLaunchKernelGGL((ew_chain_vec_kernel<U>), dim3((unsigned)grid), dim3(BLOCK), 0, s, p,
-                               out, n_vec);
-            MLXHIP_TRY(launch_check("ew_chain_vec_kernel"));
+            switch (n_inputs) {
+                case 1: MLXHIP_TRY(launch_chain_vec<1>(p, out, n_vec, s)); break;
+                case 2: MLXHIP_TRY(launch_chain_vec<2>(p, out, n_vec, s)); break;
+                case 3: MLXHIP_TRY(launch_chain_vec<3>(p, out, n_vec, s)); break;
+                case 4: MLXHIP_TRY(launch_chain_vec<4>(p, out, n_vec, s)); break;
+                case 5: MLXHIP_TRY(launch_chain_vec<5>(p, out, n_vec, s)); break;
+                case 6: MLXHIP_TRY(launch_chain_vec<6>(p, out, n_vec, s)); break;
+                case 7: MLXHIP_TRY(launch_chain_vec<7>(p, out, n_vec, s)); break;
+                default: MLXHIP_TRY(launch_chain_vec<8>(p, out, n_vec, s)); break;
+            }
         }
         done = n_vec * 4;
     }

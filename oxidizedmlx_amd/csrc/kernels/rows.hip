@@ -12,7 +12,10 @@
 //   rms_norm_vjp          :462-510
 // The arithmetic per element is the reference's (divide where it divides, no
 // contraction into FMA); only the summation order differs (per-lane partial
-// sums, then a butterfly across the wavefront and across waves).
+// sums, then a butterfly across the wavefront and across waves). The
+// per-element divisions by a row's sum / standard deviation / rms use the
+// row's reciprocal plus one exact-remainder correction (div_by), which yields
+// the same correctly rounded quotient as a division for normal values.
 //
 // Layout / launch (CDNA4, wave64): a row is owned by WPR wavefronts (64*WPR
 // lanes). Each lane keeps NV vectors of VEC floats of the row in VGPRs, so
@@ -61,6 +64,28 @@ __device__ inline float row_reduce(float v, float* slot, int wave_in_row, int la
     return v;
 }
 
+// x / d for a divisor d shared by a whole row, given r = 1 / d (one IEEE
+// division per row): q = x * r, then one Markstein correction with the exact
+// remainder fma(-q, d, x). With r correctly rounded this returns the
+// correctly rounded quotient -- the reference's x / d -- whenever the
+// quotient and x are normal numbers (subnormal quotients may differ by one
+// unit in the last place). The row divisors here are >= 1 (softmax) or
+// square roots of a sum plus eps, so r is normal unless d overflowed to +inf;
+// row_divisor turns that case into d = 1, r = 0, which gives x / inf = 0 for
+// finite x and NaN for infinite x, as the division does.
+__device__ inline float div_by(float x, float d, float r) {
+    const float q = x * r;
+    return __builtin_fmaf(__builtin_fmaf(-q, d, x), r, q);
+}
+
+__device__ inline void row_divisor(float& d, float& r) {
+    r = 1.0f / d;
+    if (__builtin_isinf(d)) {
+        d = 1.0f;
+        r = 0.0f;
+    }
+}
+
 template <int VEC>
 struct Vec;
 template <>
@@ -70,20 +95,30 @@ struct Vec<4> {
         float4 t = *reinterpret_cast<const float4*>(p);
         d[0] = t.x; d[1] = t.y; d[2] = t.z; d[3] = t.w;
     }
+    // Non-temporal: the output is not read again by this kernel; streaming it
+    // past the caches kept 1-read/1-write rows at ~80% of HBM bandwidth
+    // instead of ~62%.
     static __device__ inline void store(float* p, const float* d) {
-        *reinterpret_cast<float4*>(p) = make_float4(d[0], d[1], d[2], d[3]);
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(f32x4{d[0], d[1], d[2], d[3]}, reinterpret_cast<f32x4*>(p));
     }
 };
 template <>
 struct Vec<1> {
     static __device__ inline void load(const float* p, float* d) { d[0] = *p; }
-    static __device__ inline void store(float* p, const float* d) { *p = d[0]; }
+    static __device__ inline void store(float* p, const float* d) { __builtin_nontemporal_store(d[0], p); }
 };
 
 // a: x (forward) or dy (VJP); b: second operand of a VJP (softmax output s,
-// or the forward input x). p: eps or scale.
-template <int OP, int WPR, int NV, int VEC>
-__global__ __launch_bounds__(BLOCK) void row_kernel(const float* __restrict__ a,
+// or the forward input x). p: eps or scale. EVEN: every row of the grid
+// exists and holds exactly NV * VEC * 64 * WPR columns, so no element needs
+// a bounds predicate.
+// Single-input ops are held to 128 VGPRs so four 256-thread workgroups (16
+// waves) are resident per CU: a [4096, 4096] problem is 1024 workgroups, i.e.
+// exactly one round on 256 CUs.
+template <int OP, int WPR, int NV, int VEC, bool EVEN>
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
+    (OP == ROW_SOFTMAX_VJP || OP == ROW_LAYERNORM_VJP || OP == ROW_RMSNORM_VJP) ? 2 : 4))) void row_kernel(const float* __restrict__ a,
                                                     const float* __restrict__ b,
                                                     float* __restrict__ y, int64_t rows,
                                                     int cols, float p, int causal) {
@@ -100,7 +135,7 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(const float* __restrict__ a,
     const int wave_in_row = t / WAVE;
     const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + row_in_block;
     // Rows past the end still take part in the block barriers.
-    const bool live = row < rows;
+    const bool live = EVEN || row < rows;
     float* slot = red[row_in_block];
 
     const float* ar = a + (live ? row : 0) * (int64_t)cols;
@@ -112,7 +147,7 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(const float* __restrict__ a,
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = (j * TPR + t) * VEC;
-        ok[j] = live && c < cols;
+        ok[j] = EVEN || (live && c < cols);
         if (ok[j]) {
             Vec<VEC>::load(ar + c, &v[j * VEC]);
             if constexpr (TWO) Vec<VEC>::load(br + c, &w[j * VEC]);
@@ -155,8 +190,10 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(const float* __restrict__ a,
                 s += ex;
             }
         s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+        float r;
+        row_divisor(s, r);
 #pragma unroll
-        for (int j = 0; j < N; ++j) v[j] = v[j] / s;
+        for (int j = 0; j < N; ++j) v[j] = div_by(v[j], s, r);
     } else if constexpr (OP == ROW_LAYERNORM) {
         float s = 0.0f;
 #pragma unroll
@@ -174,17 +211,19 @@ __global__ __launch_bounds__(BLOCK) void row_kernel(const float* __restrict__ a,
                 }
         q = row_reduce<WPR, false>(q, slot, wave_in_row, lane);
         const float var = q / d;
-        const float sd = sqrtf(var + p);
+        float sd = sqrtf(var + p), r;
+        row_divisor(sd, r);
 #pragma unroll
-        for (int j = 0; j < N; ++j) v[j] = (v[j] - mean) / sd;
+        for (int j = 0; j < N; ++j) v[j] = div_by(v[j] - mean, sd, r);
     } else if constexpr (OP == ROW_RMSNORM) {
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < N; ++j) s += v[j] * v[j];
         s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
-        const float rms = sqrtf(s / d + p);
+        float rms = sqrtf(s / d + p), r;
+        row_divisor(rms, r);
 #pragma unroll
-        for (int j = 0; j < N; ++j) v[j] = v[j] / rms;
+        for (int j = 0; j < N; ++j) v[j] = div_by(v[j], rms, r);
     } else if constexpr (OP == ROW_SOFTMAX_VJP) {
         // v = dy, w = s
         float dot = 0.0f;
@@ -374,8 +413,12 @@ int launch_rows(const float* a, const float* b, float* y, int64_t rows, int64_t 
                 int causal, hipStream_t s) {
     constexpr int RPB = BLOCK / (WAVE * WPR);
     const int64_t grid = ceil_div(rows, RPB);
-    hipLaunchKernelGGL((row_kernel<OP, WPR, NV, VEC>), dim3((unsigned)grid), dim3(BLOCK), 0, s, a,
-                       b, y, rows, (int)cols, p, causal);
+    if (cols == (int64_t)NV * VEC * WAVE * WPR && rows % RPB == 0)
+        hipLaunchKernelGGL((row_kernel<OP, WPR, NV, VEC, true>), dim3((unsigned)grid), dim3(BLOCK), 0,
+                           s, a, b, y, rows, (int)cols, p, causal);
+    else
+        hipLaunchKernelGGL((row_kernel<OP, WPR, NV, VEC, false>), dim3((unsigned)grid), dim3(BLOCK), 0,
+                           s, a, b, y, rows, (int)cols, p, causal);
     return launch_check("row_kernel");
 }
 
@@ -387,19 +430,22 @@ int dispatch_rows(const float* a, const float* b, float* y, int64_t rows, int64_
                       (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
                       (!two || reinterpret_cast<uintptr_t>(b) % 16 == 0);
     if (vec4) {
-        // One wave per row up to 4096 columns (64 lanes x 16 float4), unless a
-        // wider row group is forced for tuning.
+        // force_wpr: 0 = automatic, else waves per row (1, 2 or 4) for tuning.
         if (force_wpr <= 1) {
             if (cols <= 256) return launch_rows<OP, 1, 1, 4>(a, b, y, rows, cols, p, causal, s);
             if (cols <= 512) return launch_rows<OP, 1, 2, 4>(a, b, y, rows, cols, p, causal, s);
             if (cols <= 1024) return launch_rows<OP, 1, 4, 4>(a, b, y, rows, cols, p, causal, s);
             if (cols <= 2048) return launch_rows<OP, 1, 8, 4>(a, b, y, rows, cols, p, causal, s);
-            if (cols <= 4096 && force_wpr == 1)
-                return launch_rows<OP, 1, 16, 4>(a, b, y, rows, cols, p, causal, s);
         }
-        if (force_wpr == 2 && cols <= 4096)
-            return launch_rows<OP, 2, 8, 4>(a, b, y, rows, cols, p, causal, s);
-        if (cols <= 4096) return launch_rows<OP, 4, 4, 4>(a, b, y, rows, cols, p, causal, s);
+        // 2049..4096 columns: softmax runs two waves per row (a shorter exp
+        // chain per wave measured faster), the others one.
+        constexpr bool SOFTMAX_LIKE = OP == ROW_SOFTMAX || OP == ROW_SCALED_MASKED_SOFTMAX;
+        const int wpr = force_wpr ? force_wpr : (SOFTMAX_LIKE ? 2 : 1);
+        if (cols <= 4096) {
+            if (wpr == 1) return launch_rows<OP, 1, 16, 4>(a, b, y, rows, cols, p, causal, s);
+            if (wpr == 2) return launch_rows<OP, 2, 8, 4>(a, b, y, rows, cols, p, causal, s);
+            return launch_rows<OP, 4, 4, 4>(a, b, y, rows, cols, p, causal, s);
+        }
         if (cols <= 8192) return launch_rows<OP, 4, 8, 4>(a, b, y, rows, cols, p, causal, s);
         if (cols <= 16384) return launch_rows<OP, 4, 16, 4>(a, b, y, rows, cols, p, causal, s);
     } else {
@@ -428,8 +474,8 @@ int row_op(int op, const float* a, const float* b, float* y, int64_t rows, int64
     if (rows < 0 || cols < 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: negative size");
     if (rows > (int64_t)INT32_MAX) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: too many rows");
     if (cols > INT32_MAX) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: row too long");
-    // 0 = auto: one wave per row up to 4096 columns.
-    const int fw = row_force_wpr() ? row_force_wpr() : 1;
+    // MLXHIP_ROW_WPR forces the waves per row (tuning); 0 / unset = automatic.
+    const int fw = row_force_wpr();
     switch (op) {
         case ROW_SOFTMAX: return dispatch_rows<ROW_SOFTMAX>(a, b, y, rows, cols, p, causal, s, fw);
         case ROW_SCALED_MASKED_SOFTMAX:
