@@ -5,8 +5,10 @@
 #include "gemm_impl.hpp"
 #include "gemm16_impl.hpp"
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace mlxhip {
 namespace {
@@ -21,6 +23,73 @@ __global__ __launch_bounds__(256) void zero_c_kernel(char* c, int64_t ldc, int64
 }
 
 int elem_size(int dt) { return dt == MLXHIP_DTYPE_F32 ? 4 : 2; }
+
+// Sum of the split-K partials in split order (deterministic), converted to C.
+// ws holds batch * splits slices of [m, n] f32, slice (b, s) at (b*splits+s)*m*n.
+template <int CT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, void* c, int64_t m,
+                                                            int64_t n, int64_t ldc, int64_t sc, int splits) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= m * n) return;
+    const int64_t b = blockIdx.y;
+    const float* p = ws + b * splits * m * n + idx;
+    float acc = p[0];
+    for (int s = 1; s < splits; ++s) acc += p[(int64_t)s * m * n];
+    const int64_t row = idx / n, col = idx % n;
+    gemm_detail::store_c<CT>(c, b * sc + row * ldc + col, acc);
+}
+
+// dst[r][c] = src[r][c] for r < rows, c < cols, zero elsewhere in the
+// rows_p x cols_p destination (one matrix per blockIdx.y).
+template <typename T>
+__global__ __launch_bounds__(256) void pack_kernel(const T* __restrict__ src, int64_t ld, int64_t sstride,
+                                                   int64_t rows, int64_t cols, T* __restrict__ dst,
+                                                   int64_t rows_p, int64_t cols_p) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows_p * cols_p) return;
+    const int64_t r = idx / cols_p, c = idx % cols_p, b = blockIdx.y;
+    dst[b * rows_p * cols_p + idx] = (r < rows && c < cols) ? src[b * sstride + r * ld + c] : T(0);
+}
+
+// Stream-ordered scratch: allocated on `s`, returned to the device's memory
+// pool on `s` after every kernel enqueued before the destructor has run.
+struct StreamBuf {
+    void* p = nullptr;
+    hipStream_t s;
+    explicit StreamBuf(hipStream_t st) : s(st) {}
+    int alloc(size_t bytes) {
+        static std::once_flag keep[64];
+        int dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+            std::call_once(keep[dev], [dev] {
+                // Keep freed blocks in the pool instead of returning them to the
+                // driver at every synchronisation.
+                hipMemPool_t pool;
+                if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+                    uint64_t hi = UINT64_MAX;
+                    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &hi);
+                }
+            });
+        }
+        MLXHIP_HIP(hipMallocAsync(&p, bytes ? bytes : 16, s));
+        return MLXHIP_OK;
+    }
+    ~StreamBuf() {
+        if (p) (void)hipFreeAsync(p, s);
+    }
+};
+
+int pack(int dt, const void* src, int64_t ld, int64_t sstride, int64_t rows, int64_t cols, void* dst,
+         int64_t rows_p, int64_t cols_p, int64_t batch, hipStream_t s) {
+    dim3 grid((unsigned)ceil_div(rows_p * cols_p, 256), (unsigned)batch);
+    if (dt == MLXHIP_DTYPE_F32)
+        hipLaunchKernelGGL(pack_kernel<uint32_t>, grid, dim3(256), 0, s, static_cast<const uint32_t*>(src), ld,
+                           sstride, rows, cols, static_cast<uint32_t*>(dst), rows_p, cols_p);
+    else
+        hipLaunchKernelGGL(pack_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(src), ld,
+                           sstride, rows, cols, static_cast<uint16_t*>(dst), rows_p, cols_p);
+    return launch_check("pack_kernel");
+}
 
 // MLXHIP_GEMM_PATH: unset/"auto" = choose by shape, "general" = always the
 // general kernel, "lds16" = the direct-to-LDS 16-bit kernel whenever the
@@ -66,6 +135,26 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
     const bool aligned = reinterpret_cast<uintptr_t>(a) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(b) % 16 == 0 && lda % ch == 0 &&
                          ldb % ch == 0 && (batch == 1 || (stride_a % ch == 0 && stride_b % ch == 0));
+    const int path = gemm_path();
+    if (!aligned && path != 1) {
+        // Unaligned operands (odd leading dimension, offset pointer): copy both
+        // into zero-padded buffers whose rows are whole 16-byte chunks (K and
+        // the contiguous extents rounded up to a multiple of 16 bytes) and run
+        // the aligned kernels on those. The zero padding adds nothing to C.
+        const int64_t kp = ceil_div(k, ch) * ch;
+        const int64_t a_rows = trans_a ? k : m, a_cols = trans_a ? m : k;
+        const int64_t a_rows_p = trans_a ? kp : m, a_cols_p = ceil_div(a_cols, ch) * ch;
+        const int64_t b_rows = trans_b ? n : k, b_cols = trans_b ? k : n;
+        const int64_t b_rows_p = trans_b ? n : kp, b_cols_p = ceil_div(b_cols, ch) * ch;
+        const int es = elem_size(ab_dtype);
+        StreamBuf pa(s), pb(s);
+        MLXHIP_TRY(pa.alloc((size_t)(a_rows_p * a_cols_p * batch * es)));
+        MLXHIP_TRY(pb.alloc((size_t)(b_rows_p * b_cols_p * batch * es)));
+        MLXHIP_TRY(pack(ab_dtype, a, lda, stride_a, a_rows, a_cols, pa.p, a_rows_p, a_cols_p, batch, s));
+        MLXHIP_TRY(pack(ab_dtype, b, ldb, stride_b, b_rows, b_cols, pb.p, b_rows_p, b_cols_p, batch, s));
+        return gemm(ab_dtype, c_dtype, trans_a, trans_b, m, n, kp, batch, pa.p, a_cols_p, a_rows_p * a_cols_p,
+                    pb.p, b_cols_p, b_rows_p * b_cols_p, c, ldc, stride_c, s);
+    }
 
     gemm_detail::GemmArgs g{};
     g.m = m;
@@ -84,7 +173,6 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
     // 16-bit operands on 256x256 tiles with direct-to-LDS loads when the
     // problem fills the chip and the operands meet that kernel's layout
     // requirements; the general kernel covers everything else.
-    const int path = gemm_path();
     if (ab_dtype != MLXHIP_DTYPE_F32 && path != 1) {
         const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256) * batch;
         gemm16::Args h{};
@@ -107,11 +195,59 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
                                                  : gemm16_f16(c_dtype, ta, tb, h, batch, s);
         }
     }
-    switch (ab_dtype) {
-        case MLXHIP_DTYPE_F32: return gemm_f32(c_dtype, ta, tb, g, batch, aligned, s);
-        case MLXHIP_DTYPE_BF16: return gemm_bf16(c_dtype, ta, tb, g, batch, aligned, s);
-        default: return gemm_f16(c_dtype, ta, tb, g, batch, aligned, s);
+    // General kernel: the largest block tile that still gives about one
+    // workgroup per CU; below that 64x64 tiles, and when even those leave most
+    // of the 256 CUs idle, split K over several workgroups whose f32 partials
+    // are summed in a fixed order (deterministic) by a second kernel.
+    const int bk = ab_dtype == MLXHIP_DTYPE_F32 ? 32 : 64;
+    auto tiles = [&](int w) { return ceil_div(m, 64 * w) * ceil_div(n, 64 * w) * batch; };
+    int wt = 2, splits = 1;
+    if (ab_dtype != MLXHIP_DTYPE_F32 && tiles(4) >= 240) {
+        wt = 4;
+    } else if (tiles(2) < 200) {
+        wt = 1;
+        const int64_t t = tiles(1);
+        if (t < 192 && aligned) {
+            const int64_t by_cus = std::max<int64_t>(1, 256 / t);
+            const int64_t by_k = k / (4 * bk);  // at least 4 K tiles per split
+            splits = (int)std::min<int64_t>(8, std::min(by_cus, by_k));
+            if (splits < 1) splits = 1;
+            if (batch * splits > 65535) splits = 1;
+        }
     }
+    auto run = [&](const gemm_detail::GemmArgs& ga, int ct) {
+        switch (ab_dtype) {
+            case MLXHIP_DTYPE_F32: return gemm_f32(ct, ta, tb, ga, batch, aligned, wt, s);
+            case MLXHIP_DTYPE_BF16: return gemm_bf16(ct, ta, tb, ga, batch, aligned, wt, s);
+            default: return gemm_f16(ct, ta, tb, ga, batch, aligned, wt, s);
+        }
+    };
+    if (splits == 1) return run(g, c_dtype);
+    g.k_chunk = ceil_div(ceil_div(k, splits), bk) * bk;
+    g.splits = (int)ceil_div(k, g.k_chunk);
+    StreamBuf ws(s);
+    MLXHIP_TRY(ws.alloc((size_t)(batch * g.splits * m * n) * sizeof(float)));
+    gemm_detail::GemmArgs gp = g;
+    gp.c = ws.p;
+    gp.ldc = n;
+    gp.sc = m * n;
+    MLXHIP_TRY(run(gp, MLXHIP_DTYPE_F32));
+    dim3 grid((unsigned)ceil_div(m * n, 256), (unsigned)batch);
+    switch (c_dtype) {
+        case MLXHIP_DTYPE_F32:
+            hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_F32>, grid, dim3(256), 0, s,
+                               static_cast<const float*>(ws.p), c, m, n, ldc, stride_c, g.splits);
+            break;
+        case MLXHIP_DTYPE_BF16:
+            hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_BF16>, grid, dim3(256), 0, s,
+                               static_cast<const float*>(ws.p), c, m, n, ldc, stride_c, g.splits);
+            break;
+        default:
+            hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_F16>, grid, dim3(256), 0, s,
+                               static_cast<const float*>(ws.p), c, m, n, ldc, stride_c, g.splits);
+            break;
+    }
+    return launch_check("splitk_reduce_kernel");
 }
 
 }  // namespace mlxhip

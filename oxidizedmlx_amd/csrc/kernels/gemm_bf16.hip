@@ -4,10 +4,10 @@
 namespace mlxhip {
 
 int gemm_bf16(int c_dtype, int ta, int tb, const gemm_detail::GemmArgs& a, int64_t batch,
-               bool aligned, hipStream_t s) {
+               bool aligned, int wt, hipStream_t s) {
     using namespace gemm_detail;
-    if (c_dtype == MLXHIP_DTYPE_F32) return dispatch_trans<MLXHIP_DTYPE_BF16, MLXHIP_DTYPE_F32>(a, batch, ta, tb, aligned, s);
-    if (c_dtype == MLXHIP_DTYPE_BF16) return dispatch_trans<MLXHIP_DTYPE_BF16, MLXHIP_DTYPE_BF16>(a, batch, ta, tb, aligned, s);
+    if (c_dtype == MLXHIP_DTYPE_F32) return dispatch_trans<MLXHIP_DTYPE_BF16, MLXHIP_DTYPE_F32>(a, batch, ta, tb, aligned, wt, s);
+    if (c_dtype == MLXHIP_DTYPE_BF16) return dispatch_trans<MLXHIP_DTYPE_BF16, MLXHIP_DTYPE_BF16>(a, batch, ta, tb, aligned, wt, s);
     return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: output dtype %d unsupported for bf16 inputs", c_dtype);
 }
 

@@ -49,6 +49,11 @@ struct GemmArgs {
     void* c;
     int64_t ldc, sc;
     int tiles_m, tiles_n;
+    // Split-K: blockIdx.y = batch * splits + split; split s covers
+    // k in [s * k_chunk, min(k, (s + 1) * k_chunk)) and writes its f32
+    // partial product to C + blockIdx.y * sc (a workspace the host reduces).
+    int splits = 1;
+    int64_t k_chunk = 0;
 };
 
 template <int DT>
@@ -243,9 +248,12 @@ void gemm_kernel(GemmArgs g) {
     const int tm = first_m + (id % in_group) % gsz;
     const int tn = (id % in_group) / gsz;
 
-    const int64_t batch = blockIdx.y;
-    const T* A = static_cast<const T*>(g.a) + batch * g.sa;
-    const T* B = static_cast<const T*>(g.b) + batch * g.sb;
+    const int64_t by = blockIdx.y;
+    const int64_t batch = by / g.splits, split = by % g.splits;
+    const int64_t kb = split * g.k_chunk;                       // first k of this split
+    const int64_t klen = g.splits > 1 ? min(g.k - kb, g.k_chunk) : g.k;
+    const T* A = static_cast<const T*>(g.a) + batch * g.sa + (TA ? kb * g.lda : kb);
+    const T* B = static_cast<const T*>(g.b) + batch * g.sb + (TB ? kb : kb * g.ldb);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
 
     // A is K-contiguous unless transposed; B is K-contiguous only when transposed.
@@ -260,9 +268,9 @@ void gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    const int64_t nk = (g.k + BK - 1) / BK;
-    at.load(A, g.lda, m0, 0, g.m, g.k, tid);
-    bt.load(B, g.ldb, n0, 0, g.n, g.k, tid);
+    const int64_t nk = (klen + BK - 1) / BK;
+    at.load(A, g.lda, m0, 0, g.m, klen, tid);
+    bt.load(B, g.ldb, n0, 0, g.n, klen, tid);
     at.store(lds[0], tid);
     bt.store(lds[0] + BM, tid);
     __syncthreads();
@@ -272,8 +280,8 @@ void gemm_kernel(GemmArgs g) {
         const int cur = (int)(kt & 1);
         const bool more = kt + 1 < nk;
         if (more) {
-            at.load(A, g.lda, m0, (kt + 1) * BK, g.m, g.k, tid);
-            bt.load(B, g.ldb, n0, (kt + 1) * BK, g.n, g.k, tid);
+            at.load(A, g.lda, m0, (kt + 1) * BK, g.m, klen, tid);
+            bt.load(B, g.ldb, n0, (kt + 1) * BK, g.n, klen, tid);
         }
         uint4(*As)[8] = lds[cur];
         uint4(*Bs)[8] = lds[cur] + BM;
@@ -305,7 +313,7 @@ void gemm_kernel(GemmArgs g) {
 
     // Epilogue: accumulator element v of lane l is C[8*(v/4) + 4*(l/32) + v%4][l%32].
     void* C = g.c;
-    const int64_t cbase = batch * g.sc;
+    const int64_t cbase = by * g.sc;
 #pragma unroll
     for (int i = 0; i < WTM; ++i)
 #pragma unroll
@@ -324,37 +332,37 @@ int launch(const GemmArgs& a0, int64_t batch, hipStream_t s) {
     GemmArgs a = a0;
     a.tiles_m = (int)ceil_div(a.m, 64 * WTM);
     a.tiles_n = (int)ceil_div(a.n, 64 * WTN);
-    dim3 grid((unsigned)(a.tiles_m * a.tiles_n), (unsigned)batch);
+    dim3 grid((unsigned)(a.tiles_m * a.tiles_n), (unsigned)(batch * a.splits));
     hipLaunchKernelGGL((gemm_kernel<DT, CT, TA, TB, WTM, WTN, ALIGNED>), grid, dim3(256), 0, s, a);
     return launch_check("gemm_kernel");
 }
 
-// Tile choice: 256x256 (4x4 MFMA tiles per wave) when it still yields at
-// least ~one workgroup per CU, otherwise 128x128.
+// Block tile edge of the general kernel: 64 * wt (wt = 1, 2 or 4 MFMA tiles
+// per wave and dimension). The host picks wt and the split-K factor.
 template <int DT, int CT, int TA, int TB>
-int dispatch_layout(const GemmArgs& a, int64_t batch, bool aligned, hipStream_t s) {
-    const int64_t big_tiles = ceil_div(a.m, 256) * ceil_div(a.n, 256) * batch;
+int dispatch_layout(const GemmArgs& a, int64_t batch, bool aligned, int wt, hipStream_t s) {
     if (!aligned) return launch<DT, CT, TA, TB, 2, 2, false>(a, batch, s);
-    if (DT != MLXHIP_DTYPE_F32 && big_tiles >= 240) return launch<DT, CT, TA, TB, 4, 4, true>(a, batch, s);
+    if (wt == 4 && DT != MLXHIP_DTYPE_F32) return launch<DT, CT, TA, TB, 4, 4, true>(a, batch, s);
+    if (wt == 1) return launch<DT, CT, TA, TB, 1, 1, true>(a, batch, s);
     return launch<DT, CT, TA, TB, 2, 2, true>(a, batch, s);
 }
 
 template <int DT, int CT>
-int dispatch_trans(const GemmArgs& a, int64_t batch, int ta, int tb, bool aligned, hipStream_t s) {
-    if (!ta && !tb) return dispatch_layout<DT, CT, 0, 0>(a, batch, aligned, s);
-    if (!ta && tb) return dispatch_layout<DT, CT, 0, 1>(a, batch, aligned, s);
-    if (ta && !tb) return dispatch_layout<DT, CT, 1, 0>(a, batch, aligned, s);
-    return dispatch_layout<DT, CT, 1, 1>(a, batch, aligned, s);
+int dispatch_trans(const GemmArgs& a, int64_t batch, int ta, int tb, bool aligned, int wt, hipStream_t s) {
+    if (!ta && !tb) return dispatch_layout<DT, CT, 0, 0>(a, batch, aligned, wt, s);
+    if (!ta && tb) return dispatch_layout<DT, CT, 0, 1>(a, batch, aligned, wt, s);
+    if (ta && !tb) return dispatch_layout<DT, CT, 1, 0>(a, batch, aligned, wt, s);
+    return dispatch_layout<DT, CT, 1, 1>(a, batch, aligned, wt, s);
 }
 
 }  // namespace gemm_detail
 
 // Per-input-dtype entry points (one translation unit each, compiled in parallel).
 int gemm_f32(int c_dtype, int ta, int tb, const gemm_detail::GemmArgs& a, int64_t batch,
-             bool aligned, hipStream_t s);
+             bool aligned, int wt, hipStream_t s);
 int gemm_bf16(int c_dtype, int ta, int tb, const gemm_detail::GemmArgs& a, int64_t batch,
-              bool aligned, hipStream_t s);
+              bool aligned, int wt, hipStream_t s);
 int gemm_f16(int c_dtype, int ta, int tb, const gemm_detail::GemmArgs& a, int64_t batch,
-             bool aligned, hipStream_t s);
+             bool aligned, int wt, hipStream_t s);
 
 }  // namespace mlxhip

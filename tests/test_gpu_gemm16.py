@@ -96,3 +96,33 @@ def test_output_rounding_bit_exact(gemm_path, ab):
     want = synth.bf16_bits(exact) if ab == BF16 else exact.astype(np.float16).view(np.uint16)
     bad = np.argwhere(got != want)
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0]}: got {got[tuple(bad[0])]:#06x} want {want[tuple(bad[0])]:#06x}"
+
+
+@pytest.mark.parametrize("ab,cd", [(F32, F32), (BF16, F32), (BF16, BF16), (F16, F16)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_split_k(ab, cd, ta, tb):
+    # 4 x 3 tiles of 64 x 64 per batch with K = 4096: the general kernel splits
+    # K over 8 workgroups and a second kernel sums the f32 partials.
+    check_gemm(200, 136, 4096, ab, cd, ta=bool(ta), tb=bool(tb), batch=2, seed=61,
+               rows=sample_rows(200, 20))
+
+
+def test_split_k_is_deterministic():
+    A = synth.normal(71, (200, 4096))
+    B = synth.normal(72, (4096, 136))
+    da, db = to_dev(A, F32), to_dev(B, F32)
+    outs = []
+    for _ in range(3):
+        dc = hb.DeviceBuffer(200 * 136 * 4)
+        hb.gemm(F32, F32, False, False, 200, 136, 4096, da, 4096, db, 136, dc, 136)
+        outs.append(dc.download(np.float32))
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+
+
+@pytest.mark.parametrize("ab", [BF16, F16, F32])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_unaligned_operands_are_packed(ab, ta, tb):
+    # Odd leading dimensions (and batch strides) are copied into padded,
+    # aligned buffers before the aligned kernels run.
+    check_gemm(97, 75, 131, ab, F32, ta=bool(ta), tb=bool(tb), batch=3, ld_pad=3, seed=81,
+               rows=np.arange(97))
