@@ -158,7 +158,7 @@ def main() -> int:
             hb.gemm(abi.F32, abi.F32, False, False, 512, 512, 512, A1, 512, B1, 512, C1, 512,
                     stream=stream)
         elif name.startswith("gemm_") and "batched" in name:
-            f16 = "f16" in name
+            f16 = name.startswith("gemm_f16_")
             hb.gemm(abi.F16 if f16 else abi.BF16, abi.F32, False, "_nt_" in name, nb, nb, nb,
                     Abh if f16 else Ab16, nb, Bbh if f16 else Bb16, nb, Cb, nb, batch=bt,
                     stride_a=nb * nb, stride_b=nb * nb, stride_c=nb * nb, stream=stream)

@@ -196,9 +196,11 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
         }
     }
     // General kernel: the largest block tile that still gives about one
-    // workgroup per CU; below that 64x64 tiles, and when even those leave most
-    // of the 256 CUs idle, split K over several workgroups whose f32 partials
-    // are summed in a fixed order (deterministic) by a second kernel.
+    // workgroup per CU; below that 64x64 tiles, split over K until there are
+    // about four workgroups per CU (the general kernel prefetches one K tile
+    // ahead, so small tiles need several resident workgroups to hide load
+    // latency), keeping at least four K tiles per split. The f32 partials are
+    // summed in a fixed order (deterministic) by a second kernel.
     const int bk = ab_dtype == MLXHIP_DTYPE_F32 ? 32 : 64;
     auto tiles = [&](int w) { return ceil_div(m, 64 * w) * ceil_div(n, 64 * w) * batch; };
     int wt = 2, splits = 1;
@@ -207,8 +209,8 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
     } else if (tiles(2) < 200) {
         wt = 1;
         const int64_t t = tiles(1);
-        if (t < 192 && aligned) {
-            const int64_t by_cus = std::max<int64_t>(1, 256 / t);
+        if (t < 768 && aligned) {
+            const int64_t by_cus = std::max<int64_t>(1, 1024 / t);
             const int64_t by_k = k / (4 * bk);  // at least 4 K tiles per split
             splits = (int)std::min<int64_t>(8, std::min(by_cus, by_k));
             if (splits < 1) splits = 1;
