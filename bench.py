@@ -6,13 +6,15 @@ One step = one pass of the hot path over one batch of synthetic input:
   * row softmax, LayerNorm (eps 1e-5) and RMSNorm (eps 1e-5) over a
     [4096, 4096] f32 tensor, x ~ N(0, 2^2) (config 2);
   * the fused chain y = SiLU(x*w + b), w, b ~ U(-1, 1), same shape (config 2).
-``value`` is the GEMM's TFLOP/s; every kernel's time comes from HIP events
-recorded around its launch on the stream it runs on, averaged over the K
-timed steps. Each HBM-bound kernel has its own input/output buffers, rotated
-over SETS steps, so no kernel reads data another kernel (or its own previous
-launch) just touched: between two reads of a buffer ~1.5 GB of other traffic
-passes, far more than the 256 MiB Infinity Cache, and every kernel reads its
-operands from HBM. ``ms_per_step`` is the sum of the kernels' average times
+``value`` is the GEMM's TFLOP/s. The K timed steps run kernel by kernel: each
+kernel's K launches go back to back on one stream between two HIP events, and
+its time is the events' interval / K (the launch and event-marker overheads
+overlap the previous launch instead of adding to each one). Every kernel's
+large operand and output buffers rotate over SETS copies, so between two reads of
+one buffer at least (SETS-1) x 96 MiB of other traffic passes (384 MiB for
+the GEMM, more for the row kernels), more than the 256 MiB Infinity Cache:
+operands come from HBM, not from a cache warmed by the previous launch.
+``ms_per_step`` is the sum of the per-kernel times of the five step kernels
 (one pass of the hot path).
 The CPU baseline is the oracle (the C restatement of the reference's mlx-cpu
 kernels, single-threaded) timed on a bounded sample on this host.
@@ -94,8 +96,10 @@ def main() -> int:
     log("bench: generating inputs")
     A = synth.bf16_bits(synth.normal(SEEDS["A"], (n, n)))
     B = synth.bf16_bits(synth.normal(SEEDS["B"], (n, n)))
-    dA, dB = hb.DeviceBuffer.from_array(A), hb.DeviceBuffer.from_array(B)
-    dC = hb.DeviceBuffer(n * n * 2)
+    SETS = 5
+    dA = [hb.DeviceBuffer.from_array(A) for _ in range(SETS)]
+    dB = [hb.DeviceBuffer.from_array(B) for _ in range(SETS)]
+    dC = [hb.DeviceBuffer(n * n * 2) for _ in range(SETS)]
     # Config 1: f32 512^3. Config 3: batched [32,1024,1024]^2 bf16/f16 (f32 C),
     # the transposed-B case, and the odd 1000 x 777 x 1531 (edge tiles).
     A1 = hb.DeviceBuffer.from_array(synth.normal(0x5EED0001, (512, 512)))
@@ -104,12 +108,14 @@ def main() -> int:
     nb, bt = 1024, 32
     Ab = synth.normal(0x5EED0008, (bt, nb, nb))
     Bb = synth.normal(0x5EED0009, (bt, nb, nb))
-    Ab16 = hb.DeviceBuffer.from_array(synth.bf16_bits(Ab))
-    Bb16 = hb.DeviceBuffer.from_array(synth.bf16_bits(Bb))
-    Abh = hb.DeviceBuffer.from_array(synth.f16_bits(Ab))
-    Bbh = hb.DeviceBuffer.from_array(synth.f16_bits(Bb))
-    Cb = hb.DeviceBuffer(bt * nb * nb * 4)
+    Ab16 = [hb.DeviceBuffer.from_array(synth.bf16_bits(Ab)) for _ in range(SETS)]
+    Bb16 = [hb.DeviceBuffer.from_array(synth.bf16_bits(Bb)) for _ in range(SETS)]
+    Abh = [hb.DeviceBuffer.from_array(synth.f16_bits(Ab)) for _ in range(SETS)]
+    Bbh = [hb.DeviceBuffer.from_array(synth.f16_bits(Bb)) for _ in range(SETS)]
+    Cb = [hb.DeviceBuffer(bt * nb * nb * 4) for _ in range(SETS)]
     mo, no, ko = 1000, 777, 1531
+    # The config-1 and odd-shape operands (a few MiB) stay cache-resident
+    # whatever the rotation; they get one buffer set.
     Ao = hb.DeviceBuffer.from_array(synth.bf16_bits(synth.normal(0x5EED000A, (mo, ko))))
     Bo = hb.DeviceBuffer.from_array(synth.bf16_bits(synth.normal(0x5EED000B, (ko, no))))
     Co = hb.DeviceBuffer(mo * no * 4)
@@ -117,7 +123,6 @@ def main() -> int:
     x = synth.normal(SEEDS["x"], (n, n), 0.0, 2.0)
     w = synth.uniform(SEEDS["w"], (n, n), -1.0, 1.0)
     bb = synth.uniform(SEEDS["b"], (n, n), -1.0, 1.0)
-    SETS = 2
     row_ops = ("softmax", "layernorm", "rmsnorm", "chain")
     xs = {op: [hb.DeviceBuffer.from_array(x) for _ in range(SETS)] for op in row_ops}
     ys = {op: [hb.DeviceBuffer(x.nbytes) for _ in range(SETS)] for op in row_ops}
@@ -147,7 +152,7 @@ def main() -> int:
     def launch(name: str, i: int) -> None:
         j = i % SETS
         if name == "gemm_bf16_4096":
-            hb.gemm(abi.BF16, abi.BF16, False, False, n, n, n, dA, n, dB, n, dC, n, stream=stream)
+            hb.gemm(abi.BF16, abi.BF16, False, False, n, n, n, dA[j], n, dB[j], n, dC[j], n, stream=stream)
         elif name == "softmax_4096x4096":
             hb.softmax_rows(xs["softmax"][j], ys["softmax"][j], n, n, stream=stream)
         elif name == "layernorm_4096x4096":
@@ -160,7 +165,7 @@ def main() -> int:
         elif name.startswith("gemm_") and "batched" in name:
             f16 = name.startswith("gemm_f16_")
             hb.gemm(abi.F16 if f16 else abi.BF16, abi.F32, False, "_nt_" in name, nb, nb, nb,
-                    Abh if f16 else Ab16, nb, Bbh if f16 else Bb16, nb, Cb, nb, batch=bt,
+                    (Abh if f16 else Ab16)[j], nb, (Bbh if f16 else Bb16)[j], nb, Cb[j], nb, batch=bt,
                     stride_a=nb * nb, stride_b=nb * nb, stride_c=nb * nb, stream=stream)
         elif name == "gemm_bf16_odd_1000x777x1531_cfg3":
             hb.gemm(abi.BF16, abi.F32, False, False, mo, no, ko, Ao, ko, Bo, no, Co, no,
@@ -172,27 +177,28 @@ def main() -> int:
 
     names = [k for k in kernels
              if ((k in only) if kernels[k].get("calibration") else want(k))]
-    ev = {k: [(hb.Event(), hb.Event()) for _ in range(args.steps)] for k in names}
+    ev = {k: (hb.Event(), hb.Event()) for k in names}
 
     log(f"bench: warmup {args.warmup} steps")
-    for i in range(args.warmup):
-        for k in names:
+    for k in names:
+        for i in range(args.warmup):
             launch(k, i)
     hb.synchronize(stream)
     log(f"bench: timing {args.steps} steps")
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        for k in names:
-            e0, e1 = ev[k][i]
-            e0.record(stream)
+    for k in names:
+        e0, e1 = ev[k]
+        e0.record(stream)
+        for i in range(args.steps):
             launch(k, i)
-            e1.record(stream)
+        e1.record(stream)
     hb.synchronize(stream)
     wall = time.perf_counter() - t0
 
     res = {}
     for k in names:
-        ms = sum(e0.elapsed_ms(e1) for e0, e1 in ev[k]) / args.steps
+        e0, e1 = ev[k]
+        ms = e0.elapsed_ms(e1) / args.steps
         r = {"us": ms * 1e3}
         if "flops" in kernels[k]:
             r["tflops"] = kernels[k]["flops"] / (ms * 1e-3) / 1e12

@@ -93,13 +93,15 @@ int pack(int dt, const void* src, int64_t ld, int64_t sstride, int64_t rows, int
 
 // MLXHIP_GEMM_PATH: unset/"auto" = choose by shape, "general" = always the
 // general kernel, "lds16" = the direct-to-LDS 16-bit kernel whenever the
-// operands allow it. Read on every call so one process (the tests) can
-// cover both kernels.
+// operands allow it ("lds16_256" / "lds16_128": with that block size). Read
+// on every call so one process (the tests) can cover every kernel.
 int gemm_path() {
     const char* e = getenv("MLXHIP_GEMM_PATH");
     if (!e) return 0;
     if (!strcmp(e, "general")) return 1;
     if (!strcmp(e, "lds16")) return 2;
+    if (!strcmp(e, "lds16_256")) return 3;
+    if (!strcmp(e, "lds16_128")) return 4;
     return 0;
 }
 
@@ -170,13 +172,17 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
     g.ldc = ldc;
     g.sc = stride_c;
     const int ta = trans_a ? 1 : 0, tb = trans_b ? 1 : 0;
-    // 16-bit operands on 256x256 tiles with direct-to-LDS loads when the
-    // problem fills the chip and the operands meet that kernel's layout
-    // requirements; the general kernel covers everything else.
+    // 16-bit operands go to the direct-to-LDS kernel when the operands meet
+    // its layout requirements and the problem has enough block tiles to
+    // occupy the chip: 256x256 blocks from 128 tiles (one workgroup per CU,
+    // so at least half the CUs busy), else 128x128 blocks (two per CU) from
+    // 128 tiles. The general kernel, with split-K, covers everything else.
     if (ab_dtype != MLXHIP_DTYPE_F32 && path != 1) {
         const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256) * batch;
+        const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * batch;
+        const int cfg = path == 3 ? 0 : path == 4 ? 1 : big_tiles >= 128 ? 0 : 1;
         gemm16::Args h{};
-        if ((path == 2 || big_tiles >= 200) &&
+        if ((path >= 2 || big_tiles >= 128 || mid_tiles >= 128) &&
             gemm16::supported(ta, tb, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, &h.a_bytes,
                               &h.b_bytes)) {
             h.m = m;
@@ -191,8 +197,8 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
             h.c = c;
             h.ldc = ldc;
             h.sc = stride_c;
-            return ab_dtype == MLXHIP_DTYPE_BF16 ? gemm16_bf16(c_dtype, ta, tb, h, batch, s)
-                                                 : gemm16_f16(c_dtype, ta, tb, h, batch, s);
+            return ab_dtype == MLXHIP_DTYPE_BF16 ? gemm16_bf16(c_dtype, ta, tb, h, batch, cfg, s)
+                                                 : gemm16_f16(c_dtype, ta, tb, h, batch, cfg, s);
         }
     }
     // General kernel: the largest block tile that still gives about one

@@ -6,37 +6,43 @@
 // hot path (plain, batched, and the NT/TN forms autograd's MatMul VJP
 // produces, crates/mlx-autograd/src/vjp.rs:71-80).
 //
-// Work decomposition
-//   * Block tile 256 x 256, K tile 32; 256 threads = 4 wave64s in a 2 x 2
-//     grid, each wave owning a 128 x 128 quadrant = 4 x 4 tiles of
-//     v_mfma_f32_32x32x16_{bf16,f16} (256 f32 accumulators per lane).
+// Work decomposition (Cfg below; two configurations are instantiated)
+//   * CfgLarge: block tile 256 x 256, 512 threads = 8 wave64s in a 2 x 4
+//     grid, each wave owning 128 x 64 = 4 x 2 tiles of
+//     v_mfma_f32_32x32x16_{bf16,f16} (128 f32 accumulators per lane), two
+//     waves per SIMD so one wave's LDS traffic overlaps the other's MFMAs.
+//   * CfgMid: block tile 128 x 128, 4 waves of 64 x 64, two workgroups per
+//     CU, for problems with too few 256 x 256 tiles to occupy 256 CUs.
+//   * K tile 32 (two MFMA k-steps of 16).
 //   * Operand tiles move HBM -> LDS with buffer_load_dwordx4 ... lds: each
 //     wave instruction writes 1 KiB of LDS at (base + 16 * lane), no VGPR
 //     staging. The swizzles below are applied by choosing which global
 //     16-byte chunk each lane fetches.
-//   * STAGES LDS stages of 32 KiB; the loads for tile kt+STAGES are issued as
-//     soon as tile kt's stage is released, so each load has STAGES-1 K tiles
-//     of MFMA work to land. One barrier per K tile, placed between the two
-//     16-deep MFMA batches of the tile so the matrix pipe never drains.
+//   * STAGES LDS stages (32 KiB each for 256 x 256); the loads for tile
+//     kt+STAGES are issued as soon as tile kt's stage is released, so each
+//     load has STAGES-1 K tiles of MFMA work to land. One barrier per K tile,
+//     placed between the two MFMA batches of the tile (one per k-step) so
+//     the matrix pipe never drains.
 //   * Out-of-range 16-byte chunks (M/N/K edges, and the tiles the pipeline
 //     requests past the end of K) are loaded with a buffer offset beyond the
 //     descriptor's range; the hardware returns zeros for them without a
 //     memory access.
 //
-// LDS layouts (per stage, per operand, 16 KiB)
+// LDS layouts (per stage, per operand: R rows or columns of the block tile)
 //   K-contiguous operand ([rows][K] in HBM: A when not transposed, B when
-//   transposed): 256 rows x 64 bytes; logical chunk c (8 k-values) of row r
+//   transposed): R rows x 64 bytes; logical chunk c (8 k-values) of row r
 //   sits at physical chunk c ^ ((r >> 2) & 3). Fragment reads are
 //   ds_read_b128 (lane = row, 8 consecutive k); 16 consecutive rows hit 16
 //   distinct 16-byte bank groups.
-//   MN-contiguous operand ([K][cols] in HBM): 32 k-rows x 512 bytes; logical
+//   MN-contiguous operand ([K][cols] in HBM): 32 k-rows x 2R bytes; logical
 //   chunk q of k-row k sits at q ^ ((k & 3) << 2). Fragment reads are
 //   ds_read_b64_tr_b16: within each 16-lane group, output lane i element e is
 //   source lane (4e + i/4)'s element (i % 4). Source lane t of group g points
 //   at k = k0 + 8*(g/2) + t/4, column c0 + 16*(g%2) + 4*(t%4), so lane l
 //   receives column c0 + l%32 at k0 + 8*(l/32) + {0..3}; two reads give the
 //   8 consecutive k an MFMA operand lane needs. 32 lanes touch 4 k-rows x 64
-//   bytes, spread over 16 bank groups by the swizzle.
+//   bytes, spread over 16 bank groups by the swizzle (R >= 128 so that a
+//   k-row holds the 16 chunks the swizzle permutes).
 //
 // MFMA operand roles are swapped (src_a = B fragment, src_b = A fragment):
 // the accumulator then holds C^T, so lane l owns C[m][n .. n+3] for
@@ -57,14 +63,31 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define MLXHIP_LDS __attribute__((address_space(3)))
 
-constexpr int TILE = 256;                 // BM = BN
 constexpr int BK = 32;
-constexpr int THREADS = 256;
-constexpr int OP_BYTES = TILE * BK * 2;   // 16 KiB: one operand, one stage
-constexpr int STAGE_BYTES = 2 * OP_BYTES;
-constexpr int LOADS_PER_OP = OP_BYTES / (THREADS * 16);  // 4 per thread
 constexpr uint32_t OOB = 0xFFFFFF00u;     // beyond every descriptor range
 constexpr int BUF_FLAGS = 0x00020000;     // gfx9 buffer descriptor word 3 (32-bit data format)
+
+// Block configuration: WM x WN waves, each owning TM x TN 32x32 MFMA tiles;
+// STAGES LDS stages; WPE waves per SIMD the kernel is compiled for (bounds
+// the registers per wave: 512 / WPE).
+template <int WM_, int WN_, int TM_, int TN_, int STAGES_, int WPE_>
+struct Cfg {
+    static constexpr int WM = WM_, WN = WN_, TM = TM_, TN = TN_, STAGES = STAGES_, WPE = WPE_;
+    static constexpr int WAVES = WM * WN, THREADS = 64 * WAVES;
+    static constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN;
+    static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;  // one stage
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+    static constexpr int LA = A_BYTES / (THREADS * 16), LB = B_BYTES / (THREADS * 16);  // loads per thread
+    static_assert(BM >= 128 && BN >= 128, "MN-contiguous LDS rows need >= 16 chunks for the swizzle");
+    static_assert(LA * THREADS * 16 == A_BYTES && LB * THREADS * 16 == B_BYTES, "whole 1 KiB blocks per wave");
+    static_assert(STAGES >= 3 && STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
+};
+
+// 256 x 256 block, 8 waves of 128 x 64 (two waves per SIMD): large problems.
+using CfgLarge = Cfg<2, 4, 4, 2, 4, 2>;
+// 128 x 128 block, 4 waves of 64 x 64 (two workgroups per CU): problems
+// with too few 256 x 256 tiles to occupy the chip.
+using CfgMid = Cfg<2, 2, 2, 2, 4, 2>;
 
 struct Args {
     int64_t m, n, k;
@@ -106,21 +129,26 @@ __device__ inline void lds_load16(__amdgpu_buffer_rsrc_t rsrc, MLXHIP_LDS char* 
     asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(m0) : "memory");
 }
 
-// One operand's global->LDS loader. KC: operand is K-contiguous in HBM.
-// Per thread it issues LOADS_PER_OP 16-byte loads per K tile.
-template <bool KC>
+// One operand's global->LDS loader for a block tile of ROWS rows (KC) or
+// columns (!KC). KC: operand is K-contiguous in HBM. Each wave instruction
+// fills one 1 KiB block of the operand's stage; block q = i * WAVES + wave.
+template <bool KC, int ROWS, int WAVES>
 struct Loader {
-    uint32_t off[LOADS_PER_OP];  // byte offset of the chunk for k0 = 0
-    int lim[LOADS_PER_OP];       // the chunk is in range iff k0 < lim (INT_MIN: never)
-    uint32_t k_stride_bytes;     // bytes per unit of k (KC: 2, !KC: 2 * ld)
+    static constexpr int L = ROWS * BK * 2 / (WAVES * 1024);  // loads per thread per K tile
+    static constexpr int ROWB = ROWS * 2;                     // !KC: bytes per k-row
+    static constexpr int CPR = ROWB / 16;                     // !KC: 16-byte chunks per k-row
+    uint32_t off[L];          // byte offset of the chunk for k0 = 0
+    int lim[L];               // the chunk is in range iff k0 < lim (INT_MIN: never)
+    uint32_t k_stride_bytes;  // bytes per unit of k (KC: 2, !KC: 2 * ld)
 
     // rows0: first tile row (KC) / column (!KC); R: valid rows / columns.
     __device__ inline void init(int tid, int64_t rows0, int64_t R, int64_t ld, int64_t K) {
         const int wave = tid >> 6, lane = tid & 63;
 #pragma unroll
-        for (int i = 0; i < LOADS_PER_OP; ++i) {
-            const int q = i * 4 + wave;  // 1 KiB block of the operand's stage
+        for (int i = 0; i < L; ++i) {
+            const int q = i * WAVES + wave;
             if constexpr (KC) {
+                // 16 rows x 64 bytes per block.
                 const int r = 16 * q + (lane >> 2);
                 const int c = (lane & 3) ^ ((r >> 2) & 3);
                 const int64_t row = rows0 + r;
@@ -128,8 +156,9 @@ struct Loader {
                 off[i] = ok ? (uint32_t)((row * ld + 8 * c) * 2) : 0u;
                 lim[i] = ok ? (int)(K - 8 * c) : INT32_MIN;
             } else {
-                const int kr = 2 * q + (lane >> 5);
-                const int cc = (lane & 31) ^ ((kr & 3) << 2);
+                // 64 / CPR k-rows x ROWB bytes per block.
+                const int kr = (64 / CPR) * q + lane / CPR;
+                const int cc = (lane % CPR) ^ ((kr & 3) << 2);
                 const int64_t col = rows0 + 8 * cc;
                 const bool ok = col < R;
                 off[i] = ok ? (uint32_t)((kr * ld + col) * 2) : 0u;
@@ -139,42 +168,44 @@ struct Loader {
         k_stride_bytes = KC ? 2u : (uint32_t)(ld * 2);
     }
 
-    // Load i (0 .. LOADS_PER_OP-1) of the tile starting at k0.
+    // Load i (0 .. L-1) of the tile starting at k0.
     __device__ inline void issue_one(__amdgpu_buffer_rsrc_t rsrc, MLXHIP_LDS char* stage_op, int wave,
                                      int k0, int i) const {
         const uint32_t v = k0 < lim[i] ? off[i] + (uint32_t)k0 * k_stride_bytes : OOB;
-        lds_load16(rsrc, stage_op + (i * 4 + wave) * 1024, v);
+        lds_load16(rsrc, stage_op + (i * WAVES + wave) * 1024, v);
     }
 
     __device__ inline void issue(__amdgpu_buffer_rsrc_t rsrc, MLXHIP_LDS char* stage_op, int wave,
                                  int k0) const {
 #pragma unroll
-        for (int i = 0; i < LOADS_PER_OP; ++i) issue_one(rsrc, stage_op, wave, k0, i);
+        for (int i = 0; i < L; ++i) issue_one(rsrc, stage_op, wave, k0, i);
     }
 };
 
-// Per-lane LDS byte offsets of one operand's fragments inside a stage.
+// Per-lane LDS byte offsets of one wave's T fragments (32 rows / columns
+// each) of one operand inside a stage; ROWB: bytes per k-row (!KC).
 //   KC : off(x, s) = base_s + x * 2048            (x: 32-row block, s: k-step)
-//   !KC: off(x, s, r) = base_x[x] + (16 s + 4 r) * 512
-template <bool KC>
+//   !KC: off(x, s, r) = base_x[x] + (16 s + 4 r) * ROWB
+template <bool KC, int T, int ROWB>
 struct FragAddr {
-    uint32_t base[KC ? 2 : 4];
-    __device__ inline void init(int lane, int quad_off /* 128 * wave quadrant */) {
+    uint32_t base[KC ? 2 : T];
+    __device__ inline void init(int lane, int wave_off /* first row / column of the wave */) {
         if constexpr (KC) {
             const int r = lane & 31;
             const int sw = (r >> 2) & 3;
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const int c = 2 * s + (lane >> 5);
-                base[s] = (uint32_t)((quad_off + r) * 64 + ((c ^ sw) * 16));
+                base[s] = (uint32_t)((wave_off + r) * 64 + ((c ^ sw) * 16));
             }
         } else {
             const int g = lane >> 4, t = lane & 15;
-            const int krow = 8 * (g >> 1) + (t >> 2);
+            const int krow = 8 * (g >> 1) + (t >> 2);  // krow & 3 == (t >> 2) & 3
 #pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                const int chunk = (quad_off >> 3) + 4 * (x ^ (t >> 2)) + 2 * (g & 1) + ((t >> 1) & 1);
-                base[x] = (uint32_t)(krow * 512 + chunk * 16 + (t & 1) * 8);
+            for (int x = 0; x < T; ++x) {
+                const int logical = (wave_off >> 3) + 4 * x + 2 * (g & 1) + ((t >> 1) & 1);
+                const int chunk = logical ^ ((t >> 2) << 2);
+                base[x] = (uint32_t)(krow * ROWB + chunk * 16 + (t & 1) * 8);
             }
         }
     }
@@ -190,20 +221,17 @@ __device__ inline void mfma(const u32x4& a, const u32x4& b, f32x16& acc) {
                                                      __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
 }
 
-// Number of LDS read instructions for one operand's 4 fragments of a k-step.
-template <bool KC>
-constexpr int reads_per_step() { return KC ? 4 : 8; }
-
-// Read `idx` (0 .. reads_per_step-1) of one operand's fragments for k-step s:
-// KC: fragment idx (ds_read_b128); !KC: half idx % 2 of fragment idx / 2
-// (ds_read_b64_tr_b16, k offsets 0-3 or 4-7).
-template <bool KC>
-__device__ inline void read_one(const MLXHIP_LDS char* op, const FragAddr<KC>& fa, int s, int idx, u32x4* f) {
+// Read `idx` of one operand's T fragments for k-step s: KC: fragment idx
+// (ds_read_b128, T reads); !KC: half idx % 2 of fragment idx / 2
+// (ds_read_b64_tr_b16, k offsets 0-3 or 4-7; 2T reads).
+template <bool KC, int T, int ROWB>
+__device__ inline void read_one(const MLXHIP_LDS char* op, const FragAddr<KC, T, ROWB>& fa, int s, int idx,
+                                u32x4* f) {
     if constexpr (KC) {
         f[idx] = *(const MLXHIP_LDS u32x4*)(op + fa.base[s] + idx * 2048);
     } else {
         const int x = idx >> 1, r = idx & 1;
-        const MLXHIP_LDS char* p = op + fa.base[x] + (16 * s + 4 * r) * 512;
+        const MLXHIP_LDS char* p = op + fa.base[x] + (16 * s + 4 * r) * ROWB;
         const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((MLXHIP_LDS i16x4*)p));
         if (r == 0) {
             f[x].x = v.x;
@@ -215,21 +243,11 @@ __device__ inline void read_one(const MLXHIP_LDS char* op, const FragAddr<KC>& f
     }
 }
 
-// Loads the 4 fragments of one operand for k-step s of the stage at `op`.
-template <bool KC>
-__device__ inline void read_frags(const MLXHIP_LDS char* op, const FragAddr<KC>& fa, int s, u32x4* f) {
+// All T fragments of one operand for k-step s of the stage at `op`.
+template <bool KC, int T, int ROWB>
+__device__ inline void read_frags(const MLXHIP_LDS char* op, const FragAddr<KC, T, ROWB>& fa, int s, u32x4* f) {
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-        if constexpr (KC) {
-            f[x] = *(const MLXHIP_LDS u32x4*)(op + fa.base[s] + x * 2048);
-        } else {
-            const MLXHIP_LDS char* p = op + fa.base[x] + 16 * s * 512;
-            i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MLXHIP_LDS i16x4*)p);
-            i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MLXHIP_LDS i16x4*)(p + 4 * 512));
-            const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-            f[x] = u32x4{l2.x, l2.y, h2.x, h2.y};
-        }
-    }
+    for (int idx = 0; idx < (KC ? T : 2 * T); ++idx) read_one<KC, T, ROWB>(op, fa, s, idx, f);
 }
 
 // Two f32 -> two 16-bit outputs packed in one dword (low = first), rounded
@@ -246,157 +264,178 @@ __device__ inline uint32_t pack2(float a, float b) {
     }
 }
 
-template <int DT, int CT, int TA, int TB, int STAGES, bool SPREAD>
-__global__ __attribute__((amdgpu_flat_work_group_size(THREADS, THREADS), amdgpu_waves_per_eu(1, 1)))
+// Epilogue staging: rows of one wave's sub-tile converted per pass, the
+// largest power-of-two multiple of 32 (at most the wave's rows) whose
+// padded rows for all waves fit in `budget` bytes of LDS.
+template <class C, int ES>
+constexpr int pass_rows(int budget) {
+    int r = 32 * C::TM;
+    while (r > 32 && C::WAVES * r * (32 * C::TN * ES + 16) > budget) r /= 2;
+    return r;
+}
+
+template <int DT, int CT, int TA, int TB, class C, bool SPREAD>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
+                          amdgpu_waves_per_eu(C::WPE, C::WPE)))
 void gemm16_kernel(Args g) {
     constexpr bool KCA = (TA == 0);  // A stored [M][K]
     constexpr bool KCB = (TB == 1);  // B stored [N][K]
-    static_assert(STAGES >= 3 && STAGES * STAGE_BYTES <= 160 * 1024, "LDS budget");
-    constexpr int SMEM_BYTES = STAGES * STAGE_BYTES > 4 * 128 * (256 + 16) ? STAGES * STAGE_BYTES : 4 * 128 * (256 + 16);
+    constexpr int STAGES = C::STAGES, TM = C::TM, TN = C::TN, WAVES = C::WAVES;
+    constexpr int ES = CT == MLXHIP_DTYPE_F32 ? 4 : 2;
+    constexpr int PIPE_BYTES = STAGES * C::STAGE_BYTES;
+    constexpr int PASS_ROWS = pass_rows<C, ES>(PIPE_BYTES);
+    constexpr int ROW_BYTES = 32 * TN * ES;  // one wave sub-tile row in the epilogue
+    constexpr int PITCH = ROW_BYTES + 16;
+    constexpr int EPI_BYTES = WAVES * PASS_ROWS * PITCH;
+    constexpr int SMEM_BYTES = PIPE_BYTES > EPI_BYTES ? PIPE_BYTES : EPI_BYTES;
     __shared__ __attribute__((aligned(1024))) char smem_raw[SMEM_BYTES];
     MLXHIP_LDS char* smem = (MLXHIP_LDS char*)smem_raw;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / C::WN, wn = wave % C::WN;
 
-    // XCD-aware tile order: consecutive workgroup ids go to the 8 XCDs
-    // round-robin; give each XCD a contiguous range of tile ids, then order
-    // the range in groups of 4 tile rows so neighbours share A rows / B
-    // columns inside one XCD's L2.
+    // XCD-aware order over the whole grid (every tile of every batch slice):
+    // the hardware hands consecutive workgroup ids (x fastest) to the 8 XCDs
+    // round-robin; give each XCD a contiguous range of (slice, tile) ids so
+    // the tiles of a slice share one L2, then order a slice's tiles in groups
+    // of 4 tile rows so neighbours share A rows / B columns.
     const int nwg = g.tiles_m * g.tiles_n;
-    int id = blockIdx.x;
-    if ((nwg & 7) == 0) id = (id & 7) * (nwg >> 3) + (id >> 3);
+    const int64_t total = (int64_t)nwg * gridDim.y;
+    int64_t lin = (int64_t)blockIdx.y * nwg + blockIdx.x;
+    if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+    const int64_t batch = lin / nwg;
+    const int id = (int)(lin - batch * nwg);
     constexpr int GROUP_M = 4;
     const int in_group = GROUP_M * g.tiles_n;
     const int first_m = (id / in_group) * GROUP_M;
     const int gsz = min(g.tiles_m - first_m, GROUP_M);
     const int tm = first_m + (id % in_group) % gsz;
     const int tn = (id % in_group) / gsz;
-    const int64_t m0 = (int64_t)tm * TILE, n0 = (int64_t)tn * TILE;
+    const int64_t m0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
 
-    const int64_t batch = blockIdx.y;
     const char* A = static_cast<const char*>(g.a) + batch * g.sa * 2;
     const char* B = static_cast<const char*>(g.b) + batch * g.sb * 2;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)g.a_bytes, BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)g.b_bytes, BUF_FLAGS);
 
-    Loader<KCA> la;
-    Loader<KCB> lb;
+    constexpr int ROWB_A = C::BM * 2, ROWB_B = C::BN * 2;
+    Loader<KCA, C::BM, WAVES> la;
+    Loader<KCB, C::BN, WAVES> lb;
     la.init(tid, m0, g.m, g.lda, g.k);
     lb.init(tid, n0, g.n, g.ldb, g.k);
-    FragAddr<KCA> fa;
-    FragAddr<KCB> fb;
-    fa.init(lane, 128 * wm);
-    fb.init(lane, 128 * wn);
+    FragAddr<KCA, TM, ROWB_A> fa;
+    FragAddr<KCB, TN, ROWB_B> fb;
+    fa.init(lane, 32 * TM * wm);
+    fb.init(lane, 32 * TN * wn);
 
-    f32x16 acc[4][4];
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
     const int nk = (int)((g.k + BK - 1) / BK);
-    constexpr int LOADS_PER_TILE = 2 * LOADS_PER_OP;
+    constexpr int LA = C::LA, LB = C::LB, LPT = LA + LB;
+    constexpr int B_OFF = C::A_BYTES;  // stage layout: A block, then B block
 
     // Prologue: tiles 0 .. STAGES-1 into stages 0 .. STAGES-1.
     // With SPREAD, B's loads of tile t+STAGES are issued in the first half of
-    // iteration t+1 instead (one per four MFMAs) and the prologue leaves out
-    // B of tile STAGES-1; the count of loads younger than any tile is unchanged.
+    // iteration t+1 instead (spread over its MFMAs) and the prologue leaves
+    // out B of tile STAGES-1; the count of loads younger than any tile is
+    // unchanged.
 #pragma unroll
     for (int t = 0; t < STAGES; ++t) {
-        MLXHIP_LDS char* st = smem + t * STAGE_BYTES;
+        MLXHIP_LDS char* st = smem + t * C::STAGE_BYTES;
         la.issue(ra, st, wave, t * BK);
-        if (!SPREAD || t < STAGES - 1) lb.issue(rb, st + OP_BYTES, wave, t * BK);
+        if (!SPREAD || t < STAGES - 1) lb.issue(rb, st + B_OFF, wave, t * BK);
     }
-    if constexpr (SPREAD) wait_vmcnt<(STAGES - 2) * LOADS_PER_TILE + LOADS_PER_OP>();
-    else wait_vmcnt<(STAGES - 1) * LOADS_PER_TILE>();
+    if constexpr (SPREAD) wait_vmcnt<(STAGES - 2) * LPT + LA>();
+    else wait_vmcnt<(STAGES - 1) * LPT>();
     lds_barrier();
 
-    u32x4 af[2][4], bf[2][4];
-    read_frags<KCA>(smem, fa, 0, af[0]);
-    read_frags<KCB>(smem + OP_BYTES, fb, 0, bf[0]);
+    u32x4 af[2][TM], bf[2][TN];
+    read_frags<KCA, TM, ROWB_A>(smem, fa, 0, af[0]);
+    read_frags<KCB, TN, ROWB_B>(smem + B_OFF, fb, 0, bf[0]);
 
-    // Each half-tile issues 16 MFMAs, one per 32-cycle MFMA slot, with the
-    // LDS reads / LDS-bound loads of the next half placed between them; the
-    // scheduling barriers keep that order (the compiler would otherwise sink
-    // each read next to its first use and expose the LDS latency).
-    constexpr int NA = reads_per_step<KCA>(), NB = reads_per_step<KCB>(), NR = NA + NB;
-    constexpr int OPS2 = (SPREAD ? 1 : 2) * LOADS_PER_OP + NR;
-    static_assert(NR <= 16, "one read per MFMA slot in the first half");
+    // Each half-tile issues NM MFMAs with the LDS reads / LDS-bound loads of
+    // the next half placed between them; the scheduling barriers keep that
+    // order (the compiler would otherwise sink each read next to its first
+    // use and expose the LDS latency).
+    constexpr int NM = TM * TN;
+    constexpr int NA = KCA ? TM : 2 * TM, NB = KCB ? TN : 2 * TN, NR = NA + NB;
+    constexpr int OPS2 = NR + LA + (SPREAD ? 0 : LB);
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt % STAGES;
-        const MLXHIP_LDS char* st = smem + cur * STAGE_BYTES;
+        const MLXHIP_LDS char* st = smem + cur * C::STAGE_BYTES;
+        MLXHIP_LDS char* spread_dst = smem + ((kt + STAGES - 1) % STAGES) * C::STAGE_BYTES + B_OFF;
         // First half: MFMAs of k-step 0, reads of k-step 1 of this tile.
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            mfma<DT>(bf[0][q & 3], af[0][q >> 2], acc[q >> 2][q & 3]);
-            if (q < NA) read_one<KCA>(st, fa, 1, q, af[1]);
-            else if (q < NR) read_one<KCB>(st + OP_BYTES, fb, 1, q - NA, bf[1]);
+        for (int q = 0; q < NM; ++q) {
+            mfma<DT>(bf[0][q % TN], af[0][q / TN], acc[q / TN][q % TN]);
+#pragma unroll
+            for (int o = NR <= NM ? q : (q * NR) / NM; o < (NR <= NM ? q + 1 : ((q + 1) * NR) / NM); ++o) {
+                if (o < NA) read_one<KCA, TM, ROWB_A>(st, fa, 1, o, af[1]);
+                else if (o < NR) read_one<KCB, TN, ROWB_B>(st + B_OFF, fb, 1, o - NA, bf[1]);
+            }
             if constexpr (SPREAD) {
                 // B of tile kt-1+STAGES into the stage released in iteration kt-1.
-                if ((q & 3) == 3)
-                    lb.issue_one(rb, smem + ((kt + STAGES - 1) % STAGES) * STAGE_BYTES + OP_BYTES, wave,
-                                 (kt - 1 + STAGES) * BK, q >> 2);
+                if (((q + 1) * LB) / NM > (q * LB) / NM)
+                    lb.issue_one(rb, spread_dst, wave, (kt - 1 + STAGES) * BK, (q * LB) / NM);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
         // Tile kt+1 has landed for every wave; every wave is done reading
         // this tile's stage, which then receives tile kt+STAGES.
-        wait_vmcnt<(STAGES - 2) * LOADS_PER_TILE>();
+        wait_vmcnt<(STAGES - 2) * LPT>();
         lds_barrier();
-        MLXHIP_LDS char* dst = smem + cur * STAGE_BYTES;
+        MLXHIP_LDS char* dst = smem + cur * C::STAGE_BYTES;
         const int k0 = (kt + STAGES) * BK;
-        const MLXHIP_LDS char* nx = smem + ((kt + 1) % STAGES) * STAGE_BYTES;
+        const MLXHIP_LDS char* nx = smem + ((kt + 1) % STAGES) * C::STAGE_BYTES;
         // Second half: MFMAs of k-step 1; the k-step 0 reads of tile kt+1
         // and the loads of tile kt+STAGES.
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            mfma<DT>(bf[1][q & 3], af[1][q >> 2], acc[q >> 2][q & 3]);
+        for (int q = 0; q < NM; ++q) {
+            mfma<DT>(bf[1][q % TN], af[1][q / TN], acc[q / TN][q % TN]);
 #pragma unroll
-            for (int o = (q * OPS2) / 16; o < ((q + 1) * OPS2) / 16; ++o) {
+            for (int o = (q * OPS2) / NM; o < ((q + 1) * OPS2) / NM; ++o) {
                 // Reads first: the next tile's first MFMAs consume them.
-                if (o < NA) read_one<KCA>(nx, fa, 0, o, af[0]);
-                else if (o < NR) read_one<KCB>(nx + OP_BYTES, fb, 0, o - NA, bf[0]);
-                else if (o < NR + LOADS_PER_OP) la.issue_one(ra, dst, wave, k0, o - NR);
-                else if (!SPREAD) lb.issue_one(rb, dst + OP_BYTES, wave, k0, o - NR - LOADS_PER_OP);
+                if (o < NA) read_one<KCA, TM, ROWB_A>(nx, fa, 0, o, af[0]);
+                else if (o < NR) read_one<KCB, TN, ROWB_B>(nx + B_OFF, fb, 0, o - NA, bf[0]);
+                else if (o < NR + LA) la.issue_one(ra, dst, wave, k0, o - NR);
+                else if (!SPREAD) lb.issue_one(rb, dst + B_OFF, wave, k0, o - NR - LA);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    wait_vmcnt<0>();
 
-    // Epilogue through LDS. acc[i][j][v] = C[m][n] with m = 128 wm + 32 i +
-    // lane % 32 and n = 128 wn + 32 j + 8 (v / 4) + 4 (lane / 32) + v % 4
-    // inside the tile. Each wave converts its 128 x 128 quadrant into padded
-    // LDS rows (PITCH = row bytes + 16: 16 consecutive rows fall in distinct
-    // bank groups for the 8/16-byte writes) and reads it back row by row, so
-    // every global store instruction writes whole 256- or 512-byte row
+    // Epilogue through LDS. acc[i][j][v] = C[m][n] with m = WR wm + 32 i +
+    // lane % 32 and n = WC wn + 32 j + 8 (v / 4) + 4 (lane / 32) + v % 4
+    // inside the tile (WR x WC: the wave's sub-tile). Each wave converts its
+    // sub-tile into padded LDS rows (PITCH = row bytes + 16: consecutive rows
+    // fall in distinct bank groups for the 8/16-byte writes) and reads it
+    // back row by row, so every global store instruction writes whole row
     // segments instead of 16-byte pieces of 32 rows.
     wait_vmcnt<0>();
     lds_barrier();  // every wave is done with the operand stages
-    constexpr int ES = CT == MLXHIP_DTYPE_F32 ? 4 : 2;
-    constexpr int ROW_BYTES = 128 * ES;
-    constexpr int PITCH = ROW_BYTES + 16;
-    constexpr int PASS_ROWS = ES == 2 ? 128 : 64;  // quadrant rows staged per pass
     constexpr int LANES_PER_ROW = ROW_BYTES / 16;
     constexpr int ROWS_PER_READ = 64 / LANES_PER_ROW;
-    static_assert(4 * PASS_ROWS * PITCH <= SMEM_BYTES, "epilogue staging fits in LDS");
+    static_assert(LANES_PER_ROW <= 64 && 64 % LANES_PER_ROW == 0, "epilogue read shape");
     MLXHIP_LDS char* region = smem + wave * PASS_ROWS * PITCH;
-    char* C = static_cast<char*>(g.c) + batch * g.sc * ES;
-    const int64_t row0 = m0 + 128 * wm, col0 = n0 + 128 * wn;
-    const bool vec_ok = (g.ldc * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(C) % 16) == 0;
+    char* Cp = static_cast<char*>(g.c) + batch * g.sc * ES;
+    const int64_t row0 = m0 + 32 * TM * wm, col0 = n0 + 32 * TN * wn;
+    const bool vec_ok = (g.ldc * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(Cp) % 16) == 0;
 #pragma unroll
-    for (int pass = 0; pass < 128 / PASS_ROWS; ++pass) {
+    for (int pass = 0; pass < 32 * TM / PASS_ROWS; ++pass) {
 #pragma unroll
         for (int i = 0; i < PASS_ROWS / 32; ++i) {
             const int ii = pass * (PASS_ROWS / 32) + i;
             const int r = 32 * i + (lane & 31);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int c = 32 * j + 8 * q + 4 * (lane >> 5);
@@ -420,7 +459,7 @@ void gemm16_kernel(Args g) {
             const int64_t m = row0 + pass * PASS_ROWS + r;
             const int64_t n = col0 + cb / ES;
             if (m >= g.m || n >= g.n) continue;
-            char* dst = C + (m * g.ldc + n) * ES;
+            char* dst = Cp + (m * g.ldc + n) * ES;
             if (vec_ok && n + 16 / ES <= g.n) {
                 *reinterpret_cast<u32x4*>(dst) = v;
             } else {
@@ -459,28 +498,35 @@ inline bool supported(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t b
     return true;
 }
 
-template <int DT, int CT, int TA, int TB>
+template <int DT, int CT, int TA, int TB, class C>
 int launch(const Args& a0, int64_t batch, hipStream_t s) {
     Args a = a0;
-    a.tiles_m = (int)ceil_div(a.m, TILE);
-    a.tiles_n = (int)ceil_div(a.n, TILE);
+    a.tiles_m = (int)ceil_div(a.m, C::BM);
+    a.tiles_n = (int)ceil_div(a.n, C::BN);
     dim3 grid((unsigned)(a.tiles_m * a.tiles_n), (unsigned)batch);
-    hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, 4, true>), grid, dim3(THREADS), 0, s, a);
+    hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, C, true>), grid, dim3(C::THREADS), 0, s, a);
     return launch_check("gemm16_kernel");
 }
 
+template <int DT, int CT, class C>
+int dispatch_layout(const Args& a, int64_t batch, int ta, int tb, hipStream_t s) {
+    if (!ta && !tb) return launch<DT, CT, 0, 0, C>(a, batch, s);
+    if (!ta && tb) return launch<DT, CT, 0, 1, C>(a, batch, s);
+    if (ta && !tb) return launch<DT, CT, 1, 0, C>(a, batch, s);
+    return launch<DT, CT, 1, 1, C>(a, batch, s);
+}
+
+// cfg: 0 = CfgLarge, 1 = CfgMid.
 template <int DT, int CT>
-int dispatch(const Args& a, int64_t batch, int ta, int tb, hipStream_t s) {
-    if (!ta && !tb) return launch<DT, CT, 0, 0>(a, batch, s);
-    if (!ta && tb) return launch<DT, CT, 0, 1>(a, batch, s);
-    if (ta && !tb) return launch<DT, CT, 1, 0>(a, batch, s);
-    return launch<DT, CT, 1, 1>(a, batch, s);
+int dispatch(const Args& a, int64_t batch, int ta, int tb, int cfg, hipStream_t s) {
+    if (cfg == 0) return dispatch_layout<DT, CT, CfgLarge>(a, batch, ta, tb, s);
+    return dispatch_layout<DT, CT, CfgMid>(a, batch, ta, tb, s);
 }
 
 }  // namespace gemm16
 
 // Per-dtype entry points (gemm16_bf16.hip, gemm16_f16.hip).
-int gemm16_bf16(int c_dtype, int ta, int tb, const gemm16::Args& a, int64_t batch, hipStream_t s);
-int gemm16_f16(int c_dtype, int ta, int tb, const gemm16::Args& a, int64_t batch, hipStream_t s);
+int gemm16_bf16(int c_dtype, int ta, int tb, const gemm16::Args& a, int64_t batch, int cfg, hipStream_t s);
+int gemm16_f16(int c_dtype, int ta, int tb, const gemm16::Args& a, int64_t batch, int cfg, hipStream_t s);
 
 }  // namespace mlxhip

@@ -6,9 +6,11 @@ RNE-rounded inputs.
 Tolerance as in test_gpu_gemm.py: |gpu - cpu| <= atol + rtol*|cpu| with
 atol = 1e-6 * sqrt(K) * max|A| * max|B| and rtol 1e-5 (f32 C) or 1e-2
 (bf16/f16 C). The shapes exercise what the direct-to-LDS kernel handles
-with its out-of-range buffer loads: M and N edges inside a 256 x 256 tile,
+with its out-of-range buffer loads: M and N edges inside a block tile,
 K not a multiple of the 32-wide K tile, tiles with no valid rows at all,
-and batch strides.
+and batch strides. Both block configurations of that kernel (256 x 256 with
+8 waves, 128 x 128 with 4 waves) are forced in turn ("lds16_256",
+"lds16_128").
 """
 import os
 
@@ -36,7 +38,7 @@ def gemm_path(request):
         os.environ["MLXHIP_GEMM_PATH"] = old
 
 
-@pytest.mark.parametrize("gemm_path", ["lds16"], indirect=True)
+@pytest.mark.parametrize("gemm_path", ["lds16_256", "lds16_128"], indirect=True)
 @pytest.mark.parametrize("ab,cd", [(BF16, F32), (BF16, BF16), (F16, F32), (F16, F16)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("m,n,k", [(256, 256, 32), (300, 264, 520), (64, 40, 8), (520, 776, 1528)])
@@ -45,14 +47,14 @@ def test_lds16_layouts(gemm_path, ab, cd, ta, tb, m, n, k):
                rows=sample_rows(m, 40))
 
 
-@pytest.mark.parametrize("gemm_path", ["lds16"], indirect=True)
+@pytest.mark.parametrize("gemm_path", ["lds16_256", "lds16_128"], indirect=True)
 @pytest.mark.parametrize("tb", [False, True])
 def test_lds16_batched_strided(gemm_path, tb):
     check_gemm(264, 136, 200, BF16, F32, tb=tb, batch=5, seed=77, rows=sample_rows(264, 16))
     check_gemm(128, 128, 96, F16, F16, tb=tb, batch=3, seed=78, rows=np.arange(128), ld_pad=8)
 
 
-@pytest.mark.parametrize("gemm_path", ["lds16"], indirect=True)
+@pytest.mark.parametrize("gemm_path", ["lds16_256", "lds16_128"], indirect=True)
 def test_lds16_headline_shape(gemm_path):
     check_gemm(4096, 4096, 4096, BF16, BF16, seed=12, rows=sample_rows(4096, 10))
 
@@ -71,7 +73,7 @@ def test_lds16_falls_back_when_unsupported(gemm_path):
     check_gemm(70, 64, 48, F16, F32, ld_pad=3, seed=32, rows=np.arange(70))
 
 
-@pytest.mark.parametrize("gemm_path", ["lds16", "general"], indirect=True)
+@pytest.mark.parametrize("gemm_path", ["lds16_256", "lds16_128", "general"], indirect=True)
 @pytest.mark.parametrize("ab", [BF16, F16])
 def test_output_rounding_bit_exact(gemm_path, ab):
     # K = 8 with only k = 0 non-zero: C[m, n] = a[m] * b[n], a product of two
@@ -96,6 +98,29 @@ def test_output_rounding_bit_exact(gemm_path, ab):
     want = synth.bf16_bits(exact) if ab == BF16 else exact.astype(np.float16).view(np.uint16)
     bad = np.argwhere(got != want)
     assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[0]}: got {got[tuple(bad[0])]:#06x} want {want[tuple(bad[0])]:#06x}"
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("cd", [F32, BF16])
+def test_block_configs_agree_bit_for_bit(ta, tb, cd):
+    # Both block configurations accumulate every output element over the same
+    # sequence of MFMAs (K tiles in order, two k-steps each), so their results
+    # must be identical, edges included.
+    m, n, k = 392, 520, 1000
+    A = synth.normal(101, (k, m) if ta else (m, k))
+    B = synth.normal(102, (n, k) if tb else (k, n))
+    da, db = to_dev(A, BF16), to_dev(B, BF16)
+    es = 4 if cd == F32 else 2
+    outs = []
+    for path in ("lds16_256", "lds16_128"):
+        os.environ["MLXHIP_GEMM_PATH"] = path
+        try:
+            dc = hb.DeviceBuffer(m * n * es)
+            hb.gemm(BF16, cd, bool(ta), bool(tb), m, n, k, da, A.shape[1], db, B.shape[1], dc, n)
+            outs.append(dc.download(np.uint32 if es == 4 else np.uint16, m * n))
+        finally:
+            del os.environ["MLXHIP_GEMM_PATH"]
+    assert np.array_equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("ab,cd", [(F32, F32), (BF16, F32), (BF16, BF16), (F16, F16)])
