@@ -231,6 +231,30 @@ uint64_t mlxhip_stream_launch_count(const mlxhip_stream_t* s);
 /* Enables (1, default) or disables (0) look-ahead fusion of single-consumer
  * elementwise chains and of Transpose into MatMul operand layouts. */
 int mlxhip_stream_set_fusion(mlxhip_stream_t* s, int enabled);
+/* Stream::eval over several outputs at once (Graph::topo_sort takes a slice
+ * of outputs, crates/mlx-core/src/graph.rs:268-294): one topological order
+ * and one fusion plan for all of them, one synchronisation at the end. Every
+ * requested node is materialised. */
+int mlxhip_stream_eval_many(mlxhip_stream_t* s, const uint64_t* nodes, size_t n);
+/* As mlxhip_stream_add_constant with `data` a device address: the values are
+ * copied device-to-device on the stream's queue, so `data` must stay
+ * unchanged until the next mlxhip_stream_eval* call on `s` returns. No
+ * reference counterpart (the reference's constants always come from host
+ * vectors, backend.rs:59-71); for callers whose inputs already live in HBM. */
+uint64_t mlxhip_stream_add_constant_dev(mlxhip_stream_t* s, const float* data, size_t len,
+                                        const mlxhip_meta_t* meta);
+/* value_and_grad / backward (crates/mlx-autograd/src/lib.rs:30-107) with the
+ * VJP table of crates/mlx-autograd/src/vjp.rs:8-178: `loss` must have one
+ * element (else MLXHIP_ERR_INVALID_ARGUMENT "grad requires scalar loss"); it
+ * is evaluated, seeded with ones, and VJP nodes are added to the graph in
+ * reverse topological order. grads[i] receives the node id of
+ * d(loss)/d(wrt[i]), unevaluated (evaluate with mlxhip_stream_eval_many).
+ * Several wrt nodes per call (the reference takes one, lib.rs:104-106);
+ * "gradient not found" (MLXHIP_ERR_INVALID_ARGUMENT) when a wrt node does
+ * not affect the loss; "VJP not implemented" for ops without a VJP on the
+ * path. Rank-3 MatMul differentiates with Transpose [0,2,1]. */
+int mlxhip_stream_grad(mlxhip_stream_t* s, uint64_t loss, const uint64_t* wrt, size_t n_wrt,
+                       uint64_t* grads);
 
 /* ── Direct kernel entry points (device pointers, asynchronous on `stream`) ─ */
 

@@ -279,14 +279,22 @@ static int op_matmul(ctx_t* c) {
     REQUIRE(1);
     const mlxhip_input_t* a = &c->in[0];
     const mlxhip_input_t* b = &c->in[1];
-    if (a->ndim != 2 || b->ndim != 2) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul requires 2D tensors");
-    size_t m = (size_t)a->shape[0], k = (size_t)a->shape[1];
-    size_t k2 = (size_t)b->shape[0], n = (size_t)b->shape[1];
+    /* Rank 3 ([B,M,K] @ [B,K,N]): the batched form the reference specifies in
+     * evals/tasks/003_matmul_batch_3d.json, computed as B independent rank-2
+     * products with the loop of cpu_kernels.rs:216-228. */
+    if (!((a->ndim == 2 && b->ndim == 2) || (a->ndim == 3 && b->ndim == 3)))
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul requires 2D tensors (or two 3D batched tensors)");
+    size_t r = a->ndim - 2, batch = a->ndim == 3 ? (size_t)a->shape[0] : 1;
+    if (a->ndim == 3 && (size_t)b->shape[0] != batch)
+        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "matmul: batch %zu vs %zu", batch, (size_t)b->shape[0]);
+    size_t m = (size_t)a->shape[r], k = (size_t)a->shape[r + 1];
+    size_t k2 = (size_t)b->shape[r], n = (size_t)b->shape[r + 1];
     if (k != k2) return fail(MLXHIP_ERR_SHAPE_MISMATCH, "matmul: expected [%zu, %zu], got [%zu, %zu]", m, k, k2, n);
-    float* r = alloc_out(m * n);
-    oracle_matmul(a->data, b->data, r, m, k, n);
-    *c->out = r;
-    *c->out_len = m * n;
+    float* out = alloc_out(batch * m * n);
+    for (size_t i = 0; i < batch; ++i)
+        oracle_matmul(a->data + i * m * k, b->data + i * k * n, out + i * m * n, m, k, n);
+    *c->out = out;
+    *c->out_len = batch * m * n;
     return MLXHIP_OK;
 }
 

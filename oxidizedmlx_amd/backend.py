@@ -103,6 +103,31 @@ class HipStream:
     def eval(self, nid: int) -> None:
         abi.check(self._L.mlxhip_stream_eval(self._s, nid), self._L)
 
+    def eval_many(self, nids: Sequence[int]) -> None:
+        ids = (C.c_uint64 * max(1, len(nids)))(*nids)
+        abi.check(self._L.mlxhip_stream_eval_many(self._s, ids, len(nids)), self._L)
+
+    def add_constant_dev(self, ptr: int, m: TensorMeta) -> int:
+        """Constant copied from device memory at ``ptr`` (numel(m) floats),
+        which must stay unchanged until the next eval on this stream returns."""
+        cm, keep = m.to_c()
+        nid = self._L.mlxhip_stream_add_constant_dev(self._s, ptr, m.numel(), C.byref(cm))
+        if nid == 0:
+            abi.check(self._L.mlxhip_last_status() or abi.ERR_FFI_FAILED, self._L)
+        self.metas[nid] = m
+        return nid
+
+    def grad(self, loss: int, wrt: Sequence[int]) -> list[int]:
+        """value_and_grad's backward pass (mlx-autograd lib.rs:30-107) for
+        several wrt nodes: returns the (unevaluated) gradient node ids."""
+        ids = (C.c_uint64 * max(1, len(wrt)))(*wrt)
+        out = (C.c_uint64 * max(1, len(wrt)))()
+        abi.check(self._L.mlxhip_stream_grad(self._s, loss, ids, len(wrt), out), self._L)
+        res = [int(out[i]) for i in range(len(wrt))]
+        for g, w in zip(res, wrt):
+            self.metas.setdefault(g, self.metas[w])
+        return res
+
     def get_buffer(self, nid: int) -> np.ndarray:
         n = self.metas[nid].numel()
         out = np.empty(max(n, 1), dtype=np.float32)

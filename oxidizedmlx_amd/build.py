@@ -28,6 +28,7 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
 SOURCES = [
     "backend.cpp",
     "stream.cpp",
+    "autograd.cpp",
     "kernels/rows.hip",
     "kernels/elementwise.hip",
     "kernels/gemm.hip",

@@ -219,33 +219,44 @@ int ew2(int ew_op, const float* acc, const float* other, float* out, int64_t n, 
 
 int eval_matmul(const mlxhip_input_t* in, size_t n_inputs, const mlxhip_meta_t& meta, float* out,
                 hipStream_t s, Scratch& scratch, const int* trans_hint) {
+    // Rank 2: matmul (cpu_kernels.rs:197-230). Rank 3: [B,M,K] @ [B,K,N] ->
+    // [B,M,N], one product per batch slice, the batched form the reference
+    // specifies for matmul (evals/tasks/003_matmul_batch_3d.json); ranks must
+    // agree and so must the batch sizes.
     REQUIRE(0);
     REQUIRE(1);
     const mlxhip_input_t &a = in[0], &b = in[1];
-    if (a.ndim != 2 || b.ndim != 2) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul requires 2D tensors");
+    if (!((a.ndim == 2 && b.ndim == 2) || (a.ndim == 3 && b.ndim == 3)))
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul requires 2D tensors (or two 3D batched tensors)");
+    const size_t r = a.ndim - 2;  // index of the first matrix dimension
+    const int64_t batch = a.ndim == 3 ? a.shape[0] : 1;
+    if (a.ndim == 3 && b.shape[0] != batch)
+        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: batch %lld vs %lld", (long long)batch,
+                    (long long)b.shape[0]);
     const bool ta = trans_hint && trans_hint[0], tb = trans_hint && trans_hint[1];
     // With a folded Transpose the input holds the source [K, M] / [N, K].
-    const int64_t m = ta ? a.shape[1] : a.shape[0], k = ta ? a.shape[0] : a.shape[1];
-    const int64_t k2 = tb ? b.shape[1] : b.shape[0], n = tb ? b.shape[0] : b.shape[1];
+    const int64_t m = ta ? a.shape[r + 1] : a.shape[r], k = ta ? a.shape[r] : a.shape[r + 1];
+    const int64_t k2 = tb ? b.shape[r + 1] : b.shape[r], n = tb ? b.shape[r] : b.shape[r + 1];
     if (k != k2)
         return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: expected [%lld, %lld], got [%lld, %lld]",
                     (long long)m, (long long)k, (long long)k2, (long long)n);
-    MLXHIP_TRY(expect_len(m * n, numel_of(meta.shape, meta.ndim), "matmul"));
+    MLXHIP_TRY(expect_len(batch * m * n, numel_of(meta.shape, meta.ndim), "matmul"));
     const int64_t lda = ta ? m : k, ldb = tb ? k : n;
     // The reference stores every logical dtype as f32 (crates/mlx-core/src/tensor.rs:105-125);
     // a bf16/f16 MatMul rounds both operands to that type (RNE) and runs the
     // 16-bit MFMA with f32 accumulation and f32 output.
     const int dt = meta.dtype;
-    if ((dt == MLXHIP_DTYPE_BF16 || dt == MLXHIP_DTYPE_F16) && m * n * k > 0) {
-        void* a16 = scratch.get_bytes((size_t)m * k * 2);
-        void* b16 = scratch.get_bytes((size_t)k * n * 2);
+    if ((dt == MLXHIP_DTYPE_BF16 || dt == MLXHIP_DTYPE_F16) && batch * m * n * k > 0) {
+        void* a16 = scratch.get_bytes((size_t)(batch * m * k) * 2);
+        void* b16 = scratch.get_bytes((size_t)(batch * k * n) * 2);
         if (!a16 || !b16) return fail(MLXHIP_ERR_FFI_FAILED, "matmul: scratch allocation failed");
-        MLXHIP_TRY(cast(a.data, MLXHIP_DTYPE_F32, a16, dt, m * k, s));
-        MLXHIP_TRY(cast(b.data, MLXHIP_DTYPE_F32, b16, dt, k * n, s));
-        return gemm(dt, MLXHIP_DTYPE_F32, ta, tb, m, n, k, 1, a16, lda, 0, b16, ldb, 0, out, n, 0, s);
+        MLXHIP_TRY(cast(a.data, MLXHIP_DTYPE_F32, a16, dt, batch * m * k, s));
+        MLXHIP_TRY(cast(b.data, MLXHIP_DTYPE_F32, b16, dt, batch * k * n, s));
+        return gemm(dt, MLXHIP_DTYPE_F32, ta, tb, m, n, k, batch, a16, lda, m * k, b16, ldb, k * n, out, n,
+                    m * n, s);
     }
-    return gemm(MLXHIP_DTYPE_F32, MLXHIP_DTYPE_F32, ta, tb, m, n, k, 1, a.data, lda, 0, b.data, ldb, 0,
-                out, n, 0, s);
+    return gemm(MLXHIP_DTYPE_F32, MLXHIP_DTYPE_F32, ta, tb, m, n, k, batch, a.data, lda, m * k, b.data, ldb,
+                k * n, out, n, m * n, s);
 }
 
 int eval_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,

@@ -30,56 +30,10 @@
 #include "backend.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "stream.hpp"
 
 namespace mlxhip {
 namespace {
-
-struct OpVal {
-    mlxhip_op_t op{};
-    std::vector<int64_t> shape, axes;
-    bool has_shape = false, has_axes = false;
-
-    static OpVal from(const mlxhip_op_t& o) {
-        OpVal v;
-        v.op = o;
-        if (o.shape) {
-            v.shape.assign(o.shape, o.shape + o.shape_len);
-            v.has_shape = true;
-        }
-        if (o.axes) {
-            v.axes.assign(o.axes, o.axes + o.axes_len);
-            v.has_axes = true;
-        }
-        return v;
-    }
-    mlxhip_op_t c() const {
-        mlxhip_op_t o = op;
-        o.shape = has_shape ? shape.data() : nullptr;
-        o.shape_len = shape.size();
-        o.axes = has_axes ? axes.data() : nullptr;
-        o.axes_len = axes.size();
-        return o;
-    }
-};
-
-struct MetaVal {
-    std::vector<int64_t> shape;
-    int dtype = MLXHIP_DTYPE_F32;
-    int64_t numel() const { return numel_of(shape.data(), shape.size()); }
-    mlxhip_meta_t c() const { return mlxhip_meta_t{shape.data(), shape.size(), dtype}; }
-};
-
-struct Node {
-    uint64_t id;
-    OpVal op;
-    std::vector<uint64_t> inputs;
-    MetaVal meta;
-};
-
-struct DevBuf {
-    float* ptr = nullptr;
-    size_t len = 0;
-};
 
 bool is_elementwise(int k) {
     switch (k) {
@@ -120,106 +74,23 @@ int binary_ew(int k, int acc_idx) {
     }
 }
 
-void append_bits(std::string& k, const void* p, size_t n) { k.append(static_cast<const char*>(p), n); }
-
 }  // namespace
 }  // namespace mlxhip
 
 using namespace mlxhip;
 
-struct mlxhip_stream_t {
-    std::mutex mu;  // guards everything below; eval runs under it
-    std::unordered_map<uint64_t, Node> nodes;
-    std::unordered_map<std::string, uint64_t> cse;
-    std::unordered_map<uint64_t, uint32_t> consumers;
-    std::unordered_map<uint64_t, DevBuf> buffers;
-    uint64_t next_id = 1;
-    std::atomic<uint64_t> eval_calls{0};
-    std::atomic<uint64_t> launches{0};
-    bool fusion = true;
-    hipStream_t hs = nullptr;
-    int device = 0;
-
-    ~mlxhip_stream_t() {
-        if (hs) (void)hipStreamSynchronize(hs);
-        for (auto& kv : buffers) pool_release(kv.second.ptr);
-        if (hs) (void)hipStreamDestroy(hs);
+int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
+    std::vector<uint64_t> todo;
+    for (uint64_t o : outputs) {
+        if (!nodes.count(o)) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "missing graph node");
+        if (!buffers.count(o)) todo.push_back(o);
     }
-
-    uint64_t add_node(const OpVal& op, std::vector<uint64_t> inputs, const MetaVal& meta, bool cse_ok) {
-        std::string key;
-        if (cse_ok) {
-            if ((op.op.kind == MLXHIP_OP_ADD || op.op.kind == MLXHIP_OP_MUL) && inputs.size() == 2 &&
-                inputs[0] > inputs[1])
-                std::swap(inputs[0], inputs[1]);
-            mlxhip_op_t o = op.op;
-            o.shape = nullptr;
-            o.axes = nullptr;
-            append_bits(key, &o, sizeof o);
-            key.push_back(op.has_shape ? 'S' : 's');
-            append_bits(key, op.shape.data(), op.shape.size() * sizeof(int64_t));
-            key.push_back(op.has_axes ? 'A' : 'a');
-            append_bits(key, op.axes.data(), op.axes.size() * sizeof(int64_t));
-            key.push_back('I');
-            append_bits(key, inputs.data(), inputs.size() * sizeof(uint64_t));
-            key.push_back('M');
-            append_bits(key, &meta.dtype, sizeof meta.dtype);
-            append_bits(key, meta.shape.data(), meta.shape.size() * sizeof(int64_t));
-            auto it = cse.find(key);
-            if (it != cse.end()) return it->second;
-        }
-        const uint64_t id = next_id++;
-        for (uint64_t in : inputs) consumers[in]++;
-        nodes.emplace(id, Node{id, op, std::move(inputs), meta});
-        if (cse_ok) cse.emplace(std::move(key), id);
-        return id;
-    }
-
-    // Depth-first post-order of the subgraph rooted at `out` (graph.rs:268-294),
-    // iterative so deep graphs cannot overflow the native stack.
-    std::vector<uint64_t> topo_sort(uint64_t out) {
-        std::vector<uint64_t> order;
-        std::unordered_set<uint64_t> visited;
-        std::vector<std::pair<uint64_t, size_t>> st;
-        visited.insert(out);
-        st.emplace_back(out, 0);
-        while (!st.empty()) {
-            auto& top = st.back();
-            auto it = nodes.find(top.first);
-            if (it != nodes.end() && top.second < it->second.inputs.size()) {
-                const uint64_t nxt = it->second.inputs[top.second++];
-                if (visited.insert(nxt).second) st.emplace_back(nxt, 0);
-            } else {
-                order.push_back(top.first);
-                st.pop_back();
-            }
-        }
-        return order;
-    }
-
-    mlxhip_input_t input_of(uint64_t id, const float* data) {
-        const Node& n = nodes.at(id);
-        return mlxhip_input_t{data, (size_t)n.meta.numel(), n.meta.shape.data(), n.meta.shape.size(), n.meta.dtype};
-    }
-
-    int alloc_out(uint64_t id, float** out) {
-        const Node& n = nodes.at(id);
-        const size_t len = (size_t)n.meta.numel();
-        float* p = static_cast<float*>(pool_alloc((len ? len : 1) * sizeof(float)));
-        if (!p) return fail(MLXHIP_ERR_FFI_FAILED, "stream: device allocation of %zu floats failed", len);
-        buffers[id] = DevBuf{p, len};
-        *out = p;
-        return MLXHIP_OK;
-    }
-
-    int eval(uint64_t output);
-};
-
-int mlxhip_stream_t::eval(uint64_t output) {
-    if (buffers.count(output)) return MLXHIP_OK;
-    if (!nodes.count(output)) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "missing graph node");
-    const std::vector<uint64_t> order = topo_sort(output);
+    if (todo.empty()) return MLXHIP_OK;
+    const std::vector<uint64_t> order = topo_sort(todo);
     std::unordered_set<uint64_t> in_order(order.begin(), order.end());
+    // Requested outputs are always materialised: never a chain interior or a
+    // folded Transpose.
+    const std::unordered_set<uint64_t> requested(todo.begin(), todo.end());
 
     // ── look-ahead planning ──────────────────────────────────────────────
     std::unordered_set<uint64_t> folded_transpose;                  // not materialised
@@ -235,9 +106,16 @@ int mlxhip_stream_t::eval(uint64_t output) {
                     auto it = nodes.find(in);
                     if (it == nodes.end() || buffers.count(in)) continue;
                     const Node& t = it->second;
-                    const bool swap2 = t.op.op.kind == MLXHIP_OP_TRANSPOSE && t.meta.shape.size() == 2 &&
-                                       (!t.op.has_axes || (t.op.axes.size() == 2 && t.op.axes[0] == 1 && t.op.axes[1] == 0));
-                    if (swap2 && consumers[in] == 1 && n.inputs[0] != n.inputs[1] && !t.inputs.empty())
+                    // A swap of the two matrix axes: [1,0] on rank 2, [0,2,1]
+                    // on rank 3 (the batched operand of a rank-3 MatMul).
+                    const size_t nd = t.meta.shape.size();
+                    const bool swap2 = t.op.op.kind == MLXHIP_OP_TRANSPOSE &&
+                                       ((nd == 2 && (!t.op.has_axes || (t.op.axes.size() == 2 && t.op.axes[0] == 1 &&
+                                                                        t.op.axes[1] == 0))) ||
+                                        (nd == 3 && t.op.has_axes && t.op.axes.size() == 3 && t.op.axes[0] == 0 &&
+                                         t.op.axes[1] == 2 && t.op.axes[2] == 1));
+                    if (swap2 && consumers[in] == 1 && n.inputs[0] != n.inputs[1] && !t.inputs.empty() &&
+                        !requested.count(in))
                         folded_transpose.insert(in);
                 }
             }
@@ -264,7 +142,8 @@ int mlxhip_stream_t::eval(uint64_t output) {
             for (int c : cand) {
                 const uint64_t in = n.inputs[c];
                 if (is_binary(k) && n.inputs[0] == n.inputs[1]) break;  // x op x: keep both operands materialised
-                if (!in_order.count(in) || buffers.count(in) || folded_transpose.count(in)) continue;
+                if (!in_order.count(in) || buffers.count(in) || folded_transpose.count(in) || requested.count(in))
+                    continue;
                 auto ch = chain_of.find(in);
                 if (ch == chain_of.end() || consumers[in] != 1) continue;
                 // Limits of one ew_chain launch: instructions and distinct inputs.
@@ -401,7 +280,8 @@ static MetaVal meta_from(const mlxhip_meta_t* m) {
     return v;
 }
 
-uint64_t mlxhip_stream_add_constant(mlxhip_stream_t* s, const float* data, size_t len, const mlxhip_meta_t* meta) {
+static uint64_t add_constant(mlxhip_stream_t* s, const float* data, size_t len, const mlxhip_meta_t* meta,
+                             bool device_src) {
     if (!s || !meta || (len && !data)) {
         fail(MLXHIP_ERR_NULL_PTR, "stream_add_constant: null argument");
         return 0;
@@ -411,27 +291,22 @@ uint64_t mlxhip_stream_add_constant(mlxhip_stream_t* s, const float* data, size_
         return 0;
     }
     std::lock_guard<std::mutex> g(s->mu);
-    MetaVal mv = meta_from(meta);
-    if ((int64_t)len != mv.numel()) {
-        fail(MLXHIP_ERR_SHAPE_MISMATCH, "stream_add_constant: %zu values for %lld elements", len, (long long)mv.numel());
+    if (hipSetDevice(s->device) != hipSuccess) {
+        fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: hipSetDevice failed");
         return 0;
     }
-    mlxhip_op_t op{};
-    op.kind = MLXHIP_OP_CONSTANT;
-    const uint64_t id = s->add_node(OpVal::from(op), {}, mv, false);
-    float* p = static_cast<float*>(pool_alloc((len ? len : 1) * sizeof(float)));
-    if (!p) {
-        fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: device allocation failed");
-        return 0;
-    }
-    if (len && hipMemcpyAsync(p, data, len * sizeof(float), hipMemcpyHostToDevice, s->hs) != hipSuccess) {
-        pool_release(p);
-        fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: upload failed");
-        return 0;
-    }
-    (void)hipStreamSynchronize(s->hs);  // `data` may be freed by the caller right after
-    s->buffers[id] = DevBuf{p, len};
+    uint64_t id = 0;
+    if (s->add_constant(data, len, meta_from(meta), device_src, &id) != MLXHIP_OK) return 0;
     return id;
+}
+
+uint64_t mlxhip_stream_add_constant(mlxhip_stream_t* s, const float* data, size_t len, const mlxhip_meta_t* meta) {
+    return add_constant(s, data, len, meta, false);
+}
+
+uint64_t mlxhip_stream_add_constant_dev(mlxhip_stream_t* s, const float* data, size_t len,
+                                        const mlxhip_meta_t* meta) {
+    return add_constant(s, data, len, meta, true);
 }
 
 uint64_t mlxhip_stream_add_op(mlxhip_stream_t* s, const mlxhip_op_t* op, const uint64_t* inputs, size_t n_inputs,
@@ -454,7 +329,14 @@ int mlxhip_stream_eval(mlxhip_stream_t* s, uint64_t node) {
     if (!s) return fail(MLXHIP_ERR_NULL_PTR, "stream_eval: null stream");
     std::lock_guard<std::mutex> g(s->mu);
     MLXHIP_HIP(hipSetDevice(s->device));
-    return s->eval(node);
+    return s->eval({node});
+}
+
+int mlxhip_stream_eval_many(mlxhip_stream_t* s, const uint64_t* nodes, size_t n) {
+    if (!s || (n && !nodes)) return fail(MLXHIP_ERR_NULL_PTR, "stream_eval_many: null argument");
+    std::lock_guard<std::mutex> g(s->mu);
+    MLXHIP_HIP(hipSetDevice(s->device));
+    return s->eval(std::vector<uint64_t>(nodes, nodes + n));
 }
 
 int mlxhip_stream_get_buffer(mlxhip_stream_t* s, uint64_t node, float* out, size_t len) {

@@ -1,0 +1,186 @@
+// stream.hpp — graph state of the HBM-resident Stream (stream.cpp) shared
+// with reverse-mode autograd (autograd.cpp).
+#pragma once
+
+#include <atomic>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "backend.hpp"
+#include "common.hpp"
+
+namespace mlxhip {
+
+struct OpVal {
+    mlxhip_op_t op{};
+    std::vector<int64_t> shape, axes;
+    bool has_shape = false, has_axes = false;
+
+    static OpVal from(const mlxhip_op_t& o) {
+        OpVal v;
+        v.op = o;
+        if (o.shape) {
+            v.shape.assign(o.shape, o.shape + o.shape_len);
+            v.has_shape = true;
+        }
+        if (o.axes) {
+            v.axes.assign(o.axes, o.axes + o.axes_len);
+            v.has_axes = true;
+        }
+        return v;
+    }
+    mlxhip_op_t c() const {
+        mlxhip_op_t o = op;
+        o.shape = has_shape ? shape.data() : nullptr;
+        o.shape_len = shape.size();
+        o.axes = has_axes ? axes.data() : nullptr;
+        o.axes_len = axes.size();
+        return o;
+    }
+};
+
+struct MetaVal {
+    std::vector<int64_t> shape;
+    int dtype = MLXHIP_DTYPE_F32;
+    int64_t numel() const { return numel_of(shape.data(), shape.size()); }
+    mlxhip_meta_t c() const { return mlxhip_meta_t{shape.data(), shape.size(), dtype}; }
+};
+
+struct Node {
+    uint64_t id;
+    OpVal op;
+    std::vector<uint64_t> inputs;
+    MetaVal meta;
+};
+
+struct DevBuf {
+    float* ptr = nullptr;
+    size_t len = 0;
+};
+
+inline void append_bits(std::string& k, const void* p, size_t n) { k.append(static_cast<const char*>(p), n); }
+
+
+}  // namespace mlxhip
+
+struct mlxhip_stream_t {
+    std::mutex mu;  // guards everything below; eval runs under it
+    std::unordered_map<uint64_t, mlxhip::Node> nodes;
+    std::unordered_map<std::string, uint64_t> cse;
+    std::unordered_map<uint64_t, uint32_t> consumers;
+    std::unordered_map<uint64_t, mlxhip::DevBuf> buffers;
+    uint64_t next_id = 1;
+    std::atomic<uint64_t> eval_calls{0};
+    std::atomic<uint64_t> launches{0};
+    bool fusion = true;
+    hipStream_t hs = nullptr;
+    int device = 0;
+
+    ~mlxhip_stream_t() {
+        if (hs) (void)hipStreamSynchronize(hs);
+        for (auto& kv : buffers) mlxhip::pool_release(kv.second.ptr);
+        if (hs) (void)hipStreamDestroy(hs);
+    }
+
+    uint64_t add_node(const mlxhip::OpVal& op, std::vector<uint64_t> inputs, const mlxhip::MetaVal& meta, bool cse_ok) {
+        std::string key;
+        if (cse_ok) {
+            if ((op.op.kind == MLXHIP_OP_ADD || op.op.kind == MLXHIP_OP_MUL) && inputs.size() == 2 &&
+                inputs[0] > inputs[1])
+                std::swap(inputs[0], inputs[1]);
+            mlxhip_op_t o = op.op;
+            o.shape = nullptr;
+            o.axes = nullptr;
+            mlxhip::append_bits(key, &o, sizeof o);
+            key.push_back(op.has_shape ? 'S' : 's');
+            mlxhip::append_bits(key, op.shape.data(), op.shape.size() * sizeof(int64_t));
+            key.push_back(op.has_axes ? 'A' : 'a');
+            mlxhip::append_bits(key, op.axes.data(), op.axes.size() * sizeof(int64_t));
+            key.push_back('I');
+            mlxhip::append_bits(key, inputs.data(), inputs.size() * sizeof(uint64_t));
+            key.push_back('M');
+            mlxhip::append_bits(key, &meta.dtype, sizeof meta.dtype);
+            mlxhip::append_bits(key, meta.shape.data(), meta.shape.size() * sizeof(int64_t));
+            auto it = cse.find(key);
+            if (it != cse.end()) return it->second;
+        }
+        const uint64_t id = next_id++;
+        for (uint64_t in : inputs) consumers[in]++;
+        nodes.emplace(id, mlxhip::Node{id, op, std::move(inputs), meta});
+        if (cse_ok) cse.emplace(std::move(key), id);
+        return id;
+    }
+
+    // Depth-first post-order of the subgraph rooted at `outs` (graph.rs:268-294:
+    // one shared visited set, outputs in order, inputs in order), iterative so
+    // deep graphs cannot overflow the native stack.
+    std::vector<uint64_t> topo_sort(const std::vector<uint64_t>& outs) {
+        std::vector<uint64_t> order;
+        std::unordered_set<uint64_t> visited;
+        std::vector<std::pair<uint64_t, size_t>> st;
+        for (uint64_t out : outs) {
+            if (!visited.insert(out).second) continue;
+            st.emplace_back(out, 0);
+            while (!st.empty()) {
+                auto& top = st.back();
+                auto it = nodes.find(top.first);
+                if (it != nodes.end() && top.second < it->second.inputs.size()) {
+                    const uint64_t nxt = it->second.inputs[top.second++];
+                    if (visited.insert(nxt).second) st.emplace_back(nxt, 0);
+                } else {
+                    order.push_back(top.first);
+                    st.pop_back();
+                }
+            }
+        }
+        return order;
+    }
+
+    mlxhip_input_t input_of(uint64_t id, const float* data) {
+        const mlxhip::Node& n = nodes.at(id);
+        return mlxhip_input_t{data, (size_t)n.meta.numel(), n.meta.shape.data(), n.meta.shape.size(), n.meta.dtype};
+    }
+
+    // Stream::add_constant (backend.rs:59-71): a Constant node (never CSE'd)
+    // whose data is copied into a new HBM buffer at once, from host memory or,
+    // with device_src, from device memory (ordered before every later kernel
+    // on this stream).
+    int add_constant(const float* data, size_t len, const mlxhip::MetaVal& mv, bool device_src, uint64_t* id) {
+        if ((int64_t)len != mv.numel())
+            return mlxhip::fail(MLXHIP_ERR_SHAPE_MISMATCH, "stream_add_constant: %zu values for %lld elements", len,
+                        (long long)mv.numel());
+        float* p = static_cast<float*>(mlxhip::pool_alloc((len ? len : 1) * sizeof(float)));
+        if (!p) return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: device allocation failed");
+        if (len && hipMemcpyAsync(p, data, len * sizeof(float),
+                                  device_src ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, hs) != hipSuccess) {
+            mlxhip::pool_release(p);
+            return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: copy failed");
+        }
+        // Host data may be freed by the caller right after the call returns.
+        if (!device_src && len) (void)hipStreamSynchronize(hs);
+        mlxhip_op_t op{};
+        op.kind = MLXHIP_OP_CONSTANT;
+        *id = add_node(mlxhip::OpVal::from(op), {}, mv, false);
+        buffers[*id] = mlxhip::DevBuf{p, len};
+        return MLXHIP_OK;
+    }
+
+    int alloc_out(uint64_t id, float** out) {
+        const mlxhip::Node& n = nodes.at(id);
+        const size_t len = (size_t)n.meta.numel();
+        float* p = static_cast<float*>(mlxhip::pool_alloc((len ? len : 1) * sizeof(float)));
+        if (!p) return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream: device allocation of %zu floats failed", len);
+        buffers[id] = mlxhip::DevBuf{p, len};
+        *out = p;
+        return MLXHIP_OK;
+    }
+
+    // Evaluates every node in `outputs` (and what they depend on) in one
+    // scheduling pass.
+    int eval(const std::vector<uint64_t>& outputs);
+};
+

@@ -1,0 +1,178 @@
+"""mlx-nn layers over lazy tensors (crates/mlx-nn/src): Linear, RmsNorm,
+LayerNorm, causal self-attention, the SiLU MLP and a pre-norm transformer
+block, built only from ops that have a VJP so that autograd runs through the
+whole block.
+
+The reference's MultiHeadAttention works on one [seq, d_model] sequence
+with per-head Narrow and a fused Attention op (crates/mlx-nn/src/attention.rs:
+47-111), none of which has a VJP (crates/mlx-autograd/src/vjp.rs:173-176).
+``CausalSelfAttention`` composes the same computation from differentiable
+ops instead: per-head views by Reshape/Transpose, the batched (rank-3)
+MatMul, Mul by the 1/sqrt(d_head) scale, Add of a causal mask holding -1e9
+above the diagonal (the fill value of cpu_attention, crates/mlx-core/src/
+cpu_kernels.rs:786-788), Softmax over the last axis and a second batched
+MatMul.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Dict, Optional
+
+import numpy as np
+
+from . import abi
+from .tensor import Tensor
+
+
+class Linear:
+    """y = x @ W^T + b, W [out, in], b [out] (crates/mlx-nn/src/linear.rs:34-43)."""
+
+    def __init__(self, weight: Tensor, bias: Optional[Tensor] = None):
+        self.weight = weight
+        self.bias = bias
+
+    def forward(self, x: Tensor) -> Tensor:
+        y = x.matmul(self.weight.transpose())
+        if self.bias is not None:
+            y = y.add(self.bias.broadcast_to(y.shape))
+        return y
+
+    __call__ = forward
+
+
+class RmsNorm:
+    """x / sqrt(mean(x^2) + eps) over the last axis (crates/mlx-nn/src/norm.rs:43-67)."""
+
+    def __init__(self, dim: int, eps: float = 1e-5):
+        self.dim, self.eps = dim, eps
+
+    def forward(self, x: Tensor) -> Tensor:
+        if not x.shape:
+            raise abi.InvalidArgument("RmsNorm requires at least 1D input")
+        if x.shape[-1] != self.dim:
+            raise abi.InvalidArgument(f"RmsNorm expected last dim {self.dim}, got {x.shape[-1]}")
+        return x.rms_norm(self.eps)
+
+    __call__ = forward
+
+
+class LayerNorm:
+    """(x - mean) / sqrt(var + eps) over the last axis (crates/mlx-nn/src/norm.rs:12-36)."""
+
+    def __init__(self, dim: int, eps: float = 1e-5):
+        self.dim, self.eps = dim, eps
+
+    def forward(self, x: Tensor) -> Tensor:
+        if not x.shape or x.shape[-1] != self.dim:
+            raise abi.InvalidArgument(f"LayerNorm expected last dim {self.dim}")
+        return x.layer_norm(self.eps)
+
+    __call__ = forward
+
+
+MASK_FILL = -1e9
+
+
+def causal_mask(seq: int) -> np.ndarray:
+    """[seq, seq] additive mask: 0 on and below the diagonal, -1e9 above."""
+    m = np.zeros((seq, seq), np.float32)
+    m[np.triu_indices(seq, 1)] = MASK_FILL
+    return m
+
+
+class CausalSelfAttention:
+    """Causal multi-head self-attention over x [batch*seq, d_model] (rows
+    ordered batch-major), with Q/K/V/output projections as Linear layers."""
+
+    def __init__(self, wq: Linear, wk: Linear, wv: Linear, wo: Linear, n_heads: int, batch: int, seq: int):
+        self.wq, self.wk, self.wv, self.wo = wq, wk, wv, wo
+        self.h, self.b, self.s = n_heads, batch, seq
+
+    def _heads(self, t: Tensor) -> Tensor:
+        # [B*S, D] -> [B, S, H, Dh] -> [B, H, S, Dh] -> [B*H, S, Dh]
+        d = t.shape[1]
+        dh = d // self.h
+        return (t.reshape((self.b, self.s, self.h, dh)).transpose((0, 2, 1, 3))
+                .reshape((self.b * self.h, self.s, dh)))
+
+    def forward(self, x: Tensor) -> Tensor:
+        bs, d = x.shape
+        if bs != self.b * self.s or d % self.h:
+            raise abi.InvalidArgument(f"attention input {list(x.shape)} does not match "
+                                      f"batch {self.b} x seq {self.s}, {self.h} heads")
+        dh = d // self.h
+        q, k, v = self._heads(self.wq(x)), self._heads(self.wk(x)), self._heads(self.wv(x))
+        scores = q.matmul(k.transpose((0, 2, 1)))                      # [B*H, S, S]
+        st = x.stream
+        scale = Tensor.from_f32(st, [1.0 / math.sqrt(dh)], ()).broadcast_to(scores.shape)
+        mask = Tensor.from_f32(st, causal_mask(self.s), (self.s, self.s)).broadcast_to(scores.shape)
+        p = scores.mul(scale).add(mask).softmax(-1)
+        o = p.matmul(v)                                                 # [B*H, S, Dh]
+        o = o.reshape((self.b, self.h, self.s, dh)).transpose((0, 2, 1, 3)).reshape((bs, d))
+        return self.wo(o)
+
+    __call__ = forward
+
+
+class Mlp:
+    """down(silu(up(x))), hidden = 4 * d_model in the block below."""
+
+    def __init__(self, up: Linear, down: Linear):
+        self.up, self.down = up, down
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.down(self.up(x).silu())
+
+    __call__ = forward
+
+
+@dataclass
+class BlockConfig:
+    d_model: int = 1024
+    n_heads: int = 16
+    seq: int = 512
+    batch: int = 4
+    mlp_ratio: int = 4
+    eps: float = 1e-5
+
+    @property
+    def hidden(self) -> int:
+        return self.mlp_ratio * self.d_model
+
+    @property
+    def rows(self) -> int:
+        return self.batch * self.seq
+
+    def param_shapes(self) -> Dict[str, tuple]:
+        d, h = self.d_model, self.hidden
+        return {"wq": (d, d), "bq": (d,), "wk": (d, d), "bk": (d,), "wv": (d, d), "bv": (d,),
+                "wo": (d, d), "bo": (d,), "w1": (h, d), "b1": (h,), "w2": (d, h), "b2": (d,)}
+
+    def forward_flops(self) -> int:
+        """GEMM flops of one forward pass (backward: twice this)."""
+        r, d, h, s, b, nh = self.rows, self.d_model, self.hidden, self.seq, self.batch, self.n_heads
+        proj = 2 * r * d * d * 4           # Q, K, V, output projections
+        mlp = 2 * r * d * h * 2            # up and down
+        attn = 2 * (b * nh) * s * s * (d // nh) * 2   # scores and P.V
+        return proj + mlp + attn
+
+
+class TransformerBlock:
+    """Pre-norm block: h = x + attn(rms(x)); y = h + mlp(rms(h))."""
+
+    def __init__(self, cfg: BlockConfig, params: Dict[str, Tensor]):
+        p = params
+        self.cfg = cfg
+        self.norm1 = RmsNorm(cfg.d_model, cfg.eps)
+        self.norm2 = RmsNorm(cfg.d_model, cfg.eps)
+        self.attn = CausalSelfAttention(Linear(p["wq"], p["bq"]), Linear(p["wk"], p["bk"]),
+                                        Linear(p["wv"], p["bv"]), Linear(p["wo"], p["bo"]),
+                                        cfg.n_heads, cfg.batch, cfg.seq)
+        self.mlp = Mlp(Linear(p["w1"], p["b1"]), Linear(p["w2"], p["b2"]))
+
+    def forward(self, x: Tensor) -> Tensor:
+        h = x.add(self.attn(self.norm1(x)))
+        return h.add(self.mlp(self.norm2(h)))
+
+    __call__ = forward

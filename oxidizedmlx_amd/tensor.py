@@ -1,0 +1,199 @@
+"""Lazy tensors over a Stream: the part of mlx-core's ``Tensor`` API
+(crates/mlx-core/src/tensor.rs) that mlx-nn layers and mlx-autograd use,
+plus ``value_and_grad`` (crates/mlx-autograd/src/lib.rs:30-107).
+
+A ``Tensor`` is a node id with its shape on a stream. Every method adds a
+lazy node with the output shape and validation of the matching Rust method;
+nothing runs until a value is asked for. The stream is any object with the
+methods ``add_constant(data, meta)``, ``add_op(op, inputs, meta)``,
+``eval_many(ids)``, ``get_buffer(id)`` and ``grad(loss, wrt)``:
+``backend.HipStream`` (graph, scheduler and autograd in libmlxhip.so) is the
+product; the same graph code also runs on the test oracle's CPU stream.
+"""
+from __future__ import annotations
+
+from typing import Callable, Optional, Sequence, Tuple
+
+import numpy as np
+
+from . import abi
+from .opkind import Op, OpKind, TensorMeta
+
+
+def _shape(dims) -> Tuple[int, ...]:
+    return tuple(int(d) for d in dims)
+
+
+def _numel(shape: Sequence[int]) -> int:
+    n = 1
+    for d in shape:
+        n *= int(d)
+    return n
+
+
+class Tensor:
+    """Lazy tensor handle: (stream, node id, shape, dtype)."""
+
+    __slots__ = ("stream", "node", "shape", "dtype")
+
+    def __init__(self, stream, node: int, shape: Sequence[int], dtype: int = abi.F32):
+        self.stream = stream
+        self.node = int(node)
+        self.shape = _shape(shape)
+        self.dtype = dtype
+
+    # ── creation (tensor.rs:55-103) ──────────────────────────────────────
+    @classmethod
+    def from_f32(cls, stream, data, shape: Sequence[int], dtype: int = abi.F32) -> "Tensor":
+        shape = _shape(shape)
+        d = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
+        if d.size != _numel(shape):
+            raise abi.InvalidArgument(
+                f"data length {d.size} does not match shape {list(shape)} (expected {_numel(shape)})")
+        return cls(stream, stream.add_constant(d, TensorMeta(shape, dtype)), shape, dtype)
+
+    @classmethod
+    def from_device(cls, stream, ptr: int, shape: Sequence[int], dtype: int = abi.F32) -> "Tensor":
+        """Constant copied from f32 device memory (HipStream only)."""
+        shape = _shape(shape)
+        return cls(stream, stream.add_constant_dev(ptr, TensorMeta(shape, dtype)), shape, dtype)
+
+    def _lazy(self, op: Op, inputs: Sequence["Tensor"], shape: Sequence[int]) -> "Tensor":
+        shape = _shape(shape)
+        nid = self.stream.add_op(op, [t.node for t in inputs], TensorMeta(shape, self.dtype))
+        return Tensor(self.stream, nid, shape, self.dtype)
+
+    # ── elementwise (tensor.rs:167-238): equal shapes only ───────────────
+    def _binary(self, op: Op, rhs: "Tensor") -> "Tensor":
+        if self.shape != rhs.shape:
+            raise abi.ShapeMismatch(f"expected {list(self.shape)}, got {list(rhs.shape)}")
+        return self._lazy(op, [self, rhs], self.shape)
+
+    def add(self, rhs: "Tensor") -> "Tensor":
+        return self._binary(OpKind.Add, rhs)
+
+    def sub(self, rhs: "Tensor") -> "Tensor":
+        return self._binary(OpKind.Sub, rhs)
+
+    def mul(self, rhs: "Tensor") -> "Tensor":
+        return self._binary(OpKind.Mul, rhs)
+
+    def div(self, rhs: "Tensor") -> "Tensor":
+        return self._binary(OpKind.Div, rhs)
+
+    def neg(self) -> "Tensor":
+        return self._lazy(OpKind.Neg, [self], self.shape)
+
+    def exp(self) -> "Tensor":
+        return self._lazy(OpKind.Exp, [self], self.shape)
+
+    def sqrt(self) -> "Tensor":
+        return self._lazy(OpKind.Sqrt, [self], self.shape)
+
+    def silu(self) -> "Tensor":
+        return self._lazy(OpKind.Silu, [self], self.shape)
+
+    def gelu(self) -> "Tensor":
+        return self._lazy(OpKind.Gelu, [self], self.shape)
+
+    # ── reductions (tensor.rs:243-269) ───────────────────────────────────
+    def sum_axis(self, axis: int) -> "Tensor":
+        nd = len(self.shape)
+        ax = axis + nd if axis < 0 else axis
+        if ax < 0 or ax >= nd:
+            raise abi.InvalidArgument(f"axis {axis} out of range for ndim {nd}")
+        return self._lazy(OpKind.Sum(ax), [self], self.shape[:ax] + self.shape[ax + 1:])
+
+    def sum_all(self) -> "Tensor":
+        return self._lazy(OpKind.Sum(None), [self], ())
+
+    # ── linear algebra (tensor.rs:274-296; rank 3 per
+    #    evals/tasks/003_matmul_batch_3d.json) ──────────────────────────────
+    def matmul(self, rhs: "Tensor") -> "Tensor":
+        a, b = self.shape, rhs.shape
+        if not ((len(a) == 2 and len(b) == 2) or (len(a) == 3 and len(b) == 3)):
+            raise abi.InvalidArgument("matmul requires 2D tensors (or two 3D batched tensors)")
+        if len(a) == 3 and a[0] != b[0]:
+            raise abi.ShapeMismatch(f"expected batch {a[0]}, got {b[0]}")
+        if a[-1] != b[-2]:
+            raise abi.ShapeMismatch(f"expected {list(a)}, got {list(b)}")
+        return self._lazy(OpKind.MatMul, [self, rhs], a[:-1] + (b[-1],))
+
+    # ── shape ops (tensor.rs:322-374, 769-801) ───────────────────────────
+    def reshape(self, shape: Sequence[int]) -> "Tensor":
+        shape = _shape(shape)
+        if _numel(shape) != _numel(self.shape):
+            raise abi.ShapeMismatch(f"expected {list(self.shape)}, got {list(shape)}")
+        return self._lazy(OpKind.Reshape(shape), [self], shape)
+
+    def transpose(self, axes: Optional[Sequence[int]] = None) -> "Tensor":
+        nd = len(self.shape)
+        if axes is None:
+            perm = tuple(range(nd - 1, -1, -1))
+        else:
+            perm = tuple(int(a) for a in axes)
+            if len(perm) != nd:
+                raise abi.InvalidArgument(f"transpose axes length {len(perm)} does not match ndim {nd}")
+            if sorted(perm) != list(range(nd)):
+                raise abi.InvalidArgument(f"invalid permutation {list(perm)}")
+        return self._lazy(OpKind.Transpose(None if axes is None else perm), [self],
+                          tuple(self.shape[p] for p in perm))
+
+    def broadcast_to(self, shape: Sequence[int]) -> "Tensor":
+        shape = _shape(shape)
+        if shape == self.shape:
+            return self
+        if len(self.shape) > len(shape):
+            raise abi.InvalidArgument(f"cannot broadcast shape {list(self.shape)} to {list(shape)}")
+        pad = len(shape) - len(self.shape)
+        for i, d in enumerate(self.shape):
+            if d != 1 and d != shape[pad + i]:
+                raise abi.InvalidArgument(f"cannot broadcast shape {list(self.shape)} to {list(shape)}")
+        return self._lazy(OpKind.Broadcast(shape), [self], shape)
+
+    # ── row ops (tensor.rs:379-435) ──────────────────────────────────────
+    def softmax(self, axis: int) -> "Tensor":
+        nd = len(self.shape)
+        ax = axis + nd if axis < 0 else axis
+        if ax < 0 or ax >= nd:
+            raise abi.InvalidArgument(f"axis {axis} out of range for ndim {nd}")
+        return self._lazy(OpKind.Softmax(ax), [self], self.shape)
+
+    def layer_norm(self, eps: float) -> "Tensor":
+        return self._lazy(OpKind.LayerNorm(eps), [self], self.shape)
+
+    def rms_norm(self, eps: float) -> "Tensor":
+        return self._lazy(OpKind.RmsNorm(eps), [self], self.shape)
+
+    # ── values ───────────────────────────────────────────────────────────
+    def numel(self) -> int:
+        return _numel(self.shape)
+
+    def eval(self) -> "Tensor":
+        self.stream.eval_many([self.node])
+        return self
+
+    def to_numpy(self) -> np.ndarray:
+        self.eval()
+        return np.asarray(self.stream.get_buffer(self.node), np.float32).reshape(self.shape)
+
+
+def eval_all(tensors: Sequence[Tensor]) -> None:
+    """Evaluates several tensors of one stream in one scheduling pass."""
+    if tensors:
+        tensors[0].stream.eval_many([t.node for t in tensors])
+
+
+def value_and_grad(loss: Tensor, wrt: Sequence[Tensor]) -> Tuple[Tensor, list]:
+    """Gradients of the scalar ``loss`` with respect to each of ``wrt``
+    (mlx-autograd lib.rs:30-107; the reference takes one wrt tensor per call).
+    Returns the loss and the lazy gradient tensors."""
+    if loss.numel() != 1:
+        raise abi.InvalidArgument(f"grad requires scalar loss, got {loss.numel()} elements")
+    ids = loss.stream.grad(loss.node, [w.node for w in wrt])
+    return loss, [Tensor(loss.stream, g, w.shape, w.dtype) for g, w in zip(ids, wrt)]
+
+
+def grad(f: Callable[[Tensor], Tensor], x: Tensor) -> Tensor:
+    """grad(f, x) (mlx-autograd lib.rs:20-27)."""
+    return value_and_grad(f(x), [x])[1][0]

@@ -286,3 +286,41 @@ def test_shared_stream_from_threads():
     for o in outs:
         np.testing.assert_array_equal(o, outs[0])
     assert s.eval_count() == 1
+
+
+@pytest.mark.parametrize("fusion", [False, True])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_batched_matmul_with_transposed_operands(fusion, ta, tb):
+    # Rank-3 MatMul ([B,M,K] @ [B,K,N]) whose operands are Transpose [0,2,1]
+    # nodes: with fusion the transposes fold into the batched GEMM's operand
+    # layout instead of being materialised. Checked against the oracle.
+    bt, m, k, n = 3, 37, 29, 41
+    a0 = synth.normal(401, (bt, k, m) if ta else (bt, m, k))
+    b0 = synth.normal(402, (bt, n, k) if tb else (bt, k, n))
+    outs = []
+    for s in (HipStream(fusion=fusion), cpu_ref_stream()):
+        a = s.add_constant(a0, meta(a0.shape))
+        b = s.add_constant(b0, meta(b0.shape))
+        if ta:
+            a = s.add_op(OpKind.Transpose((0, 2, 1)), [a], meta((bt, m, k)))
+        if tb:
+            b = s.add_op(OpKind.Transpose((0, 2, 1)), [b], meta((bt, k, n)))
+        c = s.add_op(OpKind.MatMul, [a, b], meta((bt, m, n)))
+        s.eval(c)
+        outs.append(s.get_buffer(c))
+    bound = 1e-6 * np.sqrt(k) * np.abs(a0).max() * np.abs(b0).max()
+    assert_allclose(outs[0], outs[1], bound, 1e-5, "batched matmul")
+
+
+def test_batched_matmul_rejects_mismatched_batch():
+    s = HipStream()
+    a = s.add_constant(np.zeros(2 * 3 * 4, np.float32), meta((2, 3, 4)))
+    b = s.add_constant(np.zeros(3 * 4 * 5, np.float32), meta((3, 4, 5)))
+    c = s.add_op(OpKind.MatMul, [a, b], meta((2, 3, 5)))
+    with pytest.raises(abi.ShapeMismatch):
+        s.eval(c)
+
+
+def cpu_ref_stream():
+    from oracle.graph import OracleStream
+    return OracleStream()
