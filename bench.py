@@ -130,6 +130,31 @@ def main() -> int:
     bs = [hb.DeviceBuffer.from_array(bb) for _ in range(SETS)]
     stream = hb.create_stream()
 
+    # Config 4: one pre-norm transformer block (d_model 1024, 16 heads,
+    # seq 512, batch 4, 4x SiLU MLP), f32, forward and backward through the
+    # Stream's autograd. Weights N(0, 0.02^2), x N(0, 1); the loss is
+    # sum(block(x) * gy) with gy N(0, 1). Inputs stay in HBM; each step builds
+    # the graph on a fresh stream from them (device-to-device constants).
+    from oxidizedmlx_amd import nn as mnn
+    bcfg = mnn.BlockConfig()
+    blk_host = {name: synth.normal(0x5EED0100 + i, shp, 0.0, 0.02)
+                for i, (name, shp) in enumerate(bcfg.param_shapes().items())}
+    blk_host["x"] = synth.normal(0x5EED0180, (bcfg.rows, bcfg.d_model))
+    blk_host["gy"] = synth.normal(0x5EED0181, (bcfg.rows, bcfg.d_model))
+    blk_dev = {k: hb.DeviceBuffer.from_array(v) for k, v in blk_host.items()}
+    del blk_host
+
+    def block_step() -> None:
+        from oxidizedmlx_amd.tensor import Tensor, value_and_grad
+        st = hb.HipStream()
+        t = {k: Tensor.from_device(st, b.ptr, (bcfg.rows, bcfg.d_model) if k in ("x", "gy")
+                                   else bcfg.param_shapes()[k]) for k, b in blk_dev.items()}
+        params = {k: t[k] for k in bcfg.param_shapes()}
+        loss = mnn.TransformerBlock(bcfg, params)(t["x"]).mul(t["gy"]).sum_all()
+        _, grads = value_and_grad(loss, list(params.values()) + [t["x"]])
+        st.eval_many([g.node for g in grads])
+        st.close()
+
     kernels = {
         "gemm_bf16_4096": dict(flops=2.0 * n * n * n, bytes=3 * n * n * 2),
         # Calibration only (never part of a step): a plain 64 MiB copy whose HBM
@@ -146,12 +171,18 @@ def main() -> int:
         "layernorm_4096x4096": dict(bytes=2 * n * n * 4),
         "rmsnorm_4096x4096": dict(bytes=2 * n * n * 4),
         "silu_fma_chain_4096x4096": dict(bytes=4 * n * n * 4),
+        # Timed by wall clock around whole synchronised steps (graph build,
+        # autograd and every kernel), not by events.
+        "transformer_block_fwd_bwd_cfg4": dict(flops=3.0 * bcfg.forward_flops(), bytes=0, peak=157.3,
+                                               wall=True),
     }
     chain = [("mul", 1), ("add", 2), ("silu", 0)]
 
     def launch(name: str, i: int) -> None:
         j = i % SETS
-        if name == "gemm_bf16_4096":
+        if name == "transformer_block_fwd_bwd_cfg4":
+            block_step()
+        elif name == "gemm_bf16_4096":
             hb.gemm(abi.BF16, abi.BF16, False, False, n, n, n, dA[j], n, dB[j], n, dC[j], n, stream=stream)
         elif name == "softmax_4096x4096":
             hb.softmax_rows(xs["softmax"][j], ys["softmax"][j], n, n, stream=stream)
@@ -186,7 +217,16 @@ def main() -> int:
     hb.synchronize(stream)
     log(f"bench: timing {args.steps} steps")
     t0 = time.perf_counter()
+    wall_ms = {}
     for k in names:
+        if kernels[k].get("wall"):
+            hb.synchronize(None)
+            w0 = time.perf_counter()
+            for i in range(args.steps):
+                launch(k, i)
+            hb.synchronize(None)
+            wall_ms[k] = (time.perf_counter() - w0) * 1e3
+            continue
         e0, e1 = ev[k]
         e0.record(stream)
         for i in range(args.steps):
@@ -197,14 +237,18 @@ def main() -> int:
 
     res = {}
     for k in names:
-        e0, e1 = ev[k]
-        ms = e0.elapsed_ms(e1) / args.steps
+        if k in wall_ms:
+            ms = wall_ms[k] / args.steps
+        else:
+            e0, e1 = ev[k]
+            ms = e0.elapsed_ms(e1) / args.steps
         r = {"us": ms * 1e3}
         if "flops" in kernels[k]:
             r["tflops"] = kernels[k]["flops"] / (ms * 1e-3) / 1e12
             r["frac_mfma_peak"] = r["tflops"] / kernels[k].get("peak", BF16_PEAK_TFLOPS)
-        r["gbs"] = kernels[k]["bytes"] / (ms * 1e-3) / 1e9
-        r["frac_hbm_peak"] = r["gbs"] / HBM_PEAK_GBS
+        if kernels[k]["bytes"]:
+            r["gbs"] = kernels[k]["bytes"] / (ms * 1e-3) / 1e9
+            r["frac_hbm_peak"] = r["gbs"] / HBM_PEAK_GBS
         res[k] = r
         log(f"bench: {k}: {json.dumps(r)}")
     step_kernels = ("gemm_bf16_4096", "softmax_4096x4096", "layernorm_4096x4096", "rmsnorm_4096x4096",

@@ -30,6 +30,11 @@ int fibre_softmax(bool vjp, const float* a, const float* b, float* y, int64_t ou
 // ── elementwise.hip ───────────────────────────────────────────────────────
 int ew_chain(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs,
              int n_inputs, float* out, int64_t numel, hipStream_t s);
+// ew_chain where input i may be periodic: periods[i] > 0 means it holds
+// periods[i] values and element j reads in[j % periods[i]] (0 or numel: a
+// full-size input). periods may be null.
+int ew_chain_periodic(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs,
+                      const int64_t* periods, int n_inputs, float* out, int64_t numel, hipStream_t s);
 // General N-D permutation (rank <= 8): y[new] = x[old], out shape = shape[perm].
 int permute(const float* x, float* y, const int64_t* shape, const int64_t* perm, int ndim,
             hipStream_t s);

@@ -72,11 +72,16 @@ __host__ __device__ inline bool ew_binary(int op) {
 
 // The whole program travels in kernel arguments, so every instruction field
 // is wave-uniform (scalar registers) and the interpreter loop costs no VGPRs.
+// period[i] > 0: input i holds `period` values repeated along the output
+// (out index j reads in[j % period]; the tiling a right-aligned Broadcast
+// makes), in float4 units in the vector kernel; 0: a full-size input.
 struct EwProg {
     const float* in[MLXHIP_EW_MAX_INPUTS];
+    int64_t period[MLXHIP_EW_MAX_INPUTS];
     int op[MLXHIP_EW_MAX_INSTR];
     int operand[MLXHIP_EW_MAX_INSTR];
     int n_instr;
+    int scalar_mask;  // bit i: input i is one value for every element (vector kernel)
 };
 
 __device__ inline float4 apply4(int op, float4 a, float4 b) {
@@ -87,7 +92,10 @@ __device__ inline float4 apply4(int op, float4 a, float4 b) {
 // input's vectors are loaded before the program runs, so a thread has all
 // NI * U loads in flight at once instead of one input's per instruction; the
 // operand of each instruction is then picked by uniform (scalar) branches.
-template <int NI, int U, bool NT>
+// PERIODIC: some inputs are periodic or scalar (prog.period / scalar_mask);
+// their index is reduced modulo the period with 32-bit arithmetic (the host
+// only sets PERIODIC when every vector index fits in 32 bits).
+template <int NI, int U, bool NT, bool PERIODIC>
 __global__ __launch_bounds__(BLOCK) void ew_chain_vec_kernel(EwProg prog, float* __restrict__ out,
                                                              int64_t n_vec) {
     const int64_t stride = (int64_t)gridDim.x * BLOCK * U;
@@ -99,8 +107,17 @@ __global__ __launch_bounds__(BLOCK) void ew_chain_vec_kernel(EwProg prog, float*
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int64_t idx = base + (int64_t)u * BLOCK;
-                in[i][u] = idx < n_vec ? reinterpret_cast<const float4*>(prog.in[i])[idx]
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+                if (PERIODIC && (prog.scalar_mask >> i) & 1) {
+                    const float v = prog.in[i][0];
+                    in[i][u] = make_float4(v, v, v, v);
+                } else if (PERIODIC && prog.period[i] > 0) {
+                    const uint32_t j = (uint32_t)idx % (uint32_t)prog.period[i];
+                    in[i][u] = idx < n_vec ? reinterpret_cast<const float4*>(prog.in[i])[j]
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {
+                    in[i][u] = idx < n_vec ? reinterpret_cast<const float4*>(prog.in[i])[idx]
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
             }
         float4 acc[U];
 #pragma unroll
@@ -133,22 +150,32 @@ __global__ __launch_bounds__(BLOCK) void ew_chain_vec_kernel(EwProg prog, float*
 // uniform dispatch is repeated per component and the chain turns VALU-bound
 // (SiLU(x*w+b) ran at 43% of HBM bandwidth with 4, 92% with 1).
 template <int NI>
-int launch_chain_vec(const EwProg& p, float* out, int64_t n_vec, hipStream_t s) {
+int launch_chain_vec(const EwProg& p, float* out, int64_t n_vec, bool periodic, hipStream_t s) {
     constexpr int U = 1;
     int64_t grid = ceil_div(n_vec, (int64_t)BLOCK * U);
     if (grid > 65536) grid = 65536;
-    hipLaunchKernelGGL((ew_chain_vec_kernel<NI, U, false>), dim3((unsigned)grid), dim3(BLOCK), 0, s, p, out, n_vec);
+    if (periodic)
+        hipLaunchKernelGGL((ew_chain_vec_kernel<NI, U, false, true>), dim3((unsigned)grid), dim3(BLOCK), 0, s, p,
+                           out, n_vec);
+    else
+        hipLaunchKernelGGL((ew_chain_vec_kernel<NI, U, false, false>), dim3((unsigned)grid), dim3(BLOCK), 0, s, p,
+                           out, n_vec);
     return launch_check("ew_chain_vec_kernel");
 }
 
 __global__ __launch_bounds__(BLOCK) void ew_chain_scalar_kernel(EwProg prog, float* __restrict__ out,
                                                                 int64_t begin, int64_t n) {
+    // Periods are in elements here.
     const int64_t i = begin + (int64_t)blockIdx.x * BLOCK + threadIdx.x;
     if (i >= n) return;
-    float acc = prog.in[0][i];
+    auto at = [&](int in) {
+        const int64_t p = prog.period[in];
+        return prog.in[in][p > 0 ? i % p : i];
+    };
+    float acc = at(0);
     for (int k = 0; k < prog.n_instr; ++k) {
         const int op = prog.op[k];
-        acc = apply(op, acc, ew_binary(op) ? prog.in[prog.operand[k]][i] : 0.f);
+        acc = apply(op, acc, ew_binary(op) ? at(prog.operand[k]) : 0.f);
     }
     out[i] = acc;
 }
@@ -210,17 +237,38 @@ __global__ __launch_bounds__(BLOCK) void broadcast_kernel(const float* __restric
 }
 
 // One thread per output element; sequential fold in the reference's order
-// (reduce_along_axis, cpu_kernels.rs:166-195; Sum folds from -0.0).
-__global__ __launch_bounds__(BLOCK) void reduce_axis_kernel(int kind, const float* __restrict__ x,
-                                                            float* __restrict__ y, int64_t outer,
-                                                            int64_t dim, int64_t inner) {
-    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
+// (reduce_along_axis, cpu_kernels.rs:166-195; Sum folds from -0.0), so the
+// result is bit-identical to the CPU's. The fold is a chain of dependent
+// adds, so each thread loads RED_U elements ahead and then folds them in
+// order: the loads overlap instead of each waiting out a memory latency. One
+// wave per workgroup spreads the (often few) outputs over more CUs.
+// KIND: 0 Sum, 1 Mean, 2 Max.
+constexpr int RED_U = 32;
+constexpr int RED_BLOCK = 64;
+
+template <int KIND>
+__device__ inline float fold(float v, float x) {
+    return KIND == 2 ? fmaxf(v, x) : v + x;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(RED_BLOCK) void reduce_axis_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                                int64_t outer, int64_t dim, int64_t inner) {
+    const int64_t f = (int64_t)blockIdx.x * RED_BLOCK + threadIdx.x;
     if (f >= outer * inner) return;
     const int64_t o = f / inner, i = f % inner;
     const float* p = x + o * dim * inner + i;
-    float v = kind == 2 ? -INFINITY : -0.0f;
-    for (int64_t d = 0; d < dim; ++d) v = kind == 2 ? fmaxf(v, p[d * inner]) : v + p[d * inner];
-    if (kind == 1) v = v / (float)dim;
+    float v = KIND == 2 ? -INFINITY : -0.0f;
+    int64_t d = 0;
+    for (; d + RED_U <= dim; d += RED_U) {
+        float t[RED_U];
+#pragma unroll
+        for (int u = 0; u < RED_U; ++u) t[u] = p[(d + u) * inner];
+#pragma unroll
+        for (int u = 0; u < RED_U; ++u) v = fold<KIND>(v, t[u]);
+    }
+    for (; d < dim; ++d) v = fold<KIND>(v, p[d * inner]);
+    if (KIND == 1) v = v / (float)dim;
     y[f] = v;
 }
 
@@ -387,6 +435,11 @@ inline unsigned grid_for(int64_t n) { return (unsigned)ceil_div(n, BLOCK); }
 
 int ew_chain(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs, int n_inputs,
              float* out, int64_t numel, hipStream_t s) {
+    return ew_chain_periodic(prog, n_instr, inputs, nullptr, n_inputs, out, numel, s);
+}
+
+int ew_chain_periodic(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs,
+                      const int64_t* periods, int n_inputs, float* out, int64_t numel, hipStream_t s) {
     if (n_instr < 0 || n_instr > MLXHIP_EW_MAX_INSTR)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: %d instructions (max %d)", n_instr,
                     MLXHIP_EW_MAX_INSTR);
@@ -396,11 +449,24 @@ int ew_chain(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inp
     if (numel < 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: negative size");
     EwProg p{};
     bool aligned = reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    bool periodic = false;
     for (int i = 0; i < n_inputs; ++i) {
         if (!inputs[i] && numel) return fail(MLXHIP_ERR_NULL_PTR, "ew_chain: input %d is null", i);
         p.in[i] = inputs[i];
+        const int64_t per = periods ? periods[i] : 0;
+        if (per < 0 || (per > 0 && numel % per))
+            return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: period %lld does not divide %lld", (long long)per,
+                        (long long)numel);
+        p.period[i] = per == numel ? 0 : per;
+        if (p.period[i] > 0) {
+            periodic = true;
+            // Vector loads need whole float4 periods (or one value for all).
+            aligned = aligned && (p.period[i] == 1 || p.period[i] % 4 == 0);
+        }
         aligned = aligned && reinterpret_cast<uintptr_t>(inputs[i]) % 16 == 0;
     }
+    // 32-bit modulo in the vector kernel.
+    if (periodic && numel / 4 > (int64_t)UINT32_MAX) aligned = false;
     for (int k = 0; k < n_instr; ++k) {
         if (prog[k].op < 0 || prog[k].op >= MLXHIP_EW_COUNT_)
             return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: bad op %d", prog[k].op);
@@ -415,16 +481,25 @@ int ew_chain(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inp
     int64_t done = 0;
     if (aligned) {
         const int64_t n_vec = numel / 4;
+        EwProg pv = p;  // periods in float4 units; one-value inputs splat
+        for (int i = 0; i < n_inputs; ++i) {
+            if (p.period[i] == 1) {
+                pv.scalar_mask |= 1 << i;
+                pv.period[i] = 0;
+            } else {
+                pv.period[i] = p.period[i] / 4;
+            }
+        }
         if (n_vec > 0) {
             switch (n_inputs) {
-                case 1: MLXHIP_TRY(launch_chain_vec<1>(p, out, n_vec, s)); break;
-                case 2: MLXHIP_TRY(launch_chain_vec<2>(p, out, n_vec, s)); break;
-                case 3: MLXHIP_TRY(launch_chain_vec<3>(p, out, n_vec, s)); break;
-                case 4: MLXHIP_TRY(launch_chain_vec<4>(p, out, n_vec, s)); break;
-                case 5: MLXHIP_TRY(launch_chain_vec<5>(p, out, n_vec, s)); break;
-                case 6: MLXHIP_TRY(launch_chain_vec<6>(p, out, n_vec, s)); break;
-                case 7: MLXHIP_TRY(launch_chain_vec<7>(p, out, n_vec, s)); break;
-                default: MLXHIP_TRY(launch_chain_vec<8>(p, out, n_vec, s)); break;
+                case 1: MLXHIP_TRY(launch_chain_vec<1>(pv, out, n_vec, periodic, s)); break;
+                case 2: MLXHIP_TRY(launch_chain_vec<2>(pv, out, n_vec, periodic, s)); break;
+                case 3: MLXHIP_TRY(launch_chain_vec<3>(pv, out, n_vec, periodic, s)); break;
+                case 4: MLXHIP_TRY(launch_chain_vec<4>(pv, out, n_vec, periodic, s)); break;
+                case 5: MLXHIP_TRY(launch_chain_vec<5>(pv, out, n_vec, periodic, s)); break;
+                case 6: MLXHIP_TRY(launch_chain_vec<6>(pv, out, n_vec, periodic, s)); break;
+                case 7: MLXHIP_TRY(launch_chain_vec<7>(pv, out, n_vec, periodic, s)); break;
+                default: MLXHIP_TRY(launch_chain_vec<8>(pv, out, n_vec, periodic, s)); break;
             }
         }
         done = n_vec * 4;
@@ -506,8 +581,10 @@ int reduce_axis(int kind, const float* x, float* y, int64_t outer, int64_t dim, 
                 hipStream_t s) {
     const int64_t n = outer * inner;
     if (n == 0) return MLXHIP_OK;
-    hipLaunchKernelGGL(reduce_axis_kernel, dim3(grid_for(n)), dim3(BLOCK), 0, s, kind, x, y, outer,
-                       dim, inner);
+    const dim3 grid((unsigned)ceil_div(n, RED_BLOCK));
+    if (kind == 0) hipLaunchKernelGGL(reduce_axis_kernel<0>, grid, dim3(RED_BLOCK), 0, s, x, y, outer, dim, inner);
+    else if (kind == 1) hipLaunchKernelGGL(reduce_axis_kernel<1>, grid, dim3(RED_BLOCK), 0, s, x, y, outer, dim, inner);
+    else hipLaunchKernelGGL(reduce_axis_kernel<2>, grid, dim3(RED_BLOCK), 0, s, x, y, outer, dim, inner);
     return launch_check("reduce_axis_kernel");
 }
 

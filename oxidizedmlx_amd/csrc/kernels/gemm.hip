@@ -201,7 +201,12 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
                                                  : gemm16_f16(c_dtype, ta, tb, h, batch, cfg, s);
         }
     }
-    // General kernel: the largest block tile that still gives about one
+    // General kernel. f32 operands (measured on MI355X): 256x256 blocks from
+    // 256 tiles (one per CU); otherwise 128x128 blocks split over K until
+    // there are about 512 workgroups (two per CU), keeping at least 256 k per
+    // split; below 64 such tiles, 64x64 blocks as for 16-bit operands.
+    // 16-bit operands that reach this kernel (too small or unaligned for the
+    // direct-to-LDS one): the largest block tile that still gives about one
     // workgroup per CU; below that 64x64 tiles, split over K until there are
     // about four workgroups per CU (the general kernel prefetches one K tile
     // ahead, so small tiles need several resident workgroups to hide load
@@ -209,8 +214,14 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
     // summed in a fixed order (deterministic) by a second kernel.
     const int bk = ab_dtype == MLXHIP_DTYPE_F32 ? 32 : 64;
     auto tiles = [&](int w) { return ceil_div(m, 64 * w) * ceil_div(n, 64 * w) * batch; };
+    auto limit = [&](int64_t sp) { return (int)(batch * sp > 65535 ? 1 : std::max<int64_t>(1, sp)); };
     int wt = 2, splits = 1;
-    if (ab_dtype != MLXHIP_DTYPE_F32 && tiles(4) >= 240) {
+    if (ab_dtype == MLXHIP_DTYPE_F32 && tiles(4) >= 256) {
+        wt = 4;
+    } else if (ab_dtype == MLXHIP_DTYPE_F32 && tiles(2) >= 64 && aligned) {
+        const int64_t want = std::min<int64_t>(8, ceil_div(512, tiles(2)));
+        splits = limit(std::min<int64_t>(want, k / 256));
+    } else if (ab_dtype != MLXHIP_DTYPE_F32 && tiles(4) >= 240) {
         wt = 4;
     } else if (tiles(2) < 200) {
         wt = 1;
@@ -218,9 +229,7 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
         if (t < 768 && aligned) {
             const int64_t by_cus = std::max<int64_t>(1, 1024 / t);
             const int64_t by_k = k / (4 * bk);  // at least 4 K tiles per split
-            splits = (int)std::min<int64_t>(8, std::min(by_cus, by_k));
-            if (splits < 1) splits = 1;
-            if (batch * splits > 65535) splits = 1;
+            splits = limit(std::min<int64_t>(8, std::min(by_cus, by_k)));
         }
     }
     auto run = [&](const gemm_detail::GemmArgs& ga, int ct) {

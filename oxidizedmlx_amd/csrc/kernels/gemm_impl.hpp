@@ -342,7 +342,7 @@ int launch(const GemmArgs& a0, int64_t batch, hipStream_t s) {
 template <int DT, int CT, int TA, int TB>
 int dispatch_layout(const GemmArgs& a, int64_t batch, bool aligned, int wt, hipStream_t s) {
     if (!aligned) return launch<DT, CT, TA, TB, 2, 2, false>(a, batch, s);
-    if (wt == 4 && DT != MLXHIP_DTYPE_F32) return launch<DT, CT, TA, TB, 4, 4, true>(a, batch, s);
+    if (wt == 4) return launch<DT, CT, TA, TB, 4, 4, true>(a, batch, s);
     if (wt == 1) return launch<DT, CT, TA, TB, 1, 1, true>(a, batch, s);
     return launch<DT, CT, TA, TB, 2, 2, true>(a, batch, s);
 }

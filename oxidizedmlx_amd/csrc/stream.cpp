@@ -79,6 +79,43 @@ int binary_ew(int k, int acc_idx) {
 
 using namespace mlxhip;
 
+namespace mlxhip {
+namespace {
+
+// A Transpose node that swaps the two matrix axes: [1,0] (or None) on rank
+// 2, [0,2,1] on rank 3 (the batched operand of a rank-3 MatMul).
+bool is_matrix_swap(const Node& t) {
+    if (t.op.op.kind != MLXHIP_OP_TRANSPOSE) return false;
+    const size_t nd = t.meta.shape.size();
+    const std::vector<int64_t>& a = t.op.axes;
+    if (nd == 2) return !t.op.has_axes || (a.size() == 2 && a[0] == 1 && a[1] == 0);
+    return nd == 3 && t.op.has_axes && a.size() == 3 && a[0] == 0 && a[1] == 2 && a[2] == 1;
+}
+
+// Period P when broadcasting `src` to `dst` only repeats src: after padding
+// src with leading 1s, src = [1,...,1, dst[j:]] for some j, so
+// out[i] = src[i % P] with P = numel(dst[j:]). 0 when it is no such tiling.
+int64_t tiling_period(const std::vector<int64_t>& src, const std::vector<int64_t>& dst) {
+    if (src.size() > dst.size()) return 0;
+    const size_t pad = dst.size() - src.size();
+    std::vector<int64_t> s(pad, 1);
+    s.insert(s.end(), src.begin(), src.end());
+    for (size_t j = 0; j <= dst.size(); ++j) {
+        bool ok = true;
+        for (size_t i = 0; i < j && ok; ++i) ok = s[i] == 1;
+        for (size_t i = j; i < dst.size() && ok; ++i) ok = s[i] == dst[i];
+        if (ok) {
+            int64_t p = 1;
+            for (size_t i = j; i < dst.size(); ++i) p *= dst[i];
+            return p;
+        }
+    }
+    return 0;
+}
+
+}  // namespace
+}  // namespace mlxhip
+
 int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     std::vector<uint64_t> todo;
     for (uint64_t o : outputs) {
@@ -94,31 +131,73 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
 
     // ── look-ahead planning ──────────────────────────────────────────────
     std::unordered_set<uint64_t> folded_transpose;                  // not materialised
+    std::unordered_set<uint64_t> swapped_matmul;                    // Transpose computed as B^T A^T
+    std::unordered_set<uint64_t> absorbed_matmul;                   // MatMul inside such a Transpose
     std::unordered_map<uint64_t, std::vector<uint64_t>> chain_of;   // chain end -> nodes
     std::unordered_map<uint64_t, int> acc_input;                    // node -> index of its acc input
     std::unordered_set<uint64_t> interior;                          // fused, not materialised
+    // Broadcasts that only tile their source and whose every consumer is an
+    // elementwise node of this evaluation: the chain kernel reads the source
+    // periodically and the broadcast is never materialised.
+    std::unordered_map<uint64_t, int64_t> virtual_bcast;            // node -> period (elements)
     if (fusion) {
+        std::unordered_map<uint64_t, std::vector<uint64_t>> users;
+        for (uint64_t id : order)
+            for (uint64_t in : nodes.at(id).inputs) users[in].push_back(id);
         for (uint64_t id : order) {
-            if (buffers.count(id)) continue;
+            if (buffers.count(id) || requested.count(id)) continue;
             const Node& n = nodes.at(id);
-            if (n.op.op.kind == MLXHIP_OP_MATMUL && n.inputs.size() == 2) {
-                for (uint64_t in : n.inputs) {
-                    auto it = nodes.find(in);
-                    if (it == nodes.end() || buffers.count(in)) continue;
-                    const Node& t = it->second;
-                    // A swap of the two matrix axes: [1,0] on rank 2, [0,2,1]
-                    // on rank 3 (the batched operand of a rank-3 MatMul).
-                    const size_t nd = t.meta.shape.size();
-                    const bool swap2 = t.op.op.kind == MLXHIP_OP_TRANSPOSE &&
-                                       ((nd == 2 && (!t.op.has_axes || (t.op.axes.size() == 2 && t.op.axes[0] == 1 &&
-                                                                        t.op.axes[1] == 0))) ||
-                                        (nd == 3 && t.op.has_axes && t.op.axes.size() == 3 && t.op.axes[0] == 0 &&
-                                         t.op.axes[1] == 2 && t.op.axes[2] == 1));
-                    if (swap2 && consumers[in] == 1 && n.inputs[0] != n.inputs[1] && !t.inputs.empty() &&
-                        !requested.count(in))
-                        folded_transpose.insert(in);
-                }
+            if (n.op.op.kind != MLXHIP_OP_BROADCAST || n.inputs.size() != 1) continue;
+            const int64_t per = tiling_period(nodes.at(n.inputs[0]).meta.shape, n.meta.shape);
+            if (per <= 0 || per != nodes.at(n.inputs[0]).meta.numel()) continue;
+            const std::vector<uint64_t>& u = users[id];
+            if (u.empty() || u.size() != consumers[id]) continue;
+            bool ok = true;
+            for (uint64_t c : u) {
+                const Node& cn = nodes.at(c);
+                const int ck = cn.op.op.kind;
+                ok = ok && is_elementwise(ck) && !buffers.count(c) && cn.meta.numel() == n.meta.numel() &&
+                     cn.inputs.size() == (is_binary(ck) ? 2u : 1u);
+                for (uint64_t ci : cn.inputs) ok = ok && nodes.at(ci).meta.numel() == cn.meta.numel();
             }
+            if (ok) virtual_bcast[id] = per;
+        }
+
+        // A Transpose that swaps the two matrix axes ([1,0] on rank 2,
+        // [0,2,1] on rank 3) and is read only by MatMuls, directly or through
+        // further such Transposes, is not materialised: each MatMul reads the
+        // untransposed source with the transposed operand layout. Consumers
+        // come later in the order, so walk it backwards.
+        for (auto it = order.rbegin(); it != order.rend(); ++it) {
+            const uint64_t id = *it;
+            if (buffers.count(id) || requested.count(id)) continue;
+            const Node& t = nodes.at(id);
+            if (!is_matrix_swap(t) || t.inputs.empty()) continue;
+            const std::vector<uint64_t>& u = users[id];
+            if (u.empty() || u.size() != consumers[id]) continue;
+            bool ok = true;
+            for (uint64_t c : u) {
+                if (buffers.count(c) || folded_transpose.count(c)) continue;
+                const Node& cn = nodes.at(c);
+                ok = ok && cn.op.op.kind == MLXHIP_OP_MATMUL && cn.inputs.size() == 2 && cn.inputs[0] != cn.inputs[1];
+            }
+            if (ok) folded_transpose.insert(id);
+        }
+        // A materialised matrix-swap Transpose of a MatMul that nothing else
+        // reads is computed as one product with swapped operands,
+        // (A B)^T = B^T A^T; the MatMul itself is not materialised.
+        for (uint64_t id : order) {
+            if (buffers.count(id) || folded_transpose.count(id)) continue;
+            const Node& t = nodes.at(id);
+            if (!is_matrix_swap(t) || t.inputs.size() != 1) continue;
+            const uint64_t m = t.inputs[0];
+            auto mn = nodes.find(m);
+            if (mn == nodes.end() || mn->second.op.op.kind != MLXHIP_OP_MATMUL || mn->second.inputs.size() != 2 ||
+                mn->second.inputs[0] == mn->second.inputs[1] || buffers.count(m) || requested.count(m) ||
+                consumers[m] != 1 || mn->second.meta.dtype != MLXHIP_DTYPE_F32)
+                continue;
+            swapped_matmul.insert(id);
+            absorbed_matmul.insert(m);
         }
         for (uint64_t id : order) {
             if (buffers.count(id) || folded_transpose.count(id)) continue;
@@ -175,27 +254,51 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     }
 
     // ── evaluation ────────────────────────────────────────────────────────
+    std::unordered_set<uint64_t> counted_virtual, counted_folded;  // eval_count covers each once
     Scratch scratch;
     int rc = MLXHIP_OK;
     for (uint64_t id : order) {
-        if (buffers.count(id) || folded_transpose.count(id) || interior.count(id)) continue;
+        if (buffers.count(id) || folded_transpose.count(id) || interior.count(id) || virtual_bcast.count(id) ||
+            absorbed_matmul.count(id))
+            continue;
         const Node& n = nodes.at(id);
         auto ch = chain_of.find(id);
-        if (ch != chain_of.end() && ch->second.size() > 1) {
+        auto reads_virtual = [&](const std::vector<uint64_t>& chain) {
+            for (uint64_t m : chain)
+                for (uint64_t in : nodes.at(m).inputs)
+                    if (virtual_bcast.count(in)) return true;
+            return false;
+        };
+        if (ch != chain_of.end() && (ch->second.size() > 1 || reads_virtual(ch->second))) {
             // One fused kernel for the whole chain.
             const std::vector<uint64_t>& nodes_in_chain = ch->second;
             std::vector<const float*> ins;
+            std::vector<int64_t> periods;
             std::vector<uint64_t> in_ids;
+            auto ready = [&](uint64_t src) {
+                auto v = virtual_bcast.find(src);
+                return buffers.count(v != virtual_bcast.end() ? nodes.at(src).inputs[0] : src) != 0;
+            };
             auto slot = [&](uint64_t src) -> int {
                 for (size_t i = 0; i < in_ids.size(); ++i)
                     if (in_ids[i] == src) return (int)i;
                 in_ids.push_back(src);
-                ins.push_back(buffers.at(src).ptr);
+                auto v = virtual_bcast.find(src);
+                if (v != virtual_bcast.end()) {
+                    ins.push_back(buffers.at(nodes.at(src).inputs[0]).ptr);
+                    periods.push_back(v->second);
+                } else {
+                    ins.push_back(buffers.at(src).ptr);
+                    periods.push_back(0);
+                }
                 return (int)in_ids.size() - 1;
             };
+            for (uint64_t m : nodes_in_chain)
+                for (uint64_t in : nodes.at(m).inputs)
+                    if (virtual_bcast.count(in) && counted_virtual.insert(in).second) eval_calls += 1;
             const Node& first = nodes.at(nodes_in_chain.front());
             const uint64_t base = first.inputs[acc_input[nodes_in_chain.front()]];
-            if (!buffers.count(base)) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "fusion: base not materialised"); break; }
+            if (!ready(base)) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "fusion: base not materialised"); break; }
             slot(base);
             std::vector<mlxhip_ew_instr_t> prog;
             for (uint64_t m : nodes_in_chain) {
@@ -204,7 +307,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
                 if (is_binary(k)) {
                     const int ai = acc_input[m];
                     const uint64_t other = mn.inputs[1 - ai];
-                    if (!buffers.count(other)) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "fusion: operand not materialised"); break; }
+                    if (!ready(other)) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "fusion: operand not materialised"); break; }
                     prog.push_back({binary_ew(k, ai), slot(other)});
                 } else {
                     prog.push_back({unary_ew(k), 0});
@@ -213,7 +316,8 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             if (rc != MLXHIP_OK) break;
             float* out = nullptr;
             if ((rc = alloc_out(id, &out)) != MLXHIP_OK) break;
-            rc = ew_chain(prog.data(), (int)prog.size(), ins.data(), (int)ins.size(), out, n.meta.numel(), hs);
+            rc = ew_chain_periodic(prog.data(), (int)prog.size(), ins.data(), periods.data(), (int)ins.size(), out,
+                                   n.meta.numel(), hs);
             eval_calls += nodes_in_chain.size();
             launches += 1;
             if (rc != MLXHIP_OK) {
@@ -223,15 +327,36 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             }
             continue;
         }
-        // Single node through HipBackend::eval_node.
+        // Reshape keeps the data as it is (row-major, contiguous): the node
+        // aliases its input's buffer, which lives as long as the stream.
+        if (n.op.op.kind == MLXHIP_OP_RESHAPE && n.inputs.size() == 1) {
+            auto src = buffers.find(n.inputs[0]);
+            if (src != buffers.end() && (int64_t)src->second.len == n.meta.numel()) {
+                buffers[id] = DevBuf{src->second.ptr, src->second.len, false};
+                eval_calls += 1;
+                continue;
+            }
+        }
+        // Single node through HipBackend::eval_node. A MatMul operand that is
+        // a folded Transpose (or a chain of them) is read from the source
+        // with the operand layout flipped once per Transpose; a swapped
+        // Transpose runs its MatMul as B^T A^T.
         std::vector<mlxhip_input_t> ins;
         int hint[2] = {0, 0};
         bool missing = false;
-        for (size_t i = 0; i < n.inputs.size(); ++i) {
-            uint64_t src = n.inputs[i];
-            if (folded_transpose.count(src) && n.op.op.kind == MLXHIP_OP_MATMUL && i < 2) {
-                hint[i] = 1;
-                src = nodes.at(src).inputs[0];
+        const bool swapped = swapped_matmul.count(id) != 0;
+        const Node& en = swapped ? nodes.at(n.inputs[0]) : n;  // the node whose op runs
+        uint64_t covered = 1 + (swapped ? 1 : 0);
+        for (size_t j = 0; j < en.inputs.size(); ++j) {
+            const size_t i = swapped ? 1 - j : j;  // swapped: operands exchange places
+            uint64_t src = en.inputs[i];
+            if (en.op.op.kind == MLXHIP_OP_MATMUL && j < 2) {
+                hint[j] = swapped ? 1 : 0;
+                while (folded_transpose.count(src)) {
+                    if (counted_folded.insert(src).second) covered += 1;
+                    hint[j] ^= 1;
+                    src = nodes.at(src).inputs[0];
+                }
             }
             auto b = buffers.find(src);
             if (b == buffers.end()) { missing = true; break; }
@@ -240,9 +365,9 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         if (missing) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "input node should be evaluated before dependents"); break; }
         float* out = nullptr;
         if ((rc = alloc_out(id, &out)) != MLXHIP_OK) break;
-        const mlxhip_op_t op = n.op.c();
+        const mlxhip_op_t op = en.op.c();
         const mlxhip_meta_t meta = n.meta.c();
-        eval_calls += 1 + (hint[0] + hint[1]);
+        eval_calls += covered;
         launches += 1;
         rc = eval_node_device(op, ins.data(), ins.size(), meta, out, hs, scratch, hint);
         if (rc != MLXHIP_OK) {

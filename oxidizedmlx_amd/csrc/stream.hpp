@@ -60,6 +60,7 @@ struct Node {
 struct DevBuf {
     float* ptr = nullptr;
     size_t len = 0;
+    bool owned = true;  // false: aliases another node's buffer (Reshape)
 };
 
 inline void append_bits(std::string& k, const void* p, size_t n) { k.append(static_cast<const char*>(p), n); }
@@ -82,7 +83,8 @@ struct mlxhip_stream_t {
 
     ~mlxhip_stream_t() {
         if (hs) (void)hipStreamSynchronize(hs);
-        for (auto& kv : buffers) mlxhip::pool_release(kv.second.ptr);
+        for (auto& kv : buffers)
+            if (kv.second.owned) mlxhip::pool_release(kv.second.ptr);
         if (hs) (void)hipStreamDestroy(hs);
     }
 

@@ -156,3 +156,16 @@ def test_gemm_argument_errors():
         hb.gemm(F32, F32, False, False, 2, 2, 4, 1, 2, 1, 2, 1, 2)  # lda < K
     with pytest.raises(abi.NullPtr):
         hb.gemm(F32, F32, False, False, 2, 2, 2, 0, 2, 0, 2, 0, 2)
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb", [
+    (2048, 1024, 1024, 0, 1),   # 128x128 blocks, K split 4 (config-4 projections)
+    (1024, 1024, 2048, 1, 0),   # 128x128 blocks, K split 8 (weight gradients)
+    (2048, 4096, 1024, 0, 0),   # 128x128 blocks, no split
+    (4096, 4096, 256, 1, 1),    # 256x256 blocks
+    (1000, 1100, 700, 0, 1),    # 128x128 blocks with edge tiles, split 2
+])
+def test_f32_block_and_split_choices(m, n, k, ta, tb):
+    # The f32 shapes of the config-4 block pick 128x128 or 256x256 blocks
+    # and split K; sampled rows against the oracle.
+    check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), seed=m + n + k, rows=sample_rows(m, 10))

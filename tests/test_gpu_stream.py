@@ -324,3 +324,106 @@ def test_batched_matmul_rejects_mismatched_batch():
 def cpu_ref_stream():
     from oracle.graph import OracleStream
     return OracleStream()
+
+
+def test_reshape_aliases_its_input():
+    # A Reshape keeps the data: no kernel runs for it, and its value (and a
+    # consumer's) is the input's.
+    s = HipStream()
+    x0 = synth.normal(501, (6, 8))
+    x = s.add_constant(x0, meta((6, 8)))
+    r = s.add_op(OpKind.Reshape((4, 12)), [x], meta((4, 12)))
+    y = s.add_op(OpKind.Neg, [r], meta((4, 12)))
+    before = s.launch_count()
+    s.eval_many([r, y])
+    assert s.launch_count() - before == 1  # the Neg only
+    np.testing.assert_array_equal(s.get_buffer(r), x0.reshape(-1))
+    np.testing.assert_array_equal(s.get_buffer(y), -x0.reshape(-1))
+
+
+def _broadcast_graph(s, b, r, c):
+    """y = ((x * bcast(scale)) + bcast(mask[r, c])) + bcast(bias[c]) with
+    x [b, r, c]: the three broadcasts tile their sources."""
+    x0 = synth.normal(511, (b, r, c))
+    mask0 = synth.normal(512, (r, c))
+    bias0 = synth.normal(513, (c,))
+    full = meta((b, r, c))
+    x = s.add_constant(x0, full)
+    sc = s.add_op(OpKind.Broadcast((b, r, c)), [s.add_constant([0.125], meta(()))], full)
+    mk = s.add_op(OpKind.Broadcast((b, r, c)), [s.add_constant(mask0, meta((r, c)))], full)
+    bi = s.add_op(OpKind.Broadcast((b, r, c)), [s.add_constant(bias0, meta((c,)))], full)
+    y = s.add_op(OpKind.Add, [s.add_op(OpKind.Add, [s.add_op(OpKind.Mul, [x, sc], full), mk], full), bi], full)
+    return y, (x0 * np.float32(0.125) + mask0) + bias0
+
+
+@pytest.mark.parametrize("shape", [(4, 16, 32), (3, 5, 7), (2, 64, 1)])
+def test_broadcast_operands_read_in_place(shape):
+    # Tiling broadcasts feeding elementwise nodes are read periodically by the
+    # chain kernel; the result must equal the unfused graph bit for bit and
+    # the oracle, and eval_count must not change.
+    res, counts = [], []
+    for fusion in (True, False):
+        s = HipStream(fusion=fusion)
+        y, want = _broadcast_graph(s, *shape)
+        s.eval(y)
+        res.append(s.get_buffer(y))
+        counts.append(s.eval_count())
+    np.testing.assert_array_equal(res[0], res[1])
+    np.testing.assert_array_equal(res[0], want.reshape(-1))
+    assert counts[0] == counts[1]
+    o = cpu_ref_stream()
+    y, _ = _broadcast_graph(o, *shape)
+    o.eval(y)
+    np.testing.assert_array_equal(res[0], o.get_buffer(y))
+
+
+def test_broadcast_requested_later_is_materialised():
+    s = HipStream()
+    full = meta((3, 8))
+    b = s.add_op(OpKind.Broadcast((3, 8)), [s.add_constant(np.arange(8, dtype=np.float32), meta((8,)))], full)
+    x = s.add_constant(np.ones(24, np.float32), full)
+    y = s.add_op(OpKind.Add, [x, b], full)
+    s.eval(y)
+    s.eval(b)  # not materialised by the first evaluation; must be now
+    np.testing.assert_array_equal(s.get_buffer(b), np.tile(np.arange(8, dtype=np.float32), 3))
+    np.testing.assert_array_equal(s.get_buffer(y), np.tile(np.arange(8, dtype=np.float32), 3) + 1)
+
+
+@pytest.mark.parametrize("shape,axis", [((2048, 1024), 0), ((3, 1000, 7), 1), ((5, 37), 1), ((4096, 3), 0)])
+def test_sum_axis_matches_sequential_fold_bitwise(shape, axis):
+    # Sum over an axis folds each output in order from -0.0, like the CPU
+    # (cpu_kernels.rs:166-195): bit-identical results.
+    x0 = synth.normal(521, shape)
+    out_shape = tuple(d for i, d in enumerate(shape) if i != axis)
+    res = []
+    for s in (HipStream(), cpu_ref_stream()):
+        x = s.add_constant(x0, meta(shape))
+        y = s.add_op(OpKind.Sum(axis), [x], meta(out_shape))
+        s.eval(y)
+        res.append(s.get_buffer(y))
+    np.testing.assert_array_equal(res[0], res[1])
+
+
+@pytest.mark.parametrize("fusion", [False, True])
+def test_transpose_rewrites_match_unfused(fusion):
+    # transpose(transpose(W)) read by a MatMul folds to W itself; a Transpose
+    # of a MatMul nothing else reads runs as one product with swapped
+    # operands. Results must equal the oracle (and the unfused graph).
+    x0, w0 = synth.normal(531, (40, 24)), synth.normal(532, (24, 24))
+    g0 = synth.normal(533, (40, 24))
+    res = []
+    for s in (HipStream(fusion=fusion), cpu_ref_stream()):
+        x = s.add_constant(x0, meta((40, 24)))
+        w = s.add_constant(w0, meta((24, 24)))
+        g = s.add_constant(g0, meta((40, 24)))
+        wt = s.add_op(OpKind.Transpose(None), [w], meta((24, 24)))
+        y = s.add_op(OpKind.MatMul, [x, wt], meta((40, 24)))                 # x W^T
+        wtt = s.add_op(OpKind.Transpose(None), [wt], meta((24, 24)))
+        dx = s.add_op(OpKind.MatMul, [g, wtt], meta((40, 24)))               # g W
+        xt = s.add_op(OpKind.Transpose(None), [x], meta((24, 40)))
+        dwt = s.add_op(OpKind.MatMul, [xt, g], meta((24, 24)))               # x^T g
+        dw = s.add_op(OpKind.Transpose((1, 0)), [dwt], meta((24, 24)))      # (x^T g)^T
+        s.eval_many([y, dx, dw])
+        res.append([s.get_buffer(t) for t in (y, dx, dw)])
+    for got, want in zip(*res):
+        assert_allclose(got, want, 1e-5, 1e-5, "transpose rewrites")
