@@ -243,7 +243,7 @@ __global__ __launch_bounds__(BLOCK) void broadcast_kernel(const float* __restric
 // order: the loads overlap instead of each waiting out a memory latency. One
 // wave per workgroup spreads the (often few) outputs over more CUs.
 // KIND: 0 Sum, 1 Mean, 2 Max.
-constexpr int RED_U = 32;
+constexpr int RED_U = 64;
 constexpr int RED_BLOCK = 64;
 
 template <int KIND>
@@ -259,15 +259,29 @@ __global__ __launch_bounds__(RED_BLOCK) void reduce_axis_kernel(const float* __r
     const int64_t o = f / inner, i = f % inner;
     const float* p = x + o * dim * inner + i;
     float v = KIND == 2 ? -INFINITY : -0.0f;
-    int64_t d = 0;
-    for (; d + RED_U <= dim; d += RED_U) {
-        float t[RED_U];
+    // Two register batches in turn: batch b is loaded while batch a is
+    // folded and the other way round, so memory latency overlaps the chain
+    // of dependent adds; neither batch is ever copied (a copy would wait for
+    // its loads).
+    const int64_t full = dim / (2 * RED_U) * (2 * RED_U);
+    float a[RED_U], b[RED_U];
+    if (full > 0) {
 #pragma unroll
-        for (int u = 0; u < RED_U; ++u) t[u] = p[(d + u) * inner];
-#pragma unroll
-        for (int u = 0; u < RED_U; ++u) v = fold<KIND>(v, t[u]);
+        for (int u = 0; u < RED_U; ++u) a[u] = p[(int64_t)u * inner];
     }
-    for (; d < dim; ++d) v = fold<KIND>(v, p[d * inner]);
+    for (int64_t d = 0; d < full; d += 2 * RED_U) {
+#pragma unroll
+        for (int u = 0; u < RED_U; ++u) b[u] = p[(d + RED_U + u) * inner];
+#pragma unroll
+        for (int u = 0; u < RED_U; ++u) v = fold<KIND>(v, a[u]);
+        if (d + 2 * RED_U < full) {
+#pragma unroll
+            for (int u = 0; u < RED_U; ++u) a[u] = p[(d + 2 * RED_U + u) * inner];
+        }
+#pragma unroll
+        for (int u = 0; u < RED_U; ++u) v = fold<KIND>(v, b[u]);
+    }
+    for (int64_t d = full; d < dim; ++d) v = fold<KIND>(v, p[d * inner]);
     if (KIND == 1) v = v / (float)dim;
     y[f] = v;
 }

@@ -15,6 +15,7 @@ MatMul.
 """
 from __future__ import annotations
 
+import functools
 import math
 from dataclasses import dataclass
 from typing import Dict, Optional
@@ -74,10 +75,12 @@ class LayerNorm:
 MASK_FILL = -1e9
 
 
+@functools.lru_cache(maxsize=8)
 def causal_mask(seq: int) -> np.ndarray:
-    """[seq, seq] additive mask: 0 on and below the diagonal, -1e9 above."""
-    m = np.zeros((seq, seq), np.float32)
-    m[np.triu_indices(seq, 1)] = MASK_FILL
+    """[seq, seq] additive mask: 0 on and below the diagonal, -1e9 above
+    (read-only, shared between calls)."""
+    m = np.triu(np.full((seq, seq), MASK_FILL, np.float32), 1)
+    m.setflags(write=False)
     return m
 
 

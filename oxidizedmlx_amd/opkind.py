@@ -7,6 +7,8 @@ and so on read like the Rust enum. ``to_c()`` packs a value into the
 """
 from __future__ import annotations
 
+import functools
+
 import ctypes as C
 from dataclasses import dataclass, field
 from typing import Optional, Sequence, Tuple
@@ -52,6 +54,11 @@ class Op:
         return KIND[self.name]
 
     def to_c(self) -> Tuple[abi.mlxhip_op_t, list]:
+        """The C form (and the arrays it points into); cached per value, the
+        C side only reads it."""
+        return _op_to_c(self)
+
+    def _build_c(self) -> Tuple[abi.mlxhip_op_t, list]:
         keep: list = []
         s = abi.mlxhip_op_t()
         s.kind = self.kind
@@ -191,12 +198,26 @@ class TensorMeta:
         return n
 
     def to_c(self) -> Tuple[abi.mlxhip_meta_t, list]:
+        """The C form (cached per value, read-only on the C side)."""
+        return _meta_to_c(self)
+
+    def _build_c(self) -> Tuple[abi.mlxhip_meta_t, list]:
         arr = abi.int64_array(self.shape)
         m = abi.mlxhip_meta_t()
         m.shape = C.cast(arr, C.POINTER(C.c_int64))
         m.ndim = len(self.shape)
         m.dtype = self.dtype
         return m, [arr]
+
+
+@functools.lru_cache(maxsize=4096)
+def _op_to_c(op: Op):
+    return op._build_c()
+
+
+@functools.lru_cache(maxsize=4096)
+def _meta_to_c(m: TensorMeta):
+    return m._build_c()
 
 
 def meta(dims: Sequence[int], dtype: int = abi.F32) -> TensorMeta:
