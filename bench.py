@@ -68,6 +68,21 @@ def cpu_baseline(target_s: float) -> dict:
     return out
 
 
+def cpu_decode_baseline(cfg, params, batch: int) -> dict:
+    """The oracle's decoder (mlx-nn layers over the oracle stream, C kernels,
+    1 thread) on a bounded sample: position 0 of `batch` sequences (one
+    decode step without cache reads; parameter upload excluded)."""
+    from oracle.graph import OracleStream
+    from oxidizedmlx_amd import nn as mnn
+    tok = np.random.default_rng(0x5EED0201).integers(0, cfg.vocab, size=(batch, 1))
+    model = mnn.DecoderLM(cfg, OracleStream(), params)
+    t0 = time.perf_counter()
+    model(tok).to_numpy()
+    dt = time.perf_counter() - t0
+    return {"tokens_per_s": batch / dt, "seconds": dt,
+            "sample": f"one decode position of {batch} sequences"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -77,6 +92,8 @@ def main() -> int:
                     help="bounded CPU-baseline sample of the GEMM (seconds)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma list of kernels to time (profiling)")
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="launch the decode step's kernels one by one instead of replaying its HIP graph")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -155,6 +172,21 @@ def main() -> int:
         st.eval_many([g.node for g in grads])
         st.close()
 
+    # Config 5: greedy decoding with a 12-layer decoder (d_model 768, 12
+    # heads, vocab 32000, 4x SiLU MLP), bf16 weights N(0, 0.02^2), batch 8,
+    # prompt of 16 uniform-random ids, 128 new tokens. One step = one whole
+    # generate (143 positions, prompt included), timed by the decoder's own
+    # HIP events around its position loop.
+    dcfg = mnn.DecoderConfig()
+    d_batch, d_prompt, d_new = 8, 16, 128
+    dec = dparams = None
+    if want("decode_cfg5"):
+        log("bench: decoder parameters")
+        dparams = mnn.decoder_params(dcfg, 0x5EED0200)
+        dec = hb.HipDecoder(dcfg)
+        dec.load(dparams)
+        dprompt = np.random.default_rng(0x5EED0201).integers(0, dcfg.vocab, size=(d_batch, d_prompt))
+
     kernels = {
         "gemm_bf16_4096": dict(flops=2.0 * n * n * n, bytes=3 * n * n * 2),
         # Calibration only (never part of a step): a plain 64 MiB copy whose HBM
@@ -175,12 +207,18 @@ def main() -> int:
         # autograd and every kernel), not by events.
         "transformer_block_fwd_bwd_cfg4": dict(flops=3.0 * bcfg.forward_flops(), bytes=0, peak=157.3,
                                                wall=True),
+        "decode_cfg5": dict(bytes=dcfg.decode_bytes(d_batch, d_prompt, d_new), decoder=True),
     }
     chain = [("mul", 1), ("add", 2), ("silu", 0)]
 
+    dec_ms = []
+
     def launch(name: str, i: int) -> None:
         j = i % SETS
-        if name == "transformer_block_fwd_bwd_cfg4":
+        if name == "decode_cfg5":
+            dec.generate(dprompt, d_new, eager=args.decode_eager)
+            dec_ms.append(dec.last_timing()[0])
+        elif name == "transformer_block_fwd_bwd_cfg4":
             block_step()
         elif name == "gemm_bf16_4096":
             hb.gemm(abi.BF16, abi.BF16, False, False, n, n, n, dA[j], n, dB[j], n, dC[j], n, stream=stream)
@@ -219,6 +257,11 @@ def main() -> int:
     t0 = time.perf_counter()
     wall_ms = {}
     for k in names:
+        if kernels[k].get("decoder"):
+            dec_ms.clear()
+            for i in range(args.steps):
+                launch(k, i)
+            continue
         if kernels[k].get("wall"):
             hb.synchronize(None)
             w0 = time.perf_counter()
@@ -237,7 +280,9 @@ def main() -> int:
 
     res = {}
     for k in names:
-        if k in wall_ms:
+        if kernels[k].get("decoder"):
+            ms = sum(dec_ms) / len(dec_ms)
+        elif k in wall_ms:
             ms = wall_ms[k] / args.steps
         else:
             e0, e1 = ev[k]
@@ -249,6 +294,9 @@ def main() -> int:
         if kernels[k]["bytes"]:
             r["gbs"] = kernels[k]["bytes"] / (ms * 1e-3) / 1e9
             r["frac_hbm_peak"] = r["gbs"] / HBM_PEAK_GBS
+        if kernels[k].get("decoder"):
+            r["tokens_per_s"] = d_batch * d_new / (ms * 1e-3)
+            r["us_per_position"] = ms * 1e3 / (d_prompt + d_new - 1)
         res[k] = r
         log(f"bench: {k}: {json.dumps(r)}")
     step_kernels = ("gemm_bf16_4096", "softmax_4096x4096", "layernorm_4096x4096", "rmsnorm_4096x4096",
@@ -267,6 +315,8 @@ def main() -> int:
                        f"1 core of {os.cpu_count()}"),
             "kernels": {k: v for k, v in cb.items() if k != "gemm"},
         }
+        if dparams is not None:
+            cpu["kernels"]["decode_cfg5"] = cpu_decode_baseline(dcfg, dparams, d_batch)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")

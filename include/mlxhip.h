@@ -345,6 +345,82 @@ int mlxhip_transpose2d(const float* x, float* y, int64_t rows, int64_t cols, voi
 int mlxhip_cast(const void* x, int32_t src_dtype, void* y, int32_t dst_dtype,
                 int64_t n, void* stream);
 
+/* ── Greedy decoding of a decoder-only language model ───────────────────────
+ * The token loop of crates/mlx-conformance/tests/ttft_behavior.rs:101-216
+ * (project the new token, append K/V to the cache, attend over the cache)
+ * for a model built from mlx-nn layers: Embedding (crates/mlx-nn/src/embed.rs),
+ * n_layers pre-norm blocks h = x + attn(rms_norm(x)), y = h + W2 silu(W1
+ * rms_norm(h) + b1) + b2 with Linear (linear.rs:34-43: y = x W^T + b) Q/K/V/O
+ * projections and n_heads heads of d_model/n_heads, a final RmsNorm and an
+ * LM-head Linear without bias, then argmax (host-side in the reference).
+ * Parameters are held in HBM as bf16 (round to nearest even of the given f32
+ * values); activations, the KV cache and accumulation are f32. The reference
+ * keeps the KV cache in host vectors and re-uploads it every step; here the
+ * cache, the token history and the argmax stay on the device and one step is
+ * replayed as a HIP graph. Prompt tokens are consumed one position per step.
+ * Requirements: max_batch <= 8, d_model and hidden multiples of 32,
+ * head_dim (d_model / n_heads) one of 8, 16, 32, 64, 128, 256. The captured
+ * graph of a (batch, prompt_len[, positions with logits]) shape is kept for
+ * later calls of the same shape. */
+typedef struct {
+    int32_t n_layers;
+    int32_t d_model;
+    int32_t n_heads;
+    int32_t hidden;      /* MLP width */
+    int32_t vocab;
+    int32_t max_batch;   /* sequences per call, <= 8 */
+    int32_t max_seq;     /* KV-cache positions: prompt_len + n_new - 1 <= max_seq */
+    float eps;           /* RmsNorm eps */
+} mlxhip_decoder_config_t;
+
+typedef enum {
+    MLXHIP_DEC_EMBEDDING = 0, /* [vocab, d_model] (layer ignored) */
+    MLXHIP_DEC_LM_HEAD = 1,   /* [vocab, d_model] (layer ignored) */
+    MLXHIP_DEC_WQ = 2,        /* [d_model, d_model], Linear weight [out, in] */
+    MLXHIP_DEC_BQ = 3,        /* [d_model] */
+    MLXHIP_DEC_WK = 4,
+    MLXHIP_DEC_BK = 5,
+    MLXHIP_DEC_WV = 6,
+    MLXHIP_DEC_BV = 7,
+    MLXHIP_DEC_WO = 8,
+    MLXHIP_DEC_BO = 9,
+    MLXHIP_DEC_W1 = 10,       /* [hidden, d_model] */
+    MLXHIP_DEC_B1 = 11,       /* [hidden] */
+    MLXHIP_DEC_W2 = 12,       /* [d_model, hidden] */
+    MLXHIP_DEC_B2 = 13        /* [d_model] */
+} mlxhip_decoder_param_t;
+
+/* generate() flag: launch the step's kernels one by one instead of replaying
+ * a captured HIP graph (same results bit for bit). */
+#define MLXHIP_DEC_EAGER 1
+
+typedef struct mlxhip_decoder_t mlxhip_decoder_t;
+
+/* Allocates the model's parameters, KV cache and step state in HBM of the
+ * current device. NULL on failure (invalid config: MLXHIP_ERR_INVALID_ARGUMENT,
+ * checked before the device; no GPU: MLXHIP_ERR_BACKEND_UNAVAILABLE). */
+mlxhip_decoder_t* mlxhip_decoder_new(const mlxhip_decoder_config_t* cfg);
+void mlxhip_decoder_free(mlxhip_decoder_t* dec);
+/* Loads one parameter from `len` row-major f32 host values (rounded to bf16).
+ * `layer` selects the block for the per-layer parameters. */
+int mlxhip_decoder_set_param(mlxhip_decoder_t* dec, int32_t layer, int32_t which,
+                             const float* values, size_t len);
+/* Greedy generation for `batch` sequences: prompt [batch, prompt_len] token
+ * ids (clamped to [0, vocab-1] as embedding_lookup does,
+ * crates/mlx-core/src/cpu_kernels.rs:317-336); tokens_out [batch, n_new]
+ * receives the argmax tokens after positions prompt_len-1 .. prompt_len+n_new-2
+ * (equal logits resolve to the lowest id). Optional outputs (NULL to skip),
+ * with S = prompt_len + n_new - 1 positions: argmax_out [batch, S], the argmax
+ * after every position; logits_out [batch, S, vocab]. Synchronous. */
+int mlxhip_decoder_generate(mlxhip_decoder_t* dec, const int32_t* prompt, int32_t batch,
+                            int32_t prompt_len, int32_t n_new, int32_t* tokens_out,
+                            int32_t* argmax_out, float* logits_out, int32_t flags);
+/* Device time (HIP events on the decoder's stream) of the last generate's
+ * S positions, and S. */
+int mlxhip_decoder_last_timing(const mlxhip_decoder_t* dec, float* ms, int32_t* steps);
+/* Bytes of bf16 parameters held in HBM (0 for NULL). */
+size_t mlxhip_decoder_weight_bytes(const mlxhip_decoder_t* dec);
+
 /* ── Timing (HIP events, for benchmarks) ─────────────────────────────────── */
 
 typedef struct mlxhip_event_t mlxhip_event_t;

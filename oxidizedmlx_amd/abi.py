@@ -118,6 +118,25 @@ class mlxhip_ew_instr_t(C.Structure):
     _fields_ = [("op", C.c_int32), ("operand", C.c_int32)]
 
 
+class mlxhip_decoder_config_t(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int32),
+        ("d_model", C.c_int32),
+        ("n_heads", C.c_int32),
+        ("hidden", C.c_int32),
+        ("vocab", C.c_int32),
+        ("max_batch", C.c_int32),
+        ("max_seq", C.c_int32),
+        ("eps", C.c_float),
+    ]
+
+
+# mlxhip_decoder_param_t
+DEC_EMBEDDING, DEC_LM_HEAD = 0, 1
+DEC_LAYER_PARAMS = {"wq": 2, "bq": 3, "wk": 4, "bk": 5, "wv": 6, "bv": 7,
+                    "wo": 8, "bo": 9, "w1": 10, "b1": 11, "w2": 12, "b2": 13}
+DEC_EAGER = 1
+
 EW_MAX_INSTR = 16
 EW_MAX_INPUTS = 8
 
@@ -175,6 +194,12 @@ PROTOTYPES = {
                              _fp, _i64, _vp]),
     "mlxhip_transpose2d": (_i, [_fp, _fp, _i64, _i64, _vp]),
     "mlxhip_cast": (_i, [_vp, _i32, _vp, _i32, _i64, _vp]),
+    "mlxhip_decoder_new": (_vp, [C.POINTER(mlxhip_decoder_config_t)]),
+    "mlxhip_decoder_free": (None, [_vp]),
+    "mlxhip_decoder_set_param": (_i, [_vp, _i32, _i32, _fp, _sz]),
+    "mlxhip_decoder_generate": (_i, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _fp, _i32]),
+    "mlxhip_decoder_last_timing": (_i, [_vp, C.POINTER(_f), C.POINTER(_i32)]),
+    "mlxhip_decoder_weight_bytes": (_sz, [_vp]),
     "mlxhip_event_create": (_vp, []),
     "mlxhip_event_destroy": (None, [_vp]),
     "mlxhip_event_record": (_i, [_vp, _vp]),

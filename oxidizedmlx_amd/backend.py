@@ -300,3 +300,74 @@ def create_stream() -> int:
 
 def destroy_stream(s: int) -> None:
     lib().mlxhip_stream_destroy_hip(s)
+
+
+class HipDecoder:
+    """Greedy decoder of a decoder-only model built from mlx-nn layers, with
+    bf16 parameters, the KV cache and the token loop resident in HBM
+    (``mlxhip_decoder_*``). ``cfg`` is an ``nn.DecoderConfig``."""
+
+    def __init__(self, cfg):
+        L = lib()
+        self._L = L
+        self.cfg = cfg
+        c = abi.mlxhip_decoder_config_t(cfg.n_layers, cfg.d_model, cfg.n_heads, cfg.hidden, cfg.vocab,
+                                        cfg.max_batch, cfg.max_seq, cfg.eps)
+        self._d = L.mlxhip_decoder_new(C.byref(c))
+        if not self._d:
+            raise abi.error_for(L.mlxhip_last_status(), L.mlxhip_last_error().decode())
+
+    def close(self) -> None:
+        if getattr(self, "_d", None):
+            self._L.mlxhip_decoder_free(self._d)
+            self._d = None
+
+    def __del__(self):
+        self.close()
+
+    def set_param(self, layer: int, which: int, values: np.ndarray) -> None:
+        v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+        abi.check(self._L.mlxhip_decoder_set_param(self._d, layer, which, v.ctypes.data, v.size), self._L)
+
+    def load(self, params: dict) -> None:
+        """``params`` as made by ``nn.decoder_params``."""
+        self.set_param(0, abi.DEC_EMBEDDING, params["embedding"])
+        self.set_param(0, abi.DEC_LM_HEAD, params["lm_head"])
+        for l, lp in enumerate(params["layers"]):
+            for name, which in abi.DEC_LAYER_PARAMS.items():
+                self.set_param(l, which, lp[name])
+
+    def generate(self, prompt: np.ndarray, n_new: int, *, argmax: bool = False, logits: bool = False,
+                 eager: bool = False):
+        """prompt [batch, prompt_len] int token ids -> tokens [batch, n_new];
+        with ``argmax``/``logits`` also the argmax [batch, S] and the logits
+        [batch, S, vocab] after each of the S = prompt_len + n_new - 1
+        positions (returned as a tuple)."""
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        if p.ndim != 2:
+            raise abi.InvalidArgument(f"prompt must be [batch, prompt_len], got shape {list(p.shape)}")
+        b, t = p.shape
+        steps = t + n_new - 1
+        toks = np.zeros((b, max(n_new, 1)), np.int32)
+        am = np.zeros((b, max(steps, 1)), np.int32) if argmax else None
+        lg = np.zeros((b, max(steps, 1), self.cfg.vocab), np.float32) if logits else None
+        rc = self._L.mlxhip_decoder_generate(
+            self._d, p.ctypes.data, b, t, n_new, toks.ctypes.data,
+            am.ctypes.data if am is not None else None, lg.ctypes.data if lg is not None else None,
+            abi.DEC_EAGER if eager else 0)
+        abi.check(rc, self._L)
+        out = [toks]
+        if argmax:
+            out.append(am)
+        if logits:
+            out.append(lg)
+        return out[0] if len(out) == 1 else tuple(out)
+
+    def last_timing(self) -> tuple[float, int]:
+        """(device milliseconds, positions) of the last generate."""
+        ms, steps = C.c_float(), C.c_int32()
+        abi.check(self._L.mlxhip_decoder_last_timing(self._d, C.byref(ms), C.byref(steps)), self._L)
+        return ms.value, steps.value
+
+    def weight_bytes(self) -> int:
+        return self._L.mlxhip_decoder_weight_bytes(self._d)

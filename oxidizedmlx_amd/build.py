@@ -29,6 +29,7 @@ SOURCES = [
     "backend.cpp",
     "stream.cpp",
     "autograd.cpp",
+    "decoder.cpp",
     "kernels/rows.hip",
     "kernels/elementwise.hip",
     "kernels/gemm.hip",
@@ -37,6 +38,7 @@ SOURCES = [
     "kernels/gemm_f32.hip",
     "kernels/gemm16_bf16.hip",
     "kernels/gemm16_f16.hip",
+    "kernels/decode.hip",
 ]
 
 

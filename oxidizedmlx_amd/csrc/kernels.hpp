@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <cstdint>
 
 #include "../../include/mlxhip.h"
@@ -66,6 +67,49 @@ int rope_interleaved(const float* x, float* y, int64_t tokens, int64_t head_dim,
 int rope_mlx(const float* x, float* y, int64_t n_rows, int64_t head_dim, int64_t offset,
              float base, int traditional, hipStream_t s);
 int fill(float* y, float v, int64_t n, hipStream_t s);
+
+// ── decode.hip (greedy decode step of a decoder-only model) ───────────────
+constexpr int DEC_MAX_BATCH = 8;          // sequences per decode step
+constexpr int DEC_LDS_LIMIT = 159 * 1024; // dynamic LDS (a CDNA4 CU has 160 KiB; 1 KiB kept for static LDS)
+enum DecEpilogue {
+    DEC_EPI_STORE = 0,   // out[b][n] = y
+    DEC_EPI_QKV = 1,     // q -> out, k / v -> KV cache at position t
+    DEC_EPI_RESID = 2,   // out[b][n] += y (residual stream)
+    DEC_EPI_SILU = 3,    // out[b][n] = silu(y)
+    DEC_EPI_ARGMAX = 4,  // logits history (optional) + per-workgroup argmax keys
+};
+// Y[b][n] = sum_k X[b][k] W[n][k] (+ bias[n]), W bf16 [N, ldw], X f32 [B, ldx].
+struct DecGemv {
+    const uint16_t* w = nullptr;
+    int64_t ldw = 0;
+    const uint16_t* bias = nullptr;  // bf16 [N] or null
+    const float* x = nullptr;
+    int64_t ldx = 0;
+    float eps = 0.0f;                // RMS-norm eps of the prologue
+    int n = 0, k = 0, batch = 0;
+    float* out = nullptr;            // STORE/SILU/RESID: [B, ldo]; QKV: q [B, ldo];
+    int64_t ldo = 0;                 // ARGMAX: logits[b*ldo + t*n + n'] (may be null)
+    float* kc = nullptr;             // QKV: K^T cache [B][H][hd][tmax]
+    float* vc = nullptr;             // QKV: V cache   [B][H][tmax][hd]
+    int dmodel = 0, heads = 0, head_dim = 0, tmax = 0;
+    const int* tctr = nullptr;       // device step counter (position t)
+    uint64_t* part = nullptr;        // ARGMAX: [groups][DEC_MAX_BATCH] per-workgroup maxima
+    int part_capacity = 0;
+};
+int dec_prepare();
+int dec_gemv(int epi, bool norm, const DecGemv& p, hipStream_t s);
+int dec_gemv_groups(int n, int k);
+size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax);
+size_t dec_attn_lds_bytes(int hd, int tmax);
+int dec_attention(const float* q, const float* kc, const float* vc, float* o, int batch, int heads, int hd,
+                  int tmax, float scale, const int* tctr, hipStream_t s);
+int dec_embed(const uint16_t* emb, const int* tokens, float* x, int d, int vocab, int batch, const int* tctr,
+              hipStream_t s);
+// argmax over the LM head's partial maxima, next token (prompt or argmax),
+// its embedding into x [batch][d], t += 1.
+int dec_finish(const uint64_t* part, int groups, int* tokens, int* argmax_out, const uint16_t* emb, float* x,
+               int d, int vocab, int batch, int prompt_len, int* tctr, hipStream_t s);
+int dec_set_counter(int* p, int v, hipStream_t s);
 
 // ── gemm.hip ──────────────────────────────────────────────────────────────
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,

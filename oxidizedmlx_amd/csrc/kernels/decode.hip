@@ -1,0 +1,615 @@
+// decode.hip — the kernels of one greedy decode step of a decoder-only
+// language model whose weights live in HBM as bf16 and whose activations and
+// KV cache are f32 (the caller is csrc/decoder.cpp).
+//
+// One step for a batch of B <= 8 sequences at position t (t is read from a
+// device counter, so one captured HIP graph serves every step), starting
+// from x[b] = f32(E[token[t][b]]) (embedding_lookup,
+// crates/mlx-core/src/cpu_kernels.rs:317-336: index clamped to [0, vocab-1]):
+//   per layer:
+//     gemv<QKV,norm> [q|k|v] = rms_norm(x)·Wqkv^T + b; k, v stored into the
+//                    layer's KV cache at position t
+//     decode_attn    o = softmax(q·K^T·scale)·V over positions 0..t, per
+//                    (sequence, head) (cpu_attention, cpu_kernels.rs:738-812
+//                    with Tq = 1, i.e. the decode loop of
+//                    crates/mlx-conformance/tests/ttft_behavior.rs:101-216)
+//     gemv<RESID>    x = x + (o·Wo^T + bo)
+//     gemv<SILU,norm> u = silu(rms_norm(x)·W1^T + b1)
+//     gemv<RESID>    x = x + (u·W2^T + b2)
+//   gemv<ARGMAX,norm> logits = rms_norm(x)·Wlm^T, per-workgroup maxima
+//   decode_finish    argmax, next token, its embedding into x, t += 1
+// (decode_embed writes x for position 0 before the first step.)
+//
+// The GEMV (Y[B,N] = X[B,K]·W[N,K]^T) is HBM-bound on W. It runs on MFMA
+// (v_mfma_f32_16x16x32_bf16) without rounding the f32 activations to bf16:
+// each activation is split into three bf16 terms x = hi + mid + lo (each term
+// the round-to-nearest-even bf16 of what the previous ones left; the
+// differences are exact in f32), so hi/mid/lo carry 24 significant bits
+// between them and bf16·bf16 products are exact in the f32 accumulator. The
+// 24 columns [hi b0..7 | mid b0..7 | lo b0..7] fill two 16-column MFMA tiles
+// (the last 8 columns are zero) and y = hi + (mid + lo) per (row, b).
+#include <algorithm>
+
+#include "../common.hpp"
+#include "../kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace mlxhip {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+constexpr int KSTEP = 32;                 // k per MFMA
+constexpr int KPASS = 256;                // k per wave per pass
+constexpr int NSTEP = KPASS / KSTEP;      // MFMA steps per pass
+constexpr int XPAD = 8;                   // bf16 padding of each LDS row
+constexpr int XROWS = 3 * DEC_MAX_BATCH;  // hi, mid, lo rows of the batch
+constexpr int TILE_N = 16;                // output features per wave tile
+constexpr int MAX_WAVES = 16;
+
+__device__ inline uint32_t bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__device__ inline float bf16_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+__device__ inline uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
+        const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
+        const uint64_t w = ((uint64_t)hi << 32) | lo;
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// Sums v[b] over the 64 lanes for each of 8 rows in 10 cross-lane steps
+// (halving the rows held per lane at each of the first three): returns the
+// total of row 4*bit5 + 2*bit4 + bit3 of the lane id. Fixed order, so the
+// result is deterministic.
+__device__ inline float wave_sum8(const float (&v)[8], int lane) {
+    float a[4], c[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool hi = lane & 32;
+        const float send = hi ? v[i] : v[i + 4];
+        a[i] = (hi ? v[i + 4] : v[i]) + __shfl_xor(send, 32, WAVE);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const bool hi = lane & 16;
+        const float send = hi ? a[i] : a[i + 2];
+        c[i] = (hi ? a[i + 2] : a[i]) + __shfl_xor(send, 16, WAVE);
+    }
+    const bool hi = lane & 8;
+    float r = (hi ? c[1] : c[0]) + __shfl_xor(hi ? c[0] : c[1], 8, WAVE);
+#pragma unroll
+    for (int o = 4; o > 0; o >>= 1) r += __shfl_xor(r, o, WAVE);
+    return r;
+}
+__device__ inline int wave_sum8_row(int lane) { return ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1); }
+
+// x / d as the correctly rounded quotient from r = 1/d (correctly rounded):
+// q = x*r, then one exact-remainder correction (Markstein).
+__device__ inline float div_by(float x, float d, float r) {
+    const float q = x * r;
+    return __builtin_fmaf(__builtin_fmaf(-q, d, x), r, q);
+}
+
+// Total order of finite floats as unsigned integers, larger value = larger key.
+__device__ inline uint32_t order_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ inline float sigmoid_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ── the split-activation GEMV ──────────────────────────────────────────────
+//
+// Workgroup = R row tiles x KS k-slices, one wave each (R*KS <= 16). Wave
+// (r, s) computes the 16 output features of tile blockIdx.x*R + r over k in
+// [s*kw, (s+1)*kw). Partials of the KS slices are summed in slice order
+// (deterministic).
+//
+// The kernel is latency-bound at decode sizes (a few MB per launch), so every
+// global load whose address does not depend on this kernel's own results is
+// issued at the start, before the first wait: the step position, the
+// epilogue's bias and residual values, the W fragments and the X rows (thread
+// c holds float4 column c of all 8 rows, since 64*KS >= K/4). The launch then
+// costs about one memory round trip plus the MFMAs.
+//
+// ARGMAX (the LM head) publishes each workgroup's per-sequence maximum key
+// for decode_finish.
+template <int EPI, bool NORM>
+__global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks, int r_tiles, int kw) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int K = p.k, N = p.n, B = p.batch;
+    const int pitch = K + XPAD;
+    constexpr int TB = TILE_N * DEC_MAX_BATCH;  // outputs of one row tile
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+    float* red = reinterpret_cast<float*>(smem + (size_t)XROWS * pitch * 2);
+    float* wss = red + r_tiles * ks * TB;                                 // [MAX_WAVES][8]
+    uint64_t* keys = reinterpret_cast<uint64_t*>(wss + MAX_WAVES * DEC_MAX_BATCH);  // [r_tiles * TB]
+
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int wave = tid / WAVE, lane = tid % WAVE;
+    const int nwaves = nthr / WAVE;
+    const int ksl = wave % ks, rl = wave / ks;
+    const int n0 = (blockIdx.x * r_tiles + rl) * TILE_N;
+    const int kb = ksl * kw;
+    const int ke = min(K, kb + kw);
+    const bool active = n0 < N && kb < K;
+    const int nitems = r_tiles * TB;
+
+    // ── loads issued up front ───────────────────────────────────────────────
+    const int t = p.tctr ? *p.tctr : 0;
+    float pre_bias[2] = {0.0f, 0.0f}, pre_res[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int i = tid + e * nthr;
+        if (i < nitems) {
+            const int rr = i / TB, row = (i % TB) / DEC_MAX_BATCH, b = i % DEC_MAX_BATCH;
+            const int n = (blockIdx.x * r_tiles + rr) * TILE_N + row;
+            if (n < N && b < B) {
+                if (p.bias) pre_bias[e] = bf16_f32(p.bias[n]);
+                if constexpr (EPI == DEC_EPI_RESID) pre_res[e] = p.out[(int64_t)b * p.ldo + n];
+            }
+        }
+    }
+    // Lane l reads 8 consecutive k of feature n0 + l%16 (MFMA A-operand layout:
+    // row l%16, k block l/16). Rows past N read row N-1 (discarded).
+    const int frow = min(n0 + (lane & 15), N - 1);
+    const uint16_t* wp = p.w + (int64_t)frow * p.ldw + 8 * (lane >> 4);
+    u32x4 a[NSTEP];
+    auto load_pass = [&](int k0) {
+        const int steps = active ? min(NSTEP, (ke - k0) / KSTEP) : 0;
+#pragma unroll
+        for (int s = 0; s < NSTEP; ++s)
+            if (s < steps) a[s] = *reinterpret_cast<const u32x4*>(wp + k0 + s * KSTEP);
+    };
+    load_pass(kb);
+    const int k4 = K / 4;
+    const bool xc = tid < k4;
+    float4 xv[DEC_MAX_BATCH];
+#pragma unroll
+    for (int b = 0; b < DEC_MAX_BATCH; ++b) {
+        xv[b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (xc && b < B) xv[b] = *reinterpret_cast<const float4*>(p.x + (int64_t)b * p.ldx + 4 * tid);
+    }
+
+    // ── prologue: X (optionally RMS-normalised) split into hi/mid/lo bf16 rows
+    if constexpr (NORM) {
+        // rms_norm, cpu_kernels.rs:647-669: sqrt(sum(x*x)/d + eps), y = x / rms.
+        float ss[DEC_MAX_BATCH];
+#pragma unroll
+        for (int b = 0; b < DEC_MAX_BATCH; ++b) {
+            const float4 v = xv[b];
+            ss[b] = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        const float tot = wave_sum8(ss, lane);
+        if ((lane & 7) == 0) wss[wave * DEC_MAX_BATCH + wave_sum8_row(lane)] = tot;
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < DEC_MAX_BATCH; ++b) {
+            float sb = wss[b];
+            for (int w = 1; w < nwaves; ++w) sb += wss[w * DEC_MAX_BATCH + b];
+            float rms = sqrtf(sb / (float)K + p.eps), r = 1.0f / rms;
+            if (__builtin_isinf(rms)) {  // x / inf, as division gives it
+                rms = 1.0f;
+                r = 0.0f;
+            }
+            xv[b].x = div_by(xv[b].x, rms, r);
+            xv[b].y = div_by(xv[b].y, rms, r);
+            xv[b].z = div_by(xv[b].z, rms, r);
+            xv[b].w = div_by(xv[b].w, rms, r);
+        }
+    }
+    if (xc) {
+#pragma unroll
+        for (int b = 0; b < DEC_MAX_BATCH; ++b) {
+            const float v[4] = {xv[b].x, xv[b].y, xv[b].z, xv[b].w};
+            uint32_t h[4], m[4], l[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                h[j] = bf16_rne(v[j]);
+                const float r1 = v[j] - bf16_f32(h[j]);
+                m[j] = bf16_rne(r1);
+                const float r2 = r1 - bf16_f32(m[j]);
+                l[j] = bf16_rne(r2);
+            }
+            const int k = 4 * tid;
+            *reinterpret_cast<uint2*>(xs + (0 * DEC_MAX_BATCH + b) * pitch + k) =
+                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            *reinterpret_cast<uint2*>(xs + (1 * DEC_MAX_BATCH + b) * pitch + k) =
+                make_uint2(m[0] | (m[1] << 16), m[2] | (m[3] << 16));
+            *reinterpret_cast<uint2*>(xs + (2 * DEC_MAX_BATCH + b) * pitch + k) =
+                make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+        }
+    }
+    __syncthreads();
+
+    // ── main loop: 2 MFMAs per 16 features x 32 k ───────────────────────────
+    // B operand (X columns): lane l holds column l%16, k block l/16. Tile 0
+    // columns are hi(b0..7), mid(b0..7); tile 1 columns are lo(b0..7), zero.
+    const int col = lane & 15, kg = lane >> 4;
+    const uint16_t* x0 = xs + col * pitch + 8 * kg;
+    const uint16_t* x1 = xs + (2 * DEC_MAX_BATCH + (col & 7)) * pitch + 8 * kg;
+    const bool zero1 = col >= 8;
+    f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = kb; k0 < ke; k0 += KPASS) {
+        if (k0 != kb) load_pass(k0);
+        const int steps = active ? min(NSTEP, (ke - k0) / KSTEP) : 0;
+#pragma unroll
+        for (int s = 0; s < NSTEP; ++s) {
+            if (s < steps) {
+                const int ko = k0 + s * KSTEP;
+                const u32x4 b0 = *reinterpret_cast<const u32x4*>(x0 + ko);
+                u32x4 b1 = {0u, 0u, 0u, 0u};
+                if (!zero1) b1 = *reinterpret_cast<const u32x4*>(x1 + ko);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[s]),
+                                                               __builtin_bit_cast(bf16x8, b0), acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[s]),
+                                                               __builtin_bit_cast(bf16x8, b1), acc1, 0, 0, 0);
+            }
+        }
+    }
+
+    // D layout: lane l holds column l%16 and features 4*(l/16) + j, j < 4.
+    // Column c < 8 of tile 0 is hi of sequence c, column c+8 its mid; column c
+    // of tile 1 its lo.
+    float* myred = red + (rl * ks + ksl) * TB;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float mid = __shfl_xor(acc0[j], 8, WAVE);
+        const float v = acc0[j] + (mid + acc1[j]);
+        if (col < 8) myred[(4 * kg + j) * DEC_MAX_BATCH + col] = v;
+    }
+    __syncthreads();
+
+    // ── epilogue: sum the k-slices in order, bias, then the op ─────────────
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int i = tid + e * nthr;
+        if (i >= nitems) continue;
+        const int rr = i / TB, ei = i % TB;
+        const int row = ei / DEC_MAX_BATCH, b = ei % DEC_MAX_BATCH;
+        const int n = (blockIdx.x * r_tiles + rr) * TILE_N + row;
+        float v = red[(rr * ks) * TB + ei];
+        for (int s = 1; s < ks; ++s) v += red[(rr * ks + s) * TB + ei];
+        const bool valid = n < N && b < B;
+        if (p.bias) v = v + pre_bias[e];
+        if constexpr (EPI == DEC_EPI_STORE) {
+            if (valid) p.out[(int64_t)b * p.ldo + n] = v;
+        } else if constexpr (EPI == DEC_EPI_SILU) {
+            if (valid) p.out[(int64_t)b * p.ldo + n] = v * sigmoid_ref(v);
+        } else if constexpr (EPI == DEC_EPI_RESID) {
+            if (valid) p.out[(int64_t)b * p.ldo + n] = pre_res[e] + v;
+        } else if constexpr (EPI == DEC_EPI_QKV) {
+            if (valid) {
+                const int d = p.dmodel, seg = n / d, nn = n - seg * d;
+                const int h = nn / p.head_dim, dd = nn - h * p.head_dim;
+                const int64_t bh = (int64_t)b * p.heads + h;
+                if (seg == 0)
+                    p.out[(int64_t)b * p.ldo + nn] = v;
+                else if (seg == 1)
+                    p.kc[(bh * p.head_dim + dd) * p.tmax + t] = v;  // K^T: [b][h][dd][pos]
+                else
+                    p.vc[(bh * p.tmax + t) * p.head_dim + dd] = v;  // V:   [b][h][pos][dd]
+            }
+        } else {  // DEC_EPI_ARGMAX
+            if (valid && p.out) p.out[(int64_t)b * p.ldo + (int64_t)t * N + n] = v;
+            keys[i] = valid ? ((uint64_t)order_key(v) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)n) : 0ull;
+        }
+    }
+    if constexpr (EPI == DEC_EPI_ARGMAX) {
+        __syncthreads();
+        if (tid < DEC_MAX_BATCH) {
+            uint64_t m = 0;
+            for (int i = tid; i < nitems; i += DEC_MAX_BATCH) m = keys[i] > m ? keys[i] : m;
+            p.part[(int64_t)blockIdx.x * DEC_MAX_BATCH + tid] = m;
+        }
+    }
+}
+
+// ── end of the step: argmax, next token and its embedding, t += 1 ──────────
+// One workgroup; wave b reduces sequence b's per-workgroup maxima (equal
+// logits resolve to the lowest index: the key's low word is 0xFFFFFFFF -
+// index). The next token is the prompt's while t+1 < prompt_len, else the
+// argmax; its embedding row becomes the residual stream x of the next step.
+constexpr int FIN_BLOCK = DEC_MAX_BATCH * WAVE;
+
+__global__ __launch_bounds__(FIN_BLOCK) void decode_finish_kernel(
+    const uint64_t* __restrict__ part, int groups, int* __restrict__ tokens, int* __restrict__ argmax_out,
+    const uint16_t* __restrict__ emb, float* __restrict__ x, int d, int vocab, int batch, int prompt_len,
+    int* __restrict__ tctr) {
+    __shared__ int s_tok[DEC_MAX_BATCH];
+    const int t = *tctr;
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (wave < batch) {
+        uint64_t m = 0;
+        for (int g = lane; g < groups; g += WAVE) {
+            const uint64_t k = part[(int64_t)g * DEC_MAX_BATCH + wave];
+            m = k > m ? k : m;
+        }
+        m = wave_max_u64(m);
+        if (lane == 0) {
+            const int idx = (int)(0xFFFFFFFFu - (uint32_t)m);
+            argmax_out[(int64_t)t * batch + wave] = idx;
+            int next = idx;
+            if (t + 1 < prompt_len)
+                next = tokens[(int64_t)(t + 1) * batch + wave];
+            else
+                tokens[(int64_t)(t + 1) * batch + wave] = idx;
+            s_tok[wave] = next < 0 ? 0 : (next > vocab - 1 ? vocab - 1 : next);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < batch * d; i += FIN_BLOCK) {
+        const int b = i / d, k = i - b * d;
+        x[(int64_t)b * d + k] = bf16_f32(emb[(int64_t)s_tok[b] * d + k]);
+    }
+    if (threadIdx.x == 0) *tctr = t + 1;
+}
+
+// ── attention of one new query per (sequence, head) over the KV cache ────
+//
+// Block = 256 threads for one (b, h). Scores s_j = (q·k_j)·scale summed over
+// the head dimension in order (as cpu_matmul_raw), softmax as
+// cpu_kernels.rs:790-806 (max, exp(x - max), sum, divide), then
+// o = sum_j p_j v_j. The cache is K^T [hd][tmax] (thread j reads column j:
+// consecutive threads, consecutive addresses) and V [tmax][hd] (a thread
+// reads float4s of a row). Every thread issues a whole chunk of its loads
+// before using any of them, so each phase costs about one memory round trip.
+constexpr int ATT_BLOCK = 256;
+constexpr int ATT_PART = 4 * ATT_BLOCK;  // partial sums of the P·V phase
+
+__device__ inline float block_reduce(float v, float* buf, bool is_max) {
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    v = is_max ? wave_max(v) : wave_sum(v);
+    __syncthreads();
+    if (lane == 0) buf[wave] = v;
+    __syncthreads();
+    float r = buf[0];
+#pragma unroll
+    for (int w = 1; w < ATT_BLOCK / WAVE; ++w) r = is_max ? fmaxf(r, buf[w]) : r + buf[w];
+    return r;
+}
+
+template <int HD>
+__global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __restrict__ q,
+                                                                const float* __restrict__ kc,
+                                                                const float* __restrict__ vc,
+                                                                float* __restrict__ o, int heads,
+                                                                int tmax, float scale,
+                                                                const int* __restrict__ tctr) {
+    extern __shared__ __attribute__((aligned(16))) float sm[];
+    float* s = sm;                  // [tmax]
+    float* qs = s + tmax;           // [HD]
+    float* part = qs + HD;          // [ATT_PART]
+    float* buf = part + ATT_PART;   // [ATT_BLOCK / WAVE]
+    const int bh = blockIdx.x, b = bh / heads, h = bh % heads;
+    const int d = heads * HD;
+    const int tid = threadIdx.x;
+    const float* kT = kc + (int64_t)bh * HD * tmax;
+    const float* vv = vc + (int64_t)bh * tmax * HD;
+    const int T = *tctr + 1;
+    for (int i = tid; i < HD; i += ATT_BLOCK) qs[i] = q[(int64_t)b * d + h * HD + i];
+
+    // P·V mapping: thread (c, g) owns columns 4c..4c+3 over positions
+    // j = g (mod G). Its first VCH rows of V are loaded together with K.
+    constexpr int C4 = HD / 4, G = ATT_BLOCK / C4, VCH = 16;
+    const int c = tid % C4, g = tid / C4;
+    float4 vr[VCH];
+#pragma unroll
+    for (int u = 0; u < VCH; ++u) {
+        const int j = g + u * G;
+        vr[u] = j < T ? *reinterpret_cast<const float4*>(vv + (int64_t)j * HD + 4 * c)
+                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    constexpr int KCH = HD < 64 ? HD : 64;  // K loads in flight per thread
+    __syncthreads();                         // qs
+
+    for (int j = tid; j < T; j += ATT_BLOCK) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int d0 = 0; d0 < HD; d0 += KCH) {
+            float kv[KCH];
+#pragma unroll
+            for (int u = 0; u < KCH; ++u) kv[u] = kT[(int64_t)(d0 + u) * tmax + j];
+#pragma unroll
+            for (int u = 0; u < KCH; ++u) acc += qs[d0 + u] * kv[u];
+        }
+        s[j] = acc * scale;
+    }
+    float m = -INFINITY;
+    for (int j = tid; j < T; j += ATT_BLOCK) m = fmaxf(m, s[j]);
+    m = block_reduce(m, buf, true);
+    float sum = 0.0f;
+    for (int j = tid; j < T; j += ATT_BLOCK) {
+        const float e = expf(s[j] - m);
+        s[j] = e;
+        sum += e;
+    }
+    sum = block_reduce(sum, buf, false);
+    for (int j = tid; j < T; j += ATT_BLOCK) s[j] = s[j] / sum;
+    __syncthreads();
+
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int u = 0; u < VCH; ++u) {
+        const int j = g + u * G;
+        const float pj = j < T ? s[j] : 0.0f;
+        acc.x += pj * vr[u].x;
+        acc.y += pj * vr[u].y;
+        acc.z += pj * vr[u].z;
+        acc.w += pj * vr[u].w;
+    }
+    for (int j0 = g + VCH * G; j0 < T; j0 += G * VCH) {
+#pragma unroll
+        for (int u = 0; u < VCH; ++u) {
+            const int j = j0 + u * G;
+            vr[u] = j < T ? *reinterpret_cast<const float4*>(vv + (int64_t)j * HD + 4 * c)
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < VCH; ++u) {
+            const int j = j0 + u * G;
+            const float pj = j < T ? s[j] : 0.0f;
+            acc.x += pj * vr[u].x;
+            acc.y += pj * vr[u].y;
+            acc.z += pj * vr[u].z;
+            acc.w += pj * vr[u].w;
+        }
+    }
+    *reinterpret_cast<float4*>(part + g * HD + 4 * c) = acc;
+    __syncthreads();
+    if (tid < HD) {
+        float r = part[tid];
+        for (int gg = 1; gg < G; ++gg) r += part[gg * HD + tid];
+        o[(int64_t)b * d + h * HD + tid] = r;
+    }
+}
+
+// ── embedding of the step's tokens ────────────────────────────────────────
+__global__ __launch_bounds__(256) void decode_embed_kernel(const uint16_t* __restrict__ emb,
+                                                           const int* __restrict__ tokens,
+                                                           float* __restrict__ x, int d, int vocab,
+                                                           int batch, const int* __restrict__ tctr) {
+    const int b = blockIdx.x;
+    const int t = *tctr;
+    int tok = tokens[(int64_t)t * batch + b];
+    tok = tok < 0 ? 0 : (tok > vocab - 1 ? vocab - 1 : tok);
+    const uint16_t* src = emb + (int64_t)tok * d;
+    for (int k = threadIdx.x; k < d; k += blockDim.x) x[(int64_t)b * d + k] = bf16_f32(src[k]);
+}
+
+__global__ void decode_set_kernel(int* __restrict__ p, int v) { *p = v; }
+
+template <int EPI, bool NORM>
+int launch_gemv(const DecGemv& p, hipStream_t s) {
+    const int ks = std::min(MAX_WAVES, (int)ceil_div(p.k, KPASS));
+    const int kw = (int)ceil_div(ceil_div(p.k, ks), KSTEP) * KSTEP;
+    const int ntiles = (int)ceil_div(p.n, TILE_N);
+    int r = 1;
+    while ((r * 2) * ks <= MAX_WAVES && ceil_div(ntiles, r * 2) >= 256) r *= 2;
+    const int grid = (int)ceil_div(ntiles, r);
+    const size_t lds = dec_gemv_lds_bytes(p.k, ks, r, EPI == DEC_EPI_ARGMAX);
+    if (lds > DEC_LDS_LIMIT)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: K = %d needs %zu bytes of LDS (limit %d)", p.k,
+                    lds, DEC_LDS_LIMIT);
+    if (EPI == DEC_EPI_ARGMAX && grid > p.part_capacity)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: %d workgroups exceed the partial-max buffer (%d)",
+                    grid, p.part_capacity);
+    hipLaunchKernelGGL((gemv_kernel<EPI, NORM>), dim3(grid), dim3(r * ks * WAVE), lds, s, p, ks, r, kw);
+    return launch_check("decode gemv_kernel");
+}
+
+template <int EPI, bool NORM>
+int set_lds_attr() {
+    MLXHIP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<EPI, NORM>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, DEC_LDS_LIMIT));
+    return MLXHIP_OK;
+}
+
+}  // namespace
+
+size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax) {
+    size_t b = (size_t)XROWS * (k + XPAD) * 2;                    // hi/mid/lo rows
+    b += (size_t)r * ks * TILE_N * DEC_MAX_BATCH * sizeof(float);  // k-slice partials
+    b += MAX_WAVES * DEC_MAX_BATCH * sizeof(float);               // per-wave sums of squares
+    if (argmax) b += (size_t)r * TILE_N * DEC_MAX_BATCH * sizeof(uint64_t);
+    return b;
+}
+
+int dec_gemv_groups(int n, int k) {
+    const int ks = std::min(MAX_WAVES, (int)ceil_div(k, KPASS));
+    const int ntiles = (int)ceil_div(n, TILE_N);
+    int r = 1;
+    while ((r * 2) * ks <= MAX_WAVES && ceil_div(ntiles, r * 2) >= 256) r *= 2;
+    return (int)ceil_div(ntiles, r);
+}
+
+int dec_prepare() {
+    MLXHIP_TRY((set_lds_attr<DEC_EPI_QKV, true>()));
+    MLXHIP_TRY((set_lds_attr<DEC_EPI_RESID, false>()));
+    MLXHIP_TRY((set_lds_attr<DEC_EPI_SILU, true>()));
+    MLXHIP_TRY((set_lds_attr<DEC_EPI_ARGMAX, true>()));
+    MLXHIP_TRY((set_lds_attr<DEC_EPI_STORE, false>()));
+    MLXHIP_TRY((set_lds_attr<DEC_EPI_STORE, true>()));
+    return MLXHIP_OK;
+}
+
+int dec_gemv(int epi, bool norm, const DecGemv& p, hipStream_t s) {
+    if (p.k <= 0 || p.k % KSTEP || p.n <= 0 || p.batch <= 0 || p.batch > DEC_MAX_BATCH || p.ldw % 8 ||
+        p.ldx % 4)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: unsupported shape n=%d k=%d batch=%d", p.n, p.k,
+                    p.batch);
+    if (epi == DEC_EPI_QKV && norm) return launch_gemv<DEC_EPI_QKV, true>(p, s);
+    if (epi == DEC_EPI_RESID && !norm) return launch_gemv<DEC_EPI_RESID, false>(p, s);
+    if (epi == DEC_EPI_SILU && norm) return launch_gemv<DEC_EPI_SILU, true>(p, s);
+    if (epi == DEC_EPI_ARGMAX && norm) return launch_gemv<DEC_EPI_ARGMAX, true>(p, s);
+    if (epi == DEC_EPI_STORE && !norm) return launch_gemv<DEC_EPI_STORE, false>(p, s);
+    if (epi == DEC_EPI_STORE && norm) return launch_gemv<DEC_EPI_STORE, true>(p, s);
+    return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: no kernel for epilogue %d (norm=%d)", epi, (int)norm);
+}
+
+size_t dec_attn_lds_bytes(int hd, int tmax) {
+    return ((size_t)tmax + hd + ATT_PART + ATT_BLOCK / WAVE) * sizeof(float);
+}
+
+int dec_attention(const float* q, const float* kc, const float* vc, float* o, int batch, int heads, int hd,
+                  int tmax, float scale, const int* tctr, hipStream_t s) {
+    if (batch <= 0 || heads <= 0 || tmax <= 0)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode attention: empty problem");
+    const size_t lds = dec_attn_lds_bytes(hd, tmax);
+    if (lds > 64 * 1024) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode attention: max_seq %d too long", tmax);
+    const dim3 grid(batch * heads), block(ATT_BLOCK);
+    switch (hd) {
+        case 8: hipLaunchKernelGGL(decode_attn_kernel<8>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
+        case 16: hipLaunchKernelGGL(decode_attn_kernel<16>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
+        case 32: hipLaunchKernelGGL(decode_attn_kernel<32>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
+        case 64: hipLaunchKernelGGL(decode_attn_kernel<64>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
+        case 128: hipLaunchKernelGGL(decode_attn_kernel<128>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
+        case 256: hipLaunchKernelGGL(decode_attn_kernel<256>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
+        default: return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode attention: head_dim %d not in {8, 16, ..., 256}", hd);
+    }
+    return launch_check("decode_attn_kernel");
+}
+
+int dec_embed(const uint16_t* emb, const int* tokens, float* x, int d, int vocab, int batch, const int* tctr,
+              hipStream_t s) {
+    hipLaunchKernelGGL(decode_embed_kernel, dim3(batch), dim3(256), 0, s, emb, tokens, x, d, vocab, batch, tctr);
+    return launch_check("decode_embed_kernel");
+}
+
+int dec_finish(const uint64_t* part, int groups, int* tokens, int* argmax_out, const uint16_t* emb, float* x,
+               int d, int vocab, int batch, int prompt_len, int* tctr, hipStream_t s) {
+    if (batch <= 0 || batch > DEC_MAX_BATCH)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode finish: batch %d outside [1, %d]", batch, DEC_MAX_BATCH);
+    hipLaunchKernelGGL(decode_finish_kernel, dim3(1), dim3(FIN_BLOCK), 0, s, part, groups, tokens, argmax_out, emb,
+                       x, d, vocab, batch, prompt_len, tctr);
+    return launch_check("decode_finish_kernel");
+}
+
+int dec_set_counter(int* p, int v, hipStream_t s) {
+    hipLaunchKernelGGL(decode_set_kernel, dim3(1), dim3(1), 0, s, p, v);
+    return launch_check("decode_set_kernel");
+}
+
+}  // namespace mlxhip

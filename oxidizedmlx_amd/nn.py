@@ -179,3 +179,106 @@ class TransformerBlock:
         return h.add(self.mlp(self.norm2(h)))
 
     __call__ = forward
+
+
+# ── decoder-only language model (greedy decode loop) ─────────────────────────
+
+@dataclass
+class DecoderConfig:
+    """Decoder-only model from mlx-nn layers: Embedding, n_layers pre-norm
+    TransformerBlocks (causal attention, SiLU MLP of ``hidden`` = mlp_ratio x
+    d_model), final RmsNorm, LM-head Linear without bias."""
+    n_layers: int = 12
+    d_model: int = 768
+    n_heads: int = 12
+    vocab: int = 32000
+    mlp_ratio: int = 4
+    eps: float = 1e-5
+    max_batch: int = 8
+    max_seq: int = 144
+
+    @property
+    def hidden(self) -> int:
+        return self.mlp_ratio * self.d_model
+
+    def block(self, batch: int, seq: int) -> BlockConfig:
+        return BlockConfig(self.d_model, self.n_heads, seq, batch, self.mlp_ratio, self.eps)
+
+    def step_weight_bytes(self) -> int:
+        """bf16 parameter bytes one decode step reads: every block's
+        projections and biases and the LM head (the embedding is gathered,
+        one row per sequence)."""
+        d, h = self.d_model, self.hidden
+        per_layer = 4 * d * d + 2 * d * h + 4 * d + h + d
+        return 2 * (self.n_layers * per_layer + self.vocab * d)
+
+    def decode_bytes(self, batch: int, prompt_len: int, n_new: int) -> int:
+        """Algorithmic HBM bytes of one greedy generate over S = prompt_len +
+        n_new - 1 positions: per position t the bf16 weights of
+        ``step_weight_bytes``, the f32 K and V cache rows of positions 0..t
+        read by every layer's attention, the new K/V rows written and the
+        gathered bf16 embedding rows."""
+        steps = prompt_len + n_new - 1
+        kv_row = 2 * batch * self.d_model * 4 * self.n_layers
+        return (steps * self.step_weight_bytes() + kv_row * steps * (steps + 1) // 2
+                + kv_row * steps + steps * batch * self.d_model * 2)
+
+
+def decoder_params(cfg: DecoderConfig, seed: int, std: float = 0.02) -> dict:
+    """Random-init parameters N(0, std^2), rounded to bf16 (the values the
+    bf16 decoder holds), as float32 numpy arrays, drawn in the order below
+    from numpy's PCG64 generator seeded with ``seed`` (standard normals in
+    float32, scaled by ``std``)."""
+    from . import synth
+    d, h, V = cfg.d_model, cfg.hidden, cfg.vocab
+    rng = np.random.default_rng(seed)
+
+    def draw(shape):
+        z = rng.standard_normal(shape, dtype=np.float32)
+        z *= np.float32(std)
+        return synth.round_bf16(z)
+
+    params = {"embedding": draw((V, d)), "lm_head": draw((V, d)), "layers": []}
+    shapes = BlockConfig(d, cfg.n_heads, 1, 1, cfg.mlp_ratio, cfg.eps).param_shapes()
+    for _ in range(cfg.n_layers):
+        params["layers"].append({name: draw(shape) for name, shape in shapes.items()})
+    return params
+
+
+class Embedding:
+    """Rows of weight [num_embeddings, dim] at integer ids (crates/mlx-nn/src/embed.rs)."""
+
+    def __init__(self, weight: Tensor):
+        self.weight = weight
+
+    def forward(self, ids: Tensor) -> Tensor:
+        return self.weight.embedding_lookup(ids)
+
+    __call__ = forward
+
+
+class DecoderLM:
+    """Causal forward of the decoder over token ids [batch, seq] on any
+    stream: logits [batch*seq, vocab] (rows batch-major). Row (b, t) is what
+    greedy decoding sees after position t of sequence b."""
+
+    def __init__(self, cfg: DecoderConfig, stream, params: dict):
+        self.cfg, self.stream = cfg, stream
+        V, d = cfg.vocab, cfg.d_model
+        self.embed = Embedding(Tensor.from_f32(stream, params["embedding"], (V, d)))
+        self.lm_head = Linear(Tensor.from_f32(stream, params["lm_head"], (V, d)))
+        shapes = cfg.block(1, 1).param_shapes()
+        self.layer_params = [{k: Tensor.from_f32(stream, lp[k], shapes[k]) for k in shapes}
+                             for lp in params["layers"]]
+        self.norm = RmsNorm(d, cfg.eps)
+
+    def forward(self, tokens: np.ndarray) -> Tensor:
+        tokens = np.asarray(tokens)
+        b, s = tokens.shape
+        ids = Tensor.from_f32(self.stream, tokens.reshape(-1).astype(np.float32), (b * s,))
+        x = self.embed(ids)
+        for lp in self.layer_params:
+            x = TransformerBlock(self.cfg.block(b, s), lp)(x)
+        return self.lm_head(self.norm(x))
+
+    __call__ = forward

@@ -119,6 +119,14 @@ class Tensor:
             raise abi.ShapeMismatch(f"expected {list(a)}, got {list(b)}")
         return self._lazy(OpKind.MatMul, [self, rhs], a[:-1] + (b[-1],))
 
+    def embedding_lookup(self, indices: "Tensor") -> "Tensor":
+        """Rows of this [num_embeddings, dim] weight at ``indices`` (ids as
+        f32, clamped by the kernel); output shape indices.shape + [dim]
+        (tensor.rs:301-317)."""
+        if len(self.shape) != 2:
+            raise abi.InvalidArgument("embedding weight must be 2D [num_embeddings, embedding_dim]")
+        return self._lazy(OpKind.Embedding, [self, indices], indices.shape + (self.shape[1],))
+
     # ── shape ops (tensor.rs:322-374, 769-801) ───────────────────────────
     def reshape(self, shape: Sequence[int]) -> "Tensor":
         shape = _shape(shape)
