@@ -114,6 +114,12 @@ __global__ __launch_bounds__(BLOCK) void ew_chain_vec_kernel(EwProg prog, float*
                     const uint32_t j = (uint32_t)idx % (uint32_t)prog.period[i];
                     in[i][u] = idx < n_vec ? reinterpret_cast<const float4*>(prog.in[i])[j]
                                            : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else if constexpr (NT) {
+                    // Full-size inputs of a large chain are read exactly once.
+                    typedef float f32x4 __attribute__((ext_vector_type(4)));
+                    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                    if (idx < n_vec) v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(prog.in[i]) + idx);
+                    in[i][u] = make_float4(v[0], v[1], v[2], v[3]);
                 } else {
                     in[i][u] = idx < n_vec ? reinterpret_cast<const float4*>(prog.in[i])[idx]
                                            : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -154,8 +160,15 @@ int launch_chain_vec(const EwProg& p, float* out, int64_t n_vec, bool periodic, 
     constexpr int U = 1;
     int64_t grid = ceil_div(n_vec, (int64_t)BLOCK * U);
     if (grid > 65536) grid = 65536;
+    // A chain whose traffic is at least half the 256 MiB Infinity Cache
+    // streams: non-temporal loads of its full-size inputs and non-temporal
+    // stores.
+    const bool stream = n_vec * 16 * (NI + 1) >= (int64_t(128) << 20);
     if (periodic)
         hipLaunchKernelGGL((ew_chain_vec_kernel<NI, U, false, true>), dim3((unsigned)grid), dim3(BLOCK), 0, s, p,
+                           out, n_vec);
+    else if (stream)
+        hipLaunchKernelGGL((ew_chain_vec_kernel<NI, U, true, false>), dim3((unsigned)grid), dim3(BLOCK), 0, s, p,
                            out, n_vec);
     else
         hipLaunchKernelGGL((ew_chain_vec_kernel<NI, U, false, false>), dim3((unsigned)grid), dim3(BLOCK), 0, s, p,
