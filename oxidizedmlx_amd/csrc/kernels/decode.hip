@@ -79,32 +79,6 @@ __device__ inline uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
-// Sums v[b] over the 64 lanes for each of 8 rows in 10 cross-lane steps
-// (halving the rows held per lane at each of the first three): returns the
-// total of row 4*bit5 + 2*bit4 + bit3 of the lane id. Fixed order, so the
-// result is deterministic.
-__device__ inline float wave_sum8(const float (&v)[8], int lane) {
-    float a[4], c[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const bool hi = lane & 32;
-        const float send = hi ? v[i] : v[i + 4];
-        a[i] = (hi ? v[i + 4] : v[i]) + __shfl_xor(send, 32, WAVE);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const bool hi = lane & 16;
-        const float send = hi ? a[i] : a[i + 2];
-        c[i] = (hi ? a[i + 2] : a[i]) + __shfl_xor(send, 16, WAVE);
-    }
-    const bool hi = lane & 8;
-    float r = (hi ? c[1] : c[0]) + __shfl_xor(hi ? c[0] : c[1], 8, WAVE);
-#pragma unroll
-    for (int o = 4; o > 0; o >>= 1) r += __shfl_xor(r, o, WAVE);
-    return r;
-}
-__device__ inline int wave_sum8_row(int lane) { return ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1); }
-
 // x / d as the correctly rounded quotient from r = 1/d (correctly rounded):
 // q = x*r, then one exact-remainder correction (Markstein).
 __device__ inline float div_by(float x, float d, float r) {
@@ -130,12 +104,16 @@ __device__ inline float sigmoid_ref(float x) { return 1.0f / (1.0f + expf(-x)); 
 // The kernel is latency-bound at decode sizes (a few MB per launch), so every
 // global load whose address does not depend on this kernel's own results is
 // issued at the start, before the first wait: the step position, the
-// epilogue's bias and residual values, the W fragments and the X rows (thread
-// c holds float4 column c of all 8 rows, since 64*KS >= K/4). The launch then
-// costs about one memory round trip plus the MFMAs.
+// epilogue's bias and residual values, the X rows and the W fragments. Each
+// thread then normalises and splits at most XU float4s of X (a workgroup has
+// at least 8*K/4/XU threads): the split costs ~25 VALU operations per value,
+// so it is spread over every thread of the workgroup. The RMS of row b is
+// summed by wave b (mod waves), lane by lane in k order, then across lanes.
 //
 // ARGMAX (the LM head) publishes each workgroup's per-sequence maximum key
 // for decode_finish.
+constexpr int XU = 8;  // float4s of X per thread, at most
+
 template <int EPI, bool NORM>
 __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks, int r_tiles, int kw) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -144,7 +122,7 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     constexpr int TB = TILE_N * DEC_MAX_BATCH;  // outputs of one row tile
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
     float* red = reinterpret_cast<float*>(smem + (size_t)XROWS * pitch * 2);
-    float* wss = red + r_tiles * ks * TB;                                 // [MAX_WAVES][8]
+    float* wss = red + r_tiles * ks * TB;                                 // [2][8]: rms, 1/rms
     uint64_t* keys = reinterpret_cast<uint64_t*>(wss + MAX_WAVES * DEC_MAX_BATCH);  // [r_tiles * TB]
 
     const int tid = threadIdx.x, nthr = blockDim.x;
@@ -172,6 +150,16 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
             }
         }
     }
+    // X unit u = tid + i*nthr is float4 column u % (K/4) of row u / (K/4).
+    const int k4 = K / 4, nunits = DEC_MAX_BATCH * k4;
+    float4 xv[XU];
+#pragma unroll
+    for (int i = 0; i < XU; ++i) {
+        const int u = tid + i * nthr;
+        const int b = u / k4;
+        xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (u < nunits && b < B) xv[i] = *reinterpret_cast<const float4*>(p.x + (int64_t)b * p.ldx + 4 * (u - b * k4));
+    }
     // Lane l reads 8 consecutive k of feature n0 + l%16 (MFMA A-operand layout:
     // row l%16, k block l/16). Rows past N read row N-1 (discarded).
     const int frow = min(n0 + (lane & 15), N - 1);
@@ -184,46 +172,46 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
             if (s < steps) a[s] = *reinterpret_cast<const u32x4*>(wp + k0 + s * KSTEP);
     };
     load_pass(kb);
-    const int k4 = K / 4;
-    const bool xc = tid < k4;
-    float4 xv[DEC_MAX_BATCH];
-#pragma unroll
-    for (int b = 0; b < DEC_MAX_BATCH; ++b) {
-        xv[b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (xc && b < B) xv[b] = *reinterpret_cast<const float4*>(p.x + (int64_t)b * p.ldx + 4 * tid);
-    }
 
     // ── prologue: X (optionally RMS-normalised) split into hi/mid/lo bf16 rows
     if constexpr (NORM) {
         // rms_norm, cpu_kernels.rs:647-669: sqrt(sum(x*x)/d + eps), y = x / rms.
-        float ss[DEC_MAX_BATCH];
-#pragma unroll
-        for (int b = 0; b < DEC_MAX_BATCH; ++b) {
-            const float4 v = xv[b];
-            ss[b] = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        }
-        const float tot = wave_sum8(ss, lane);
-        if ((lane & 7) == 0) wss[wave * DEC_MAX_BATCH + wave_sum8_row(lane)] = tot;
-        __syncthreads();
-#pragma unroll
-        for (int b = 0; b < DEC_MAX_BATCH; ++b) {
-            float sb = wss[b];
-            for (int w = 1; w < nwaves; ++w) sb += wss[w * DEC_MAX_BATCH + b];
-            float rms = sqrtf(sb / (float)K + p.eps), r = 1.0f / rms;
-            if (__builtin_isinf(rms)) {  // x / inf, as division gives it
-                rms = 1.0f;
-                r = 0.0f;
+        for (int b = wave; b < B; b += nwaves) {
+            const float* xr = p.x + (int64_t)b * p.ldx;
+            float ss = 0.0f;
+            for (int c = lane; c < k4; c += WAVE) {
+                const float4 v = *reinterpret_cast<const float4*>(xr + 4 * c);
+                ss += v.x * v.x;
+                ss += v.y * v.y;
+                ss += v.z * v.z;
+                ss += v.w * v.w;
             }
-            xv[b].x = div_by(xv[b].x, rms, r);
-            xv[b].y = div_by(xv[b].y, rms, r);
-            xv[b].z = div_by(xv[b].z, rms, r);
-            xv[b].w = div_by(xv[b].w, rms, r);
+            ss = wave_sum(ss);
+            if (lane == 0) {
+                float rms = sqrtf(ss / (float)K + p.eps), r = 1.0f / rms;
+                if (__builtin_isinf(rms)) {  // x / inf, as division gives it
+                    rms = 1.0f;
+                    r = 0.0f;
+                }
+                wss[b] = rms;
+                wss[DEC_MAX_BATCH + b] = r;
+            }
         }
+        __syncthreads();
     }
-    if (xc) {
 #pragma unroll
-        for (int b = 0; b < DEC_MAX_BATCH; ++b) {
-            const float v[4] = {xv[b].x, xv[b].y, xv[b].z, xv[b].w};
+    for (int i = 0; i < XU; ++i) {
+        const int u = tid + i * nthr;
+        if (u < nunits) {
+            const int b = u / k4, k = 4 * (u - b * k4);
+            float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            if constexpr (NORM) {
+                if (b < B) {
+                    const float d = wss[b], r = wss[DEC_MAX_BATCH + b];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) v[j] = div_by(v[j], d, r);
+                }
+            }
             uint32_t h[4], m[4], l[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -233,7 +221,6 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
                 const float r2 = r1 - bf16_f32(m[j]);
                 l[j] = bf16_rne(r2);
             }
-            const int k = 4 * tid;
             *reinterpret_cast<uint2*>(xs + (0 * DEC_MAX_BATCH + b) * pitch + k) =
                 make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
             *reinterpret_cast<uint2*>(xs + (1 * DEC_MAX_BATCH + b) * pitch + k) =
@@ -328,43 +315,64 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
 }
 
 // ── end of the step: argmax, next token and its embedding, t += 1 ──────────
-// One workgroup; wave b reduces sequence b's per-workgroup maxima (equal
-// logits resolve to the lowest index: the key's low word is 0xFFFFFFFF -
-// index). The next token is the prompt's while t+1 < prompt_len, else the
-// argmax; its embedding row becomes the residual stream x of the next step.
+// One workgroup of 512 threads. Thread i reduces the keys of sequence i % 8
+// from workgroups g = i/8, i/8 + 64, ... (all loaded before the first use),
+// then lanes with equal i % 8 and the 8 waves combine theirs. Equal logits
+// resolve to the lowest index (the key's low word is 0xFFFFFFFF - index). The
+// next token is the prompt's while t+1 < prompt_len, else the argmax; its
+// embedding row becomes the residual stream x of the next step.
 constexpr int FIN_BLOCK = DEC_MAX_BATCH * WAVE;
+constexpr int FIN_KEYS = 8;  // keys per thread loaded at once
 
 __global__ __launch_bounds__(FIN_BLOCK) void decode_finish_kernel(
     const uint64_t* __restrict__ part, int groups, int* __restrict__ tokens, int* __restrict__ argmax_out,
     const uint16_t* __restrict__ emb, float* __restrict__ x, int d, int vocab, int batch, int prompt_len,
     int* __restrict__ tctr) {
+    __shared__ uint64_t s_max[FIN_BLOCK / WAVE][DEC_MAX_BATCH];
     __shared__ int s_tok[DEC_MAX_BATCH];
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int b = tid % DEC_MAX_BATCH;
+    constexpr int GSTRIDE = FIN_BLOCK / DEC_MAX_BATCH;
     const int t = *tctr;
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    if (wave < batch) {
-        uint64_t m = 0;
-        for (int g = lane; g < groups; g += WAVE) {
-            const uint64_t k = part[(int64_t)g * DEC_MAX_BATCH + wave];
-            m = k > m ? k : m;
+    uint64_t m = 0;
+    for (int g0 = tid / DEC_MAX_BATCH; g0 < groups; g0 += GSTRIDE * FIN_KEYS) {
+        uint64_t k[FIN_KEYS];
+#pragma unroll
+        for (int j = 0; j < FIN_KEYS; ++j) {
+            const int g = g0 + j * GSTRIDE;
+            k[j] = g < groups ? part[(int64_t)g * DEC_MAX_BATCH + b] : 0ull;
         }
-        m = wave_max_u64(m);
-        if (lane == 0) {
-            const int idx = (int)(0xFFFFFFFFu - (uint32_t)m);
-            argmax_out[(int64_t)t * batch + wave] = idx;
-            int next = idx;
-            if (t + 1 < prompt_len)
-                next = tokens[(int64_t)(t + 1) * batch + wave];
-            else
-                tokens[(int64_t)(t + 1) * batch + wave] = idx;
-            s_tok[wave] = next < 0 ? 0 : (next > vocab - 1 ? vocab - 1 : next);
-        }
+#pragma unroll
+        for (int j = 0; j < FIN_KEYS; ++j) m = k[j] > m ? k[j] : m;
+    }
+#pragma unroll
+    for (int o = 8; o < WAVE; o <<= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)m, o, WAVE);
+        const uint32_t hi = __shfl_xor((uint32_t)(m >> 32), o, WAVE);
+        const uint64_t w = ((uint64_t)hi << 32) | lo;
+        m = w > m ? w : m;
+    }
+    if (lane < DEC_MAX_BATCH) s_max[wave][lane] = m;
+    __syncthreads();
+    if (tid < batch) {
+        uint64_t mm = s_max[0][tid];
+#pragma unroll
+        for (int w = 1; w < FIN_BLOCK / WAVE; ++w) mm = s_max[w][tid] > mm ? s_max[w][tid] : mm;
+        const int idx = (int)(0xFFFFFFFFu - (uint32_t)mm);
+        argmax_out[(int64_t)t * batch + tid] = idx;
+        int next = idx;
+        if (t + 1 < prompt_len)
+            next = tokens[(int64_t)(t + 1) * batch + tid];
+        else
+            tokens[(int64_t)(t + 1) * batch + tid] = idx;
+        s_tok[tid] = next < 0 ? 0 : (next > vocab - 1 ? vocab - 1 : next);
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < batch * d; i += FIN_BLOCK) {
-        const int b = i / d, k = i - b * d;
-        x[(int64_t)b * d + k] = bf16_f32(emb[(int64_t)s_tok[b] * d + k]);
+    for (int i = tid; i < batch * d; i += FIN_BLOCK) {
+        const int bb = i / d, k = i - bb * d;
+        x[(int64_t)bb * d + k] = bf16_f32(emb[(int64_t)s_tok[bb] * d + k]);
     }
-    if (threadIdx.x == 0) *tctr = t + 1;
+    if (tid == 0) *tctr = t + 1;
 }
 
 // ── attention of one new query per (sequence, head) over the KV cache ────
@@ -501,14 +509,31 @@ __global__ __launch_bounds__(256) void decode_embed_kernel(const uint16_t* __res
 
 __global__ void decode_set_kernel(int* __restrict__ p, int v) { *p = v; }
 
+// Launch shape: a problem with fewer than 512 row tiles splits K into
+// slices of ~64 (up to 16 waves), so the workgroup has threads enough to
+// split X quickly and its W loads spread over many waves; a wide problem
+// (the LM head) uses 256-k slices and up to 16/KS row tiles per workgroup
+// while that still leaves >= 256 workgroups, so fewer workgroups repeat the
+// prologue.
+void gemv_shape(int n, int k, int& ks, int& r, int& kw, int& grid) {
+    const int ntiles = (int)ceil_div(n, TILE_N);
+    r = 1;
+    if (ntiles >= 512) {
+        ks = std::min(MAX_WAVES, (int)ceil_div(k, KPASS));
+        while ((r * 2) * ks <= MAX_WAVES && ceil_div(ntiles, r * 2) >= 256) r *= 2;
+    } else {
+        ks = std::max(1, std::min(MAX_WAVES, (int)ceil_div(k, 64)));
+    }
+    kw = (int)ceil_div(ceil_div(k, ks), KSTEP) * KSTEP;
+    grid = (int)ceil_div(ntiles, r);
+}
+
 template <int EPI, bool NORM>
 int launch_gemv(const DecGemv& p, hipStream_t s) {
-    const int ks = std::min(MAX_WAVES, (int)ceil_div(p.k, KPASS));
-    const int kw = (int)ceil_div(ceil_div(p.k, ks), KSTEP) * KSTEP;
-    const int ntiles = (int)ceil_div(p.n, TILE_N);
-    int r = 1;
-    while ((r * 2) * ks <= MAX_WAVES && ceil_div(ntiles, r * 2) >= 256) r *= 2;
-    const int grid = (int)ceil_div(ntiles, r);
+    int ks, r, kw, grid;
+    gemv_shape(p.n, p.k, ks, r, kw, grid);
+    if (ceil_div((int64_t)DEC_MAX_BATCH * (p.k / 4), (int64_t)r * ks * WAVE) > XU)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: K = %d too wide for one workgroup", p.k);
     const size_t lds = dec_gemv_lds_bytes(p.k, ks, r, EPI == DEC_EPI_ARGMAX);
     if (lds > DEC_LDS_LIMIT)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: K = %d needs %zu bytes of LDS (limit %d)", p.k,
@@ -532,17 +557,15 @@ int set_lds_attr() {
 size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax) {
     size_t b = (size_t)XROWS * (k + XPAD) * 2;                    // hi/mid/lo rows
     b += (size_t)r * ks * TILE_N * DEC_MAX_BATCH * sizeof(float);  // k-slice partials
-    b += MAX_WAVES * DEC_MAX_BATCH * sizeof(float);               // per-wave sums of squares
+    b += MAX_WAVES * DEC_MAX_BATCH * sizeof(float);               // row rms and 1 / rms
     if (argmax) b += (size_t)r * TILE_N * DEC_MAX_BATCH * sizeof(uint64_t);
     return b;
 }
 
 int dec_gemv_groups(int n, int k) {
-    const int ks = std::min(MAX_WAVES, (int)ceil_div(k, KPASS));
-    const int ntiles = (int)ceil_div(n, TILE_N);
-    int r = 1;
-    while ((r * 2) * ks <= MAX_WAVES && ceil_div(ntiles, r * 2) >= 256) r *= 2;
-    return (int)ceil_div(ntiles, r);
+    int ks, r, kw, grid;
+    gemv_shape(n, k, ks, r, kw, grid);
+    return grid;
 }
 
 int dec_prepare() {
