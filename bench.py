@@ -187,6 +187,17 @@ def main() -> int:
         dec.load(dparams)
         dprompt = np.random.default_rng(0x5EED0201).integers(0, dcfg.vocab, size=(d_batch, d_prompt))
 
+    # Fused causal attention over config 4's heads: 64 heads of [512, 64] f32
+    # (mlxhip_attention). Algorithmic work counts the unmasked products only:
+    # 2 * dh per (query, visible key) for the scores and again for P.V.
+    at_bh, at_t, at_dh = bcfg.batch * bcfg.n_heads, bcfg.seq, bcfg.d_model // bcfg.n_heads
+    at_flops = 4.0 * at_dh * at_bh * (at_t * (at_t + 1) // 2)
+    at_bufs = {}
+    if want("attention_fused_cfg4"):
+        at_bufs = {nm: hb.DeviceBuffer.from_array(synth.normal(0x5EED0300 + i, (at_bh, at_t, at_dh)))
+                   for i, nm in enumerate("qkv")}
+        at_bufs["o"] = hb.DeviceBuffer(at_bh * at_t * at_dh * 4)
+
     kernels = {
         "gemm_bf16_4096": dict(flops=2.0 * n * n * n, bytes=3 * n * n * 2),
         # Calibration only (never part of a step): a plain 64 MiB copy whose HBM
@@ -208,6 +219,7 @@ def main() -> int:
         "transformer_block_fwd_bwd_cfg4": dict(flops=3.0 * bcfg.forward_flops(), bytes=0, peak=157.3,
                                                wall=True),
         "decode_cfg5": dict(bytes=dcfg.decode_bytes(d_batch, d_prompt, d_new), decoder=True),
+        "attention_fused_cfg4": dict(flops=at_flops, bytes=4 * at_bh * at_t * at_dh * 4, peak=157.3),
     }
     chain = [("mul", 1), ("add", 2), ("silu", 0)]
 
@@ -215,7 +227,10 @@ def main() -> int:
 
     def launch(name: str, i: int) -> None:
         j = i % SETS
-        if name == "decode_cfg5":
+        if name == "attention_fused_cfg4":
+            hb.attention(at_bufs["q"], at_bufs["k"], at_bufs["v"], at_bufs["o"], at_bh, at_t, at_t, at_dh,
+                         1.0 / np.sqrt(at_dh), True, stream=stream)
+        elif name == "decode_cfg5":
             dec.generate(dprompt, d_new, eager=args.decode_eager)
             dec_ms.append(dec.last_timing()[0])
         elif name == "transformer_block_fwd_bwd_cfg4":

@@ -336,6 +336,22 @@ int mlxhip_ew_chain(const mlxhip_ew_instr_t* prog, size_t n_instr,
                     const float* const* inputs, size_t n_inputs,
                     float* out, int64_t numel, void* stream);
 
+/* Fused scaled, masked attention of `batch` heads (cpu_attention,
+ * crates/mlx-core/src/cpu_kernels.rs:738-812, per head): for each b,
+ *   O_b = softmax(Q_b K_b^T * scale, with -1e9 where causal && key > query) V_b,
+ * Q_b and O_b [tq, dh], K_b and V_b [tk, dh], f32, contiguous and packed one
+ * head after another (head b starts at b*tq*dh / b*tk*dh); Q and K 16-byte
+ * aligned. The 16 score rows of a query block stay in LDS: dh must be 16, 32,
+ * 64 or 128, and 16*(tk+1) floats must fit in 159 KiB (tk up to 2542);
+ * otherwise MLXHIP_ERR_INVALID_ARGUMENT. The Attention op
+ * of mlxhip_eval_node* uses this kernel when the shape allows and the
+ * GEMM + softmax + GEMM sequence otherwise. Replaces the per-head Narrow +
+ * Attention of MultiHeadAttention (crates/mlx-nn/src/attention.rs:47-111)
+ * with one launch. */
+int mlxhip_attention(const float* q, const float* k, const float* v, float* o,
+                     int64_t batch, int64_t tq, int64_t tk, int64_t dh,
+                     float scale, int32_t causal, void* stream);
+
 /* 2-D transpose y[cols, rows] = x[rows, cols]^T of 4-byte elements
  * (transpose, cpu_kernels.rs:232-274, axes = None on rank 2). Bit-exact. */
 int mlxhip_transpose2d(const float* x, float* y, int64_t rows, int64_t cols, void* stream);

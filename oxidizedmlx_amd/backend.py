@@ -261,6 +261,12 @@ def ew_chain(prog: Sequence[tuple], inputs: Sequence, out, numel: int, stream=No
     abi.check(lib().mlxhip_ew_chain(ins, len(prog), ptrs, len(inputs), _p(out), numel, stream))
 
 
+def attention(q, k, v, o, batch: int, tq: int, tk: int, dh: int, scale: float, causal: bool,
+              stream=None) -> None:
+    """Fused attention of `batch` packed heads (device buffers)."""
+    abi.check(lib().mlxhip_attention(_p(q), _p(k), _p(v), _p(o), batch, tq, tk, dh, scale, int(causal), stream))
+
+
 def transpose2d(x, y, rows: int, cols: int, stream=None) -> None:
     abi.check(lib().mlxhip_transpose2d(_p(x), _p(y), rows, cols, stream))
 

@@ -39,6 +39,7 @@ SOURCES = [
     "kernels/gemm16_bf16.hip",
     "kernels/gemm16_f16.hip",
     "kernels/decode.hip",
+    "kernels/attention.hip",
 ]
 
 

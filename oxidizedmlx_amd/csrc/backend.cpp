@@ -276,6 +276,9 @@ int eval_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inp
                     (long long)tk, (long long)dh, (long long)tkv, (long long)dhv);
     MLXHIP_TRY(expect_len(tq * dh, numel_of(meta.shape, meta.ndim), "attention"));
     if (tq * dh == 0) return MLXHIP_OK;
+    if (tk > 0 && attention_fused_supported(dh, tq, tk) &&
+        ((reinterpret_cast<uintptr_t>(q.data) | reinterpret_cast<uintptr_t>(k.data)) % 16) == 0)
+        return attention_fused(q.data, k.data, v.data, out, 1, tq, tk, dh, 0, 0, 0, 0, op.scale, op.causal, s);
     float* scores = scratch.get((size_t)std::max<int64_t>(1, tq * tk));
     float* probs = scratch.get((size_t)std::max<int64_t>(1, tq * tk));
     if (!scores || !probs) return fail(MLXHIP_ERR_FFI_FAILED, "attention: scratch allocation failed");
@@ -730,6 +733,18 @@ int mlxhip_ew_chain(const mlxhip_ew_instr_t* prog, size_t n_instr, const float* 
     if ((n_instr && !prog) || !inputs || (numel && !out)) return fail(MLXHIP_ERR_NULL_PTR, "ew_chain: null argument");
     MLXHIP_TRY(ensure_device());
     return ew_chain(prog, (int)n_instr, inputs, (int)n_inputs, out, numel, as_stream(stream));
+}
+
+int mlxhip_attention(const float* q, const float* k, const float* v, float* o, int64_t batch, int64_t tq,
+                     int64_t tk, int64_t dh, float scale, int32_t causal, void* stream) {
+    MLXHIP_TRY(ensure_device());
+    if (batch < 0 || tq < 0 || tk < 0 || dh < 0)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: negative size");
+    if (batch == 0 || tq == 0 || dh == 0) return MLXHIP_OK;
+    if (!q || !k || !v || !o) return fail(MLXHIP_ERR_NULL_PTR, "attention: null operand");
+    if (tk == 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: no keys");
+    return attention_fused(q, k, v, o, batch, tq, tk, dh, tq * dh, tk * dh, tk * dh, tq * dh, scale, causal,
+                           as_stream(stream));
 }
 
 int mlxhip_transpose2d(const float* x, float* y, int64_t rows, int64_t cols, void* stream) {

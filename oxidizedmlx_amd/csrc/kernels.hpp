@@ -111,6 +111,18 @@ int dec_finish(const uint64_t* part, int groups, int* tokens, int* argmax_out, c
                int d, int vocab, int batch, int prompt_len, int* tctr, hipStream_t s);
 int dec_set_counter(int* p, int v, hipStream_t s);
 
+// ── attention.hip (fused scaled, masked attention of a batch of heads) ────
+constexpr int ATTN_LDS_LIMIT = 159 * 1024;
+size_t attention_fused_lds_bytes(int dh, int64_t tk);
+// dh in {16, 32, 64, 128} and the score rows of 16 queries fit in LDS
+// (tk up to 2542).
+bool attention_fused_supported(int64_t dh, int64_t tq, int64_t tk);
+// Q [batch][tq][dh], K/V [batch][tk][dh], O [batch][tq][dh], row-major with
+// batch strides sq/sk/sv/so (elements).
+int attention_fused(const float* q, const float* k, const float* v, float* o, int64_t batch, int64_t tq,
+                    int64_t tk, int64_t dh, int64_t sq, int64_t sk, int64_t sv, int64_t so, float scale,
+                    int causal, hipStream_t s);
+
 // ── gemm.hip ──────────────────────────────────────────────────────────────
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,

@@ -1,0 +1,106 @@
+"""Fused attention (kernels/attention.hip) against the oracle's cpu_attention
+(crates/mlx-core/src/cpu_kernels.rs:738-812), through the Stream's Attention
+op and the batched mlxhip_attention entry point.
+
+Tolerance: |gpu - cpu| <= 2e-6 * max|V| + 1e-5 * |cpu|. The output is a
+convex combination of V rows; the GPU sums the score and P·V products in MFMA
+order instead of the reference's sequential order and takes exp on the
+device."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle.cpu_ref import CpuRefBackend
+from oxidizedmlx_amd import abi, synth
+from oxidizedmlx_amd import backend as hb
+from oxidizedmlx_amd.opkind import NodeInput, OpKind, meta
+from parity import assert_allclose, run_parity
+
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip", "oracle_lib")]
+
+
+def qkv(tq, tk, dh, seed, batch=None):
+    pre = (batch,) if batch else ()
+    return (synth.normal(seed, pre + (tq, dh)), synth.normal(seed + 1, pre + (tk, dh)),
+            synth.normal(seed + 2, pre + (tk, dh)))
+
+
+def cpu_attention(q, k, v, scale, causal):
+    tq, dh = q.shape
+    return CpuRefBackend().eval_node(OpKind.Attention(scale, causal),
+                                     [NodeInput(q.ravel(), q.shape), NodeInput(k.ravel(), k.shape),
+                                      NodeInput(v.ravel(), v.shape)], meta([tq, dh])).reshape(tq, dh)
+
+
+@pytest.mark.parametrize("tq,tk,dh,causal", [
+    (1, 17, 64, False),      # one decode query over a cache
+    (64, 64, 64, True),
+    (100, 77, 32, True),     # tq != tk, partial query block and key tile
+    (77, 100, 32, True),
+    (512, 512, 64, True),    # one head of config 4
+    (33, 300, 128, False),
+    (5, 2000, 16, True),
+    (3, 2540, 32, False),    # near the LDS limit of the score rows
+    (16, 16, 16, False),
+    (40, 24, 48, True),      # head dim without a fused kernel: GEMM + softmax + GEMM
+])
+def test_attention_op_matches_oracle(tq, tk, dh, causal):
+    print(f"attention tq={tq} tk={tk} dh={dh} causal={causal}", flush=True)
+    q, k, v = qkv(tq, tk, dh, 7 * tq + tk + dh)
+    scale = 1.0 / math.sqrt(dh)
+
+    def g(s):
+        nq = s.add_constant(q, meta([tq, dh]))
+        nk = s.add_constant(k, meta([tk, dh]))
+        nv = s.add_constant(v, meta([tk, dh]))
+        return s.add_op(OpKind.Attention(scale, causal), [nq, nk, nv], meta([tq, dh]))
+
+    run_parity(g, 2e-6 * float(np.abs(v).max()), 1e-5, f"Attention {tq}x{tk}x{dh}")
+
+
+def test_attention_reference_known_answer():
+    """Causal row 0 attends to key 0 only: O[0] = V[0] exactly; with equal
+    keys every visible key gets the same weight."""
+    tq = tk = 32
+    dh = 16
+    q = synth.normal(1, (tq, dh))
+    k = np.tile(synth.normal(2, (1, dh)), (tk, 1))
+    v = synth.normal(3, (tk, dh))
+    s = hb.HipStream()
+    nq, nk, nv = (s.add_constant(a, meta(list(a.shape))) for a in (q, k, v))
+    y = s.add_op(OpKind.Attention(0.25, True), [nq, nk, nv], meta([tq, dh]))
+    s.eval(y)
+    out = s.get_buffer(y).reshape(tq, dh)
+    np.testing.assert_array_equal(out[0], v[0])
+    ref = np.cumsum(v.astype(np.float64), axis=0) / np.arange(1, tk + 1)[:, None]
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("batch,t,dh,causal", [(6, 128, 64, True), (3, 50, 32, False), (64, 512, 64, True)])
+def test_batched_entry_point(batch, t, dh, causal):
+    """mlxhip_attention over packed heads equals the oracle head by head."""
+    q, k, v = qkv(t, t, dh, 100 + batch, batch=batch)
+    dq, dk, dv = (hb.DeviceBuffer.from_array(a) for a in (q, k, v))
+    do = hb.DeviceBuffer(q.nbytes)
+    scale = 1.0 / math.sqrt(dh)
+    hb.attention(dq, dk, dv, do, batch, t, t, dh, scale, causal)
+    hb.synchronize()
+    out = do.download(np.float32, q.size).reshape(q.shape)
+    heads = range(batch) if batch <= 8 else (0, 1, batch // 2, batch - 1)
+    for b in heads:
+        ref = cpu_attention(q[b], k[b], v[b], scale, causal)
+        assert_allclose(out[b], ref, 2e-6 * float(np.abs(v[b]).max()), 1e-5, f"head {b}")
+
+
+def test_entry_point_errors():
+    q = hb.DeviceBuffer(64 * 48 * 4)
+    with pytest.raises(abi.InvalidArgument):
+        hb.attention(q, q, q, q, 1, 64, 16, 48, 1.0, False)          # no fused kernel for dh 48
+    with pytest.raises(abi.InvalidArgument):
+        hb.attention(q, q, q, q, 1, 4, 100000, 64, 1.0, False)       # scores do not fit in LDS
+    with pytest.raises(abi.InvalidArgument):
+        hb.attention(q, q, q, q, 1, 4, 0, 64, 1.0, False)            # no keys
+    L = abi.load_library()
+    assert L.mlxhip_attention(None, None, None, None, 1, 4, 4, 16, 1.0, 0, None) == abi.ERR_NULL_PTR
+    hb.attention(q, q, q, q, 0, 4, 4, 16, 1.0, False)                # empty batch: nothing to do
