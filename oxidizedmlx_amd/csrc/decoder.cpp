@@ -191,9 +191,12 @@ int validate_config(const mlxhip_decoder_config_t& c) {
                     hd);
     if (c.d_model % 32 || c.hidden % 32)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decoder config: d_model and hidden must be multiples of 32");
-    for (int k : {c.d_model, c.hidden})
-        if (dec_gemv_lds_bytes(k, 16, 1, true) > (size_t)DEC_LDS_LIMIT)
-            return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decoder config: width %d exceeds the GEMV's LDS staging", k);
+    // d_model feeds the RMS-normalising GEMVs (Q/K/V, up, LM head), hidden the
+    // down projection; both must fit the GEMV's LDS staging.
+    if (dec_gemv_lds_bytes(c.d_model, 16, 1, true, true) > (size_t)DEC_LDS_LIMIT ||
+        dec_gemv_lds_bytes(c.hidden, 16, 1, false, false) > (size_t)DEC_LDS_LIMIT)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decoder config: d_model %d / hidden %d exceed the GEMV's LDS staging",
+                    c.d_model, c.hidden);
     if (dec_attn_lds_bytes(hd, c.max_seq) > 64 * 1024)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decoder config: max_seq %d too long", c.max_seq);
     if (!(c.eps >= 0.0f)) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decoder config: eps must be >= 0");

@@ -99,7 +99,7 @@ struct DecGemv {
 int dec_prepare();
 int dec_gemv(int epi, bool norm, const DecGemv& p, hipStream_t s);
 int dec_gemv_groups(int n, int k);
-size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax);
+size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax, bool norm);
 size_t dec_attn_lds_bytes(int hd, int tmax);
 int dec_attention(const float* q, const float* kc, const float* vc, float* o, int batch, int heads, int hd,
                   int tmax, float scale, const int* tctr, hipStream_t s);

@@ -124,6 +124,7 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     float* red = reinterpret_cast<float*>(smem + (size_t)XROWS * pitch * 2);
     float* wss = red + r_tiles * ks * TB;                                 // [2][8]: rms, 1/rms
     uint64_t* keys = reinterpret_cast<uint64_t*>(wss + MAX_WAVES * DEC_MAX_BATCH);  // [r_tiles * TB]
+    float* psum = reinterpret_cast<float*>(keys + (EPI == DEC_EPI_ARGMAX ? r_tiles * TB : 0));  // NORM: [8 * K/4]
 
     const int tid = threadIdx.x, nthr = blockDim.x;
     const int wave = tid / WAVE, lane = tid % WAVE;
@@ -176,16 +177,25 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     // ── prologue: X (optionally RMS-normalised) split into hi/mid/lo bf16 rows
     if constexpr (NORM) {
         // rms_norm, cpu_kernels.rs:647-669: sqrt(sum(x*x)/d + eps), y = x / rms.
-        for (int b = wave; b < B; b += nwaves) {
-            const float* xr = p.x + (int64_t)b * p.ldx;
-            float ss = 0.0f;
-            for (int c = lane; c < k4; c += WAVE) {
-                const float4 v = *reinterpret_cast<const float4*>(xr + 4 * c);
-                ss += v.x * v.x;
-                ss += v.y * v.y;
-                ss += v.z * v.z;
-                ss += v.w * v.w;
+        // The squares come from the X units already in registers (no second
+        // read of X, which would also wait behind the W loads): each unit's
+        // sum goes to LDS, then wave b (mod waves) adds row b's in k order.
+#pragma unroll
+        for (int i = 0; i < XU; ++i) {
+            const int u = tid + i * nthr;
+            if (u < nunits) {
+                const float4 v = xv[i];
+                float q = v.x * v.x;
+                q += v.y * v.y;
+                q += v.z * v.z;
+                q += v.w * v.w;
+                psum[u] = q;
             }
+        }
+        __syncthreads();
+        for (int b = wave; b < B; b += nwaves) {
+            float ss = 0.0f;
+            for (int c = lane; c < k4; c += WAVE) ss += psum[b * k4 + c];
             ss = wave_sum(ss);
             if (lane == 0) {
                 float rms = sqrtf(ss / (float)K + p.eps), r = 1.0f / rms;
@@ -534,7 +544,7 @@ int launch_gemv(const DecGemv& p, hipStream_t s) {
     gemv_shape(p.n, p.k, ks, r, kw, grid);
     if (ceil_div((int64_t)DEC_MAX_BATCH * (p.k / 4), (int64_t)r * ks * WAVE) > XU)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: K = %d too wide for one workgroup", p.k);
-    const size_t lds = dec_gemv_lds_bytes(p.k, ks, r, EPI == DEC_EPI_ARGMAX);
+    const size_t lds = dec_gemv_lds_bytes(p.k, ks, r, EPI == DEC_EPI_ARGMAX, NORM);
     if (lds > DEC_LDS_LIMIT)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: K = %d needs %zu bytes of LDS (limit %d)", p.k,
                     lds, DEC_LDS_LIMIT);
@@ -554,11 +564,12 @@ int set_lds_attr() {
 
 }  // namespace
 
-size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax) {
+size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax, bool norm) {
     size_t b = (size_t)XROWS * (k + XPAD) * 2;                    // hi/mid/lo rows
     b += (size_t)r * ks * TILE_N * DEC_MAX_BATCH * sizeof(float);  // k-slice partials
     b += MAX_WAVES * DEC_MAX_BATCH * sizeof(float);               // row rms and 1 / rms
     if (argmax) b += (size_t)r * TILE_N * DEC_MAX_BATCH * sizeof(uint64_t);
+    if (norm) b += (size_t)DEC_MAX_BATCH * (k / 4) * sizeof(float);  // squares of the X units
     return b;
 }
 
