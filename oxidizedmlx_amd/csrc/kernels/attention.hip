@@ -25,6 +25,7 @@
 
 #include "../common.hpp"
 #include "../kernels.hpp"
+#include "device_math.hpp"
 
 #pragma clang fp contract(off)
 
@@ -38,22 +39,11 @@ constexpr int ATT_WAVES = 4;
 constexpr int ATT_THREADS = ATT_WAVES * WAVE;
 constexpr int QB = 16;  // query rows per workgroup
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
-}
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
-// x / d as the correctly rounded quotient from r = 1/d (correctly rounded):
-// q = x*r, then one exact-remainder correction (Markstein).
-__device__ inline float div_by(float x, float d, float r) {
-    const float q = x * r;
-    return __builtin_fmaf(__builtin_fmaf(-q, d, x), r, q);
-}
+using dev::div_by;
+using dev::shared_divisor;
+using dev::wave_max;
+using dev::wave_sum;
+
 
 template <int DH>
 __global__ __launch_bounds__(ATT_THREADS) void attn_fused_kernel(const float* __restrict__ q,
@@ -151,11 +141,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_fused_kernel(const float* __
                 sum += x[u];
             }
             sum = wave_sum(sum);
-            float r = 1.0f / sum;
-            if (__builtin_isinf(sum)) {  // x / inf, as division gives it
-                sum = 1.0f;
-                r = 0.0f;
-            }
+            float r;
+            shared_divisor(sum, r);
 #pragma unroll
             for (int u = 0; u < SU; ++u) {
                 const int j = lane + WAVE * u;

@@ -32,11 +32,18 @@
 
 #include "../common.hpp"
 #include "../kernels.hpp"
+#include "device_math.hpp"
 
 #pragma clang fp contract(off)
 
 namespace mlxhip {
 namespace {
+
+using dev::div_by;
+using dev::shared_divisor;
+using dev::sigmoid_ref;
+using dev::wave_max;
+using dev::wave_sum;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -58,16 +65,6 @@ __device__ inline uint32_t bf16_rne(float f) {
 }
 __device__ inline float bf16_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
-}
 __device__ inline uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -79,20 +76,11 @@ __device__ inline uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
-// x / d as the correctly rounded quotient from r = 1/d (correctly rounded):
-// q = x*r, then one exact-remainder correction (Markstein).
-__device__ inline float div_by(float x, float d, float r) {
-    const float q = x * r;
-    return __builtin_fmaf(__builtin_fmaf(-q, d, x), r, q);
-}
-
 // Total order of finite floats as unsigned integers, larger value = larger key.
 __device__ inline uint32_t order_key(float f) {
     const uint32_t u = __float_as_uint(f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
-
-__device__ inline float sigmoid_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // ── the split-activation GEMV ──────────────────────────────────────────────
 //
@@ -198,11 +186,8 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
             for (int c = lane; c < k4; c += WAVE) ss += psum[b * k4 + c];
             ss = wave_sum(ss);
             if (lane == 0) {
-                float rms = sqrtf(ss / (float)K + p.eps), r = 1.0f / rms;
-                if (__builtin_isinf(rms)) {  // x / inf, as division gives it
-                    rms = 1.0f;
-                    r = 0.0f;
-                }
+                float rms = sqrtf(ss / (float)K + p.eps), r;
+                shared_divisor(rms, r);
                 wss[b] = rms;
                 wss[DEC_MAX_BATCH + b] = r;
             }

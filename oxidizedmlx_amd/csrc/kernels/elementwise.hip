@@ -14,6 +14,7 @@
 // grid-stride step so each wave keeps multiple 1 KiB loads in flight.
 #include "../common.hpp"
 #include "../kernels.hpp"
+#include "device_math.hpp"
 
 #pragma clang fp contract(off)
 
@@ -22,7 +23,7 @@ namespace {
 
 constexpr int BLOCK = 256;
 
-__device__ inline float sigmoidf_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+using dev::sigmoid_ref;
 
 __device__ inline float gelu_ref(float x) {
     const float k = sqrtf(2.0f / 3.14159265358979323846f);
@@ -30,7 +31,7 @@ __device__ inline float gelu_ref(float x) {
 }
 
 __device__ inline float silu_vjp_ref(float dy, float x) {
-    const float sig = sigmoidf_ref(x);
+    const float sig = sigmoid_ref(x);
     return dy * sig * (1.0f + x * (1.0f - sig));
 }
 
@@ -56,7 +57,7 @@ __device__ inline float apply(int op, float acc, float in) {
         case MLXHIP_EW_EXP: return expf(acc);
         case MLXHIP_EW_LOG: return logf(acc);
         case MLXHIP_EW_SQRT: return sqrtf(acc);
-        case MLXHIP_EW_SILU: return acc * sigmoidf_ref(acc);
+        case MLXHIP_EW_SILU: return acc * sigmoid_ref(acc);
         case MLXHIP_EW_GELU: return gelu_ref(acc);
         case MLXHIP_EW_SILU_VJP: return silu_vjp_ref(in, acc);
         case MLXHIP_EW_GELU_VJP: return gelu_vjp_ref(in, acc);

@@ -26,6 +26,7 @@
 // kernel that re-reads the row (three passes).
 #include "../common.hpp"
 #include "../kernels.hpp"
+#include "device_math.hpp"
 
 #pragma clang fp contract(off)
 
@@ -35,17 +36,14 @@ namespace {
 constexpr int WAVE = 64;
 constexpr int BLOCK = 256;
 
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
+using dev::div_by;
+using dev::wave_max;
+using dev::wave_sum;
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
-}
+// The row divisors here are >= 1 (softmax) or square roots of a sum plus
+// eps, so 1/d is normal unless d overflowed to +inf (handled by
+// shared_divisor).
+__device__ inline void row_divisor(float& d, float& r) { dev::shared_divisor(d, r); }
 
 // Reduction across the WPR waves that share a row. `slot` is this row's
 // LDS slot array (WPR floats); every lane of the row gets the same value.
@@ -62,28 +60,6 @@ __device__ inline float row_reduce(float v, float* slot, int wave_in_row, int la
         v = r;
     }
     return v;
-}
-
-// x / d for a divisor d shared by a whole row, given r = 1 / d (one IEEE
-// division per row): q = x * r, then one Markstein correction with the exact
-// remainder fma(-q, d, x). With r correctly rounded this returns the
-// correctly rounded quotient -- the reference's x / d -- whenever the
-// quotient and x are normal numbers (subnormal quotients may differ by one
-// unit in the last place). The row divisors here are >= 1 (softmax) or
-// square roots of a sum plus eps, so r is normal unless d overflowed to +inf;
-// row_divisor turns that case into d = 1, r = 0, which gives x / inf = 0 for
-// finite x and NaN for infinite x, as the division does.
-__device__ inline float div_by(float x, float d, float r) {
-    const float q = x * r;
-    return __builtin_fmaf(__builtin_fmaf(-q, d, x), r, q);
-}
-
-__device__ inline void row_divisor(float& d, float& r) {
-    r = 1.0f / d;
-    if (__builtin_isinf(d)) {
-        d = 1.0f;
-        r = 0.0f;
-    }
 }
 
 template <int VEC>
