@@ -450,6 +450,22 @@ int mlxhip_event_elapsed_ms(const mlxhip_event_t* start, const mlxhip_event_t* e
 void* mlxhip_stream_create_hip(void);
 void mlxhip_stream_destroy_hip(void* stream);
 
+/* ── Recorded launch sequences (HIP graphs) ──────────────────────────────
+ * For callers whose loops are launch-bound (many small kernels): the direct
+ * kernel entry points called on `stream` between mlxhip_graph_begin and
+ * mlxhip_graph_end, by the calling thread, are recorded instead of run;
+ * mlxhip_graph_launch replays the whole sequence with the same arguments.
+ * `stream` must be a created stream (not NULL). The Stream and decoder
+ * objects and mlxhip_eval_node synchronise internally and cannot be
+ * recorded. No reference counterpart (the reference evaluates each node
+ * when asked, crates/mlx-core/src/backend.rs:85-159). */
+typedef struct mlxhip_graph_t mlxhip_graph_t;
+int mlxhip_graph_begin(void* stream);
+/* NULL on failure (e.g. a recorded call failed or synchronised). */
+mlxhip_graph_t* mlxhip_graph_end(void* stream);
+int mlxhip_graph_launch(mlxhip_graph_t* graph, void* stream);
+void mlxhip_graph_free(mlxhip_graph_t* graph);
+
 #ifdef __cplusplus
 }
 #endif

@@ -207,6 +207,10 @@ PROTOTYPES = {
     "mlxhip_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f)]),
     "mlxhip_stream_create_hip": (_vp, []),
     "mlxhip_stream_destroy_hip": (None, [_vp]),
+    "mlxhip_graph_begin": (_i, [_vp]),
+    "mlxhip_graph_end": (_vp, [_vp]),
+    "mlxhip_graph_launch": (_i, [_vp, _vp]),
+    "mlxhip_graph_free": (None, [_vp]),
 }
 
 _lib = None

@@ -377,3 +377,36 @@ class HipDecoder:
 
     def weight_bytes(self) -> int:
         return self._L.mlxhip_decoder_weight_bytes(self._d)
+
+
+class Graph:
+    """The direct kernel calls issued on `stream` inside the ``with`` block,
+    recorded once and replayed by ``launch`` (mlxhip_graph_*)."""
+
+    def __init__(self, stream: int):
+        if not stream:
+            raise abi.NullPtr("Graph: record on a created stream, not the null stream")
+        self.stream = stream
+        self._g = None
+
+    def __enter__(self) -> "Graph":
+        abi.check(lib().mlxhip_graph_begin(self.stream))
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> None:
+        L = lib()
+        g = L.mlxhip_graph_end(self.stream)
+        if exc_type is None and not g:
+            raise abi.error_for(L.mlxhip_last_status(), L.mlxhip_last_error().decode())
+        self._g = g
+
+    def launch(self, stream: int | None = None) -> None:
+        abi.check(lib().mlxhip_graph_launch(self._g, stream if stream is not None else self.stream))
+
+    def close(self) -> None:
+        if getattr(self, "_g", None):
+            lib().mlxhip_graph_free(self._g)
+            self._g = None
+
+    def __del__(self):
+        self.close()

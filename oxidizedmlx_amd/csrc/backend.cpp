@@ -804,4 +804,51 @@ void mlxhip_stream_destroy_hip(void* stream) {
     if (stream) (void)hipStreamDestroy(as_stream(stream));
 }
 
+struct mlxhip_graph_t {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int mlxhip_graph_begin(void* stream) {
+    MLXHIP_TRY(ensure_device());
+    if (!stream) return fail(MLXHIP_ERR_NULL_PTR, "graph_begin: the null stream cannot be recorded");
+    MLXHIP_HIP(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal));
+    return MLXHIP_OK;
+}
+
+mlxhip_graph_t* mlxhip_graph_end(void* stream) {
+    if (!stream) {
+        fail(MLXHIP_ERR_NULL_PTR, "graph_end: null stream");
+        return nullptr;
+    }
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(as_stream(stream), &g);
+    if (e != hipSuccess || !g) {
+        if (g) (void)hipGraphDestroy(g);
+        hip_fail(e != hipSuccess ? e : hipErrorInvalidValue, "hipStreamEndCapture");
+        return nullptr;
+    }
+    hipGraphExec_t x = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (ei != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        hip_fail(ei, "hipGraphInstantiate");
+        return nullptr;
+    }
+    return new mlxhip_graph_t{g, x};
+}
+
+int mlxhip_graph_launch(mlxhip_graph_t* g, void* stream) {
+    if (!g) return fail(MLXHIP_ERR_NULL_PTR, "graph_launch: null graph");
+    MLXHIP_HIP(hipGraphLaunch(g->exec, as_stream(stream)));
+    return MLXHIP_OK;
+}
+
+void mlxhip_graph_free(mlxhip_graph_t* g) {
+    if (!g) return;
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
 }  // extern "C"

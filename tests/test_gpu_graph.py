@@ -1,0 +1,75 @@
+"""Recorded launch sequences (mlxhip_graph_*): direct kernel calls recorded
+on a stream and replayed must give exactly the eager results, on every
+replay, with the program's own eager work and synchronisations between
+replays (a recorded graph must not hold memset nodes whose effect fades
+after the first replay)."""
+import math
+
+import numpy as np
+import pytest
+
+from oxidizedmlx_amd import abi, synth
+from oxidizedmlx_amd import backend as hb
+
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip")]
+
+
+def test_recorded_sequence_replays_exactly():
+    s = hb.create_stream()
+    try:
+        n1, mo, no, ko = 512, 300, 277, 531          # split-K f32 GEMM; unaligned bf16 GEMM (pack path)
+        A1 = hb.DeviceBuffer.from_array(synth.normal(1, (n1, n1)))
+        B1 = hb.DeviceBuffer.from_array(synth.normal(2, (n1, n1)))
+        C1 = hb.DeviceBuffer(n1 * n1 * 4)
+        Ao = hb.DeviceBuffer.from_array(synth.bf16_bits(synth.normal(3, (mo, ko))))
+        Bo = hb.DeviceBuffer.from_array(synth.bf16_bits(synth.normal(4, (ko, no))))
+        Co = hb.DeviceBuffer(mo * no * 4)
+        x = synth.normal(5, (256, 1000), 0.0, 2.0)
+        X = hb.DeviceBuffer.from_array(x)
+        Y = hb.DeviceBuffer(x.nbytes)
+        Z = hb.DeviceBuffer(x.nbytes)
+        q, k, v = (synth.normal(6 + i, (4, 64, 32)) for i in range(3))
+        Q, K, V = (hb.DeviceBuffer.from_array(a) for a in (q, k, v))
+        O = hb.DeviceBuffer(q.nbytes)
+        outs = [(C1, n1 * n1), (Co, mo * no), (Y, x.size), (Z, x.size), (O, q.size)]
+
+        def seq():
+            hb.gemm(abi.F32, abi.F32, False, False, n1, n1, n1, A1, n1, B1, n1, C1, n1, stream=s)
+            hb.gemm(abi.BF16, abi.F32, False, False, mo, no, ko, Ao, ko, Bo, no, Co, no, stream=s)
+            hb.softmax_rows(X, Y, 256, 1000, stream=s)
+            hb.ew_chain([("mul", 1), ("silu", 0)], [Y, X], Z, x.size, stream=s)
+            hb.attention(Q, K, V, O, 4, 64, 64, 32, 1.0 / math.sqrt(32), True, stream=s)
+
+        seq()
+        hb.synchronize(s)
+        eager = [b.download(np.float32, n) for b, n in outs]
+        with hb.Graph(s) as g:
+            seq()
+        junk = np.full(max(n for _, n in outs), np.nan, np.float32)
+        for rep in range(4):
+            for b, n in outs:
+                b.upload(junk[:n])
+            hb.softmax_rows(X, Y, 256, 1000, stream=s)   # eager work between replays
+            hb.synchronize(s)
+            g.launch()
+            hb.synchronize(s)
+            for (b, n), ref in zip(outs, eager):
+                np.testing.assert_array_equal(b.download(np.float32, n), ref, err_msg=f"replay {rep}")
+        g.close()
+    finally:
+        hb.destroy_stream(s)
+
+
+def test_graph_errors():
+    with pytest.raises(abi.NullPtr):
+        hb.Graph(0)
+    L = abi.load_library()
+    assert L.mlxhip_graph_begin(None) == abi.ERR_NULL_PTR
+    s = hb.create_stream()
+    try:
+        assert not L.mlxhip_graph_end(s)             # nothing is being recorded
+        assert L.mlxhip_last_status() == abi.ERR_FFI_FAILED
+        assert L.mlxhip_graph_launch(None, s) == abi.ERR_NULL_PTR
+        L.mlxhip_graph_free(None)
+    finally:
+        hb.destroy_stream(s)
