@@ -340,10 +340,10 @@ int mlxhip_ew_chain(const mlxhip_ew_instr_t* prog, size_t n_instr,
  * crates/mlx-core/src/cpu_kernels.rs:738-812, per head): for each b,
  *   O_b = softmax(Q_b K_b^T * scale, with -1e9 where causal && key > query) V_b,
  * Q_b and O_b [tq, dh], K_b and V_b [tk, dh], f32, contiguous and packed one
- * head after another (head b starts at b*tq*dh / b*tk*dh); Q and K 16-byte
- * aligned. The 16 score rows of a query block stay in LDS: dh must be 16, 32,
- * 64 or 128, and 16*(tk+1) floats must fit in 159 KiB (tk up to 2542);
- * otherwise MLXHIP_ERR_INVALID_ARGUMENT. The Attention op
+ * head after another (head b starts at b*tq*dh / b*tk*dh); Q, K, V and O
+ * 16-byte aligned. Keys are streamed in tiles with a running softmax, so tk is
+ * not bounded by on-chip memory; dh must be 16, 32, 64 or 128, otherwise
+ * MLXHIP_ERR_INVALID_ARGUMENT. The Attention op
  * of mlxhip_eval_node* uses this kernel when the shape allows and the
  * GEMM + softmax + GEMM sequence otherwise. Replaces the per-head Narrow +
  * Attention of MultiHeadAttention (crates/mlx-nn/src/attention.rs:47-111)

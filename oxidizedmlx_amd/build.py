@@ -43,10 +43,18 @@ SOURCES = [
 ]
 
 
+# Per-source flags. The attention kernel rescales its MFMA accumulators with
+# VALU multiplies every key tile; in the VGPR form of the MFMA instructions
+# they are not copied to and from the accumulation registers for that.
+EXTRA = {
+    "kernels/attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: str) -> tuple[str, float]:
     path = os.path.join(CSRC, src)
     obj = os.path.join(BUILD, src.replace("/", "_") + ".o")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, "-c", path, "-o", obj]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, *EXTRA.get(src, []), "-c", path, "-o", obj]
     if src.endswith(".cpp"):
         cmd = [HIPCC, "-x", "hip", f"--offload-arch={ARCH}", *COMMON, "-c", path, "-o", obj]
     t = time.time()

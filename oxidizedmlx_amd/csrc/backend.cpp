@@ -42,6 +42,9 @@ int fail(int code, const char* fmt, ...) {
 }
 
 int hip_fail(hipError_t e, const char* what) {
+    // A failed runtime call also sets the thread's last error, which the next
+    // launch check would report again for an unrelated kernel: consume it.
+    (void)hipGetLastError();
     return fail(MLXHIP_ERR_FFI_FAILED, "%s failed: %s", what, hipGetErrorString(e));
 }
 
@@ -277,7 +280,8 @@ int eval_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inp
     MLXHIP_TRY(expect_len(tq * dh, numel_of(meta.shape, meta.ndim), "attention"));
     if (tq * dh == 0) return MLXHIP_OK;
     if (tk > 0 && attention_fused_supported(dh, tq, tk) &&
-        ((reinterpret_cast<uintptr_t>(q.data) | reinterpret_cast<uintptr_t>(k.data)) % 16) == 0)
+        ((reinterpret_cast<uintptr_t>(q.data) | reinterpret_cast<uintptr_t>(k.data) |
+          reinterpret_cast<uintptr_t>(v.data) | reinterpret_cast<uintptr_t>(out)) % 16) == 0)
         return attention_fused(q.data, k.data, v.data, out, 1, tq, tk, dh, 0, 0, 0, 0, op.scale, op.causal, s);
     float* scores = scratch.get((size_t)std::max<int64_t>(1, tq * tk));
     float* probs = scratch.get((size_t)std::max<int64_t>(1, tq * tk));

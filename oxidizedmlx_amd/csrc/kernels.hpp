@@ -112,13 +112,10 @@ int dec_finish(const uint64_t* part, int groups, int* tokens, int* argmax_out, c
 int dec_set_counter(int* p, int v, hipStream_t s);
 
 // ── attention.hip (fused scaled, masked attention of a batch of heads) ────
-constexpr int ATTN_LDS_LIMIT = 159 * 1024;
-size_t attention_fused_lds_bytes(int dh, int64_t tk);
-// dh in {16, 32, 64, 128} and the score rows of 16 queries fit in LDS
-// (tk up to 2542).
+// dh in {16, 32, 64, 128}; any tq, tk >= 1 (keys are streamed in tiles).
 bool attention_fused_supported(int64_t dh, int64_t tq, int64_t tk);
 // Q [batch][tq][dh], K/V [batch][tk][dh], O [batch][tq][dh], row-major with
-// batch strides sq/sk/sv/so (elements).
+// batch strides sq/sk/sv/so (elements); Q, K, V and O 16-byte aligned.
 int attention_fused(const float* q, const float* k, const float* v, float* o, int64_t batch, int64_t tq,
                     int64_t tk, int64_t dh, int64_t sq, int64_t sk, int64_t sv, int64_t so, float scale,
                     int causal, hipStream_t s);

@@ -69,6 +69,12 @@ def test_graph_errors():
     try:
         assert not L.mlxhip_graph_end(s)             # nothing is being recorded
         assert L.mlxhip_last_status() == abi.ERR_FFI_FAILED
+        # The failed end of capture is reported once, not again by the next launch.
+        x = synth.normal(9, (4, 100))
+        X, Y = hb.DeviceBuffer.from_array(x), hb.DeviceBuffer(x.nbytes)
+        hb.softmax_rows(X, Y, 4, 100, stream=s)
+        hb.synchronize(s)
+        np.testing.assert_allclose(Y.download(np.float32, x.size).reshape(x.shape).sum(1), 1.0, rtol=1e-5)
         assert L.mlxhip_graph_launch(None, s) == abi.ERR_NULL_PTR
         L.mlxhip_graph_free(None)
     finally:
