@@ -477,20 +477,25 @@ void gemm16_kernel(Args g) {
 }
 
 // Host-side check of what the kernel assumes about its operands; returns
-// false when the general GEMM must run instead.
+// false when the general GEMM must run instead. `padded`: every row of both
+// operands may be read up to its leading dimension (the zero-padded copies
+// the dispatcher makes of unaligned operands); then an M or N extent need not
+// be a multiple of 8 (the chunk that crosses it only feeds rows / columns of
+// C that are never stored). K extents must be, in any case: a chunk crossing
+// K would multiply what lies past it.
 inline bool supported(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
                       int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, uint32_t* a_bytes,
-                      uint32_t* b_bytes) {
+                      uint32_t* b_bytes, bool padded = false) {
     if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(b) % 16) return false;
     if (k >= (1 << 30)) return false;  // k offsets are 32-bit in the kernel
     if (lda % 8 || ldb % 8) return false;
     if (batch > 1 && (sa % 8 || sb % 8)) return false;
     // The contiguous extent of each operand must hold whole 16-byte chunks.
-    if ((ta == 0 ? k : m) % 8) return false;
-    if ((tb == 1 ? k : n) % 8) return false;
+    if ((ta == 0 ? k : m) % 8 && !(padded && ta == 1)) return false;
+    if ((tb == 1 ? k : n) % 8 && !(padded && tb == 0)) return false;
     const int64_t a_rows = ta ? k : m, b_rows = tb ? n : k;
-    const int64_t a_ext = ((a_rows - 1) * lda + (ta ? m : k)) * 2;
-    const int64_t b_ext = ((b_rows - 1) * ldb + (tb ? k : n)) * 2;
+    const int64_t a_ext = ((a_rows - 1) * lda + (padded ? lda : (ta ? m : k))) * 2;
+    const int64_t b_ext = ((b_rows - 1) * ldb + (padded ? ldb : (tb ? k : n))) * 2;
     const int64_t lim = (int64_t)OOB - 4096;
     if (a_ext <= 0 || b_ext <= 0 || a_ext >= lim || b_ext >= lim) return false;
     *a_bytes = (uint32_t)a_ext;
