@@ -125,3 +125,27 @@ def test_entry_point_errors():
     L = abi.load_library()
     assert L.mlxhip_attention(None, None, None, None, 1, 4, 4, 16, 1.0, 0, None) == abi.ERR_NULL_PTR
     hb.attention(q, q, q, q, 0, 4, 4, 16, 1.0, False)                # empty batch: nothing to do
+
+
+@pytest.mark.parametrize("misalign", ["q", "out"])
+def test_misaligned_operands_take_the_unfused_path(misalign):
+    """The fused kernel needs 16-byte aligned Q, K, V and O rows; an Attention
+    node on operands offset by one float (mlxhip_eval_node_dev) runs the GEMM
+    + scaled-masked softmax + GEMM sequence and still matches the oracle."""
+    tq, tk, dh = 40, 72, 64
+    q, k, v = qkv(tq, tk, dh, 31)
+    scale = 1.0 / math.sqrt(dh)
+    bufs = {}
+    for name, a in (("q", q), ("k", k), ("v", v)):
+        off = 1 if name == misalign else 0
+        b = hb.DeviceBuffer((a.size + 4) * 4)
+        b.upload(np.concatenate([np.zeros(off, np.float32), a.ravel(), np.zeros(4 - off, np.float32)]))
+        bufs[name] = (b, off)
+    out_off = 1 if misalign == "out" else 0
+    out = hb.DeviceBuffer((tq * dh + 4) * 4)
+    ins = [(bufs[n][0].ptr + 4 * bufs[n][1], a.shape) for n, a in (("q", q), ("k", k), ("v", v))]
+    hb.eval_node_dev(OpKind.Attention(scale, True), ins, meta([tq, dh]), out.ptr + 4 * out_off)
+    hb.synchronize()
+    got = out.download(np.float32, tq * dh, offset=4 * out_off).reshape(tq, dh)
+    assert_allclose(got, cpu_attention(q, k, v, scale, True), 2e-6 * float(np.abs(v).max()), 1e-5,
+                    f"misaligned {misalign}")
