@@ -343,7 +343,10 @@ int mlxhip_ew_chain(const mlxhip_ew_instr_t* prog, size_t n_instr,
  * head after another (head b starts at b*tq*dh / b*tk*dh); Q, K, V and O
  * 16-byte aligned. Keys are streamed in tiles with a running softmax, so tk is
  * not bounded by on-chip memory; dh must be 16, 32, 64 or 128, otherwise
- * MLXHIP_ERR_INVALID_ARGUMENT. The Attention op
+ * MLXHIP_ERR_INVALID_ARGUMENT. The f32 products run on the bf16 matrix
+ * cores as exact three-term splits (f32-level accuracy); a non-finite Q, K
+ * or V element makes its rows NaN where the reference may give +-inf. The
+ * Attention op
  * of mlxhip_eval_node* uses this kernel when the shape allows and the
  * GEMM + softmax + GEMM sequence otherwise. Replaces the per-head Narrow +
  * Attention of MultiHeadAttention (crates/mlx-nn/src/attention.rs:47-111)
