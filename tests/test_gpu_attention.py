@@ -149,3 +149,35 @@ def test_misaligned_operands_take_the_unfused_path(misalign):
     got = out.download(np.float32, tq * dh, offset=4 * out_off).reshape(tq, dh)
     assert_allclose(got, cpu_attention(q, k, v, scale, True), 2e-6 * float(np.abs(v).max()), 1e-5,
                     f"misaligned {misalign}")
+
+
+def f64_attention(q, k, v, scale, causal):
+    q, k, v = (a.astype(np.float64) for a in (q, k, v))
+    sc = q @ k.T * scale
+    if causal:
+        sc = np.where(np.arange(k.shape[0])[None, :] > np.arange(q.shape[0])[:, None], -np.inf, sc)
+    e = np.exp(sc - sc.max(1, keepdims=True))
+    return (e / e.sum(1, keepdims=True)) @ v
+
+
+@pytest.mark.parametrize("dh,causal", [(128, True), (64, False), (32, True)])
+def test_large_scores(dh, causal):
+    """Q and K of N(0, 3^2) put scores in the tens. There the reference's own
+    f32 rounding of a score (about |s| * 2^-24 per term) moves the output by
+    ~1e-5, as much as the usual tolerance, so both are held against float64:
+    the GPU's largest error must stay within twice the reference's (plus
+    2e-6 * max|V|). A split that lost bits would be off by ~1e-3."""
+    tq, tk = 96, 300
+    q, k, v = qkv(tq, tk, dh, 53)
+    q, k = (q * 3.0).astype(np.float32), (k * 3.0).astype(np.float32)
+    scale = 1.0 / math.sqrt(dh)
+    s = hb.HipStream()
+    nq, nk, nv = (s.add_constant(a, meta(list(a.shape))) for a in (q, k, v))
+    y = s.add_op(OpKind.Attention(scale, causal), [nq, nk, nv], meta([tq, dh]))
+    s.eval(y)
+    got = s.get_buffer(y).reshape(tq, dh).astype(np.float64)
+    exact = f64_attention(q, k, v, scale, causal)
+    ref_err = float(np.abs(cpu_attention(q, k, v, scale, causal) - exact).max())
+    gpu_err = float(np.abs(got - exact).max())
+    print(f"dh={dh} causal={causal}: max |gpu - f64| {gpu_err:.3e}, max |oracle - f64| {ref_err:.3e}")
+    assert gpu_err <= 2.0 * ref_err + 2e-6 * float(np.abs(v).max())
