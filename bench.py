@@ -98,7 +98,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only; --gpus must be 1 "
-              "(multi-GPU sharding is described in DESIGN.md, not run).", file=sys.stderr)
+              "(sharding over several GPUs is designed, not built or run).", file=sys.stderr)
         return 2
 
     from oxidizedmlx_amd import abi
