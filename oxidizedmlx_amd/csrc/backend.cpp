@@ -118,7 +118,10 @@ void* pool_alloc(size_t bytes) {
     }
     void* p = nullptr;
     if (hipMalloc(&p, sz) != hipSuccess) {
-        // Drop cached blocks of this device and retry once.
+        // A failed hipMalloc also sets the thread's last error, which the next
+        // launch check would report for an unrelated kernel: consume it. Then
+        // drop cached blocks of this device and retry once.
+        (void)hipGetLastError();
         std::vector<void*> drop;
         {
             std::lock_guard<std::mutex> g(P.mu);
@@ -127,7 +130,10 @@ void* pool_alloc(size_t bytes) {
             for (void* q : drop) P.owned.erase(q);
         }
         for (void* q : drop) (void)hipFree(q);
-        if (hipMalloc(&p, sz) != hipSuccess) return nullptr;
+        if (hipMalloc(&p, sz) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
     }
     std::lock_guard<std::mutex> g(P.mu);
     P.owned[p] = {dev, sz};
@@ -616,6 +622,7 @@ mlxhip_buffer_t* mlxhip_buffer_alloc(size_t bytes) {
     if (ensure_device() != MLXHIP_OK) return nullptr;
     void* p = nullptr;
     if (bytes && hipMalloc(&p, bytes) != hipSuccess) {
+        (void)hipGetLastError();  // not to be reported by a later launch check
         fail(MLXHIP_ERR_FFI_FAILED, "hipMalloc(%zu) failed", bytes);
         return nullptr;
     }

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/mlxhip.h"
@@ -49,5 +50,33 @@ inline int launch_check(const char* kernel) {
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Stream-ordered scratch: allocated on `s`, returned to the device's memory
+// pool on `s` after every kernel enqueued before the destructor has run.
+struct StreamBuf {
+    void* p = nullptr;
+    hipStream_t s;
+    explicit StreamBuf(hipStream_t st) : s(st) {}
+    int alloc(size_t bytes) {
+        static std::once_flag keep[64];
+        int dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+            std::call_once(keep[dev], [dev] {
+                // Keep freed blocks in the pool instead of returning them to the
+                // driver at every synchronisation.
+                hipMemPool_t pool;
+                if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+                    uint64_t hi = UINT64_MAX;
+                    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &hi);
+                }
+            });
+        }
+        MLXHIP_HIP(hipMallocAsync(&p, bytes ? bytes : 16, s));
+        return MLXHIP_OK;
+    }
+    ~StreamBuf() {
+        if (p) (void)hipFreeAsync(p, s);
+    }
+};
 
 }  // namespace mlxhip

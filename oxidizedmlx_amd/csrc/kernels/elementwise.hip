@@ -310,11 +310,13 @@ __global__ void reduce_all_seq_kernel(int kind, const float* __restrict__ x, flo
     y[0] = v;
 }
 
-// Tree reduction for large inputs: per-block partials, then one block folds them.
+// Tree reduction for large inputs (more than 65536 values): per-block
+// partials, then one block folds them. The order of the additions differs
+// from the sequential fold, so a sum or mean agrees with it to rounding.
 __global__ __launch_bounds__(BLOCK) void reduce_partial_kernel(int kind, const float* __restrict__ x,
                                                                float* __restrict__ part, int64_t n) {
     __shared__ float sm[BLOCK];
-    float v = kind == 2 ? -INFINITY : 0.0f;
+    float v = kind == 2 ? -INFINITY : -0.0f;  // -0.0: a sum of -0.0s stays -0.0, as in the sequential fold
     for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < n; i += (int64_t)gridDim.x * BLOCK)
         v = kind == 2 ? fmaxf(v, x[i]) : v + x[i];
     sm[threadIdx.x] = v;
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(BLOCK) void reduce_partial_kernel(int kind, const f
 __global__ __launch_bounds__(BLOCK) void reduce_final_kernel(int kind, const float* __restrict__ part,
                                                              float* __restrict__ y, int np, int64_t n) {
     __shared__ float sm[BLOCK];
-    float v = kind == 2 ? -INFINITY : 0.0f;
+    float v = kind == 2 ? -INFINITY : -0.0f;
     for (int i = threadIdx.x; i < np; i += BLOCK) v = kind == 2 ? fmaxf(v, part[i]) : v + part[i];
     sm[threadIdx.x] = v;
     __syncthreads();
@@ -616,31 +618,17 @@ int reduce_axis(int kind, const float* x, float* y, int64_t outer, int64_t dim, 
     return launch_check("reduce_axis_kernel");
 }
 
-// Scratch for the tree reduction: a per-device partials buffer, grown on
-// demand and kept for the process lifetime.
-static float* partials(int need) {
-    static thread_local float* buf[64] = {};
-    static thread_local int cap[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    if (cap[dev] < need) {
-        if (buf[dev]) (void)hipFree(buf[dev]);
-        buf[dev] = nullptr;
-        cap[dev] = 0;
-        if (hipMalloc(&buf[dev], sizeof(float) * need) != hipSuccess) return nullptr;
-        cap[dev] = need;
-    }
-    return buf[dev];
-}
-
 int reduce_all(int kind, const float* x, float* y, int64_t n, hipStream_t s) {
     if (n <= 65536) {
         hipLaunchKernelGGL(reduce_all_seq_kernel, dim3(1), dim3(64), 0, s, kind, x, y, n);
         return launch_check("reduce_all_seq_kernel");
     }
+    // Partials of the tree reduction: stream-ordered scratch, so calls on
+    // different streams never share it.
     const int np = 1024;
-    float* part = partials(np);
-    if (!part) return fail(MLXHIP_ERR_FFI_FAILED, "reduce_all: scratch allocation failed");
+    StreamBuf pb(s);
+    MLXHIP_TRY(pb.alloc(sizeof(float) * np));
+    float* part = static_cast<float*>(pb.p);
     hipLaunchKernelGGL(reduce_partial_kernel, dim3(np), dim3(BLOCK), 0, s, kind, x, part, n);
     MLXHIP_TRY(launch_check("reduce_partial_kernel"));
     hipLaunchKernelGGL(reduce_final_kernel, dim3(1), dim3(BLOCK), 0, s, kind, part, y, np, n);

@@ -51,34 +51,6 @@ __global__ __launch_bounds__(256) void pack_kernel(const T* __restrict__ src, in
     dst[b * rows_p * cols_p + idx] = (r < rows && c < cols) ? src[b * sstride + r * ld + c] : T(0);
 }
 
-// Stream-ordered scratch: allocated on `s`, returned to the device's memory
-// pool on `s` after every kernel enqueued before the destructor has run.
-struct StreamBuf {
-    void* p = nullptr;
-    hipStream_t s;
-    explicit StreamBuf(hipStream_t st) : s(st) {}
-    int alloc(size_t bytes) {
-        static std::once_flag keep[64];
-        int dev = 0;
-        if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
-            std::call_once(keep[dev], [dev] {
-                // Keep freed blocks in the pool instead of returning them to the
-                // driver at every synchronisation.
-                hipMemPool_t pool;
-                if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-                    uint64_t hi = UINT64_MAX;
-                    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &hi);
-                }
-            });
-        }
-        MLXHIP_HIP(hipMallocAsync(&p, bytes ? bytes : 16, s));
-        return MLXHIP_OK;
-    }
-    ~StreamBuf() {
-        if (p) (void)hipFreeAsync(p, s);
-    }
-};
-
 int pack(int dt, const void* src, int64_t ld, int64_t sstride, int64_t rows, int64_t cols, void* dst,
          int64_t rows_p, int64_t cols_p, int64_t batch, hipStream_t s) {
     dim3 grid((unsigned)ceil_div(rows_p * cols_p, 256), (unsigned)batch);

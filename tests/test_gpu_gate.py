@@ -203,3 +203,25 @@ def test_parity_broadcast_narrow_concat_embedding_rope_mlx():
     for trad in (True, False):
         run_parity(lambda s: unary_op(s, OpKind.RoPE(10000.0, 3, trad), r, meta([6, 16])),
                    5e-4, 5e-3, f"RoPE traditional={trad}")
+
+
+def test_reductions_over_all_large_input():
+    # More than 65536 values take the tree reduction (per-block partials,
+    # then one folding block): Max is exact; Sum and Mean differ from the
+    # sequential f32 fold only by rounding, bounded by n·eps·Σ|x|, and so
+    # does each from the float64 sum.
+    n = 300_001
+    x = gen_data(n, 160)
+    x64 = x.astype(np.float64)
+    bound = n * float(np.finfo(np.float32).eps) * float(np.abs(x64).sum())
+    for op, tol, exact in [(OpKind.Sum(None), bound, x64.sum()), (OpKind.Mean(None), bound / n, x64.sum() / n)]:
+        h, _ = run_parity(lambda s: s.add_op(op, [s.add_constant(x, meta([n]))], meta([])), tol, 0.0, repr(op))
+        assert abs(float(h[0]) - exact) <= tol
+    h, c = run_parity(lambda s: s.add_op(OpKind.Max(None), [s.add_constant(x, meta([n]))], meta([])),
+                      0.0, 0.0, "Max(None)")
+    assert float(h[0]) == float(x.max())
+    # A sum of negative zeros is -0.0 on both paths (sign bit checked).
+    z = np.full(n, -0.0, np.float32)
+    h, c = run_parity(lambda s: s.add_op(OpKind.Sum(None), [s.add_constant(z, meta([n]))], meta([])),
+                      0.0, 0.0, "Sum(-0.0)")
+    assert np.signbit(h[0]) and np.signbit(c[0])
