@@ -16,12 +16,21 @@
 #include "../kernels.hpp"
 #include "device_math.hpp"
 
+#include <algorithm>
+
 #pragma clang fp contract(off)
 
 namespace mlxhip {
 namespace {
 
 constexpr int BLOCK = 256;
+
+// Per-element kernels walk [0, n) with a grid-stride loop and the host caps
+// their grid at MAX_GRID workgroups (grid_for), so no launch exceeds the
+// 32-bit work-item count of a dispatch, whatever the tensor size.
+constexpr int64_t MAX_GRID = int64_t(1) << 18;
+#define FOR_EACH_ELEMENT(i, n) \
+    for (int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x; i < (n); i += (int64_t)gridDim.x * BLOCK)
 
 using dev::sigmoid_ref;
 
@@ -180,18 +189,19 @@ int launch_chain_vec(const EwProg& p, float* out, int64_t n_vec, bool periodic, 
 __global__ __launch_bounds__(BLOCK) void ew_chain_scalar_kernel(EwProg prog, float* __restrict__ out,
                                                                 int64_t begin, int64_t n) {
     // Periods are in elements here.
-    const int64_t i = begin + (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (i >= n) return;
-    auto at = [&](int in) {
-        const int64_t p = prog.period[in];
-        return prog.in[in][p > 0 ? i % p : i];
-    };
-    float acc = at(0);
-    for (int k = 0; k < prog.n_instr; ++k) {
-        const int op = prog.op[k];
-        acc = apply(op, acc, ew_binary(op) ? at(prog.operand[k]) : 0.f);
+    FOR_EACH_ELEMENT(j, n - begin) {
+        const int64_t i = begin + j;
+        auto at = [&](int in) {
+            const int64_t p = prog.period[in];
+            return prog.in[in][p > 0 ? i % p : i];
+        };
+        float acc = at(0);
+        for (int k = 0; k < prog.n_instr; ++k) {
+            const int op = prog.op[k];
+            acc = apply(op, acc, ew_binary(op) ? at(prog.operand[k]) : 0.f);
+        }
+        out[i] = acc;
     }
-    out[i] = acc;
 }
 
 // 2-D transpose through a padded 64x64 LDS tile (the +1 column breaks the
@@ -224,30 +234,30 @@ __global__ __launch_bounds__(BLOCK) void permute_kernel(const float* __restrict_
                                                         float* __restrict__ y, Dims new_shape,
                                                         Dims old_stride_of_new, int ndim,
                                                         int64_t total) {
-    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (f >= total) return;
-    int64_t rem = f, src = 0;
-    for (int d = ndim - 1; d >= 0; --d) {
-        const int64_t c = rem % new_shape.v[d];
-        rem /= new_shape.v[d];
-        src += c * old_stride_of_new.v[d];
+    FOR_EACH_ELEMENT(f, total) {
+        int64_t rem = f, src = 0;
+        for (int d = ndim - 1; d >= 0; --d) {
+            const int64_t c = rem % new_shape.v[d];
+            rem /= new_shape.v[d];
+            src += c * old_stride_of_new.v[d];
+        }
+        y[f] = x[src];
     }
-    y[f] = x[src];
 }
 
 __global__ __launch_bounds__(BLOCK) void broadcast_kernel(const float* __restrict__ x,
                                                           float* __restrict__ y, Dims out_shape,
                                                           Dims in_stride, int out_ndim,
                                                           int64_t total) {
-    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (f >= total) return;
-    int64_t rem = f, src = 0;
-    for (int d = out_ndim - 1; d >= 0; --d) {
-        const int64_t c = rem % out_shape.v[d];
-        rem /= out_shape.v[d];
-        src += c * in_stride.v[d];
+    FOR_EACH_ELEMENT(f, total) {
+        int64_t rem = f, src = 0;
+        for (int d = out_ndim - 1; d >= 0; --d) {
+            const int64_t c = rem % out_shape.v[d];
+            rem /= out_shape.v[d];
+            src += c * in_stride.v[d];
+        }
+        y[f] = x[src];
     }
-    y[f] = x[src];
 }
 
 // One thread per output element; sequential fold in the reference's order
@@ -255,7 +265,8 @@ __global__ __launch_bounds__(BLOCK) void broadcast_kernel(const float* __restric
 // result is bit-identical to the CPU's. The fold is a chain of dependent
 // adds, so each thread loads RED_U elements ahead and then folds them in
 // order: the loads overlap instead of each waiting out a memory latency. One
-// wave per workgroup spreads the (often few) outputs over more CUs.
+// wave per workgroup spreads the (often few) outputs over more CUs; the
+// grid is capped and strides over the outputs.
 // KIND: 0 Sum, 1 Mean, 2 Max.
 constexpr int RED_U = 64;
 constexpr int RED_BLOCK = 64;
@@ -268,36 +279,37 @@ __device__ inline float fold(float v, float x) {
 template <int KIND>
 __global__ __launch_bounds__(RED_BLOCK) void reduce_axis_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                                 int64_t outer, int64_t dim, int64_t inner) {
-    const int64_t f = (int64_t)blockIdx.x * RED_BLOCK + threadIdx.x;
-    if (f >= outer * inner) return;
-    const int64_t o = f / inner, i = f % inner;
-    const float* p = x + o * dim * inner + i;
-    float v = KIND == 2 ? -INFINITY : -0.0f;
-    // Two register batches in turn: batch b is loaded while batch a is
-    // folded and the other way round, so memory latency overlaps the chain
-    // of dependent adds; neither batch is ever copied (a copy would wait for
-    // its loads).
-    const int64_t full = dim / (2 * RED_U) * (2 * RED_U);
-    float a[RED_U], b[RED_U];
-    if (full > 0) {
+    for (int64_t f = (int64_t)blockIdx.x * RED_BLOCK + threadIdx.x; f < outer * inner;
+         f += (int64_t)gridDim.x * RED_BLOCK) {
+        const int64_t o = f / inner, i = f % inner;
+        const float* p = x + o * dim * inner + i;
+        float v = KIND == 2 ? -INFINITY : -0.0f;
+        // Two register batches in turn: batch b is loaded while batch a is
+        // folded and the other way round, so memory latency overlaps the chain
+        // of dependent adds; neither batch is ever copied (a copy would wait for
+        // its loads).
+        const int64_t full = dim / (2 * RED_U) * (2 * RED_U);
+        float a[RED_U], b[RED_U];
+        if (full > 0) {
 #pragma unroll
-        for (int u = 0; u < RED_U; ++u) a[u] = p[(int64_t)u * inner];
-    }
-    for (int64_t d = 0; d < full; d += 2 * RED_U) {
-#pragma unroll
-        for (int u = 0; u < RED_U; ++u) b[u] = p[(d + RED_U + u) * inner];
-#pragma unroll
-        for (int u = 0; u < RED_U; ++u) v = fold<KIND>(v, a[u]);
-        if (d + 2 * RED_U < full) {
-#pragma unroll
-            for (int u = 0; u < RED_U; ++u) a[u] = p[(d + 2 * RED_U + u) * inner];
+            for (int u = 0; u < RED_U; ++u) a[u] = p[(int64_t)u * inner];
         }
+        for (int64_t d = 0; d < full; d += 2 * RED_U) {
 #pragma unroll
-        for (int u = 0; u < RED_U; ++u) v = fold<KIND>(v, b[u]);
+            for (int u = 0; u < RED_U; ++u) b[u] = p[(d + RED_U + u) * inner];
+#pragma unroll
+            for (int u = 0; u < RED_U; ++u) v = fold<KIND>(v, a[u]);
+            if (d + 2 * RED_U < full) {
+#pragma unroll
+                for (int u = 0; u < RED_U; ++u) a[u] = p[(d + 2 * RED_U + u) * inner];
+            }
+#pragma unroll
+            for (int u = 0; u < RED_U; ++u) v = fold<KIND>(v, b[u]);
+        }
+        for (int64_t d = full; d < dim; ++d) v = fold<KIND>(v, p[d * inner]);
+        if (KIND == 1) v = v / (float)dim;
+        y[f] = v;
     }
-    for (int64_t d = full; d < dim; ++d) v = fold<KIND>(v, p[d * inner]);
-    if (KIND == 1) v = v / (float)dim;
-    y[f] = v;
 }
 
 // Sequential fold of all elements on one lane (bit-identical to the CPU fold).
@@ -355,15 +367,15 @@ __device__ inline uint16_t f32_to_bf16_rne(float f) {
 
 __global__ __launch_bounds__(BLOCK) void cast_kernel(const void* __restrict__ x, int src,
                                                      void* __restrict__ y, int dst, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (i >= n) return;
-    float v;
-    if (src == MLXHIP_DTYPE_F32) v = static_cast<const float*>(x)[i];
-    else if (src == MLXHIP_DTYPE_BF16) v = __uint_as_float((uint32_t)static_cast<const uint16_t*>(x)[i] << 16);
-    else v = (float)static_cast<const _Float16*>(x)[i];
-    if (dst == MLXHIP_DTYPE_F32) static_cast<float*>(y)[i] = v;
-    else if (dst == MLXHIP_DTYPE_BF16) static_cast<uint16_t*>(y)[i] = f32_to_bf16_rne(v);
-    else static_cast<_Float16*>(y)[i] = (_Float16)v;
+    FOR_EACH_ELEMENT(i, n) {
+        float v;
+        if (src == MLXHIP_DTYPE_F32) v = static_cast<const float*>(x)[i];
+        else if (src == MLXHIP_DTYPE_BF16) v = __uint_as_float((uint32_t)static_cast<const uint16_t*>(x)[i] << 16);
+        else v = (float)static_cast<const _Float16*>(x)[i];
+        if (dst == MLXHIP_DTYPE_F32) static_cast<float*>(y)[i] = v;
+        else if (dst == MLXHIP_DTYPE_BF16) static_cast<uint16_t*>(y)[i] = f32_to_bf16_rne(v);
+        else static_cast<_Float16*>(y)[i] = (_Float16)v;
+    }
 }
 
 // Rust's `f as i32`: saturating, NaN -> 0.
@@ -378,32 +390,32 @@ __global__ __launch_bounds__(BLOCK) void embedding_kernel(const float* __restric
                                                           const float* __restrict__ idx,
                                                           float* __restrict__ y, int64_t n_idx,
                                                           int64_t num_emb, int64_t dim) {
-    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (f >= n_idx * dim) return;
-    const int64_t i = f / dim, d = f % dim;
-    int64_t row = f2i_sat(idx[i]);
-    row = row < 0 ? 0 : (row > num_emb - 1 ? num_emb - 1 : row);
-    y[f] = w[row * dim + d];
+    FOR_EACH_ELEMENT(f, n_idx * dim) {
+        const int64_t i = f / dim, d = f % dim;
+        int64_t row = f2i_sat(idx[i]);
+        row = row < 0 ? 0 : (row > num_emb - 1 ? num_emb - 1 : row);
+        y[f] = w[row * dim + d];
+    }
 }
 
 __global__ __launch_bounds__(BLOCK) void narrow_kernel(const float* __restrict__ x,
                                                        float* __restrict__ y, int64_t outer,
                                                        int64_t dim, int64_t inner, int64_t start,
                                                        int64_t length) {
-    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (f >= outer * length * inner) return;
-    const int64_t o = f / (length * inner), r = f % (length * inner);
-    y[f] = x[o * dim * inner + start * inner + r];
+    FOR_EACH_ELEMENT(f, outer * length * inner) {
+        const int64_t o = f / (length * inner), r = f % (length * inner);
+        y[f] = x[o * dim * inner + start * inner + r];
+    }
 }
 
 __global__ __launch_bounds__(BLOCK) void concat_kernel(const float* __restrict__ x,
                                                        float* __restrict__ y, int64_t outer,
                                                        int64_t d, int64_t inner, int64_t total,
                                                        int64_t at) {
-    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (f >= outer * d * inner) return;
-    const int64_t o = f / (d * inner), r = f % (d * inner);
-    y[o * total * inner + at * inner + r] = x[f];
+    FOR_EACH_ELEMENT(f, outer * d * inner) {
+        const int64_t o = f / (d * inner), r = f % (d * inner);
+        y[o * total * inner + at * inner + r] = x[f];
+    }
 }
 
 // OpKind::Rope (cpu_rope, cpu_kernels.rs:608-645): interleaved pairs of the
@@ -413,20 +425,20 @@ __global__ __launch_bounds__(BLOCK) void rope_interleaved_kernel(const float* __
                                                                  int64_t tokens, int64_t hd,
                                                                  int64_t rd, int64_t pos_offset,
                                                                  float theta, int64_t len) {
-    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (f >= len) return;
-    const int64_t t = f / hd, c = f % hd;
-    if (t >= tokens || c >= rd) {
-        y[f] = x[f];
-        return;
+    FOR_EACH_ELEMENT(f, len) {
+        const int64_t t = f / hd, c = f % hd;
+        if (t >= tokens || c >= rd) {
+            y[f] = x[f];
+            continue;
+        }
+        const int64_t i = c / 2;
+        const float inv_freq = powf(theta, -2.0f * (float)i / (float)rd);
+        const float angle = (float)(pos_offset + t) * inv_freq;
+        const float sn = sinf(angle), cs = cosf(angle);
+        const int64_t base = t * hd + i * 2;
+        const float x0 = x[base], x1 = x[base + 1];
+        y[f] = (c % 2 == 0) ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
     }
-    const int64_t i = c / 2;
-    const float inv_freq = powf(theta, -2.0f * (float)i / (float)rd);
-    const float angle = (float)(pos_offset + t) * inv_freq;
-    const float sn = sinf(angle), cs = cosf(angle);
-    const int64_t base = t * hd + i * 2;
-    const float x0 = x[base], x1 = x[base + 1];
-    y[f] = (c % 2 == 0) ? x0 * cs - x1 * sn : x0 * sn + x1 * cs;
 }
 
 // OpKind::RoPE (rope, cpu_kernels.rs:896-956).
@@ -434,32 +446,31 @@ __global__ __launch_bounds__(BLOCK) void rope_mlx_kernel(const float* __restrict
                                                          float* __restrict__ y, int64_t n_rows,
                                                          int64_t hd, int64_t offset, float base,
                                                          int traditional) {
-    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
     const int64_t half = hd / 2;
-    if (f >= n_rows * half) return;
-    const int64_t i = f / half, d = f % half;
-    const float pos = (float)(offset + i);
-    const float th = pos * powf(base, -(2.0f * (float)d / (float)hd));
-    const float ct = cosf(th), st = sinf(th);
-    int64_t i0, i1;
-    if (traditional) {
-        i0 = i * hd + 2 * d;
-        i1 = i0 + 1;
-    } else {
-        i0 = i * hd + d;
-        i1 = i * hd + d + half;
+    FOR_EACH_ELEMENT(f, n_rows * half) {
+        const int64_t i = f / half, d = f % half;
+        const float pos = (float)(offset + i);
+        const float th = pos * powf(base, -(2.0f * (float)d / (float)hd));
+        const float ct = cosf(th), st = sinf(th);
+        int64_t i0, i1;
+        if (traditional) {
+            i0 = i * hd + 2 * d;
+            i1 = i0 + 1;
+        } else {
+            i0 = i * hd + d;
+            i1 = i * hd + d + half;
+        }
+        const float x0 = x[i0], x1 = x[i1];
+        y[i0] = x0 * ct - x1 * st;
+        y[i1] = x0 * st + x1 * ct;
     }
-    const float x0 = x[i0], x1 = x[i1];
-    y[i0] = x0 * ct - x1 * st;
-    y[i1] = x0 * st + x1 * ct;
 }
 
 __global__ __launch_bounds__(BLOCK) void fill_kernel(float* __restrict__ y, float v, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (i < n) y[i] = v;
+    FOR_EACH_ELEMENT(i, n) y[i] = v;
 }
 
-inline unsigned grid_for(int64_t n) { return (unsigned)ceil_div(n, BLOCK); }
+inline unsigned grid_for(int64_t n) { return (unsigned)std::min<int64_t>(ceil_div(n, BLOCK), MAX_GRID); }
 
 }  // namespace
 
@@ -611,7 +622,7 @@ int reduce_axis(int kind, const float* x, float* y, int64_t outer, int64_t dim, 
                 hipStream_t s) {
     const int64_t n = outer * inner;
     if (n == 0) return MLXHIP_OK;
-    const dim3 grid((unsigned)ceil_div(n, RED_BLOCK));
+    const dim3 grid((unsigned)std::min<int64_t>(ceil_div(n, RED_BLOCK), MAX_GRID));
     if (kind == 0) hipLaunchKernelGGL(reduce_axis_kernel<0>, grid, dim3(RED_BLOCK), 0, s, x, y, outer, dim, inner);
     else if (kind == 1) hipLaunchKernelGGL(reduce_axis_kernel<1>, grid, dim3(RED_BLOCK), 0, s, x, y, outer, dim, inner);
     else hipLaunchKernelGGL(reduce_axis_kernel<2>, grid, dim3(RED_BLOCK), 0, s, x, y, outer, dim, inner);

@@ -13,13 +13,23 @@
 namespace mlxhip {
 namespace {
 
+// The per-element helper kernels below walk [0, n) of one matrix with a
+// grid-stride loop; elem_grid caps their x extent so no launch exceeds the
+// 32-bit work-item count of a dispatch, whatever the matrix size.
+#define FOR_EACH_ELEMENT(i, n) \
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < (n); i += (int64_t)gridDim.x * 256)
+
+dim3 elem_grid(int64_t n, int64_t batch) {
+    return dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), int64_t(1) << 18), (unsigned)batch);
+}
+
 __global__ __launch_bounds__(256) void zero_c_kernel(char* c, int64_t ldc, int64_t sc, int64_t m,
                                                      int64_t n, int elem) {
-    const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (f >= m * n) return;
-    const int64_t r = f / n, col = f % n;
-    char* p = c + ((int64_t)blockIdx.y * sc + r * ldc + col) * elem;
-    for (int e = 0; e < elem; ++e) p[e] = 0;
+    FOR_EACH_ELEMENT(f, m * n) {
+        const int64_t r = f / n, col = f % n;
+        char* p = c + ((int64_t)blockIdx.y * sc + r * ldc + col) * elem;
+        for (int e = 0; e < elem; ++e) p[e] = 0;
+    }
 }
 
 int elem_size(int dt) { return dt == MLXHIP_DTYPE_F32 ? 4 : 2; }
@@ -29,14 +39,14 @@ int elem_size(int dt) { return dt == MLXHIP_DTYPE_F32 ? 4 : 2; }
 template <int CT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, void* c, int64_t m,
                                                             int64_t n, int64_t ldc, int64_t sc, int splits) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= m * n) return;
     const int64_t b = blockIdx.y;
-    const float* p = ws + b * splits * m * n + idx;
-    float acc = p[0];
-    for (int s = 1; s < splits; ++s) acc += p[(int64_t)s * m * n];
-    const int64_t row = idx / n, col = idx % n;
-    gemm_detail::store_c<CT>(c, b * sc + row * ldc + col, acc);
+    FOR_EACH_ELEMENT(idx, m * n) {
+        const float* p = ws + b * splits * m * n + idx;
+        float acc = p[0];
+        for (int s = 1; s < splits; ++s) acc += p[(int64_t)s * m * n];
+        const int64_t row = idx / n, col = idx % n;
+        gemm_detail::store_c<CT>(c, b * sc + row * ldc + col, acc);
+    }
 }
 
 // dst[r][c] = src[r][c] for r < rows, c < cols, zero elsewhere in the
@@ -45,15 +55,16 @@ template <typename T>
 __global__ __launch_bounds__(256) void pack_kernel(const T* __restrict__ src, int64_t ld, int64_t sstride,
                                                    int64_t rows, int64_t cols, T* __restrict__ dst,
                                                    int64_t rows_p, int64_t cols_p) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= rows_p * cols_p) return;
-    const int64_t r = idx / cols_p, c = idx % cols_p, b = blockIdx.y;
-    dst[b * rows_p * cols_p + idx] = (r < rows && c < cols) ? src[b * sstride + r * ld + c] : T(0);
+    const int64_t b = blockIdx.y;
+    FOR_EACH_ELEMENT(idx, rows_p * cols_p) {
+        const int64_t r = idx / cols_p, c = idx % cols_p;
+        dst[b * rows_p * cols_p + idx] = (r < rows && c < cols) ? src[b * sstride + r * ld + c] : T(0);
+    }
 }
 
 int pack(int dt, const void* src, int64_t ld, int64_t sstride, int64_t rows, int64_t cols, void* dst,
          int64_t rows_p, int64_t cols_p, int64_t batch, hipStream_t s) {
-    dim3 grid((unsigned)ceil_div(rows_p * cols_p, 256), (unsigned)batch);
+    const dim3 grid = elem_grid(rows_p * cols_p, batch);
     if (dt == MLXHIP_DTYPE_F32)
         hipLaunchKernelGGL(pack_kernel<uint32_t>, grid, dim3(256), 0, s, static_cast<const uint32_t*>(src), ld,
                            sstride, rows, cols, static_cast<uint32_t*>(dst), rows_p, cols_p);
@@ -109,7 +120,7 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     if (ldc < n) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: ldc %lld < n %lld", (long long)ldc, (long long)n);
     if (batch > 65535) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: batch %lld > 65535", (long long)batch);
     if (k == 0) {
-        dim3 grid((unsigned)ceil_div(m * n, 256), (unsigned)batch);
+        const dim3 grid = elem_grid(m * n, batch);
         hipLaunchKernelGGL(zero_c_kernel, grid, dim3(256), 0, s, static_cast<char*>(c), ldc, stride_c,
                            m, n, elem_size(c_dtype));
         return launch_check("zero_c_kernel");
@@ -240,7 +251,7 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     gp.ldc = n;
     gp.sc = m * n;
     MLXHIP_TRY(run(gp, MLXHIP_DTYPE_F32));
-    dim3 grid((unsigned)ceil_div(m * n, 256), (unsigned)batch);
+    const dim3 grid = elem_grid(m * n, batch);
     switch (c_dtype) {
         case MLXHIP_DTYPE_F32:
             hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_F32>, grid, dim3(256), 0, s,

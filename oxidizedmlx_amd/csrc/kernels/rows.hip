@@ -28,6 +28,8 @@
 #include "../kernels.hpp"
 #include "device_math.hpp"
 
+#include <algorithm>
+
 #pragma clang fp contract(off)
 
 namespace mlxhip {
@@ -372,21 +374,21 @@ __global__ __launch_bounds__(BLOCK) void fibre_softmax_kernel(const float* __res
                                                               float* __restrict__ y,
                                                               int64_t outer, int64_t dim,
                                                               int64_t inner) {
-    const int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x;
-    if (f >= outer * inner) return;
-    const int64_t o = f / inner, i = f % inner;
-    const int64_t base = o * dim * inner + i;
-    if (!VJP) {
-        float m = -INFINITY;
-        for (int64_t d = 0; d < dim; ++d) m = fmaxf(m, a[base + d * inner]);
-        float s = 0.0f;
-        for (int64_t d = 0; d < dim; ++d) s += expf(a[base + d * inner] - m);
-        for (int64_t d = 0; d < dim; ++d) y[base + d * inner] = expf(a[base + d * inner] - m) / s;
-    } else {
-        float dot = 0.0f;
-        for (int64_t d = 0; d < dim; ++d) dot += a[base + d * inner] * b[base + d * inner];
-        for (int64_t d = 0; d < dim; ++d)
-            y[base + d * inner] = b[base + d * inner] * (a[base + d * inner] - dot);
+    for (int64_t f = (int64_t)blockIdx.x * BLOCK + threadIdx.x; f < outer * inner; f += (int64_t)gridDim.x * BLOCK) {
+        const int64_t o = f / inner, i = f % inner;
+        const int64_t base = o * dim * inner + i;
+        if (!VJP) {
+            float m = -INFINITY;
+            for (int64_t d = 0; d < dim; ++d) m = fmaxf(m, a[base + d * inner]);
+            float s = 0.0f;
+            for (int64_t d = 0; d < dim; ++d) s += expf(a[base + d * inner] - m);
+            for (int64_t d = 0; d < dim; ++d) y[base + d * inner] = expf(a[base + d * inner] - m) / s;
+        } else {
+            float dot = 0.0f;
+            for (int64_t d = 0; d < dim; ++d) dot += a[base + d * inner] * b[base + d * inner];
+            for (int64_t d = 0; d < dim; ++d)
+                y[base + d * inner] = b[base + d * inner] * (a[base + d * inner] - dot);
+        }
     }
 }
 
@@ -458,6 +460,18 @@ int row_op(int op, const float* a, const float* b, float* y, int64_t rows, int64
     if (rows < 0 || cols < 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: negative size");
     if (rows > (int64_t)INT32_MAX) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: too many rows");
     if (cols > INT32_MAX) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "row op: row too long");
+    // Rows are independent: a long non-causal batch runs as launches of at
+    // most ROW_CHUNK rows, so no grid (up to 256 work-items per row) exceeds
+    // the 32-bit work-item count of a dispatch. A causal mask is indexed by
+    // the row, and causal score matrices are far below that size.
+    constexpr int64_t ROW_CHUNK = int64_t(1) << 22;
+    if (rows > ROW_CHUNK && !causal) {
+        for (int64_t r0 = 0; r0 < rows; r0 += ROW_CHUNK) {
+            const int64_t off = r0 * cols, n = std::min(ROW_CHUNK, rows - r0);
+            MLXHIP_TRY(row_op(op, a + off, b ? b + off : nullptr, y + off, n, cols, p, 0, s));
+        }
+        return MLXHIP_OK;
+    }
     // MLXHIP_ROW_WPR forces the waves per row (tuning); 0 / unset = automatic.
     const int fw = row_force_wpr();
     switch (op) {
@@ -480,7 +494,7 @@ int fibre_softmax(bool vjp, const float* a, const float* b, float* y, int64_t ou
                   int64_t inner, hipStream_t s) {
     const int64_t n = outer * inner;
     if (n == 0 || dim == 0) return MLXHIP_OK;
-    const int64_t grid = ceil_div(n, BLOCK);
+    const int64_t grid = std::min<int64_t>(ceil_div(n, BLOCK), int64_t(1) << 18);  // grid-stride beyond
     if (vjp)
         hipLaunchKernelGGL((fibre_softmax_kernel<true>), dim3((unsigned)grid), dim3(BLOCK), 0, s, a,
                            b, y, outer, dim, inner);
