@@ -350,7 +350,8 @@ int mlxhip_ew_chain(const mlxhip_ew_instr_t* prog, size_t n_instr,
  * of mlxhip_eval_node* uses this kernel when the shape allows and the
  * GEMM + softmax + GEMM sequence otherwise. Replaces the per-head Narrow +
  * Attention of MultiHeadAttention (crates/mlx-nn/src/attention.rs:47-111)
- * with one launch. */
+ * with one launch (several for a batch whose workgroups exceed one
+ * dispatch's 32-bit work-item count). */
 int mlxhip_attention(const float* q, const float* k, const float* v, float* o,
                      int64_t batch, int64_t tq, int64_t tk, int64_t dh,
                      float scale, int32_t causal, void* stream);

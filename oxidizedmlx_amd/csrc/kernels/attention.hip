@@ -443,23 +443,33 @@ bool attention_fused_supported(int64_t dh, int64_t tq, int64_t tk) {
 int attention_fused(const float* q, const float* k, const float* v, float* o, int64_t batch, int64_t tq,
                     int64_t tk, int64_t dh, int64_t sq, int64_t sk, int64_t sv, int64_t so, float scale,
                     int causal, hipStream_t s) {
-    if (batch <= 0 || batch > 65535) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: batch %lld", (long long)batch);
+    if (batch <= 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: batch %lld", (long long)batch);
     if (!attention_fused_supported(dh, tq, tk))
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: fused kernel unsupported for dh=%lld tq=%lld tk=%lld",
                     (long long)dh, (long long)tq, (long long)tk);
-    if (pairs_of(tq) * batch > INT32_MAX)
-        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: %lld heads of %lld queries exceed one launch",
-                    (long long)batch, (long long)tq);
+    // A dispatch counts its work-items in 32 bits: one launch holds at most
+    // (2^32 - 1) / ATT_THREADS workgroups. Heads are independent, so a larger
+    // batch runs as several launches.
+    const int64_t max_wg = int64_t(UINT32_MAX) / ATT_THREADS, np = pairs_of(tq);
+    if (np > max_wg)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: %lld queries exceed one launch", (long long)tq);
     const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                          reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
     if (al % 16 || (sq | sk | sv | so) % 4)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: Q, K, V and O need 16-byte aligned rows");
-    switch (dh) {
-        case 16: return launch<16>(q, k, v, o, batch, tq, tk, sq, sk, sv, so, scale, causal, s);
-        case 32: return launch<32>(q, k, v, o, batch, tq, tk, sq, sk, sv, so, scale, causal, s);
-        case 64: return launch<64>(q, k, v, o, batch, tq, tk, sq, sk, sv, so, scale, causal, s);
-        default: return launch<128>(q, k, v, o, batch, tq, tk, sq, sk, sv, so, scale, causal, s);
+    const int64_t per = max_wg / np;
+    for (int64_t b0 = 0; b0 < batch; b0 += per) {
+        const int64_t nb = std::min(per, batch - b0);
+        const float *qb = q + b0 * sq, *kb = k + b0 * sk, *vb = v + b0 * sv;
+        float* ob = o + b0 * so;
+        switch (dh) {
+            case 16: MLXHIP_TRY(launch<16>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, s)); break;
+            case 32: MLXHIP_TRY(launch<32>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, s)); break;
+            case 64: MLXHIP_TRY(launch<64>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, s)); break;
+            default: MLXHIP_TRY(launch<128>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, s)); break;
+        }
     }
+    return MLXHIP_OK;
 }
 
 }  // namespace mlxhip
