@@ -1,0 +1,148 @@
+"""Property-based parity over random shapes, in the manner of the
+reference's shape properties (crates/mlx-ops/tests/proptest_shapes.rs:89-262,
+broadcastable pairs and axis draws) but applied to the kernels: GEMMs with
+ragged extents in every layout and input dtype, row ops over any row length
+and alignment, N-d transposes, broadcasts, axis reductions and elementwise
+chains through the fusing stream.
+
+hypothesis runs derandomized, so every run draws the same cases. Each case is
+checked against the CPU oracle (numpy for pure data movement) at the
+tolerance its family uses in the other tests: GEMM 1e-5 rel + the
+summation-order bound (1e-2 rel for 16-bit inputs), row ops 1e-5 rel / 1e-6
+abs, elementwise 1e-5 rel / 1e-6 abs, data movement and axis sums bit for
+bit."""
+import numpy as np
+import pytest
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
+
+from oxidizedmlx_amd import backend as hb
+from oxidizedmlx_amd import synth
+from oxidizedmlx_amd.opkind import OpKind, meta
+from parity import assert_allclose, cpu_stream, hip_stream
+from test_gpu_gemm import BF16, F16, F32, check_gemm
+from test_gpu_rows import oracle, run_rows
+
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip", "oracle_lib")]
+
+CASES = settings(max_examples=150, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+
+
+@CASES
+@given(m=st.integers(1, 300), n=st.integers(1, 300), k=st.integers(0, 300), ta=st.booleans(), tb=st.booleans(),
+       ab=st.sampled_from([F32, BF16, F16]), batch=st.integers(1, 3))
+def test_gemm_any_shape(m, n, k, ta, tb, ab, batch):
+    print(f"gemm m={m} n={n} k={k} ta={ta} tb={tb} ab={ab} batch={batch}", flush=True)
+    check_gemm(m, n, k, ab, F32, ta, tb, batch=batch, seed=m * 7919 + n * 31 + k)
+
+
+@CASES
+@given(rows=st.integers(1, 40), cols=st.integers(1, 5000), offset=st.integers(0, 3),
+       op=st.sampled_from(["softmax", "layernorm", "rmsnorm"]))
+def test_row_ops_any_shape(rows, cols, offset, op):
+    print(f"{op} rows={rows} cols={cols} offset={offset}", flush=True)
+    x = synth.normal(rows * 10007 + cols, (rows, cols), 0.0, 2.0)
+    fn, kind = {"softmax": (hb.softmax_rows, OpKind.Softmax(-1)),
+                "layernorm": (lambda a, b, r, c: hb.layernorm_rows(a, b, r, c, 1e-5), OpKind.LayerNorm(1e-5)),
+                "rmsnorm": (lambda a, b, r, c: hb.rmsnorm_rows(a, b, r, c, 1e-5), OpKind.RmsNorm(1e-5))}[op]
+    assert_allclose(run_rows(fn, x, offset=offset), oracle(kind, x), 1e-6, 1e-5, f"{op} {rows}x{cols}+{offset}")
+
+
+@st.composite
+def shape_and_perm(draw):
+    shape = tuple(draw(st.lists(st.integers(1, 12), min_size=1, max_size=4)))
+    perm = tuple(draw(st.permutations(range(len(shape)))))
+    return shape, perm
+
+
+@CASES
+@given(sp=shape_and_perm())
+def test_transpose_any_rank(sp):
+    shape, perm = sp
+    print(f"transpose {shape} by {perm}", flush=True)
+    x = synth.normal(len(shape) * 101 + sum(shape), shape)
+    xb, yb = hb.DeviceBuffer.from_array(x), hb.DeviceBuffer(max(x.nbytes, 4))
+    out_shape = [shape[p] for p in perm]
+    hb.eval_node_dev(OpKind.Transpose(perm), [(xb, shape)], meta(out_shape), yb)
+    hb.synchronize()
+    np.testing.assert_array_equal(yb.download(count=x.size).reshape(out_shape), x.transpose(perm))
+
+
+@st.composite
+def broadcastable(draw):
+    out = draw(st.lists(st.integers(1, 6), min_size=1, max_size=4))
+    keep = draw(st.integers(0, len(out)))  # the input is a suffix of the output shape
+    src = [d if draw(st.booleans()) else 1 for d in out[len(out) - keep:]]
+    return tuple(src), tuple(out)
+
+
+@CASES
+@given(pair=broadcastable())
+def test_broadcast_any_pair(pair):
+    src, out = pair
+    print(f"broadcast {src} -> {out}", flush=True)
+    x = synth.normal(len(src) * 13 + len(out), src if src else (1,)).reshape(src)
+    xb, yb = hb.DeviceBuffer.from_array(np.ascontiguousarray(x).reshape(-1)), hb.DeviceBuffer(4 * int(np.prod(out)))
+    hb.eval_node_dev(OpKind.Broadcast(out), [(xb, src)], meta(out), yb)
+    hb.synchronize()
+    np.testing.assert_array_equal(yb.download(count=int(np.prod(out))).reshape(out), np.broadcast_to(x, out))
+
+
+@st.composite
+def shape_and_axis(draw):
+    shape = tuple(draw(st.lists(st.integers(1, 40), min_size=1, max_size=3)))
+    axis = draw(st.integers(0, len(shape) - 1))
+    return shape, axis - len(shape) if draw(st.booleans()) else axis
+
+
+@CASES
+@given(sa=shape_and_axis(), kind=st.sampled_from(["sum", "mean", "max"]))
+def test_axis_reduction_any_shape(sa, kind):
+    shape, axis = sa
+    print(f"{kind} over axis {axis} of {shape}", flush=True)
+    op = {"sum": OpKind.Sum(axis), "mean": OpKind.Mean(axis), "max": OpKind.Max(axis)}[kind]
+    x = synth.normal(sum(shape) * 17 + len(shape), shape)
+    out_shape = [d for i, d in enumerate(shape) if i != axis % len(shape)]
+    xb, yb = hb.DeviceBuffer.from_array(x), hb.DeviceBuffer(4 * max(1, int(np.prod(out_shape))))
+    hb.eval_node_dev(op, [(xb, shape)], meta(out_shape), yb)
+    hb.synchronize()
+    np.testing.assert_array_equal(yb.download(count=int(np.prod(out_shape))), oracle_reduce(op, x, out_shape))
+
+
+def oracle_reduce(op, x, out_shape):
+    from oracle.cpu_ref import CpuRefBackend
+    from oxidizedmlx_amd.opkind import NodeInput
+    return CpuRefBackend().eval_node(op, [NodeInput(x.reshape(-1), x.shape)], meta(out_shape)).reshape(-1)
+
+
+UNARY = [OpKind.Neg, OpKind.Silu, OpKind.Gelu]
+BINARY = [OpKind.Add, OpKind.Sub, OpKind.Mul]
+
+
+@CASES
+@given(n=st.integers(1, 3000), prog=st.lists(st.tuples(st.integers(0, 5), st.integers(0, 2), st.booleans()),
+                                              min_size=1, max_size=8), fusion=st.booleans())
+def test_elementwise_chain_any_program(n, prog, fusion):
+    """A random chain over three inputs: step i applies a unary op, or a
+    binary op with input j on either side; the fusing stream must match the
+    oracle's node-by-node evaluation."""
+    print(f"chain n={n} prog={prog} fusion={fusion}", flush=True)
+    ins = [synth.normal(n * 3 + j, (n,), 0.0, 1.0) for j in range(3)]
+
+    def build(s):
+        leaves = [s.add_constant(a, meta([n])) for a in ins]
+        acc = leaves[0]
+        for code, j, left in prog:
+            if code < 3:
+                acc = s.add_op(UNARY[code], [acc], meta([n]))
+            else:
+                other = leaves[j]
+                acc = s.add_op(BINARY[code - 3], [acc, other] if left else [other, acc], meta([n]))
+        return acc
+
+    cpu, hip = cpu_stream(), hip_stream()
+    hip.set_fusion(fusion)
+    c_out, h_out = build(cpu), build(hip)
+    cpu.eval(c_out)
+    hip.eval(h_out)
+    assert_allclose(hip.get_buffer(h_out), cpu.get_buffer(c_out), 1e-6, 1e-5, "chain")
