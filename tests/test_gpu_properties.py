@@ -36,6 +36,16 @@ def test_gemm_any_shape(m, n, k, ta, tb, ab, batch):
     check_gemm(m, n, k, ab, F32, ta, tb, batch=batch, seed=m * 7919 + n * 31 + k)
 
 
+@settings(max_examples=40, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+@given(m=st.integers(200, 1500), n=st.integers(200, 1500), k=st.integers(1, 1200), ta=st.booleans(),
+       tb=st.booleans(), ab=st.sampled_from([BF16, F16]), cd=st.sampled_from([F32, BF16]))
+def test_gemm16_tiled_shapes(m, n, k, ta, tb, ab, cd):
+    """Extents large enough for the direct-to-LDS kernel's tile counts
+    (and the padded-copy route when an extent is not a multiple of 8)."""
+    print(f"gemm16 m={m} n={n} k={k} ta={ta} tb={tb} ab={ab} cd={cd}", flush=True)
+    check_gemm(m, n, k, ab, cd if ab == BF16 else F32, ta, tb, seed=m * 131 + n * 17 + k)
+
+
 @CASES
 @given(rows=st.integers(1, 40), cols=st.integers(1, 5000), offset=st.integers(0, 3),
        op=st.sampled_from(["softmax", "layernorm", "rmsnorm"]))
