@@ -6,6 +6,7 @@
 #include "gemm16_impl.hpp"
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -86,6 +87,19 @@ int gemm_path() {
     if (!strcmp(e, "lds16_256")) return 3;
     if (!strcmp(e, "lds16_128")) return 4;
     return 0;
+}
+
+// MLXHIP_GEMM_GENERAL="wt,splits" forces the general kernel's block tile
+// (64*wt, wt = 1, 2 or 4) and split-K factor (1..8) for aligned operands;
+// unset = chosen by shape. Read on every call (tuning and tests).
+bool general_override(int* wt, int* splits) {
+    const char* e = getenv("MLXHIP_GEMM_GENERAL");
+    int w = 0, sp = 0;
+    if (!e || sscanf(e, "%d,%d", &w, &sp) != 2) return false;
+    if (!(w == 1 || w == 2 || w == 4) || sp < 1 || sp > 8) return false;
+    *wt = w;
+    *splits = sp;
+    return true;
 }
 
 }  // namespace
@@ -204,9 +218,9 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
         }
     }
     // General kernel. f32 operands (measured on MI355X): 256x256 blocks from
-    // 256 tiles (one per CU); otherwise 128x128 blocks split over K until
-    // there are about 512 workgroups (two per CU), keeping at least 256 k per
-    // split; below 64 such tiles, 64x64 blocks as for 16-bit operands.
+    // 256 tiles (one per CU); otherwise 128x128 blocks split over K by the
+    // smallest power of two that gives at least 512 workgroups (two per CU),
+    // keeping at least 256 k per split; below 64 such tiles, 64x64 blocks as for 16-bit operands.
     // 16-bit operands that reach this kernel (too small or unaligned for the
     // direct-to-LDS one): the largest block tile that still gives about one
     // workgroup per CU; below that 64x64 tiles, split over K until there are
@@ -221,7 +235,11 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     if (ab_dtype == MLXHIP_DTYPE_F32 && tiles(4) >= 256) {
         wt = 4;
     } else if (ab_dtype == MLXHIP_DTYPE_F32 && tiles(2) >= 64 && aligned) {
-        const int64_t want = std::min<int64_t>(8, ceil_div(512, tiles(2)));
+        // A power of two: 192 tiles split 3 ways make 576 workgroups, one
+        // round of 512 plus a tail of 64 (qkv dW of config 4 took ~40 % longer
+        // than split 4 ways).
+        int64_t want = 1;
+        while (want < 8 && want * tiles(2) < 512) want *= 2;
         splits = limit(std::min<int64_t>(want, k / 256));
     } else if (ab_dtype != MLXHIP_DTYPE_F32 && tiles(4) >= 240) {
         wt = 4;
@@ -232,6 +250,13 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
             const int64_t by_cus = std::max<int64_t>(1, 1024 / t);
             const int64_t by_k = k / (4 * bk);  // at least 4 K tiles per split
             splits = limit(std::min<int64_t>(8, std::min(by_cus, by_k)));
+        }
+    }
+    if (aligned) {
+        int w = 0, sp = 0;
+        if (general_override(&w, &sp)) {
+            wt = w;
+            splits = limit(std::min<int64_t>(sp, ceil_div(k, bk)));
         }
     }
     auto run = [&](const gemm_detail::GemmArgs& ga, int ct) {
