@@ -231,9 +231,22 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     const int bk = ab_dtype == MLXHIP_DTYPE_F32 ? 32 : 64;
     auto tiles = [&](int w) { return ceil_div(m, 64 * w) * ceil_div(n, 64 * w) * batch; };
     auto limit = [&](int64_t sp) { return (int)(batch * sp > 65535 ? 1 : std::max<int64_t>(1, sp)); };
+    // Fraction of the padded block tiles that holds C: a 128-wide tile over
+    // N = 64 does twice the MFMA work it keeps.
+    auto fill = [&](int w) {
+        const int64_t e = 64 * w;
+        return (double)(m * n) / ((double)(ceil_div(m, e) * e) * (double)(ceil_div(n, e) * e));
+    };
     int wt = 2, splits = 1;
-    if (ab_dtype == MLXHIP_DTYPE_F32 && tiles(4) >= 256) {
+    if (ab_dtype == MLXHIP_DTYPE_F32 && tiles(4) >= 256 && fill(4) >= 0.75) {
         wt = 4;
+    } else if (ab_dtype == MLXHIP_DTYPE_F32 && aligned && fill(2) < 0.75 && tiles(1) >= 256) {
+        // Narrow products (config 4's 64 heads of P·V, [512, 512] x [512, 64]:
+        // 34 us with 64x64 blocks against 56 us with 128x128 blocks split 2).
+        wt = 1;
+        int64_t want = 1;
+        while (want < 8 && want * tiles(1) < 512) want *= 2;
+        splits = limit(std::min<int64_t>(want, k / 256));
     } else if (ab_dtype == MLXHIP_DTYPE_F32 && tiles(2) >= 64 && aligned) {
         // A power of two: 192 tiles split 3 ways make 576 workgroups, one
         // round of 512 plus a tail of 64 (qkv dW of config 4 took ~40 % longer
