@@ -73,13 +73,29 @@ int ensure_device() {
     return MLXHIP_OK;
 }
 
-hipStream_t thread_stream() {
-    static thread_local hipStream_t s[64] = {};
-    int dev = t_device < 0 ? 0 : t_device;
-    if (!s[dev]) {
-        if (hipStreamCreateWithFlags(&s[dev], hipStreamNonBlocking) != hipSuccess) s[dev] = nullptr;
+namespace {
+// The calling thread's own stream per device, destroyed when the thread ends
+// (every call that uses it synchronises before returning, so no work is
+// pending then).
+struct ThreadStreams {
+    hipStream_t s[64] = {};
+    ~ThreadStreams() {
+        for (hipStream_t& x : s)
+            if (x) (void)hipStreamDestroy(x);
     }
-    return s[dev];
+};
+}  // namespace
+
+hipStream_t thread_stream() {
+    static thread_local ThreadStreams ts;
+    const int dev = t_device < 0 ? 0 : t_device;
+    if (!ts.s[dev]) {
+        if (hipStreamCreateWithFlags(&ts.s[dev], hipStreamNonBlocking) != hipSuccess) {
+            (void)hipGetLastError();
+            ts.s[dev] = nullptr;
+        }
+    }
+    return ts.s[dev];
 }
 
 // ── device memory pool ────────────────────────────────────────────────────
