@@ -164,8 +164,19 @@ def test_gemm_argument_errors():
     (2048, 4096, 1024, 0, 0),   # 128x128 blocks, no split
     (4096, 4096, 256, 1, 1),    # 256x256 blocks
     (1000, 1100, 700, 0, 1),    # 128x128 blocks with edge tiles, split 2
+    (1024, 3072, 2048, 1, 0),   # 192 tiles of 128x128: K split 4 (a power of two)
 ])
 def test_f32_block_and_split_choices(m, n, k, ta, tb):
     # The f32 shapes of the config-4 block pick 128x128 or 256x256 blocks
     # and split K; sampled rows against the oracle.
     check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), seed=m + n + k, rows=sample_rows(m, 10))
+
+
+@pytest.mark.parametrize("m,n,k,ta,tb,batch", [
+    (512, 64, 512, 0, 0, 64),   # config-4 P.V per head: 64x64 blocks (128-wide tiles half empty)
+    (512, 64, 512, 1, 0, 64),   # its dV = P^T dY
+    (64, 512, 2048, 0, 1, 8),   # narrow M, split over K
+])
+def test_f32_narrow_products(m, n, k, ta, tb, batch):
+    check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), batch=batch, seed=m + n + k + batch,
+               rows=sample_rows(m, 6))
