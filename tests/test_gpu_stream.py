@@ -389,16 +389,21 @@ def test_broadcast_requested_later_is_materialised():
     np.testing.assert_array_equal(s.get_buffer(y), np.tile(np.arange(8, dtype=np.float32), 3) + 1)
 
 
-@pytest.mark.parametrize("shape,axis", [((2048, 1024), 0), ((3, 1000, 7), 1), ((5, 37), 1), ((4096, 3), 0)])
-def test_sum_axis_matches_sequential_fold_bitwise(shape, axis):
-    # Sum over an axis folds each output in order from -0.0, like the CPU
-    # (cpu_kernels.rs:166-195): bit-identical results.
+@pytest.mark.parametrize("shape,axis", [((2048, 1024), 0), ((3, 1000, 7), 1), ((5, 37), 1), ((4096, 3), 0),
+                                        ((3, 1300, 48), 1), ((2049, 16), 0), ((256, 4096), 0), ((777, 32), -2)])
+@pytest.mark.parametrize("kind", ["sum", "mean", "max"])
+def test_sum_axis_matches_sequential_fold_bitwise(shape, axis, kind):
+    # Sum / Mean / Max over an axis fold each output in order (Sum from
+    # -0.0), like the CPU (cpu_kernels.rs:166-195): bit-identical results,
+    # with row counts that leave partial register batches.
     x0 = synth.normal(521, shape)
-    out_shape = tuple(d for i, d in enumerate(shape) if i != axis)
+    ax = axis % len(shape)
+    out_shape = tuple(d for i, d in enumerate(shape) if i != ax)
+    op = {"sum": OpKind.Sum(axis), "mean": OpKind.Mean(axis), "max": OpKind.Max(axis)}[kind]
     res = []
     for s in (HipStream(), cpu_ref_stream()):
         x = s.add_constant(x0, meta(shape))
-        y = s.add_op(OpKind.Sum(axis), [x], meta(out_shape))
+        y = s.add_op(op, [x], meta(out_shape))
         s.eval(y)
         res.append(s.get_buffer(y))
     np.testing.assert_array_equal(res[0], res[1])
