@@ -51,21 +51,36 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 }
 
 // dst[r][c] = src[r][c] for r < rows, c < cols, zero elsewhere in the
-// rows_p x cols_p destination (one matrix per blockIdx.y).
+// rows_p x cols_p destination (one matrix per blockIdx.y). Each thread writes
+// one 16-byte chunk of a destination row (cols_p is a multiple of the chunk
+// and the destination is 16-byte aligned); the source, whose rows need not
+// be aligned, is read element by element.
 template <typename T>
 __global__ __launch_bounds__(256) void pack_kernel(const T* __restrict__ src, int64_t ld, int64_t sstride,
                                                    int64_t rows, int64_t cols, T* __restrict__ dst,
                                                    int64_t rows_p, int64_t cols_p) {
-    const int64_t b = blockIdx.y;
-    FOR_EACH_ELEMENT(idx, rows_p * cols_p) {
-        const int64_t r = idx / cols_p, c = idx % cols_p;
-        dst[b * rows_p * cols_p + idx] = (r < rows && c < cols) ? src[b * sstride + r * ld + c] : T(0);
+    constexpr int CH = 16 / sizeof(T);
+    const int64_t b = blockIdx.y, chunks = cols_p / CH;
+    const T* sb = src + b * sstride;
+    uint4* db = reinterpret_cast<uint4*>(dst + b * rows_p * cols_p);
+    FOR_EACH_ELEMENT(q, rows_p * chunks) {
+        const int64_t r = q / chunks, c0 = (q % chunks) * CH;
+        union {
+            uint4 v;
+            T e[CH];
+        } u;
+#pragma unroll
+        for (int e = 0; e < CH; ++e) u.e[e] = (r < rows && c0 + e < cols) ? sb[r * ld + c0 + e] : T(0);
+        db[q] = u.v;
     }
 }
 
 int pack(int dt, const void* src, int64_t ld, int64_t sstride, int64_t rows, int64_t cols, void* dst,
          int64_t rows_p, int64_t cols_p, int64_t batch, hipStream_t s) {
-    const dim3 grid = elem_grid(rows_p * cols_p, batch);
+    const int ch = dt == MLXHIP_DTYPE_F32 ? 4 : 8;
+    if (cols_p % ch || reinterpret_cast<uintptr_t>(dst) % 16)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "pack: destination rows must be whole 16-byte chunks");
+    const dim3 grid = elem_grid(rows_p * (cols_p / ch), batch);
     if (dt == MLXHIP_DTYPE_F32)
         hipLaunchKernelGGL(pack_kernel<uint32_t>, grid, dim3(256), 0, s, static_cast<const uint32_t*>(src), ld,
                            sstride, rows, cols, static_cast<uint32_t*>(dst), rows_p, cols_p);
