@@ -50,43 +50,54 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     }
 }
 
-// dst[r][c] = src[r][c] for r < rows, c < cols, zero elsewhere in the
-// rows_p x cols_p destination (one matrix per blockIdx.y). Each thread writes
-// one 16-byte chunk of a destination row (cols_p is a multiple of the chunk
-// and the destination is 16-byte aligned); the source, whose rows need not
-// be aligned, is read element by element.
+// One operand to copy into a zero-padded rows_p x cols_p buffer per batch
+// slice: dst[r][c] = src[r][c] for r < rows, c < cols, zero elsewhere.
+struct PackOp {
+    const void* src;
+    int64_t ld, sstride, rows, cols;
+    void* dst;
+    int64_t rows_p, cols_p;
+};
+struct PackPair {
+    PackOp op[2];
+};
+
+// Both operands of one GEMM in one launch (blockIdx.z picks the operand,
+// blockIdx.y the batch slice). Each thread writes one 16-byte chunk of a
+// destination row (cols_p is a multiple of the chunk and the destination is
+// 16-byte aligned); the source, whose rows need not be aligned, is read
+// element by element.
 template <typename T>
-__global__ __launch_bounds__(256) void pack_kernel(const T* __restrict__ src, int64_t ld, int64_t sstride,
-                                                   int64_t rows, int64_t cols, T* __restrict__ dst,
-                                                   int64_t rows_p, int64_t cols_p) {
+__global__ __launch_bounds__(256) void pack_kernel(PackPair pp) {
     constexpr int CH = 16 / sizeof(T);
-    const int64_t b = blockIdx.y, chunks = cols_p / CH;
-    const T* sb = src + b * sstride;
-    uint4* db = reinterpret_cast<uint4*>(dst + b * rows_p * cols_p);
-    FOR_EACH_ELEMENT(q, rows_p * chunks) {
+    const PackOp& p = pp.op[blockIdx.z];
+    const int64_t b = blockIdx.y, chunks = p.cols_p / CH;
+    const T* sb = static_cast<const T*>(p.src) + b * p.sstride;
+    uint4* db = reinterpret_cast<uint4*>(static_cast<T*>(p.dst) + b * p.rows_p * p.cols_p);
+    FOR_EACH_ELEMENT(q, p.rows_p * chunks) {
         const int64_t r = q / chunks, c0 = (q % chunks) * CH;
         union {
             uint4 v;
             T e[CH];
         } u;
 #pragma unroll
-        for (int e = 0; e < CH; ++e) u.e[e] = (r < rows && c0 + e < cols) ? sb[r * ld + c0 + e] : T(0);
+        for (int e = 0; e < CH; ++e) u.e[e] = (r < p.rows && c0 + e < p.cols) ? sb[r * p.ld + c0 + e] : T(0);
         db[q] = u.v;
     }
 }
 
-int pack(int dt, const void* src, int64_t ld, int64_t sstride, int64_t rows, int64_t cols, void* dst,
-         int64_t rows_p, int64_t cols_p, int64_t batch, hipStream_t s) {
+int pack2(int dt, const PackPair& pp, int64_t batch, hipStream_t s) {
     const int ch = dt == MLXHIP_DTYPE_F32 ? 4 : 8;
-    if (cols_p % ch || reinterpret_cast<uintptr_t>(dst) % 16)
-        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "pack: destination rows must be whole 16-byte chunks");
-    const dim3 grid = elem_grid(rows_p * (cols_p / ch), batch);
-    if (dt == MLXHIP_DTYPE_F32)
-        hipLaunchKernelGGL(pack_kernel<uint32_t>, grid, dim3(256), 0, s, static_cast<const uint32_t*>(src), ld,
-                           sstride, rows, cols, static_cast<uint32_t*>(dst), rows_p, cols_p);
-    else
-        hipLaunchKernelGGL(pack_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(src), ld,
-                           sstride, rows, cols, static_cast<uint16_t*>(dst), rows_p, cols_p);
+    int64_t most = 0;
+    for (const PackOp& p : pp.op) {
+        if (p.cols_p % ch || reinterpret_cast<uintptr_t>(p.dst) % 16)
+            return fail(MLXHIP_ERR_INVALID_ARGUMENT, "pack: destination rows must be whole 16-byte chunks");
+        most = std::max(most, p.rows_p * (p.cols_p / ch));
+    }
+    dim3 grid = elem_grid(most, batch);
+    grid.z = 2;
+    if (dt == MLXHIP_DTYPE_F32) hipLaunchKernelGGL(pack_kernel<uint32_t>, grid, dim3(256), 0, s, pp);
+    else hipLaunchKernelGGL(pack_kernel<uint16_t>, grid, dim3(256), 0, s, pp);
     return launch_check("pack_kernel");
 }
 
@@ -177,13 +188,20 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
         const int64_t b_rows = trans_b ? n : k, b_cols = trans_b ? k : n;
         const int64_t b_rows_p = trans_b ? n : kp, b_cols_p = ceil_div(b_cols, ch) * ch;
         const int es = elem_size(ab_dtype);
-        StreamBuf pa(s), pb(s);
-        MLXHIP_TRY(pa.alloc((size_t)(a_rows_p * a_cols_p * batch * es)));
-        MLXHIP_TRY(pb.alloc((size_t)(b_rows_p * b_cols_p * batch * es)));
-        MLXHIP_TRY(pack(ab_dtype, a, lda, stride_a, a_rows, a_cols, pa.p, a_rows_p, a_cols_p, batch, s));
-        MLXHIP_TRY(pack(ab_dtype, b, ldb, stride_b, b_rows, b_cols, pb.p, b_rows_p, b_cols_p, batch, s));
-        return gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, kp, batch, pa.p, a_cols_p, a_rows_p * a_cols_p,
-                         pb.p, b_cols_p, b_rows_p * b_cols_p, c, ldc, stride_c, s, true);
+        // One stream-ordered allocation holds both copies (B at a 256-byte
+        // boundary) and one launch fills both: the host work per call is
+        // what such small products wait on.
+        const size_t a_sz = (size_t)(a_rows_p * a_cols_p * batch * es);
+        const size_t b_off = (a_sz + 255) & ~size_t(255);
+        StreamBuf ws(s);
+        MLXHIP_TRY(ws.alloc(b_off + (size_t)(b_rows_p * b_cols_p * batch * es)));
+        void* pa = ws.p;
+        void* pb = static_cast<char*>(ws.p) + b_off;
+        PackPair pp{{PackOp{a, lda, stride_a, a_rows, a_cols, pa, a_rows_p, a_cols_p},
+                     PackOp{b, ldb, stride_b, b_rows, b_cols, pb, b_rows_p, b_cols_p}}};
+        MLXHIP_TRY(pack2(ab_dtype, pp, batch, s));
+        return gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, kp, batch, pa, a_cols_p, a_rows_p * a_cols_p,
+                         pb, b_cols_p, b_rows_p * b_cols_p, c, ldc, stride_c, s, true);
     }
 
     gemm_detail::GemmArgs g{};
