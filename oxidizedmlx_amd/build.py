@@ -88,26 +88,6 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
     return LIB
 
 
-# Measurement tools (not part of the library): the MFMA and HBM ceilings the
-# kernels are compared with. Built only on request (--probes).
-PROBES = ["probes/mfma_ceiling.hip", "probes/hbm_ceiling.hip"]
-
-
-def build_probes(verbose: bool = True) -> list[str]:
-    os.makedirs(BUILD, exist_ok=True)
-    outs = []
-    for src in PROBES:
-        exe = os.path.join(BUILD, os.path.splitext(os.path.basename(src))[0])
-        cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, os.path.join(CSRC, src), "-o", exe]
-        r = subprocess.run(cmd, capture_output=True, text=True)
-        if r.returncode != 0:
-            raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr[-4000:]}")
-        outs.append(exe)
-        if verbose:
-            print(f"  built {exe}", flush=True)
-    return outs
-
-
 def clean() -> None:
     shutil.rmtree(BUILD, ignore_errors=True)
     if os.path.exists(LIB):
@@ -115,8 +95,5 @@ def clean() -> None:
 
 
 if __name__ == "__main__":
-    if "--probes" in sys.argv[1:]:
-        build_probes()
-    else:
-        build()
+    build()
     sys.exit(0)
