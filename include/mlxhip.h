@@ -277,6 +277,26 @@ int mlxhip_gemm(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t tran
                 void* c, int64_t ldc, int64_t stride_c,
                 void* stream);
 
+/* mlxhip_gemm for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Same arguments, kernels, split-K plan and
+ * results (bit for bit) as mlxhip_gemm, but its workspace (split-K partials,
+ * zero-padded copies of unaligned operands) comes from one fixed device array
+ * of mlxhip_gemm_noalloc_scratch_bytes() bytes (64 MiB) per device, held
+ * until the process ends; it calls no hipMalloc/hipFree and no allocating
+ * library routine. A product whose workspace exceeds that array returns
+ * MLXHIP_ERR_INVALID_ARGUMENT (C is then unchanged). Every call on one device
+ * shares that device's array: calls that overlap on one device (several
+ * streams or threads at once) race, so the caller serialises them. */
+int mlxhip_gemm_noalloc(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t trans_b,
+                        int64_t m, int64_t n, int64_t k, int64_t batch,
+                        const void* a, int64_t lda, int64_t stride_a,
+                        const void* b, int64_t ldb, int64_t stride_b,
+                        void* c, int64_t ldc, int64_t stride_c,
+                        void* stream);
+/* Bytes of the fixed device scratch mlxhip_gemm_noalloc draws from. */
+size_t mlxhip_gemm_noalloc_scratch_bytes(void);
+
 /* Row-wise softmax over the last axis of a [rows, cols] f32 matrix
  * (softmax, crates/mlx-core/src/cpu_kernels.rs:276-315, axis = -1). */
 int mlxhip_softmax_rows(const float* x, float* y, int64_t rows, int64_t cols, void* stream);

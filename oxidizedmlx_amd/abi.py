@@ -183,6 +183,9 @@ PROTOTYPES = {
     "mlxhip_stream_grad": (_i, [_vp, _u64, C.POINTER(_u64), _sz, C.POINTER(_u64)]),
     "mlxhip_gemm": (_i, [_i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64,
                          _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp]),
+    "mlxhip_gemm_noalloc": (_i, [_i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64,
+                                 _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp]),
+    "mlxhip_gemm_noalloc_scratch_bytes": (_sz, []),
     "mlxhip_softmax_rows": (_i, [_fp, _fp, _i64, _i64, _vp]),
     "mlxhip_scaled_masked_softmax_rows": (_i, [_fp, _fp, _i64, _i64, _f, _i32, _vp]),
     "mlxhip_layernorm_rows": (_i, [_fp, _fp, _i64, _i64, _f, _vp]),

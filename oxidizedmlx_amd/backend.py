@@ -218,6 +218,23 @@ def gemm(ab_dtype: int, c_dtype: int, trans_a: bool, trans_b: bool, m: int, n: i
                             stream), L)
 
 
+def gemm_noalloc(ab_dtype: int, c_dtype: int, trans_a: bool, trans_b: bool, m: int, n: int,
+                 k: int, a, lda: int, b, ldb: int, c, ldc: int, batch: int = 1,
+                 stride_a: int = 0, stride_b: int = 0, stride_c: int = 0,
+                 stream: int | None = None) -> None:
+    """``gemm`` without any device allocation: its workspace comes from the
+    library's fixed per-device scratch (``gemm_noalloc_scratch_bytes()``);
+    calls that overlap on one device race."""
+    L = lib()
+    abi.check(L.mlxhip_gemm_noalloc(ab_dtype, c_dtype, int(trans_a), int(trans_b), m, n, k, batch,
+                                    _p(a), lda, stride_a, _p(b), ldb, stride_b, _p(c), ldc,
+                                    stride_c, stream), L)
+
+
+def gemm_noalloc_scratch_bytes() -> int:
+    return lib().mlxhip_gemm_noalloc_scratch_bytes()
+
+
 def softmax_rows(x, y, rows: int, cols: int, stream=None) -> None:
     abi.check(lib().mlxhip_softmax_rows(_p(x), _p(y), rows, cols, stream))
 

@@ -710,6 +710,17 @@ int mlxhip_gemm(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t tran
                 stride_c, as_stream(stream));
 }
 
+int mlxhip_gemm_noalloc(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t trans_b, int64_t m,
+                        int64_t n, int64_t k, int64_t batch, const void* a, int64_t lda, int64_t stride_a,
+                        const void* b, int64_t ldb, int64_t stride_b, void* c, int64_t ldc, int64_t stride_c,
+                        void* stream) {
+    MLXHIP_TRY(ensure_device());
+    return gemm_noalloc(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
+                        ldc, stride_c, as_stream(stream));
+}
+
+size_t mlxhip_gemm_noalloc_scratch_bytes(void) { return GEMM_NOALLOC_SCRATCH_BYTES; }
+
 int mlxhip_softmax_rows(const float* x, float* y, int64_t rows, int64_t cols, void* stream) {
     if ((rows * cols) && (!x || !y)) return fail(MLXHIP_ERR_NULL_PTR, "softmax_rows: null pointer");
     MLXHIP_TRY(ensure_device());

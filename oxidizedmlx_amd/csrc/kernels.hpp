@@ -124,5 +124,13 @@ int attention_fused(const float* q, const float* k, const float* v, float* o, in
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
          int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s);
+// gemm with the same kernels and plan, its split-K partials and padded
+// operand copies taken from a fixed device array of
+// GEMM_NOALLOC_SCRATCH_BYTES instead of the memory pool: no allocation.
+// Calls that overlap on one device share that array and race.
+constexpr size_t GEMM_NOALLOC_SCRATCH_BYTES = size_t(64) << 20;
+int gemm_noalloc(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
+                 int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
+                 int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s);
 
 }  // namespace mlxhip

@@ -130,25 +130,99 @@ bool general_override(int* wt, int* splits) {
 
 }  // namespace
 
+// ── Fixed device scratch of gemm_noalloc ─────────────────────────────────
+// The split-K partials and the zero-padded operand copies of gemm_noalloc
+// live in this array instead of stream-ordered allocations. Each device that
+// loads the library holds its own copy until the process ends. In host code
+// `scratch` names a host-side stand-in, never the device memory: the device
+// address comes from hipGetSymbolAddress, once per device, and only that
+// address reaches kernels.
+static __device__ __align__(256) unsigned char scratch[GEMM_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+// Bump allocator over one call's share of the fixed scratch (nullptr in the
+// allocating path). Every region it hands out is written in full by the
+// kernel that uses it before any kernel reads it (each split-K slice covers
+// all of [m, n]; a packed copy writes its zero padding too), so nothing is
+// cleared between calls.
+struct FixedScratch {
+    char* base;
+    size_t cap;
+    size_t used;
+};
+
+// `bytes` of device workspace for this call: stream-ordered from the
+// device's pool (fs == nullptr, owned by `sb`), or the next 256-byte aligned
+// region of the fixed scratch.
+int take_workspace(FixedScratch* fs, StreamBuf& sb, size_t bytes, void** out) {
+    if (!fs) {
+        MLXHIP_TRY(sb.alloc(bytes));
+        *out = sb.p;
+        return MLXHIP_OK;
+    }
+    const size_t at = (fs->used + 255) & ~size_t(255);
+    if (at > fs->cap || bytes > fs->cap - at)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT,
+                    "gemm_noalloc: this product needs %zu bytes of device scratch, more than the %zu bytes "
+                    "of the fixed scratch (C is unchanged); use mlxhip_gemm",
+                    at + bytes, fs->cap);
+    *out = fs->base + at;
+    fs->used = at + bytes;
+    return MLXHIP_OK;
+}
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[64];  // device address of `scratch` per device (null until resolved)
+
+// Device address of the current device's fixed scratch, resolved on the
+// first call on that device (with that device current).
+int fixed_scratch(void** out) {
+    int dev = 0;
+    MLXHIP_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        MLXHIP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(MLXHIP_ERR_FFI_FAILED, "gemm_noalloc: scratch has no device address");
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return MLXHIP_OK;
+}
+
 int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
               int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
-              int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, bool padded);
+              int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, bool padded,
+              FixedScratch* fs);
 }  // namespace
 
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
          int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s) {
     return gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
-                     ldc, stride_c, s, false);
+                     ldc, stride_c, s, false, nullptr);
+}
+
+int gemm_noalloc(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
+                 int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
+                 int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s) {
+    void* base = nullptr;
+    MLXHIP_TRY(fixed_scratch(&base));
+    FixedScratch fs{static_cast<char*>(base), GEMM_NOALLOC_SCRATCH_BYTES, 0};
+    return gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
+                     ldc, stride_c, s, false, &fs);
 }
 
 namespace {
 // padded: the operands are the dispatcher's zero-padded copies (rows
-// readable up to their leading dimension).
+// readable up to their leading dimension). fs: the fixed scratch of
+// gemm_noalloc, or nullptr to take workspace from the device's pool.
 int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
               int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
-              int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, bool padded) {
+              int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, bool padded,
+              FixedScratch* fs) {
     if (ab_dtype != MLXHIP_DTYPE_F32 && ab_dtype != MLXHIP_DTYPE_BF16 && ab_dtype != MLXHIP_DTYPE_F16)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: input dtype %d unsupported", ab_dtype);
     if (c_dtype != MLXHIP_DTYPE_F32 && c_dtype != MLXHIP_DTYPE_BF16 && c_dtype != MLXHIP_DTYPE_F16)
@@ -194,14 +268,14 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
         const size_t a_sz = (size_t)(a_rows_p * a_cols_p * batch * es);
         const size_t b_off = (a_sz + 255) & ~size_t(255);
         StreamBuf ws(s);
-        MLXHIP_TRY(ws.alloc(b_off + (size_t)(b_rows_p * b_cols_p * batch * es)));
-        void* pa = ws.p;
-        void* pb = static_cast<char*>(ws.p) + b_off;
+        void* pa = nullptr;
+        MLXHIP_TRY(take_workspace(fs, ws, b_off + (size_t)(b_rows_p * b_cols_p * batch * es), &pa));
+        void* pb = static_cast<char*>(pa) + b_off;
         PackPair pp{{PackOp{a, lda, stride_a, a_rows, a_cols, pa, a_rows_p, a_cols_p},
                      PackOp{b, ldb, stride_b, b_rows, b_cols, pb, b_rows_p, b_cols_p}}};
         MLXHIP_TRY(pack2(ab_dtype, pp, batch, s));
         return gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, kp, batch, pa, a_cols_p, a_rows_p * a_cols_p,
-                         pb, b_cols_p, b_rows_p * b_cols_p, c, ldc, stride_c, s, true);
+                         pb, b_cols_p, b_rows_p * b_cols_p, c, ldc, stride_c, s, true, fs);
     }
 
     gemm_detail::GemmArgs g{};
@@ -323,9 +397,10 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     g.k_chunk = ceil_div(ceil_div(k, splits), bk) * bk;
     g.splits = (int)ceil_div(k, g.k_chunk);
     StreamBuf ws(s);
-    MLXHIP_TRY(ws.alloc((size_t)(batch * g.splits * m * n) * sizeof(float)));
+    void* part = nullptr;
+    MLXHIP_TRY(take_workspace(fs, ws, (size_t)(batch * g.splits * m * n) * sizeof(float), &part));
     gemm_detail::GemmArgs gp = g;
-    gp.c = ws.p;
+    gp.c = part;
     gp.ldc = n;
     gp.sc = m * n;
     MLXHIP_TRY(run(gp, MLXHIP_DTYPE_F32));
@@ -333,15 +408,15 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     switch (c_dtype) {
         case MLXHIP_DTYPE_F32:
             hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_F32>, grid, dim3(256), 0, s,
-                               static_cast<const float*>(ws.p), c, m, n, ldc, stride_c, g.splits);
+                               static_cast<const float*>(part), c, m, n, ldc, stride_c, g.splits);
             break;
         case MLXHIP_DTYPE_BF16:
             hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_BF16>, grid, dim3(256), 0, s,
-                               static_cast<const float*>(ws.p), c, m, n, ldc, stride_c, g.splits);
+                               static_cast<const float*>(part), c, m, n, ldc, stride_c, g.splits);
             break;
         default:
             hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_F16>, grid, dim3(256), 0, s,
-                               static_cast<const float*>(ws.p), c, m, n, ldc, stride_c, g.splits);
+                               static_cast<const float*>(part), c, m, n, ldc, stride_c, g.splits);
             break;
     }
     return launch_check("splitk_reduce_kernel");
