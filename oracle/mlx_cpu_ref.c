@@ -25,7 +25,10 @@
  *       reference's own method, crates/mlx-autograd/src/lib.rs:157-175) and
  *       the LayerNorm invariant "grad rows sum to 0" (autograd/src/vjp.rs:236-261).
  *   rope (Rope and RoPE): the reference's known answer (cpu_kernels.rs:1093-1127)
- *       and a float64 re-derivation.
+ *       and closed forms on one-hot inputs: each pair rotates by the angle
+ *       (offset + row) * base^(-2d/hd) into (cos, sin) / (-sin, cos) on the
+ *       pair (2d, 2d+1) (traditional, and Rope) or (d, d+hd/2), every other
+ *       output zero, dims past rotary_dim unchanged.
  *   gen_data: integer LCG restated; checked for determinism, range and a
  *       float64 re-derivation with Python integers.
  */

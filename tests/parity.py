@@ -7,6 +7,8 @@ oracle stream and a fresh mlx-hip stream, evaluates both and asserts
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 
 from oracle.cpu_ref import CpuRefBackend, gen_data, gen_positive_data  # noqa: F401
@@ -123,3 +125,123 @@ def run_parity(build_graph, atol: float, rtol: float, what: str = ""):
     h = hip.get_buffer(h_out)
     assert_allclose(h, c, atol, rtol, what)
     return h, c
+
+
+# ── Rigorous bounds shared by the GPU parity tests and their CPU self-checks ──
+
+U32 = 2.0 ** -24     # unit roundoff of f32 (round to nearest)
+U_OUT = {"f32": 0.0, "bf16": 2.0 ** -8, "f16": 2.0 ** -11}  # unit roundoff of the C type (8 / 11 significant bits)
+
+
+def gamma(k: int) -> float:
+    """gamma_k = k*u / (1 - k*u): the bound on the relative error of any
+    f32 sum of k+1 products accumulated in any order (Higham, Accuracy and
+    Stability of Numerical Algorithms, 2nd ed., eq. 3.4)."""
+    return k * U32 / (1.0 - k * U32)
+
+
+def gemm_full_check(c, a, b, out: str = "f32", what: str = "") -> tuple[float, float]:
+    """Every element of C (one product, [M, N]) against float64 A @ B on the
+    same (already rounded) inputs a [M, K], b [K, N]:
+
+        |C - AB| <= gamma_K (|A| |B|) + u_out (|AB| + gamma_K (|A| |B|))
+
+    holds for an f32 accumulation in any order followed by one rounding of
+    the output to `out`; a dropped k-term, a wrong or shifted tile, or a
+    transposed operand gives errors of the order of |AB| itself and fails.
+    Returns (max_abs, max error / bound)."""
+    a64 = np.asarray(a, np.float64)
+    b64 = np.asarray(b, np.float64)
+    k = a64.shape[1]
+    exact = a64 @ b64
+    mag = np.abs(a64) @ np.abs(b64)
+    g = gamma(k)
+    bound = g * mag + U_OUT[out] * (np.abs(exact) + g * mag)
+    # A zero bound (an all-zero row or column of A or B) allows only an exact zero.
+    err = np.abs(np.asarray(c, np.float64) - exact)
+    bad = ~(err <= bound)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ratio = np.where(bound > 0, err / bound, np.where(err == 0, 0.0, np.inf))
+    if bad.any():
+        i, j = np.unravel_index(int(np.argmax(bad)), bad.shape)
+        raise AssertionError(
+            f"{what}: C[{i},{j}]={float(c[i, j])!r} exact={exact[i, j]!r} err={err[i, j]:.3e} "
+            f"bound={bound[i, j]:.3e} ({int(bad.sum())} of {bad.size} outside the bound)")
+    print(f"  {what} full {c.shape}: max_abs={float(err.max()):.3e} "
+          f"max err/bound={float(ratio.max()):.3f}", flush=True)
+    return float(err.max()), float(ratio.max())
+
+
+def tree_sum_bound(x, extra_depth: int = 4) -> float:
+    """Bound on |s - sum(x)| for an f32 sum s of x formed by any summation
+    tree of depth <= ceil(log2 n) + extra_depth (each value passes through at
+    most that many roundings): gamma_depth * sum|x|."""
+    n = int(np.asarray(x).size)
+    depth = max(1, math.ceil(math.log2(max(n, 2)))) + extra_depth
+    return gamma(depth) * float(np.abs(np.asarray(x, np.float64)).sum())
+
+
+def rope_closed_form_check(fn, head_dim: int, rows: int, offset: int, base: float,
+                           traditional: bool, what: str = "") -> float:
+    """OpKind::RoPE (cpu_kernels.rs:896-956) on one-hot inputs: for row i at
+    position p = offset + i and pair d, theta = p * base^(-2d/head_dim), with
+    the pair (2d, 2d+1) when `traditional`, else (d, d + head_dim/2). A one
+    at the pair's first index must come out as (cos theta, sin theta) on the
+    pair, a one at its second index as (-sin theta, cos theta), and zero at
+    every other index. `fn(x, shape)` evaluates RoPE on a [rows, head_dim]
+    float32 array. Tolerance: the f32 angle carries a few ulp of |theta|.
+    Returns the largest error seen."""
+    half = head_dim // 2
+    worst = 0.0
+    for d in range(half):
+        i0, i1 = (2 * d, 2 * d + 1) if traditional else (d, d + half)
+        for which, role in ((i0, "first"), (i1, "second")):
+            x = np.zeros((rows, head_dim), np.float32)
+            x[:, which] = 1.0
+            y = np.asarray(fn(x, (rows, head_dim)), np.float64).reshape(rows, head_dim)
+            for i in range(rows):
+                th = (offset + i) * base ** (-(2.0 * d) / head_dim)
+                want = np.zeros(head_dim)
+                if role == "first":
+                    want[i0], want[i1] = math.cos(th), math.sin(th)
+                else:
+                    want[i0], want[i1] = -math.sin(th), math.cos(th)
+                tol = 1e-6 + 16 * float(np.finfo(np.float32).eps) * max(1.0, abs(th))
+                err = float(np.abs(y[i] - want).max())
+                worst = max(worst, err)
+                if err > tol:
+                    raise AssertionError(
+                        f"{what}: RoPE one-hot at {which} (pair {d}, {role}), row {i}: got "
+                        f"{y[i].tolist()} want {want.tolist()} (err {err:.3e} > {tol:.3e})")
+    return worst
+
+
+def tree_sum_f32(x, blocks: int = 1024, threads: int = 256) -> np.float32:
+    """The f32 summation order of the library's whole-tensor Sum above 65536
+    values (reduce_partial_kernel / reduce_final_kernel): thread t of block b
+    folds x[b*threads + t + j*blocks*threads], j = 0, 1, ..., from -0.0; each
+    block halves its threads' values pairwise (t += t + o for o = threads/2
+    .. 1); one block then folds partial t, t + threads, ... and halves the
+    same way. numpy float32 additions round as the GPU's do, so this gives
+    the kernel's bits. A planted reorder or dropped term is a different sum."""
+    x = np.asarray(x, np.float32).reshape(-1)
+    n = x.size
+    stride = blocks * threads
+    acc = np.full(stride, -0.0, np.float32)
+    for j in range(0, n, stride):
+        chunk = x[j:j + stride]
+        acc[:chunk.size] = acc[:chunk.size] + chunk
+
+    def halve(v):
+        v = v.copy()
+        o = v.size // 2
+        while o > 0:
+            v[:o] = v[:o] + v[o:2 * o]
+            o //= 2
+        return v[0]
+
+    part = np.array([halve(acc[b * threads:(b + 1) * threads]) for b in range(blocks)], np.float32)
+    fin = np.full(threads, -0.0, np.float32)
+    for j in range(0, blocks, threads):
+        fin = fin + part[j:j + threads]
+    return np.float32(halve(fin))

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from oxidizedmlx_amd.opkind import OpKind, meta
-from parity import binary_op, gen_data, gen_positive_data, run_parity, unary_op
+from parity import binary_op, cpu_stream, gen_data, gen_positive_data, hip_stream, run_parity, unary_op
 
 pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip", "oracle_lib")]
 
@@ -206,17 +206,39 @@ def test_parity_broadcast_narrow_concat_embedding_rope_mlx():
 
 
 def test_reductions_over_all_large_input():
-    # More than 65536 values take the tree reduction (per-block partials,
-    # then one folding block): Max is exact; Sum and Mean differ from the
-    # sequential f32 fold only by rounding, bounded by n·eps·Σ|x|, and so
-    # does each from the float64 sum.
+    # More than 65536 values take the tree reduction (1024 blocks of 256
+    # threads, then one folding block): depth <= ceil(log2 n) + 4 roundings
+    # per value, so |sum - exact| <= gamma_depth * sum|x| (tree_sum_bound:
+    # 0.21 here, against a true sum of -138.7). Against the oracle's
+    # sequential fold the bound grows by that fold's own error. The kernel's
+    # order is also restated in numpy float32 (tree_sum_f32), which must give
+    # the same bits. tests/test_checkers.py shows that dropping block 0's
+    # partial (|partial| = 8.2) or nearly any other block's fails the bound.
+    from parity import tree_sum_bound, tree_sum_f32
     n = 300_001
-    x = gen_data(n, 160)
-    x64 = x.astype(np.float64)
-    bound = n * float(np.finfo(np.float32).eps) * float(np.abs(x64).sum())
-    for op, tol, exact in [(OpKind.Sum(None), bound, x64.sum()), (OpKind.Mean(None), bound / n, x64.sum() / n)]:
-        h, _ = run_parity(lambda s: s.add_op(op, [s.add_constant(x, meta([n]))], meta([])), tol, 0.0, repr(op))
-        assert abs(float(h[0]) - exact) <= tol
+    for name, x in (("signed", gen_data(n, 160)),
+                    ("positive", (np.float32(0.5) + np.float32(0.5) * np.abs(gen_data(n, 161))).astype(np.float32))):
+        x64 = x.astype(np.float64)
+        exact = float(x64.sum())
+        bound = tree_sum_bound(x)
+        if name == "positive":
+            assert float(x.min()) > bound  # any one value left out would fail
+        for op, scale in ((OpKind.Sum(None), 1.0), (OpKind.Mean(None), 1.0 / n)):
+            hip = hip_stream()
+            hid = hip.add_op(op, [hip.add_constant(x, meta([n]))], meta([]))
+            hip.eval(hid)
+            h = float(hip.get_buffer(hid)[0])
+            cpu = cpu_stream()
+            cid = cpu.add_op(op, [cpu.add_constant(x, meta([n]))], meta([]))
+            cpu.eval(cid)
+            c = float(cpu.get_buffer(cid)[0])
+            # Mean divides once more in f32: one more rounding of the result.
+            tol = (bound + 2.0 ** -23 * (abs(exact) + bound)) * scale if scale != 1.0 else bound
+            print(f"  {name} {op!r}: hip={h!r} cpu={c!r} exact={exact * scale!r} bound={tol:.3e}", flush=True)
+            assert abs(h - exact * scale) <= tol, (name, op, h, exact * scale, tol)
+            assert abs(h - c) <= tol + abs(c - exact * scale), (name, op, h, c)
+            if scale == 1.0:
+                assert np.float32(h) == tree_sum_f32(x), (name, h, float(tree_sum_f32(x)))
     h, c = run_parity(lambda s: s.add_op(OpKind.Max(None), [s.add_constant(x, meta([n]))], meta([])),
                       0.0, 0.0, "Max(None)")
     assert float(h[0]) == float(x.max())

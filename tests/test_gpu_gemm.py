@@ -20,11 +20,12 @@ from oracle import cpu_ref
 from oxidizedmlx_amd import abi
 from oxidizedmlx_amd import backend as hb
 from oxidizedmlx_amd import synth
-from parity import assert_allclose
+from parity import assert_allclose, gemm_full_check
 
 pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip", "oracle_lib")]
 
 F32, BF16, F16 = abi.F32, abi.BF16, abi.F16
+OUT_NAME = {F32: "f32", BF16: "bf16", F16: "f16"}
 
 
 def to_dev(x, dt):
@@ -64,8 +65,10 @@ def sample_rows(m, count):
     return r
 
 
-def check_gemm(m, n, k, ab, cd, ta=False, tb=False, batch=1, seed=1, rows=None, ld_pad=0):
-    """Runs one (batched) GEMM and checks sampled rows of every batch slice."""
+def check_gemm(m, n, k, ab, cd, ta=False, tb=False, batch=1, seed=1, rows=None, ld_pad=0, full=False):
+    """Runs one (batched) GEMM and checks sampled rows of every batch slice
+    against the oracle; with `full`, also every element of every slice
+    against float64 with the accumulation bound (gemm_full_check)."""
     A = synth.normal(seed, (batch, k, m) if ta else (batch, m, k))
     B = synth.normal(seed + 1, (batch, n, k) if tb else (batch, k, n))
     Ar, Br = rounded(A, ab), rounded(B, ab)
@@ -90,6 +93,9 @@ def check_gemm(m, n, k, ab, cd, ta=False, tb=False, batch=1, seed=1, rows=None, 
         atol = 1e-6 * math.sqrt(k) * float(np.abs(opA).max()) * float(np.abs(opB).max()) if k else 0
         assert_allclose(C[bi][rows], ref, atol, rtol,
                         f"gemm {m}x{n}x{k} ab={ab} c={cd} ta={ta} tb={tb} batch {bi}")
+        if full:
+            gemm_full_check(C[bi], opA, opB, OUT_NAME[cd],
+                            f"gemm {m}x{n}x{k} ab={ab} c={cd} ta={ta} tb={tb} batch {bi}")
     return C
 
 
@@ -100,20 +106,27 @@ def test_f32_512_cfg1():
 
 @pytest.mark.parametrize("cd", [BF16, F32])
 def test_bf16_4096_headline(cd):
-    check_gemm(4096, 4096, 4096, BF16, cd, seed=11, rows=sample_rows(4096, 10))
+    # Sampled rows against the oracle, and every element of C against
+    # float64 on the same rounded inputs within the accumulation bound, so
+    # every 256x256 tile of the product (and the XCD / group ordering that
+    # places it) is checked.
+    check_gemm(4096, 4096, 4096, BF16, cd, seed=11, rows=sample_rows(4096, 10), full=True)
 
 
 @pytest.mark.parametrize("ab", [BF16, F16])
 @pytest.mark.parametrize("tb", [False, True])
 def test_batched_cfg3(ab, tb):
     # Config 3: [32,1024,1024] x [32,1024,1024] with f32 accumulate; tb = transposed-B case.
-    check_gemm(1024, 1024, 1024, ab, F32, tb=tb, batch=32, seed=21, rows=np.array([0, 511, 1023]))
+    # Three rows per slice against the oracle; every element of all 32 slices
+    # against float64 within the accumulation bound.
+    check_gemm(1024, 1024, 1024, ab, F32, tb=tb, batch=32, seed=21, rows=np.array([0, 511, 1023]),
+               full=True)
 
 
 @pytest.mark.parametrize("ab", [BF16, F16, F32])
 def test_odd_cfg3(ab):
     # Config 3 odd shape M=1000, N=777, K=1531 (edge tiles; unaligned rows).
-    check_gemm(1000, 777, 1531, ab, F32, seed=31, rows=sample_rows(1000, 24))
+    check_gemm(1000, 777, 1531, ab, F32, seed=31, rows=sample_rows(1000, 24), full=True)
 
 
 @pytest.mark.parametrize("ab", [BF16, F16, F32])

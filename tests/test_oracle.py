@@ -345,6 +345,47 @@ def test_rope_known_answer():
     assert r.size == 8 and r[0] == 1.0  # position 0 is the identity
 
 
+@pytest.mark.parametrize("traditional", [True, False])
+@pytest.mark.parametrize("hd,rows,offset,base", [(8, 4, 0, 10000.0), (16, 6, 5, 10000.0),
+                                                 (4, 3, 17, 500.0), (2, 2, 1, 10.0)])
+def test_rope_mlx_closed_form(traditional, hd, rows, offset, base):
+    # OpKind::RoPE (cpu_kernels.rs:896-956) on one-hot inputs: each pair
+    # rotates by theta = (offset + row) * base^(-2d/hd), the pair being
+    # (2d, 2d+1) when traditional, else (d, d + hd/2). A swapped pairing, a
+    # wrong exponent or a sign error fails (tests/test_checkers.py plants each).
+    from parity import rope_closed_form_check
+
+    def fn(x, shape):
+        return ev(OpKind.RoPE(base, offset, traditional), (x, shape))
+
+    rope_closed_form_check(fn, hd, rows, offset, base, traditional, f"oracle RoPE trad={traditional}")
+
+
+@pytest.mark.parametrize("rd,hd,off,theta", [(4, 4, 0, 10000.0), (4, 8, 3, 10000.0), (6, 6, 11, 100.0)])
+def test_rope_closed_form(rd, hd, off, theta):
+    # OpKind::Rope (cpu_rope, cpu_kernels.rs:608-645): token t, pair i < rd/2
+    # at (2i, 2i+1) rotates by (off + t) * theta^(-2i/rd); dims >= rd pass
+    # through unchanged.
+    tokens = 4
+    for col in range(hd):
+        x = np.zeros((tokens, hd), np.float32)
+        x[:, col] = 1.0
+        y = ev(OpKind.Rope(rd, off, theta), (x, (tokens, hd))).reshape(tokens, hd).astype(np.float64)
+        for t in range(tokens):
+            want = np.zeros(hd)
+            if col >= rd:
+                want[col] = 1.0
+            else:
+                i = col // 2
+                a = (off + t) * theta ** (-2.0 * i / rd)
+                if col % 2 == 0:
+                    want[col], want[col + 1] = math.cos(a), math.sin(a)
+                else:
+                    want[col - 1], want[col] = -math.sin(a), math.cos(a)
+            tol = 1e-6 + 16 * F32_EPS * max(1.0, (off + t))
+            assert np.abs(y[t] - want).max() <= tol, (col, t, y[t], want)
+
+
 def test_embedding_clamps():
     w = np.arange(12, dtype=np.float32).reshape(4, 3)
     idx = np.array([0, 3, 7, -2, 1.9], np.float32)
