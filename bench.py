@@ -42,10 +42,26 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo (platform.processor()
+    gives only the architecture on Linux)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(target_s: float) -> dict:
-    """Oracle timings on bounded samples (rank 0, N = 1 only)."""
+    """Oracle timings on bounded samples (rank 0, N = 1 only): the 4096^3
+    GEMM on a row sample scaled by flop count, config 1 (f32 512^3), the row
+    ops and the SiLU(x*w+b) chain at full size."""
     from oracle import cpu_ref
     from oxidizedmlx_amd import synth
+    from oxidizedmlx_amd.opkind import NodeInput, OpKind, meta
     out = {}
     n = 4096
     A = synth.round_bf16(synth.normal(SEEDS["A"], (n, n)))
@@ -57,6 +73,13 @@ def cpu_baseline(target_s: float) -> dict:
         rows += 4
     dt = time.perf_counter() - t0
     out["gemm"] = {"tflops": 2.0 * rows * n * n / dt / 1e12, "rows": rows, "seconds": dt}
+    A1 = synth.normal(0x5EED0001, (512, 512))
+    B1 = synth.normal(0x5EED0002, (512, 512))
+    C1 = np.zeros((512, 512), np.float32)
+    t0 = time.perf_counter()
+    cpu_ref.matmul_rows(A1, B1, C1, 0, 512)
+    dt = time.perf_counter() - t0
+    out["gemm_f32_512_cfg1"] = {"tflops": 2.0 * 512 ** 3 / dt / 1e12, "seconds": dt, "sample": "full"}
     x = synth.normal(SEEDS["x"], (n, n), 0.0, 2.0)
     for name, fn in [("softmax", lambda: cpu_ref.softmax_lastdim(x)),
                      ("layernorm", lambda: cpu_ref.layer_norm(x, 1e-5)),
@@ -65,7 +88,89 @@ def cpu_baseline(target_s: float) -> dict:
         fn()
         dt = time.perf_counter() - t0
         out[name] = {"gbs": 2 * x.nbytes / dt / 1e9, "seconds": dt}
+    # The reference's unfused graph: Mul, Add, Silu, each its own node.
+    w = synth.uniform(SEEDS["w"], (n, n), -1.0, 1.0)
+    bb = synth.uniform(SEEDS["b"], (n, n), -1.0, 1.0)
+    cpu, m = cpu_ref.CpuRefBackend(), meta([n, n])
+    t0 = time.perf_counter()
+    y = cpu.eval_node(OpKind.Mul, [NodeInput(x.reshape(-1), (n, n)), NodeInput(w.reshape(-1), (n, n))], m)
+    y = cpu.eval_node(OpKind.Add, [NodeInput(y, (n, n)), NodeInput(bb.reshape(-1), (n, n))], m)
+    y = cpu.eval_node(OpKind.Silu, [NodeInput(y, (n, n))], m)
+    dt = time.perf_counter() - t0
+    out["silu_fma_chain"] = {"gbs": 4 * x.nbytes / dt / 1e9, "seconds": dt,
+                             "sample": "full, three oracle nodes (Mul, Add, Silu)"}
     return out
+
+
+def parity_samples(outs: dict) -> dict:
+    """The oracle as checker (part of the CPU-baseline leg, after the timed
+    region): sampled rows of each timed output against the oracle on the
+    same inputs, as max-abs / max-rel error with the test suite's tolerance
+    (assert_allclose semantics, crates/mlx-conformance/src/lib.rs:32-48).
+    `outs` maps a kernel name to its downloaded output and inputs."""
+    from oracle import cpu_ref
+    from oxidizedmlx_amd.opkind import NodeInput, OpKind, meta
+
+    def summary(got, ref, atol, rtol, rows):
+        got = np.asarray(got, np.float64).reshape(-1)
+        ref = np.asarray(ref, np.float64).reshape(-1)
+        d = np.abs(got - ref)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            rel = np.where(ref != 0, d / np.abs(ref), np.where(d == 0, 0.0, np.inf))
+        ok = bool(np.all(d <= atol + rtol * np.abs(ref)))
+        return {"max_abs": float(d.max()), "max_rel": float(rel.max()), "rows": rows,
+                "atol": atol, "rtol": rtol, "pass": ok}
+
+    res = {}
+    for name, o in outs.items():
+        kind = o["kind"]
+        if kind == "gemm":
+            a, b, c, rows = o["a"], o["b"], o["c"], o["rows"]
+            ref = np.zeros((a.shape[0], b.shape[1]), np.float32)
+            for r in rows:
+                cpu_ref.matmul_rows(a, b, ref, int(r), 1)
+            atol = 1e-6 * np.sqrt(a.shape[1]) * float(np.abs(a).max()) * float(np.abs(b).max())
+            res[name] = summary(c[rows], ref[rows], atol, o["rtol"], len(rows))
+        elif kind == "batched":
+            got, ref, nrows = [], [], 0
+            for bi in range(o["a"].shape[0]):
+                a, b = o["a"][bi], o["b"][bi]
+                r = np.zeros((a.shape[0], b.shape[1]), np.float32)
+                for row in o["rows"]:
+                    cpu_ref.matmul_rows(a, b, r, int(row), 1)
+                got.append(o["c"][bi][o["rows"]])
+                ref.append(r[o["rows"]])
+                nrows += len(o["rows"])
+            atol = 1e-6 * np.sqrt(o["a"].shape[2]) * float(np.abs(o["a"]).max()) * float(np.abs(o["b"]).max())
+            res[name] = summary(np.stack(got), np.stack(ref), atol, o["rtol"], nrows)
+        elif kind == "rows":
+            x = np.ascontiguousarray(o["x"])
+            ref = {"softmax": lambda: cpu_ref.softmax_lastdim(x),
+                   "layernorm": lambda: cpu_ref.layer_norm(x, 1e-5),
+                   "rmsnorm": lambda: cpu_ref.rms_norm(x, 1e-5)}[o["op"]]()
+            res[name] = summary(o["y"], ref, 1e-6, 1e-5, x.shape[0])
+        elif kind == "chain":
+            x, w, bb = (np.ascontiguousarray(o[k]) for k in ("x", "w", "b"))
+            shp = x.shape
+            cpu, m = cpu_ref.CpuRefBackend(), meta(list(shp))
+            y = cpu.eval_node(OpKind.Mul, [NodeInput(x.reshape(-1), shp), NodeInput(w.reshape(-1), shp)], m)
+            y = cpu.eval_node(OpKind.Add, [NodeInput(y, shp), NodeInput(bb.reshape(-1), shp)], m)
+            y = cpu.eval_node(OpKind.Silu, [NodeInput(y, shp)], m)
+            res[name] = summary(o["y"], y, 1e-6, 1e-6, shp[0])
+        elif kind == "attention":
+            cpu = cpu_ref.CpuRefBackend()
+            got, ref = [], []
+            for h in o["heads"]:
+                q, k, v = o["q"][h], o["k"][h], o["v"][h]
+                t, dh = q.shape
+                r = cpu.eval_node(OpKind.Attention(o["scale"], True),
+                                  [NodeInput(q.reshape(-1), (t, dh)), NodeInput(k.reshape(-1), (t, dh)),
+                                   NodeInput(v.reshape(-1), (t, dh))], meta([t, dh]))
+                got.append(o["o"][h])
+                ref.append(r)
+            vmax = float(np.abs(o["v"]).max())
+            res[name] = summary(np.stack(got), np.stack(ref), 2e-6 * vmax, 1e-5, len(o["heads"]) * o["q"].shape[1])
+    return res
 
 
 def cpu_decode_baseline(cfg, params, batch: int) -> dict:
@@ -164,8 +269,8 @@ def main() -> int:
     def block_step() -> None:
         from oxidizedmlx_amd.tensor import Tensor, value_and_grad
         st = hb.HipStream()
-        t = {k: Tensor.from_device(st, b.ptr, (bcfg.rows, bcfg.d_model) if k in ("x", "gy")
-                                   else bcfg.param_shapes()[k]) for k, b in blk_dev.items()}
+        t = {k: Tensor.from_device(b.ptr, (bcfg.rows, bcfg.d_model) if k in ("x", "gy")
+                                   else bcfg.param_shapes()[k], st) for k, b in blk_dev.items()}
         params = {k: t[k] for k in bcfg.param_shapes()}
         loss = mnn.TransformerBlock(bcfg, params)(t["x"]).mul(t["gy"]).sum_all()
         _, grads = value_and_grad(loss, list(params.values()) + [t["x"]])
@@ -332,9 +437,61 @@ def main() -> int:
         log(f"bench: {k}: {json.dumps(r)}")
     step_kernels = ("gemm_bf16_4096", "softmax_4096x4096", "layernorm_4096x4096", "rmsnorm_4096x4096",
                     "silu_fma_chain_4096x4096")
+
+    def collect_outputs() -> dict:
+        """Downloads a sample of every timed output with its inputs. Every
+        rotating buffer set holds the same inputs, so set 0's output (written
+        by the warmup and the timed launches) stands for all of them."""
+        outs = {}
+        # One row in each 256-row tile row of the 4096^3 product.
+        grows = np.array([256 * t + (37 * t + 5) % 256 for t in range(16)])
+        if "gemm_bf16_4096" in res:
+            c = synth.bf16_to_f32(dC[0].download(np.uint16, n * n)).reshape(n, n)
+            outs["gemm_bf16_4096"] = dict(kind="gemm", a=synth.bf16_to_f32(A), b=synth.bf16_to_f32(B),
+                                          c=c, rows=grows, rtol=1e-2)
+        if "gemm_f32_512_cfg1" in res:
+            outs["gemm_f32_512_cfg1"] = dict(
+                kind="gemm", a=synth.normal(0x5EED0001, (512, 512)), b=synth.normal(0x5EED0002, (512, 512)),
+                c=C1.download(np.float32, 512 * 512).reshape(512, 512), rows=np.arange(512), rtol=1e-5)
+        for k in ("gemm_bf16_batched_32x1024_cfg3", "gemm_f16_batched_32x1024_cfg3",
+                  "gemm_bf16_batched_32x1024_nt_cfg3"):
+            if k not in res:
+                continue
+            f16 = k.startswith("gemm_f16_")
+            rnd = synth.round_f16 if f16 else synth.round_bf16
+            a = rnd(synth.normal(0x5EED0008, (bt, nb, nb)))
+            b = rnd(synth.normal(0x5EED0009, (bt, nb, nb)))
+            if "_nt_" in k:
+                b = np.ascontiguousarray(b.transpose(0, 2, 1))
+            # The output buffers are shared by the three batched products:
+            # rerun this one into set 0 before reading it.
+            launch(k, 0)
+            hb.synchronize(stream)
+            c = Cb[0].download(np.float32, bt * nb * nb).reshape(bt, nb, nb)
+            outs[k] = dict(kind="batched", a=a, b=b, c=c, rows=np.array([0, 300, 700, 1023]), rtol=1e-2)
+        if "gemm_bf16_odd_1000x777x1531_cfg3" in res:
+            outs["gemm_bf16_odd_1000x777x1531_cfg3"] = dict(
+                kind="gemm", a=synth.round_bf16(synth.normal(0x5EED000A, (mo, ko))),
+                b=synth.round_bf16(synth.normal(0x5EED000B, (ko, no))),
+                c=Co.download(np.float32, mo * no).reshape(mo, no), rows=np.arange(0, mo, 40), rtol=1e-2)
+        rsel = np.arange(0, n, 64)
+        for op, k in (("softmax", "softmax_4096x4096"), ("layernorm", "layernorm_4096x4096"),
+                      ("rmsnorm", "rmsnorm_4096x4096")):
+            if k in res:
+                y = ys[op][0].download(np.float32, n * n).reshape(n, n)
+                outs[k] = dict(kind="rows", op=op, x=x[rsel], y=y[rsel])
+        if "silu_fma_chain_4096x4096" in res:
+            y = ys["chain"][0].download(np.float32, n * n).reshape(n, n)
+            outs["silu_fma_chain_4096x4096"] = dict(kind="chain", x=x[rsel], w=w[rsel], b=bb[rsel], y=y[rsel])
+        if "attention_fused_cfg4" in res:
+            q, k_, v = (synth.normal(0x5EED0300 + i, (at_bh, at_t, at_dh)) for i in range(3))
+            o = at_bufs["o"].download(np.float32, at_bh * at_t * at_dh).reshape(at_bh, at_t, at_dh)
+            outs["attention_fused_cfg4"] = dict(kind="attention", q=q, k=k_, v=v, o=o, heads=[0, 37, 63],
+                                                scale=float(np.float32(1.0 / np.sqrt(at_dh))))
+        return outs
     total_ms = sum(r["us"] for k, r in res.items() if k in step_kernels) / 1e3
 
-    cpu = None
+    cpu = parity = None
     if not args.no_cpu and not only:
         log(f"bench: CPU baseline (oracle, 1 thread, ~{args.cpu_seconds:.0f}s GEMM sample)")
         cb = cpu_baseline(args.cpu_seconds)
@@ -342,12 +499,15 @@ def main() -> int:
             "value": cb["gemm"]["tflops"], "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": (f"{cb['gemm']['rows']} of 4096 rows of the 4096^3 product by the oracle's "
                        f"i-j-p f32 loop on bf16-rounded inputs ({cb['gemm']['seconds']:.1f}s), "
-                       f"scaled by flop count; host {platform.processor() or platform.machine()}, "
-                       f"1 core of {os.cpu_count()}"),
+                       f"scaled by flop count; host {cpu_model()}, 1 core of {os.cpu_count()}"),
             "kernels": {k: v for k, v in cb.items() if k != "gemm"},
         }
         if dparams is not None:
             cpu["kernels"]["decode_cfg5"] = cpu_decode_baseline(dcfg, dparams, d_batch)
+        log("bench: parity of sampled outputs against the oracle")
+        parity = parity_samples(collect_outputs())
+        for k, v in parity.items():
+            log(f"bench: parity {k}: {json.dumps(v)}")
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
@@ -376,6 +536,7 @@ def main() -> int:
                       "unit": "TFLOP/s", "frac": g["tflops"] / BF16_PEAK_TFLOPS,
                       "traffic": traffic} if g else None),
         "cpu_baseline": cpu,
+        "parity": parity,
         "kernels": res,
         "wall_s": wall,
     }
