@@ -144,6 +144,19 @@ const char* mlxhip_last_error(void);
  * callers of the handle/id-returning functions recover the MlxError variant. */
 int mlxhip_last_status(void);
 
+/* The payload of MlxError::ShapeMismatch{expected, got}
+ * (crates/mlx-core/src/lib.rs:40-41) for the last failure on this thread,
+ * when that failure was MLXHIP_ERR_SHAPE_MISMATCH: copies up to `cap` dims of
+ * each shape into `expected` / `got` (either may be NULL) and stores their
+ * full lengths in *expected_ndim / *got_ndim. Returns MLXHIP_OK, or
+ * MLXHIP_ERR_INVALID_ARGUMENT (without recording a new error) when the last
+ * failure was not a shape mismatch. The shapes are the reference's for the
+ * same failure: e.g. matmul K mismatch expected [M, K], got [K2, N]
+ * (cpu_kernels.rs:212-217); binary ops expected = lhs shape, got = rhs shape
+ * (:117-121); VJPs expected = the forward input's shape, got = dy's. */
+int mlxhip_last_shape_mismatch(int64_t* expected, size_t* expected_ndim,
+                               int64_t* got, size_t* got_ndim, size_t cap);
+
 /* Number of visible HIP devices (0 when no GPU; never fails). */
 int mlxhip_device_count(void);
 

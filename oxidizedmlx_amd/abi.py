@@ -49,7 +49,15 @@ class FfiFailed(MlxError):
 
 
 class ShapeMismatch(MlxError):
+    """MlxError::ShapeMismatch{expected, got}; `expected` / `got` carry the
+    shapes (from mlxhip_last_shape_mismatch) when the library recorded them."""
+
     code = ERR_SHAPE_MISMATCH
+
+    def __init__(self, msg: str = "", expected=None, got=None):
+        super().__init__(msg)
+        self.expected = expected
+        self.got = got
 
 
 class InvalidArgument(MlxError):
@@ -154,6 +162,8 @@ PROTOTYPES = {
     "mlxhip_abi_version": (_i, []),
     "mlxhip_last_error": (C.c_char_p, []),
     "mlxhip_last_status": (_i, []),
+    "mlxhip_last_shape_mismatch": (_i, [C.POINTER(_i64), C.POINTER(_sz), C.POINTER(_i64),
+                                        C.POINTER(_sz), _sz]),
     "mlxhip_device_count": (_i, []),
     "mlxhip_init": (_i, [_i]),
     "mlxhip_synchronize": (_i, [_vp]),
@@ -242,12 +252,25 @@ def load_library(path: str | None = None) -> C.CDLL:
         return lib
 
 
+def last_shape_mismatch(lib: C.CDLL) -> tuple[list[int], list[int]] | None:
+    """(expected, got) of the calling thread's last ShapeMismatch, or None."""
+    cap = 16
+    e, g = (C.c_int64 * cap)(), (C.c_int64 * cap)()
+    ne, ng = C.c_size_t(0), C.c_size_t(0)
+    if lib.mlxhip_last_shape_mismatch(e, C.byref(ne), g, C.byref(ng), cap) != OK:
+        return None
+    return [e[i] for i in range(min(cap, ne.value))], [g[i] for i in range(min(cap, ng.value))]
+
+
 def check(rc: int, lib: C.CDLL | None = None) -> None:
     """Raises the MlxError subclass matching a non-zero status code."""
     if rc != OK:
         lib = lib or load_library()
-        msg = lib.mlxhip_last_error() or b""
-        raise error_for(rc, msg.decode(errors="replace"))
+        msg = (lib.mlxhip_last_error() or b"").decode(errors="replace")
+        if rc == ERR_SHAPE_MISMATCH:
+            shapes = last_shape_mismatch(lib)
+            raise ShapeMismatch(msg, *(shapes or (None, None)))
+        raise error_for(rc, msg)
 
 
 def int64_array(vals) -> C.Array:

@@ -97,7 +97,7 @@ struct Builder {
     bool same_shape(uint64_t a, uint64_t b, const char* what) {
         if (!a || !b) return false;
         if (shape(a) == shape(b)) return true;
-        fail(MLXHIP_ERR_SHAPE_MISMATCH, "%s: operand shapes differ", what);
+        fail_shape(shape(a), shape(b), what);
         return false;
     }
 
@@ -136,7 +136,7 @@ struct Builder {
         const size_t r = sa.size();
         if (!((r == 2 && sb.size() == 2) || (r == 3 && sb.size() == 3 && sa[0] == sb[0])) ||
             sa[r - 1] != sb[r - 2]) {
-            fail(MLXHIP_ERR_SHAPE_MISMATCH, "MatMul: incompatible operand shapes");
+            fail_shape(sa, sb, "MatMul");
             return 0;
         }
         std::vector<int64_t> out(sa.begin(), sa.end() - 1);
@@ -287,7 +287,7 @@ int vjp(Builder& b, uint64_t id, const Node& n, uint64_t g, const std::vector<bo
             const std::vector<int64_t> ish = b.shape(in[0]);
             uint64_t gi = g;
             if (b.shape(g).size() < ish.size())
-                return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Broadcast gradient has fewer axes than the input");
+                return fail_shape(ish, b.shape(g), "Broadcast gradient");
             const size_t pad = b.shape(g).size() - ish.size();
             for (size_t i = 0; i < pad && gi; ++i) gi = b.sum_axis(gi, 0);
             for (size_t i = 0; i < ish.size() && gi; ++i) {

@@ -29,6 +29,9 @@ std::string& last_error() {
 }
 
 static thread_local int t_last_status = MLXHIP_OK;
+// expected / got of the last ShapeMismatch on this thread (cleared by every
+// other failure).
+static thread_local std::vector<int64_t> t_shape_expected, t_shape_got;
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -38,7 +41,25 @@ int fail(int code, const char* fmt, ...) {
     va_end(ap);
     last_error() = buf;
     t_last_status = code;
+    t_shape_expected.clear();
+    t_shape_got.clear();
     return code;
+}
+
+namespace {
+std::string dims_str(const std::vector<int64_t>& d) {
+    std::string r = "[";
+    for (size_t i = 0; i < d.size(); ++i) r += (i ? ", " : "") + std::to_string(d[i]);
+    return r + "]";
+}
+}  // namespace
+
+int fail_shape(std::vector<int64_t> expected, std::vector<int64_t> got, const char* context) {
+    fail(MLXHIP_ERR_SHAPE_MISMATCH, "%s%sShape mismatch: expected %s, got %s", context ? context : "",
+         context ? ": " : "", dims_str(expected).c_str(), dims_str(got).c_str());
+    t_shape_expected = std::move(expected);
+    t_shape_got = std::move(got);
+    return MLXHIP_ERR_SHAPE_MISMATCH;
 }
 
 int hip_fail(hipError_t e, const char* what) {
@@ -146,6 +167,13 @@ void* pool_alloc(size_t bytes) {
             for (void* q : drop) P.owned.erase(q);
         }
         for (void* q : drop) (void)hipFree(q);
+        // Stream-ordered scratch (StreamBuf) returns to the device's default
+        // async pool, which keeps freed blocks (release threshold UINT64_MAX):
+        // hand those back to the driver too before the retry.
+        hipMemPool_t ap;
+        if (hipDeviceSynchronize() == hipSuccess && hipDeviceGetDefaultMemPool(&ap, dev) == hipSuccess)
+            (void)hipMemPoolTrimTo(ap, 0);
+        (void)hipGetLastError();
         if (hipMalloc(&p, sz) != hipSuccess) {
             (void)hipGetLastError();
             return nullptr;
@@ -212,9 +240,7 @@ int64_t prod(const int64_t* s, size_t lo, size_t hi) {
 
 // Output size the op produces must match the buffer sized from out_meta.
 int expect_len(int64_t have, int64_t want, const char* op) {
-    if (have != want)
-        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "%s: output has %lld elements but out_meta holds %lld", op,
-                    (long long)have, (long long)want);
+    if (have != want) return fail_shape({want}, {have}, op);
     return MLXHIP_OK;
 }
 
@@ -256,30 +282,21 @@ int eval_matmul(const mlxhip_input_t* in, size_t n_inputs, const mlxhip_meta_t& 
     const size_t r = a.ndim - 2;  // index of the first matrix dimension
     const int64_t batch = a.ndim == 3 ? a.shape[0] : 1;
     if (a.ndim == 3 && b.shape[0] != batch)
-        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: batch %lld vs %lld", (long long)batch,
-                    (long long)b.shape[0]);
+        return fail_shape(std::vector<int64_t>(a.shape, a.shape + a.ndim),
+                          std::vector<int64_t>(b.shape, b.shape + b.ndim), "matmul batch");
     const bool ta = trans_hint && trans_hint[0], tb = trans_hint && trans_hint[1];
     // With a folded Transpose the input holds the source [K, M] / [N, K].
     const int64_t m = ta ? a.shape[r + 1] : a.shape[r], k = ta ? a.shape[r] : a.shape[r + 1];
     const int64_t k2 = tb ? b.shape[r + 1] : b.shape[r], n = tb ? b.shape[r] : b.shape[r + 1];
-    if (k != k2)
-        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: expected [%lld, %lld], got [%lld, %lld]",
-                    (long long)m, (long long)k, (long long)k2, (long long)n);
+    if (k != k2) return fail_shape({m, k}, {k2, n});
     MLXHIP_TRY(expect_len(batch * m * n, numel_of(meta.shape, meta.ndim), "matmul"));
     const int64_t lda = ta ? m : k, ldb = tb ? k : n;
-    // The reference stores every logical dtype as f32 (crates/mlx-core/src/tensor.rs:105-125);
-    // a bf16/f16 MatMul rounds both operands to that type (RNE) and runs the
-    // 16-bit MFMA with f32 accumulation and f32 output.
-    const int dt = meta.dtype;
-    if ((dt == MLXHIP_DTYPE_BF16 || dt == MLXHIP_DTYPE_F16) && batch * m * n * k > 0) {
-        void* a16 = scratch.get_bytes((size_t)(batch * m * k) * 2);
-        void* b16 = scratch.get_bytes((size_t)(batch * k * n) * 2);
-        if (!a16 || !b16) return fail(MLXHIP_ERR_FFI_FAILED, "matmul: scratch allocation failed");
-        MLXHIP_TRY(cast(a.data, MLXHIP_DTYPE_F32, a16, dt, batch * m * k, s));
-        MLXHIP_TRY(cast(b.data, MLXHIP_DTYPE_F32, b16, dt, batch * k * n, s));
-        return gemm(dt, MLXHIP_DTYPE_F32, ta, tb, m, n, k, batch, a16, lda, m * k, b16, ldb, k * n, out, n,
-                    m * n, s);
-    }
+    // The reference stores every logical dtype as f32 (crates/mlx-core/src/tensor.rs:105-125)
+    // and its matmul multiplies those stored values (cpu_kernels.rs:197-230),
+    // whatever the dtype tag: a bf16/f16-tagged MatMul node is an f32 product
+    // here too. The 16-bit MFMA path (operands held as bf16/f16) is the
+    // explicit mlxhip_gemm with ab_dtype BF16/F16.
+    (void)scratch;
     return gemm(MLXHIP_DTYPE_F32, MLXHIP_DTYPE_F32, ta, tb, m, n, k, batch, a.data, lda, m * k, b.data, ldb,
                 k * n, out, n, m * n, s);
 }
@@ -293,12 +310,8 @@ int eval_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inp
     if (q.ndim != 2 || k.ndim != 2 || v.ndim != 2) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "Attention inputs must be 2D");
     const int64_t tq = q.shape[0], dh = q.shape[1], tk = k.shape[0], dhk = k.shape[1];
     const int64_t tkv = v.shape[0], dhv = v.shape[1];
-    if (dh != dhk)
-        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: expected [%lld, %lld], got [%lld, %lld]",
-                    (long long)tq, (long long)dh, (long long)tk, (long long)dhk);
-    if (tk != tkv || dh != dhv)
-        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: expected [%lld, %lld], got [%lld, %lld]",
-                    (long long)tk, (long long)dh, (long long)tkv, (long long)dhv);
+    if (dh != dhk) return fail_shape({tq, dh}, {tk, dhk});
+    if (tk != tkv || dh != dhv) return fail_shape({tk, dh}, {tkv, dhv});
     MLXHIP_TRY(expect_len(tq * dh, numel_of(meta.shape, meta.ndim), "attention"));
     if (tq * dh == 0) return MLXHIP_OK;
     if (tk > 0 && attention_fused_supported(dh, tq, tk) &&
@@ -325,8 +338,7 @@ int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_i
     for (size_t i = 0; i < n_inputs; ++i) {
         if (in[i].ndim && !in[i].shape) return fail(MLXHIP_ERR_NULL_PTR, "input %zu has a null shape", i);
         if ((int64_t)in[i].len != numel_of(in[i].shape, in[i].ndim))
-            return fail(MLXHIP_ERR_SHAPE_MISMATCH, "input %zu holds %zu values for shape %s", i, in[i].len,
-                        shape_str(in[i].shape, in[i].ndim).c_str());
+            return fail_shape({numel_of(in[i].shape, in[i].ndim)}, {(int64_t)in[i].len}, "input length");
         if (in[i].len && !in[i].data) return fail(MLXHIP_ERR_NULL_PTR, "input %zu is null", i);
     }
     if (meta.ndim && !meta.shape) return fail(MLXHIP_ERR_NULL_PTR, "out_meta has a null shape");
@@ -341,8 +353,8 @@ int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_i
             REQUIRE(0);
             REQUIRE(1);
             if (in[0].len != in[1].len)
-                return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: expected %s, got %s",
-                            shape_str(in[0].shape, in[0].ndim).c_str(), shape_str(in[1].shape, in[1].ndim).c_str());
+                return fail_shape(std::vector<int64_t>(in[0].shape, in[0].shape + in[0].ndim),
+                              std::vector<int64_t>(in[1].shape, in[1].shape + in[1].ndim));
             MLXHIP_TRY(expect_len((int64_t)in[0].len, out_n, "binary"));
             const int ew = op.kind == MLXHIP_OP_ADD ? MLXHIP_EW_ADD
                            : op.kind == MLXHIP_OP_SUB ? MLXHIP_EW_SUB
@@ -371,8 +383,8 @@ int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_i
             REQUIRE(0);
             REQUIRE(1);
             if (in[0].len != in[1].len)
-                return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: expected %s, got %s",
-                            shape_str(in[1].shape, in[1].ndim).c_str(), shape_str(in[0].shape, in[0].ndim).c_str());
+                return fail_shape(std::vector<int64_t>(in[1].shape, in[1].shape + in[1].ndim),
+                              std::vector<int64_t>(in[0].shape, in[0].shape + in[0].ndim));
             MLXHIP_TRY(expect_len((int64_t)in[0].len, out_n, "activation vjp"));
             // acc = x (input 1), operand = dy (input 0)
             return ew2(op.kind == MLXHIP_OP_SILU_VJP ? MLXHIP_EW_SILU_VJP : MLXHIP_EW_GELU_VJP, in[1].data,
@@ -490,8 +502,8 @@ int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_i
             REQUIRE(1);
             const mlxhip_input_t &dy = in[0], &x = in[1];
             if (!same_shape(dy, x) || dy.len != x.len)
-                return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: expected %s, got %s",
-                            shape_str(x.shape, x.ndim).c_str(), shape_str(dy.shape, dy.ndim).c_str());
+                return fail_shape(std::vector<int64_t>(x.shape, x.shape + x.ndim),
+                              std::vector<int64_t>(dy.shape, dy.shape + dy.ndim));
             MLXHIP_TRY(expect_len((int64_t)x.len, out_n, "norm vjp"));
             if (x.ndim == 0) return copy_dev(out, dy.data, out_n, s);
             const int64_t d = x.shape[x.ndim - 1];
@@ -504,8 +516,8 @@ int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_i
             REQUIRE(1);
             const mlxhip_input_t &dy = in[0], &sm = in[1];
             if (dy.len != sm.len)
-                return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: expected %s, got %s",
-                            shape_str(sm.shape, sm.ndim).c_str(), shape_str(dy.shape, dy.ndim).c_str());
+                return fail_shape(std::vector<int64_t>(sm.shape, sm.shape + sm.ndim),
+                              std::vector<int64_t>(dy.shape, dy.shape + dy.ndim));
             size_t ax;
             MLXHIP_TRY(resolve_axis(op.axis, sm.ndim, "", &ax));
             MLXHIP_TRY(expect_len((int64_t)sm.len, out_n, "softmax vjp"));
@@ -537,8 +549,8 @@ int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_i
                     return fail(MLXHIP_ERR_INVALID_ARGUMENT, "Concatenate: all inputs must have same ndim");
                 for (size_t d = 0; d < f.ndim; ++d)
                     if (d != ax && in[i].shape[d] != f.shape[d])
-                        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "Shape mismatch: expected %s, got %s",
-                                    shape_str(f.shape, f.ndim).c_str(), shape_str(in[i].shape, in[i].ndim).c_str());
+                        return fail_shape(std::vector<int64_t>(f.shape, f.shape + f.ndim),
+                              std::vector<int64_t>(in[i].shape, in[i].shape + in[i].ndim));
                 total += in[i].shape[ax];
             }
             const int64_t outer = prod(f.shape, 0, ax), inner = prod(f.shape, ax + 1, f.ndim);
@@ -578,6 +590,17 @@ const char* mlxhip_last_error(void) { return last_error().c_str(); }
 
 int mlxhip_last_status(void) { return t_last_status; }
 
+int mlxhip_last_shape_mismatch(int64_t* expected, size_t* expected_ndim, int64_t* got, size_t* got_ndim,
+                               size_t cap) {
+    if (t_last_status != MLXHIP_ERR_SHAPE_MISMATCH || (t_shape_expected.empty() && t_shape_got.empty()))
+        return MLXHIP_ERR_INVALID_ARGUMENT;  // not recorded through fail(): leaves the last error as it is
+    if (expected_ndim) *expected_ndim = t_shape_expected.size();
+    if (got_ndim) *got_ndim = t_shape_got.size();
+    for (size_t i = 0; expected && i < t_shape_expected.size() && i < cap; ++i) expected[i] = t_shape_expected[i];
+    for (size_t i = 0; got && i < t_shape_got.size() && i < cap; ++i) got[i] = t_shape_got[i];
+    return MLXHIP_OK;
+}
+
 int mlxhip_device_count(void) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess) return 0;
@@ -606,8 +629,7 @@ int mlxhip_eval_node(const mlxhip_op_t* op, const mlxhip_input_t* inputs, size_t
     if (!op || !out_meta || (n_inputs && !inputs)) return fail(MLXHIP_ERR_NULL_PTR, "eval_node: null argument");
     const int64_t want = numel_of(out_meta->shape, out_meta->ndim);
     if ((int64_t)out_len != want)
-        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "eval_node: out_len %zu but out_meta holds %lld", out_len,
-                    (long long)want);
+        return fail_shape({want}, {(int64_t)out_len}, "eval_node out_len");
     if (want && !out_host) return fail(MLXHIP_ERR_NULL_PTR, "eval_node: null output");
     MLXHIP_TRY(ensure_device());
     hipStream_t s = thread_stream();

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/mlxhip.h"
 
@@ -19,6 +20,12 @@ std::string& last_error();
 
 // Records a failure and returns its status code.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Records MlxError::ShapeMismatch{expected, got} (crates/mlx-core/src/lib.rs:40-41):
+// the message "[context: ]Shape mismatch: expected [..], got [..]" and both
+// shapes, which mlxhip_last_shape_mismatch returns. Returns
+// MLXHIP_ERR_SHAPE_MISMATCH.
+int fail_shape(std::vector<int64_t> expected, std::vector<int64_t> got, const char* context = nullptr);
 
 // Maps a HIP runtime error onto MlxError::FfiFailed with the call site.
 int hip_fail(hipError_t e, const char* what);

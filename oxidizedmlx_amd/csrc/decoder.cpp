@@ -364,8 +364,7 @@ int mlxhip_decoder_set_param(mlxhip_decoder_t* D, int32_t layer, int32_t which, 
         }
     }
     if (len != want)
-        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "decoder_set_param: parameter %d has %zu values, expected %zu", which,
-                    len, want);
+        return fail_shape({(int64_t)want}, {(int64_t)len}, "decoder_set_param");
     std::vector<uint16_t> h(len);
     for (size_t i = 0; i < len; ++i) h[i] = bf16_rne_host(values[i]);
     std::lock_guard<std::mutex> g(D->mu);

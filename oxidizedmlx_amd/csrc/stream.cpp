@@ -470,7 +470,7 @@ int mlxhip_stream_get_buffer(mlxhip_stream_t* s, uint64_t node, float* out, size
     auto it = s->buffers.find(node);
     if (it == s->buffers.end()) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "stream_get_buffer: node not materialised");
     if (len != it->second.len)
-        return fail(MLXHIP_ERR_SHAPE_MISMATCH, "stream_get_buffer: %zu requested, buffer holds %zu", len, it->second.len);
+        return fail_shape({(int64_t)it->second.len}, {(int64_t)len}, "stream_get_buffer");
     if (!len) return MLXHIP_OK;
     MLXHIP_HIP(hipSetDevice(s->device));
     MLXHIP_HIP(hipMemcpyAsync(out, it->second.ptr, len * sizeof(float), hipMemcpyDeviceToHost, s->hs));

@@ -88,3 +88,22 @@ def test_no_gpu_means_backend_unavailable(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(abi.BackendUnavailable):
         abi.load_library(str(tmp_path / "nope.so"))
+
+
+def test_shape_mismatch_payload_without_gpu(lib):
+    # mlxhip_eval_node checks out_len against out_meta before any device call;
+    # the failure carries MlxError::ShapeMismatch{expected, got}.
+    from oxidizedmlx_amd.opkind import OpKind, meta
+    cop, k1 = OpKind.Neg.to_c()
+    cm, k2 = meta([2, 3]).to_c()
+    out = (C.c_float * 5)()
+    rc = lib.mlxhip_eval_node(C.byref(cop), None, 0, C.byref(cm), C.addressof(out), 5)
+    assert rc == abi.ERR_SHAPE_MISMATCH
+    assert abi.last_shape_mismatch(lib) == ([6], [5])
+    with pytest.raises(abi.ShapeMismatch) as ei:
+        abi.check(rc, lib)
+    assert (ei.value.expected, ei.value.got) == ([6], [5])
+    assert b"Shape mismatch: expected [6], got [5]" in lib.mlxhip_last_error()
+    # Any other failure clears the payload.
+    assert lib.mlxhip_eval_node(None, None, 0, None, None, 0) == abi.ERR_NULL_PTR
+    assert abi.last_shape_mismatch(lib) is None

@@ -195,8 +195,10 @@ def test_stream_errors_match_reference():
     a = s.add_constant(np.ones(6, np.float32), meta([2, 3]))
     b = s.add_constant(np.ones(8, np.float32), meta([4, 2]))
     mm = s.add_op(OpKind.MatMul, [a, b], meta([2, 2]))
-    with pytest.raises(abi.ShapeMismatch):
+    with pytest.raises(abi.ShapeMismatch) as ei:
         s.eval(mm)
+    # MlxError::ShapeMismatch{expected: [m, k], got: [k2, n]} (cpu_kernels.rs:212-217)
+    assert (ei.value.expected, ei.value.got) == ([2, 3], [4, 2])
     v = s.add_constant(np.ones(3, np.float32), meta([3]))
     mm1 = s.add_op(OpKind.MatMul, [v, v], meta([1]))
     with pytest.raises(abi.InvalidArgument):
@@ -219,13 +221,18 @@ def test_eval_node_host_contract_matches_oracle():
         h = HipBackend().eval_node(op, inp, meta([64, 96]))
         c = cpu_ref.CpuRefBackend().eval_node(op, inp, meta([64, 96]))
         assert_allclose(h, c, 1e-6, 1e-5, repr(op))
-    # bf16 MatMul: operands rounded to bf16, f32 accumulate (logical dtype tag)
+    # bf16/f16-tagged MatMul: the tag is logical only (tensor.rs:105-125); the
+    # stored f32 values are multiplied unrounded, as the oracle does.
     a, b = gen_data(33 * 40, 10), gen_data(40 * 21, 11)
-    h = HipBackend().eval_node(OpKind.MatMul, [NodeInput(a, (33, 40), abi.BF16),
-                                               NodeInput(b, (40, 21), abi.BF16)],
-                               meta([33, 21], abi.BF16))
-    c = synth.round_bf16(a).reshape(33, 40).astype(np.float64) @ synth.round_bf16(b).reshape(40, 21)
-    np.testing.assert_allclose(h.reshape(33, 21), c, rtol=1e-4, atol=1e-5)
+    for dt in (abi.BF16, abi.F16):
+        inp = [NodeInput(a, (33, 40), dt), NodeInput(b, (40, 21), dt)]
+        h = HipBackend().eval_node(OpKind.MatMul, inp, meta([33, 21], dt))
+        c = cpu_ref.CpuRefBackend().eval_node(OpKind.MatMul, inp, meta([33, 21], dt))
+        assert_allclose(h, c, 1e-6 * np.sqrt(40), 1e-5, f"MatMul tagged {dt}")
+        # Rounding the operands to 16 bits would move results by ~1e-3.
+        r16 = synth.round_bf16(a).reshape(33, 40).astype(np.float64) @ synth.round_bf16(b).reshape(40, 21)
+        if dt == abi.BF16:
+            assert np.abs(h.reshape(33, 21) - r16).max() > 1e-4
 
 
 def test_empty_tensors():
