@@ -108,14 +108,46 @@ class CausalSelfAttention:
         q, k, v = self._heads(self.wq(x)), self._heads(self.wk(x)), self._heads(self.wv(x))
         scores = q.matmul(k.transpose((0, 2, 1)))                      # [B*H, S, S]
         st = x.stream
-        scale = Tensor.from_f32(st, [1.0 / math.sqrt(dh)], ()).broadcast_to(scores.shape)
-        mask = Tensor.from_f32(st, causal_mask(self.s), (self.s, self.s)).broadcast_to(scores.shape)
+        scale = Tensor.from_f32_on_stream([1.0 / math.sqrt(dh)], (), st).broadcast_to(scores.shape)
+        mask = Tensor.from_f32_on_stream(causal_mask(self.s), (self.s, self.s), st).broadcast_to(scores.shape)
         p = scores.mul(scale).add(mask).softmax(-1)
         o = p.matmul(v)                                                 # [B*H, S, Dh]
         o = o.reshape((self.b, self.h, self.s, dh)).transpose((0, 2, 1, 3)).reshape((bs, d))
         return self.wo(o)
 
     __call__ = forward
+
+
+class MultiHeadAttention:
+    """The reference's multi-head causal self-attention over one sequence x
+    [seq, model_dim] (crates/mlx-nn/src/attention.rs:12-111): Q/K/V Linear
+    projections, [seq, H, Dh] -> [H, seq, Dh] per projection, then per head a
+    Narrow of one head, a Reshape to [seq, Dh] and the fused Attention op
+    (scale 1/sqrt(Dh), causal), the heads concatenated along axis 1 and the
+    output projection. Forward only: Narrow, Attention and Concatenate have
+    no VJP in the reference (crates/mlx-autograd/src/vjp.rs:173-176)."""
+
+    def __init__(self, wq: Linear, wk: Linear, wv: Linear, wo: Linear, n_heads: int):
+        self.wq, self.wk, self.wv, self.wo = wq, wk, wv, wo
+        self.n_heads = n_heads
+        self.head_dim = wq.weight.shape[0] // n_heads   # attention.rs:28-31
+
+    def forward_causal(self, x: Tensor) -> Tensor:
+        seq = x.shape[0]
+        h, dh = self.n_heads, self.head_dim
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(dh)))
+
+        def heads(t: Tensor) -> Tensor:
+            return t.reshape((seq, h, dh)).transpose((1, 0, 2))
+
+        q, k, v = heads(self.wq(x)), heads(self.wk(x)), heads(self.wv(x))
+        outs = []
+        for i in range(h):
+            qh = q.narrow(0, i, 1).reshape((seq, dh))
+            kh = k.narrow(0, i, 1).reshape((seq, dh))
+            vh = v.narrow(0, i, 1).reshape((seq, dh))
+            outs.append(qh.attention(kh, vh, scale, True))
+        return self.wo(Tensor.cat(outs, 1))
 
 
 class Mlp:
@@ -265,17 +297,17 @@ class DecoderLM:
     def __init__(self, cfg: DecoderConfig, stream, params: dict):
         self.cfg, self.stream = cfg, stream
         V, d = cfg.vocab, cfg.d_model
-        self.embed = Embedding(Tensor.from_f32(stream, params["embedding"], (V, d)))
-        self.lm_head = Linear(Tensor.from_f32(stream, params["lm_head"], (V, d)))
+        self.embed = Embedding(Tensor.from_f32_on_stream(params["embedding"], (V, d), stream))
+        self.lm_head = Linear(Tensor.from_f32_on_stream(params["lm_head"], (V, d), stream))
         shapes = cfg.block(1, 1).param_shapes()
-        self.layer_params = [{k: Tensor.from_f32(stream, lp[k], shapes[k]) for k in shapes}
+        self.layer_params = [{k: Tensor.from_f32_on_stream(lp[k], shapes[k], stream) for k in shapes}
                              for lp in params["layers"]]
         self.norm = RmsNorm(d, cfg.eps)
 
     def forward(self, tokens: np.ndarray) -> Tensor:
         tokens = np.asarray(tokens)
         b, s = tokens.shape
-        ids = Tensor.from_f32(self.stream, tokens.reshape(-1).astype(np.float32), (b * s,))
+        ids = Tensor.from_f32_on_stream(tokens.reshape(-1).astype(np.float32), (b * s,), self.stream)
         x = self.embed(ids)
         for lp in self.layer_params:
             x = TransformerBlock(self.cfg.block(b, s), lp)(x)

@@ -9,10 +9,22 @@ methods ``add_constant(data, meta)``, ``add_op(op, inputs, meta)``,
 ``eval_many(ids)``, ``get_buffer(id)`` and ``grad(loss, wrt)``:
 ``backend.HipStream`` (graph, scheduler and autograd in libmlxhip.so) is the
 product; the same graph code also runs on the test oracle's CPU stream.
+
+Constructors without a stream (``from_f32``, ``zeros``, ``ones``,
+``from_data_with_dtype``) bind to the process default stream, as the
+reference's do (tensor.rs:55-78,127-141 over ``default_stream()``,
+crates/mlx-core/src/backend.rs:193-200). The reference's default is fixed to
+its CPU backend; here it is selectable: ``set_default_stream(stream)``, or the
+environment variable ``MLX_RS_BACKEND`` read when the default is first needed
+("hip", the default, makes a ``HipStream``; this package has no other
+backend, so any other value raises ``BackendUnavailable``).
 """
 from __future__ import annotations
 
-from typing import Callable, Optional, Sequence, Tuple
+import contextlib
+import os
+import threading
+from typing import Callable, Iterator, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -31,6 +43,47 @@ def _numel(shape: Sequence[int]) -> int:
     return n
 
 
+_default_lock = threading.Lock()
+_default_stream = None
+
+
+def set_default_stream(stream) -> None:
+    """Makes ``stream`` the process default for constructors without an
+    explicit stream (None: back to ``MLX_RS_BACKEND``'s choice on next use)."""
+    global _default_stream
+    with _default_lock:
+        _default_stream = stream
+
+
+def default_stream():
+    """The process default stream (``default_stream()``, backend.rs:198-200),
+    created on first use from ``MLX_RS_BACKEND`` unless one was set."""
+    global _default_stream
+    with _default_lock:
+        if _default_stream is None:
+            which = os.environ.get("MLX_RS_BACKEND", "hip").strip().lower()
+            if which != "hip":
+                raise abi.BackendUnavailable(
+                    f"MLX_RS_BACKEND={which!r}: this package provides the 'hip' backend only")
+            from .backend import HipStream
+            _default_stream = HipStream()
+        return _default_stream
+
+
+@contextlib.contextmanager
+def default_stream_scope(stream) -> Iterator[object]:
+    """Sets the default stream for the ``with`` body, then restores the
+    previous one."""
+    global _default_stream
+    with _default_lock:
+        prev, _default_stream = _default_stream, stream
+    try:
+        yield stream
+    finally:
+        with _default_lock:
+            _default_stream = prev
+
+
 class Tensor:
     """Lazy tensor handle: (stream, node id, shape, dtype)."""
 
@@ -42,9 +95,10 @@ class Tensor:
         self.shape = _shape(shape)
         self.dtype = dtype
 
-    # ── creation (tensor.rs:55-103) ──────────────────────────────────────
+    # ── creation (tensor.rs:55-141) ──────────────────────────────────────
     @classmethod
-    def from_f32(cls, stream, data, shape: Sequence[int], dtype: int = abi.F32) -> "Tensor":
+    def from_f32_on_stream(cls, data, shape: Sequence[int], stream, dtype: int = abi.F32) -> "Tensor":
+        """A Constant on ``stream`` (tensor.rs:81-103)."""
         shape = _shape(shape)
         d = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
         if d.size != _numel(shape):
@@ -53,13 +107,39 @@ class Tensor:
         return cls(stream, stream.add_constant(d, TensorMeta(shape, dtype)), shape, dtype)
 
     @classmethod
-    def from_device(cls, stream, ptr: int, shape: Sequence[int], dtype: int = abi.F32) -> "Tensor":
-        """Constant copied from f32 device memory (HipStream only)."""
+    def from_f32(cls, data, shape: Sequence[int], stream=None) -> "Tensor":
+        """A Constant on the default stream (tensor.rs:66-78), or on
+        ``stream`` when one is given."""
+        return cls.from_f32_on_stream(data, shape, stream if stream is not None else default_stream())
+
+    @classmethod
+    def from_data_with_dtype(cls, data, shape: Sequence[int], dtype: int, stream=None) -> "Tensor":
+        """f32 data with a logical dtype tag (tensor.rs:105-125)."""
+        return cls.from_f32_on_stream(data, shape, stream if stream is not None else default_stream(), dtype)
+
+    @classmethod
+    def zeros(cls, shape: Sequence[int], dtype: int = abi.F32, stream=None) -> "Tensor":
+        """tensor.rs:55-59."""
+        return cls.from_data_with_dtype(np.zeros(_numel(_shape(shape)), np.float32), shape, dtype, stream)
+
+    @classmethod
+    def ones(cls, shape: Sequence[int], dtype: int = abi.F32, stream=None) -> "Tensor":
+        """tensor.rs:61-65."""
+        return cls.from_data_with_dtype(np.ones(_numel(_shape(shape)), np.float32), shape, dtype, stream)
+
+    @classmethod
+    def from_device(cls, ptr: int, shape: Sequence[int], stream=None, dtype: int = abi.F32) -> "Tensor":
+        """Constant copied from f32 device memory (HipStream only; the
+        default stream when none is given)."""
         shape = _shape(shape)
+        stream = stream if stream is not None else default_stream()
         return cls(stream, stream.add_constant_dev(ptr, TensorMeta(shape, dtype)), shape, dtype)
 
     def _lazy(self, op: Op, inputs: Sequence["Tensor"], shape: Sequence[int]) -> "Tensor":
         shape = _shape(shape)
+        for t in inputs:
+            if t.stream is not self.stream:
+                raise abi.InvalidArgument("tensors on different streams cannot be combined")
         nid = self.stream.add_op(op, [t.node for t in inputs], TensorMeta(shape, self.dtype))
         return Tensor(self.stream, nid, shape, self.dtype)
 
@@ -158,6 +238,53 @@ class Tensor:
             if d != 1 and d != shape[pad + i]:
                 raise abi.InvalidArgument(f"cannot broadcast shape {list(self.shape)} to {list(shape)}")
         return self._lazy(OpKind.Broadcast(shape), [self], shape)
+
+    def narrow(self, axis: int, start: int, length: int) -> "Tensor":
+        """tensor.rs:584-611."""
+        nd = len(self.shape)
+        ax = axis + nd if axis < 0 else axis
+        if ax < 0 or ax >= nd:
+            raise abi.InvalidArgument(f"narrow: axis {axis} out of range for ndim {nd}")
+        if start < 0 or start + length > self.shape[ax]:
+            raise abi.InvalidArgument(
+                f"narrow: start {start} + length {length} exceeds dim size {self.shape[ax]}")
+        shape = self.shape[:ax] + (int(length),) + self.shape[ax + 1:]
+        return self._lazy(OpKind.Narrow(ax, int(start), int(length)), [self], shape)
+
+    @staticmethod
+    def cat(tensors: Sequence["Tensor"], axis: int) -> "Tensor":
+        """tensor.rs:614-660."""
+        if not tensors:
+            raise abi.InvalidArgument("cat requires at least one tensor")
+        first = tensors[0]
+        nd = len(first.shape)
+        ax = axis + nd if axis < 0 else axis
+        if ax < 0 or ax >= nd:
+            raise abi.InvalidArgument(f"cat: axis {axis} out of range for ndim {nd}")
+        total = 0
+        for t in tensors:
+            if len(t.shape) != nd:
+                raise abi.InvalidArgument("cat: all tensors must have same ndim")
+            for d, (a, b) in enumerate(zip(first.shape, t.shape)):
+                if d != ax and a != b:
+                    raise abi.ShapeMismatch(f"expected {list(first.shape)}, got {list(t.shape)}",
+                                            list(first.shape), list(t.shape))
+            total += t.shape[ax]
+        shape = first.shape[:ax] + (total,) + first.shape[ax + 1:]
+        return first._lazy(OpKind.Concatenate(ax), list(tensors), shape)
+
+    def attention(self, k: "Tensor", v: "Tensor", scale: float, causal: bool) -> "Tensor":
+        """Single-head attention Q [Tq, Dh], K/V [Tk, Dh] -> [Tq, Dh]
+        (tensor.rs:664-690)."""
+        if len(self.shape) != 2 or len(k.shape) != 2 or len(v.shape) != 2:
+            raise abi.InvalidArgument("attention requires 2D tensors [seq, head_dim]")
+        if k.shape[1] != self.shape[1]:
+            raise abi.ShapeMismatch(f"expected {list(self.shape)}, got {list(k.shape)}",
+                                    list(self.shape), list(k.shape))
+        if v.shape[1] != self.shape[1] or k.shape[0] != v.shape[0]:
+            raise abi.ShapeMismatch(f"expected {list(k.shape)}, got {list(v.shape)}",
+                                    list(k.shape), list(v.shape))
+        return self._lazy(OpKind.Attention(scale, causal), [self, k, v], self.shape)
 
     # ── row ops (tensor.rs:379-435) ──────────────────────────────────────
     def softmax(self, axis: int) -> "Tensor":

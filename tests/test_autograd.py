@@ -82,8 +82,8 @@ STREAMS = {"oracle": OracleStream, "hip": hip_stream}
 
 def scalar(make, f, x_data, shape) -> float:
     s = make()
-    c = lambda d, sh: Tensor.from_f32(s, d, sh)  # noqa: E731
-    return float(f(Tensor.from_f32(s, x_data, shape), c).to_numpy().reshape(-1)[0])
+    c = lambda d, sh: Tensor.from_f32_on_stream(d, sh, s)  # noqa: E731
+    return float(f(Tensor.from_f32_on_stream(x_data, shape, s), c).to_numpy().reshape(-1)[0])
 
 
 def numerical_grad(make, f, x_data, shape, eps=1e-3):
@@ -100,8 +100,8 @@ def numerical_grad(make, f, x_data, shape, eps=1e-3):
 
 def check_reference_case(make, x_data, shape, f, expected, tol):
     s = make()
-    c = lambda d, sh: Tensor.from_f32(s, d, sh)  # noqa: E731
-    x = Tensor.from_f32(s, x_data, shape)
+    c = lambda d, sh: Tensor.from_f32_on_stream(d, sh, s)  # noqa: E731
+    x = Tensor.from_f32_on_stream(x_data, shape, s)
     g = grad(lambda t: f(t, c), x).to_numpy().reshape(-1)
     if tol == EXACT:
         np.testing.assert_array_equal(g, np.asarray(expected, np.float32))
@@ -133,10 +133,10 @@ def test_grad_errors(kind, request):
     if kind == "hip":
         request.getfixturevalue("hip")
     s = STREAMS[kind]()
-    x = Tensor.from_f32(s, [1, 2, 3], [3])
+    x = Tensor.from_f32_on_stream([1, 2, 3], [3], s)
     with pytest.raises(abi.InvalidArgument, match="scalar loss"):
         value_and_grad(x.mul(x), [x])
-    other = Tensor.from_f32(s, [1, 2, 3], [3])
+    other = Tensor.from_f32_on_stream([1, 2, 3], [3], s)
     with pytest.raises(abi.InvalidArgument, match="gradient not found"):
         value_and_grad(x.sum_all(), [other])
     with pytest.raises(abi.InvalidArgument, match="VJP not implemented"):
@@ -179,10 +179,10 @@ def block_arrays(cfg: nn.BlockConfig, seed: int = 7):
 
 
 def block_loss(s, cfg, arrs, x, gy):
-    params = {k: Tensor.from_f32(s, v, v.shape) for k, v in arrs.items()}
-    xt = Tensor.from_f32(s, x, x.shape)
+    params = {k: Tensor.from_f32_on_stream(v, v.shape, s) for k, v in arrs.items()}
+    xt = Tensor.from_f32_on_stream(x, x.shape, s)
     y = nn.TransformerBlock(cfg, params)(xt)
-    loss = y.mul(Tensor.from_f32(s, gy, gy.shape)).sum_all()
+    loss = y.mul(Tensor.from_f32_on_stream(gy, gy.shape, s)).sum_all()
     return loss, params, xt
 
 
