@@ -47,13 +47,15 @@ using dev::wave_sum;
 // shared_divisor).
 __device__ inline void row_divisor(float& d, float& r) { dev::shared_divisor(d, r); }
 
-// Reduction across the WPR waves that share a row. `slot` is this row's
-// LDS slot array (WPR floats); every lane of the row gets the same value.
+// Reductions across the WPR waves that share a row. Each reduction of a
+// kernel has its own LDS slots (`slot`: WPR floats, or pairs), written once
+// and read once, so one barrier per reduction suffices: nothing can
+// overwrite a slot another wave has yet to read. Every lane of the row gets
+// the same value.
 template <int WPR, bool MAX>
 __device__ inline float row_reduce(float v, float* slot, int wave_in_row, int lane) {
     v = MAX ? wave_max(v) : wave_sum(v);
     if constexpr (WPR > 1) {
-        __syncthreads();  // previous readers of `slot` are done
         if (lane == 0) slot[wave_in_row] = v;
         __syncthreads();
         float r = slot[0];
@@ -62,6 +64,72 @@ __device__ inline float row_reduce(float v, float* slot, int wave_in_row, int la
         v = r;
     }
     return v;
+}
+
+// Softmax statistics of a row in one exchange: each lane holds (m, s) with
+// s = sum of exp(x - m) over its values; two pairs merge as
+// m = max(m1, m2), s = s1 exp(m1 - m) + s2 exp(m2 - m). Butterfly inside
+// the wave, then one LDS exchange across the row's waves (pairs in `slot`,
+// 2 * WPR floats).
+__device__ inline void merge_max_sum(float& m, float& s, float m2, float s2) {
+    const float mn = fmaxf(m, m2);
+    // exp of the (non-positive) differences; an empty side (s = 0, m = -inf)
+    // contributes nothing.
+    const float a = m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - mn) * 1.44269504088896340736f);
+    const float b = m2 == -INFINITY ? 0.0f : s2 * __builtin_amdgcn_exp2f((m2 - mn) * 1.44269504088896340736f);
+    m = mn;
+    s = a + b;
+}
+
+template <int WPR>
+__device__ inline void row_reduce_max_sum(float& m, float& s, float* slot, int wave_in_row, int lane) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) merge_max_sum(m, s, __shfl_xor(m, o, WAVE), __shfl_xor(s, o, WAVE));
+    if constexpr (WPR > 1) {
+        if (lane == 0) {
+            slot[2 * wave_in_row] = m;
+            slot[2 * wave_in_row + 1] = s;
+        }
+        __syncthreads();
+        m = slot[0];
+        s = slot[1];
+#pragma unroll
+        for (int w = 1; w < WPR; ++w) merge_max_sum(m, s, slot[2 * w], slot[2 * w + 1]);
+    }
+}
+
+// LayerNorm statistics in one exchange (Chan, Golub and LeVeque's pairwise
+// update): each lane holds (n, mean, M2) of its values, M2 the sum of
+// squared deviations from that mean; two groups merge as
+// mean = mean1 + (mean2 - mean1) n2 / n, M2 = M2a + M2b + (mean2 - mean1)^2 n1 n2 / n.
+__device__ inline void merge_moments(float& n, float& mean, float& m2, float n2, float mean2, float m22) {
+    const float nn = n + n2;
+    if (nn == 0.0f) return;
+    const float delta = mean2 - mean;
+    const float f = n2 / nn;
+    mean = mean + delta * f;
+    m2 = m2 + m22 + delta * delta * (n * f);
+    n = nn;
+}
+
+template <int WPR>
+__device__ inline void row_reduce_moments(float& n, float& mean, float& m2, float* slot, int wave_in_row, int lane) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1)
+        merge_moments(n, mean, m2, __shfl_xor(n, o, WAVE), __shfl_xor(mean, o, WAVE), __shfl_xor(m2, o, WAVE));
+    if constexpr (WPR > 1) {
+        if (lane == 0) {
+            slot[3 * wave_in_row] = n;
+            slot[3 * wave_in_row + 1] = mean;
+            slot[3 * wave_in_row + 2] = m2;
+        }
+        __syncthreads();
+        n = slot[0];
+        mean = slot[1];
+        m2 = slot[2];
+#pragma unroll
+        for (int w = 1; w < WPR; ++w) merge_moments(n, mean, m2, slot[3 * w], slot[3 * w + 1], slot[3 * w + 2]);
+    }
 }
 
 template <int VEC>
@@ -107,7 +175,9 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
     constexpr int TPR = WAVE * WPR;  // threads per row
     constexpr int N = NV * VEC;
     constexpr bool TWO = (OP == ROW_SOFTMAX_VJP || OP == ROW_LAYERNORM_VJP || OP == ROW_RMSNORM_VJP);
-    __shared__ float red[ROWS_PER_BLOCK][WPR > 1 ? WPR : 1];
+    // Up to four reductions per kernel, each with its own slots (3 floats per
+    // wave for the moment triples).
+    __shared__ float red[4][ROWS_PER_BLOCK][WPR > 1 ? 3 * WPR : 1];
 
     const int tid = threadIdx.x;
     const int row_in_block = tid / TPR;
@@ -117,7 +187,10 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
     const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + row_in_block;
     // Rows past the end still take part in the block barriers.
     const bool live = EVEN || row < rows;
-    float* slot = red[row_in_block];
+    float* slot0 = red[0][row_in_block];
+    float* slot1 = red[1][row_in_block];
+    float* slot2 = red[2][row_in_block];
+    float* slot3 = red[3][row_in_block];
 
     const float* ar = a + (live ? row : 0) * (int64_t)cols;
     const float* br = TWO ? b + (live ? row : 0) * (int64_t)cols : nullptr;
@@ -154,36 +227,52 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
                     v[j * VEC + e] = x;
                 }
         }
-        float m = -INFINITY;
+        // Lane statistics (m, s = sum exp(x - m)) merged across the row in
+        // one exchange; then y = exp(x - m_row) / s_row, each lane's stored
+        // exp(x - m_lane) rescaled by exp(m_lane - m_row). exp(d) is
+        // 2^(d log2 e) on arguments d <= 0: relative error ~|d| * 2^-24 plus
+        // one v_exp_f32 ulp per factor, far inside the 1e-5 tolerance, at a
+        // quarter of expf's VALU cost.
+        float ml = -INFINITY;
 #pragma unroll
         for (int j = 0; j < NV; ++j)
             if (ok[j])
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) m = fmaxf(m, v[j * VEC + e]);
-        m = row_reduce<WPR, true>(m, slot, wave_in_row, lane);
+                for (int e = 0; e < VEC; ++e) ml = fmaxf(ml, v[j * VEC + e]);
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < NV; ++j)
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
-                // exp(d) as 2^(d log2 e) on the subtracted argument d <= 0:
-                // relative error ~|d| * 2^-24 plus one v_exp_f32 ulp, far
-                // inside the 1e-5 tolerance, at a quarter of expf's VALU cost.
-                float ex = ok[j] ? __builtin_amdgcn_exp2f((v[j * VEC + e] - m) * 1.44269504088896340736f) : 0.0f;
+                // A lane whose values are all -inf adds nothing (its exps are
+                // 0 against any finite row maximum); a row that is all -inf
+                // still ends as NaN, as exp(-inf - -inf) makes it in the reference.
+                float ex = (ok[j] && ml != -INFINITY)
+                               ? __builtin_amdgcn_exp2f((v[j * VEC + e] - ml) * 1.44269504088896340736f)
+                               : 0.0f;
                 v[j * VEC + e] = ex;
                 s += ex;
             }
-        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+        float m = ml;
+        row_reduce_max_sum<WPR>(m, s, slot0, wave_in_row, lane);
+        const float scale = ml == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml - m) * 1.44269504088896340736f);
         float r;
         row_divisor(s, r);
 #pragma unroll
-        for (int j = 0; j < N; ++j) v[j] = div_by(v[j], s, r);
+        for (int j = 0; j < N; ++j) v[j] = div_by(v[j] * scale, s, r);
     } else if constexpr (OP == ROW_LAYERNORM) {
-        float s = 0.0f;
+        // Lane moments (count, mean, sum of squared deviations) by an exact
+        // two-pass over the lane's values, merged across the row in one
+        // exchange; var = M2 / d as the reference's biased variance.
+        float cnt = 0.0f, ls = 0.0f;
 #pragma unroll
-        for (int j = 0; j < N; ++j) s += v[j];
-        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
-        const float mean = s / d;
+        for (int j = 0; j < NV; ++j)
+            if (ok[j]) {
+                cnt += (float)VEC;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) ls += v[j * VEC + e];
+            }
+        float mean = cnt > 0.0f ? ls / cnt : 0.0f;
         float q = 0.0f;
 #pragma unroll
         for (int j = 0; j < NV; ++j)
@@ -193,7 +282,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
                     float dv = v[j * VEC + e] - mean;
                     q += dv * dv;
                 }
-        q = row_reduce<WPR, false>(q, slot, wave_in_row, lane);
+        row_reduce_moments<WPR>(cnt, mean, q, slot0, wave_in_row, lane);
         const float var = q / d;
         float sd = sqrtf(var + p), r;
         row_divisor(sd, r);
@@ -203,7 +292,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < N; ++j) s += v[j] * v[j];
-        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+        s = row_reduce<WPR, false>(s, slot0, wave_in_row, lane);
         float rms = sqrtf(s / d + p), r;
         row_divisor(rms, r);
 #pragma unroll
@@ -213,7 +302,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
         float dot = 0.0f;
 #pragma unroll
         for (int j = 0; j < N; ++j) dot += v[j] * w[j];
-        dot = row_reduce<WPR, false>(dot, slot, wave_in_row, lane);
+        dot = row_reduce<WPR, false>(dot, slot0, wave_in_row, lane);
 #pragma unroll
         for (int j = 0; j < N; ++j) v[j] = w[j] * (v[j] - dot);
     } else if constexpr (OP == ROW_LAYERNORM_VJP) {
@@ -221,7 +310,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < N; ++j) s += w[j];
-        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+        s = row_reduce<WPR, false>(s, slot0, wave_in_row, lane);
         const float mean = s / d;
         float q = 0.0f;
 #pragma unroll
@@ -232,7 +321,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
                     float dv = w[j * VEC + e] - mean;
                     q += dv * dv;
                 }
-        q = row_reduce<WPR, false>(q, slot, wave_in_row, lane);
+        q = row_reduce<WPR, false>(q, slot1, wave_in_row, lane);
         const float var = q / d;
         const float inv_std = 1.0f / sqrtf(var + p);
         float sdy = 0.0f, sdx = 0.0f;
@@ -246,8 +335,8 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
                     sdy += v[j * VEC + e];
                     sdx += v[j * VEC + e] * xh;
                 }
-        sdy = row_reduce<WPR, false>(sdy, slot, wave_in_row, lane);
-        sdx = row_reduce<WPR, false>(sdx, slot, wave_in_row, lane);
+        sdy = row_reduce<WPR, false>(sdy, slot2, wave_in_row, lane);
+        sdx = row_reduce<WPR, false>(sdx, slot3, wave_in_row, lane);
         const float mdy = sdy / d, mdx = sdx / d;
 #pragma unroll
         for (int j = 0; j < N; ++j) v[j] = inv_std * (v[j] - mdy - w[j] * mdx);
@@ -255,7 +344,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < N; ++j) s += w[j] * w[j];
-        s = row_reduce<WPR, false>(s, slot, wave_in_row, lane);
+        s = row_reduce<WPR, false>(s, slot0, wave_in_row, lane);
         const float inv_rms = 1.0f / sqrtf(s / d + p);
         float sdy = 0.0f;
 #pragma unroll
@@ -263,7 +352,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
             w[j] = w[j] * inv_rms;
             sdy += v[j] * w[j];
         }
-        sdy = row_reduce<WPR, false>(sdy, slot, wave_in_row, lane);
+        sdy = row_reduce<WPR, false>(sdy, slot1, wave_in_row, lane);
         const float m = sdy / d;
 #pragma unroll
         for (int j = 0; j < N; ++j) v[j] = inv_rms * (v[j] - w[j] * m);

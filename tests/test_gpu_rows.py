@@ -116,3 +116,44 @@ def test_softmax_non_last_axis_via_eval_node():
                                         meta(x.shape))
         ref = ORACLE.eval_node(OpKind.Softmax(axis), [NodeInput(x.reshape(-1), x.shape)], meta(x.shape))
         assert_allclose(out, ref, 1e-6, 1e-5, f"softmax axis {axis}")
+
+
+@pytest.mark.parametrize("cols", [96, 1000, 4096, 6000])
+def test_softmax_non_finite_rows(cols):
+    # Rows with -inf entries (masked scores), whole lanes of -inf, a row of
+    # all -inf (NaN in the reference: exp(-inf - -inf)), +inf and NaN
+    # entries. Each row's merged (max, sum) must give the oracle's values:
+    # 0 where the oracle has 0, NaN where it has NaN.
+    rows = 8
+    x = synth.normal(77 + cols, (rows, cols))
+    x[0, : cols // 2] = -np.inf             # half a row masked: whole lanes of -inf
+    x[1, 1::2] = -np.inf
+    x[2, :] = -np.inf                        # all masked
+    x[3, cols // 3] = np.inf
+    x[4, 7] = np.nan
+    x[5, -1] = -np.inf
+    y = run_rows(hb.softmax_rows, x)
+    ref = oracle(OpKind.Softmax(-1), x)
+    assert np.array_equal(np.isnan(y), np.isnan(ref)), (np.isnan(y).sum(1), np.isnan(ref).sum(1))
+    fin = ~np.isnan(ref)
+    assert_allclose(y[fin], ref[fin], 1e-6, 1e-5, f"softmax non-finite rows, {cols} cols")
+    assert np.all(y[0, : cols // 2] == 0.0) and np.all(y[1, 1::2] == 0.0)
+
+
+@pytest.mark.parametrize("cols", [96, 4096])
+def test_layernorm_large_offset_rows(cols):
+    # Rows with a large common offset: the per-lane moments and their merge
+    # must keep the variance of the small deviations (a one-pass sum of
+    # squares would cancel catastrophically here).
+    x = (np.float32(1000.0) + synth.normal(91, (64, cols), 0.0, 0.01)).astype(np.float32)
+    y = run_rows(lambda a, b, r, c: hb.layernorm_rows(a, b, r, c, 1e-5), x)
+    ref = oracle(OpKind.LayerNorm(1e-5), x)
+    # The reference's own mean carries ~1e-4 relative error of the deviations
+    # at this offset; hold both to float64.
+    x64 = x.astype(np.float64)
+    mu = x64.mean(1, keepdims=True)
+    ex = (x64 - mu) / np.sqrt(((x64 - mu) ** 2).mean(1, keepdims=True) + 1e-5)
+    e_hip = float(np.abs(y - ex).max())
+    e_ref = float(np.abs(ref - ex).max())
+    print(f"  layernorm offset 1000: hip {e_hip:.3e}, oracle {e_ref:.3e}", flush=True)
+    assert e_hip <= 2 * e_ref + 1e-4
