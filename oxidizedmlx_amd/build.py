@@ -33,6 +33,7 @@ SOURCES = [
     "kernels/rows.hip",
     "kernels/elementwise.hip",
     "kernels/gemm.hip",
+    "kernels/gemm_small.hip",
     "kernels/gemm_bf16.hip",
     "kernels/gemm_f16.hip",
     "kernels/gemm_f32.hip",

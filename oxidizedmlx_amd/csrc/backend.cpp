@@ -101,8 +101,16 @@ namespace {
 struct ThreadStreams {
     hipStream_t s[64] = {};
     ~ThreadStreams() {
-        for (hipStream_t& x : s)
-            if (x) (void)hipStreamDestroy(x);
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        for (int d = 0; d < 64; ++d)
+            if (s[d]) {
+                (void)hipSetDevice(d);
+                if (hipStreamSynchronize(s[d]) == hipSuccess) release_stream_workspaces(s[d]);
+                (void)hipStreamDestroy(s[d]);
+            }
+        (void)hipSetDevice(cur);
+        (void)hipGetLastError();
     }
 };
 }  // namespace
@@ -191,6 +199,84 @@ void pool_release(void* p) {
     auto it = P.owned.find(p);
     if (it == P.owned.end()) return;
     P.free_blocks[it->second.first].emplace(it->second.second, p);
+}
+
+// ── per-stream workspaces ─────────────────────────────────────────────────
+
+namespace {
+struct WsBlock {
+    void* p = nullptr;
+    size_t cap = 0;
+};
+struct WsKey {
+    int dev;
+    hipStream_t s;
+    int slot;
+    bool operator<(const WsKey& o) const {
+        if (dev != o.dev) return dev < o.dev;
+        if (s != o.s) return s < o.s;
+        return slot < o.slot;
+    }
+};
+struct WsCache {
+    std::mutex mu;
+    std::map<WsKey, WsBlock> live;
+    std::multimap<std::pair<int, hipStream_t>, void*> retired;
+};
+WsCache& ws_cache() {
+    static WsCache* c = new WsCache();  // never destroyed: outlives late calls at exit
+    return *c;
+}
+}  // namespace
+
+int stream_workspace(hipStream_t s, int slot, size_t bytes, void** out) {
+    int dev = 0;
+    MLXHIP_HIP(hipGetDevice(&dev));
+    WsCache& C = ws_cache();
+    std::lock_guard<std::mutex> g(C.mu);
+    WsBlock& b = C.live[WsKey{dev, s, slot}];
+    if (b.cap < bytes || !b.p) {
+        // Grow geometrically (256-byte granules) so a slowly growing sequence
+        // of requests allocates O(log) times.
+        size_t cap = std::max<size_t>(bytes, b.cap + b.cap / 2);
+        cap = std::max<size_t>((cap + 255) & ~size_t(255), 256);
+        // During stream capture (mlxhip_graph_begin) an allocation is not a
+        // stream operation: switch this thread to relaxed capture mode around
+        // it, then back. The block outlives the recorded graph (retired
+        // blocks are kept), so a replay never sees freed memory.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        const bool exchanged = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
+        void* p = pool_alloc(cap);
+        if (exchanged) (void)hipThreadExchangeStreamCaptureMode(&mode);
+        (void)hipGetLastError();
+        if (!p) return fail(MLXHIP_ERR_FFI_FAILED, "workspace: device allocation of %zu bytes failed", cap);
+        if (b.p) C.retired.emplace(std::make_pair(dev, s), b.p);
+        b.p = p;
+        b.cap = cap;
+    }
+    *out = b.p;
+    return MLXHIP_OK;
+}
+
+void release_stream_workspaces(hipStream_t s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    WsCache& C = ws_cache();
+    std::lock_guard<std::mutex> g(C.mu);
+    for (auto it = C.live.begin(); it != C.live.end();) {
+        if (it->first.dev == dev && it->first.s == s) {
+            pool_release(it->second.p);
+            it = C.live.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    auto range = C.retired.equal_range(std::make_pair(dev, s));
+    for (auto it = range.first; it != range.second; ++it) pool_release(it->second);
+    C.retired.erase(range.first, range.second);
 }
 
 float* Scratch::get(size_t n_floats) { return static_cast<float*>(get_bytes(n_floats * sizeof(float))); }
@@ -861,7 +947,11 @@ void* mlxhip_stream_create_hip(void) {
 }
 
 void mlxhip_stream_destroy_hip(void* stream) {
-    if (stream) (void)hipStreamDestroy(as_stream(stream));
+    if (!stream) return;
+    // The stream's cached workspaces go back to the pool once its work ends.
+    if (hipStreamSynchronize(as_stream(stream)) == hipSuccess) release_stream_workspaces(as_stream(stream));
+    (void)hipGetLastError();
+    (void)hipStreamDestroy(as_stream(stream));
 }
 
 struct mlxhip_graph_t {

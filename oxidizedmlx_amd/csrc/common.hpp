@@ -58,32 +58,17 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Stream-ordered scratch: allocated on `s`, returned to the device's memory
-// pool on `s` after every kernel enqueued before the destructor has run.
-struct StreamBuf {
-    void* p = nullptr;
-    hipStream_t s;
-    explicit StreamBuf(hipStream_t st) : s(st) {}
-    int alloc(size_t bytes) {
-        static std::once_flag keep[64];
-        int dev = 0;
-        if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
-            std::call_once(keep[dev], [dev] {
-                // Keep freed blocks in the pool instead of returning them to the
-                // driver at every synchronisation.
-                hipMemPool_t pool;
-                if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
-                    uint64_t hi = UINT64_MAX;
-                    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &hi);
-                }
-            });
-        }
-        MLXHIP_HIP(hipMallocAsync(&p, bytes ? bytes : 16, s));
-        return MLXHIP_OK;
-    }
-    ~StreamBuf() {
-        if (p) (void)hipFreeAsync(p, s);
-    }
-};
+// Per-stream device workspace for kernels that need scratch (split-K
+// partials, padded operand copies, reduction partials). Slot `slot` of
+// stream `s` (and of the current device) is one cached block that grows on
+// demand and is reused by every later call on that stream: work on one
+// stream runs in order, so a block is never in use by two kernels at once,
+// and no call allocates once the block is large enough. A block that is
+// outgrown is retired, not freed (a HIP graph recorded earlier may still name
+// it); retired and live blocks are released by release_stream_workspaces(s)
+// after `s` has drained. Calls on different streams use different blocks.
+enum WsSlot { WS_PACK = 0, WS_SPLITK = 1, WS_REDUCE = 2 };
+int stream_workspace(hipStream_t s, int slot, size_t bytes, void** out);
+void release_stream_workspaces(hipStream_t s);
 
 }  // namespace mlxhip

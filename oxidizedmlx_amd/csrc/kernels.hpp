@@ -124,6 +124,12 @@ int attention_fused(const float* q, const float* k, const float* v, float* o, in
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
          int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s);
+// gemm_small.hip: f32 products small enough for one or two rounds of 32 x 32
+// tiles with K <= 512, one launch, no workspace, any alignment.
+bool gemm_small_f32_fits(int64_t m, int64_t n, int64_t k, int64_t batch);
+int gemm_small_f32(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const float* a, int64_t lda,
+                   int64_t sa, const float* b, int64_t ldb, int64_t sb, float* c, int64_t ldc, int64_t sc,
+                   hipStream_t s);
 // gemm with the same kernels and plan, its split-K partials and padded
 // operand copies taken from a fixed device array of
 // GEMM_NOALLOC_SCRATCH_BYTES instead of the memory pool: no allocation.

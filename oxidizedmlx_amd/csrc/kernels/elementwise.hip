@@ -634,12 +634,12 @@ int reduce_all(int kind, const float* x, float* y, int64_t n, hipStream_t s) {
         hipLaunchKernelGGL(reduce_all_seq_kernel, dim3(1), dim3(64), 0, s, kind, x, y, n);
         return launch_check("reduce_all_seq_kernel");
     }
-    // Partials of the tree reduction: stream-ordered scratch, so calls on
-    // different streams never share it.
+    // Partials of the tree reduction: the stream's cached workspace, so calls
+    // on different streams never share it and no call allocates.
     const int np = 1024;
-    StreamBuf pb(s);
-    MLXHIP_TRY(pb.alloc(sizeof(float) * np));
-    float* part = static_cast<float*>(pb.p);
+    void* pb = nullptr;
+    MLXHIP_TRY(stream_workspace(s, WS_REDUCE, sizeof(float) * np, &pb));
+    float* part = static_cast<float*>(pb);
     hipLaunchKernelGGL(reduce_partial_kernel, dim3(np), dim3(BLOCK), 0, s, kind, x, part, n);
     MLXHIP_TRY(launch_check("reduce_partial_kernel"));
     hipLaunchKernelGGL(reduce_final_kernel, dim3(1), dim3(BLOCK), 0, s, kind, part, y, np, n);

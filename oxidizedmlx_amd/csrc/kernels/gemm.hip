@@ -36,18 +36,75 @@ __global__ __launch_bounds__(256) void zero_c_kernel(char* c, int64_t ldc, int64
 int elem_size(int dt) { return dt == MLXHIP_DTYPE_F32 ? 4 : 2; }
 
 // Sum of the split-K partials in split order (deterministic), converted to C.
-// ws holds batch * splits slices of [m, n] f32, slice (b, s) at (b*splits+s)*m*n.
-template <int CT>
+// ws holds batch * splits slices of [m, n] f32 with row pitch ldw, slice
+// (b, s) at (b*splits+s)*m*ldw. Thread (row, 4-column group) of a 2-D grid:
+// blockIdx.x walks rows of RED_COLS x RED_ROWS work items, blockIdx.y the
+// batch; no 64-bit division. VEC: ldw and the partials are 16-byte aligned,
+// so each split contributes one float4 load per thread.
+constexpr int RED_COLS = 64;  // 4-column groups per row of work items
+constexpr int RED_ROWS = 4;
+constexpr int SPLIT_MAX = 8;  // every split plan uses at most 8 splits
+template <int CT, bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, void* c, int64_t m,
-                                                            int64_t n, int64_t ldc, int64_t sc, int splits) {
+                                                            int64_t n, int64_t ldw, int64_t ldc, int64_t sc,
+                                                            int splits) {
     const int64_t b = blockIdx.y;
-    FOR_EACH_ELEMENT(idx, m * n) {
-        const float* p = ws + b * splits * m * n + idx;
-        float acc = p[0];
-        for (int s = 1; s < splits; ++s) acc += p[(int64_t)s * m * n];
-        const int64_t row = idx / n, col = idx % n;
-        gemm_detail::store_c<CT>(c, b * sc + row * ldc + col, acc);
+    const int64_t groups = (n + 3) / 4;
+    const int gx = threadIdx.x % RED_COLS, gy = threadIdx.x / RED_COLS;
+    const int64_t slice = m * ldw;
+    for (int64_t row = (int64_t)blockIdx.x * RED_ROWS + gy; row < m; row += (int64_t)gridDim.x * RED_ROWS) {
+        const float* pr = ws + b * splits * slice + row * ldw;
+        for (int64_t g = gx; g < groups; g += RED_COLS) {
+            const int64_t col = 4 * g;
+            // Every split's values are loaded before the first add (one memory
+            // latency, not one per split), then summed in split order.
+            float v[SPLIT_MAX][4];
+#pragma unroll
+            for (int s = 0; s < SPLIT_MAX; ++s) {
+                if (s >= splits) break;
+                const float* p = pr + (int64_t)s * slice + col;
+                if (VEC) {
+                    const float4 t = *reinterpret_cast<const float4*>(p);
+                    v[s][0] = t.x, v[s][1] = t.y, v[s][2] = t.z, v[s][3] = t.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[s][e] = col + e < n ? p[e] : 0.0f;
+                }
+            }
+            float acc[4] = {v[0][0], v[0][1], v[0][2], v[0][3]};
+#pragma unroll
+            for (int s = 1; s < SPLIT_MAX; ++s) {
+                if (s >= splits) break;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] += v[s][e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < n) gemm_detail::store_c<CT>(c, b * sc + row * ldc + col + e, acc[e]);
+        }
     }
+}
+
+int splitk_reduce(int c_dtype, const float* ws, void* c, int64_t m, int64_t n, int64_t ldw, int64_t ldc,
+                  int64_t sc, int splits, int64_t batch, hipStream_t s) {
+    // VEC: every float4 read stays inside a row of the partials (ldw a
+    // multiple of 4; reads past n up to ldw stay in the row padding).
+    const bool vec = ldw % 4 == 0 && reinterpret_cast<uintptr_t>(ws) % 16 == 0 && ceil_div(n, 4) * 4 <= ldw;
+    const dim3 grid((unsigned)std::min<int64_t>(ceil_div(m, RED_ROWS), 65535), (unsigned)batch);
+#define MLXHIP_RED(CT)                                                                                       \
+    do {                                                                                                    \
+        if (vec) hipLaunchKernelGGL((splitk_reduce_kernel<CT, true>), grid, dim3(256), 0, s, ws, c, m, n, ldw, \
+                                    ldc, sc, splits);                                                        \
+        else hipLaunchKernelGGL((splitk_reduce_kernel<CT, false>), grid, dim3(256), 0, s, ws, c, m, n, ldw,    \
+                                ldc, sc, splits);                                                            \
+    } while (0)
+    switch (c_dtype) {
+        case MLXHIP_DTYPE_F32: MLXHIP_RED(MLXHIP_DTYPE_F32); break;
+        case MLXHIP_DTYPE_BF16: MLXHIP_RED(MLXHIP_DTYPE_BF16); break;
+        default: MLXHIP_RED(MLXHIP_DTYPE_F16); break;
+    }
+#undef MLXHIP_RED
+    return launch_check("splitk_reduce_kernel");
 }
 
 // One operand to copy into a zero-padded rows_p x cols_p buffer per batch
@@ -71,31 +128,57 @@ template <typename T>
 __global__ __launch_bounds__(256) void pack_kernel(PackPair pp) {
     constexpr int CH = 16 / sizeof(T);
     const PackOp& p = pp.op[blockIdx.z];
-    const int64_t b = blockIdx.y, chunks = p.cols_p / CH;
+    const int64_t b = blockIdx.y;
+    const int chunks = (int)(p.cols_p / CH);  // per destination row (host-checked to fit 32 bits)
     const T* sb = static_cast<const T*>(p.src) + b * p.sstride;
     uint4* db = reinterpret_cast<uint4*>(static_cast<T*>(p.dst) + b * p.rows_p * p.cols_p);
-    FOR_EACH_ELEMENT(q, p.rows_p * chunks) {
-        const int64_t r = q / chunks, c0 = (q % chunks) * CH;
-        union {
-            uint4 v;
-            T e[CH];
-        } u;
+    // Threads walk (row, chunk) pairs; rows advance by the grid's row count,
+    // so no index needs a 64-bit division.
+    const int per_block = 256 / chunks > 0 ? 256 / chunks : 1;       // whole rows per block when they fit
+    const int t = threadIdx.x;
+    if (chunks <= 256) {
+        const int rloc = t / chunks, q = t - rloc * chunks;
+        if (rloc >= per_block) return;
+        for (int64_t r = (int64_t)blockIdx.x * per_block + rloc; r < p.rows_p; r += (int64_t)gridDim.x * per_block) {
+            const int c0 = q * CH;
+            union {
+                uint4 v;
+                T e[CH];
+            } u;
+            const T* src = sb + r * p.ld;
 #pragma unroll
-        for (int e = 0; e < CH; ++e) u.e[e] = (r < p.rows && c0 + e < p.cols) ? sb[r * p.ld + c0 + e] : T(0);
-        db[q] = u.v;
+            for (int e = 0; e < CH; ++e) u.e[e] = (r < p.rows && c0 + e < p.cols) ? src[c0 + e] : T(0);
+            db[r * chunks + q] = u.v;
+        }
+    } else {
+        for (int64_t r = blockIdx.x; r < p.rows_p; r += gridDim.x) {
+            const T* src = sb + r * p.ld;
+            for (int q = t; q < chunks; q += 256) {
+                const int c0 = q * CH;
+                union {
+                    uint4 v;
+                    T e[CH];
+                } u;
+#pragma unroll
+                for (int e = 0; e < CH; ++e) u.e[e] = (r < p.rows && c0 + e < p.cols) ? src[c0 + e] : T(0);
+                db[r * chunks + q] = u.v;
+            }
+        }
     }
 }
 
 int pack2(int dt, const PackPair& pp, int64_t batch, hipStream_t s) {
     const int ch = dt == MLXHIP_DTYPE_F32 ? 4 : 8;
-    int64_t most = 0;
+    int64_t blocks = 1;
     for (const PackOp& p : pp.op) {
         if (p.cols_p % ch || reinterpret_cast<uintptr_t>(p.dst) % 16)
             return fail(MLXHIP_ERR_INVALID_ARGUMENT, "pack: destination rows must be whole 16-byte chunks");
-        most = std::max(most, p.rows_p * (p.cols_p / ch));
+        const int64_t chunks = p.cols_p / ch;
+        if (chunks > INT32_MAX) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "pack: rows too long");
+        const int64_t per_block = chunks <= 256 ? 256 / chunks : 1;
+        blocks = std::max(blocks, ceil_div(p.rows_p, per_block));
     }
-    dim3 grid = elem_grid(most, batch);
-    grid.z = 2;
+    const dim3 grid((unsigned)std::min<int64_t>(blocks, int64_t(1) << 16), (unsigned)batch, 2);
     if (dt == MLXHIP_DTYPE_F32) hipLaunchKernelGGL(pack_kernel<uint32_t>, grid, dim3(256), 0, s, pp);
     else hipLaunchKernelGGL(pack_kernel<uint16_t>, grid, dim3(256), 0, s, pp);
     return launch_check("pack_kernel");
@@ -152,15 +235,11 @@ struct FixedScratch {
     size_t used;
 };
 
-// `bytes` of device workspace for this call: stream-ordered from the
-// device's pool (fs == nullptr, owned by `sb`), or the next 256-byte aligned
-// region of the fixed scratch.
-int take_workspace(FixedScratch* fs, StreamBuf& sb, size_t bytes, void** out) {
-    if (!fs) {
-        MLXHIP_TRY(sb.alloc(bytes));
-        *out = sb.p;
-        return MLXHIP_OK;
-    }
+// `bytes` of device workspace for this call: the stream's cached block of
+// `slot` (fs == nullptr), or the next 256-byte aligned region of the fixed
+// scratch.
+int take_workspace(FixedScratch* fs, hipStream_t s, int slot, size_t bytes, void** out) {
+    if (!fs) return stream_workspace(s, slot, bytes, out);
     const size_t at = (fs->used + 255) & ~size_t(255);
     if (at > fs->cap || bytes > fs->cap - at)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT,
@@ -246,6 +325,15 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     if (ceil_div(m, 64) * ceil_div(n, 64) > INT32_MAX)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: too many tiles");
 
+    // Small f32 products (config 1's 512^3): one launch of 32 x 32 tiles with
+    // K split across the workgroup's waves, instead of split-K partials and
+    // a reduction (measured 13.7 us per call for 512^3 that way, kernels
+    // and launches included).
+    if (ab_dtype == MLXHIP_DTYPE_F32 && c_dtype == MLXHIP_DTYPE_F32 && gemm_path() == 0 &&
+        ceil_div(m, 64) * ceil_div(n, 64) * batch < 256 && gemm_small_f32_fits(m, n, k, batch))
+        return gemm_small_f32(trans_a, trans_b, m, n, k, batch, static_cast<const float*>(a), lda, stride_a,
+                              static_cast<const float*>(b), ldb, stride_b, static_cast<float*>(c), ldc, stride_c, s);
+
     const int ch = 16 / elem_size(ab_dtype);
     const bool aligned = reinterpret_cast<uintptr_t>(a) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(b) % 16 == 0 && lda % ch == 0 &&
@@ -267,9 +355,8 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
         // what such small products wait on.
         const size_t a_sz = (size_t)(a_rows_p * a_cols_p * batch * es);
         const size_t b_off = (a_sz + 255) & ~size_t(255);
-        StreamBuf ws(s);
         void* pa = nullptr;
-        MLXHIP_TRY(take_workspace(fs, ws, b_off + (size_t)(b_rows_p * b_cols_p * batch * es), &pa));
+        MLXHIP_TRY(take_workspace(fs, s, WS_PACK, b_off + (size_t)(b_rows_p * b_cols_p * batch * es), &pa));
         void* pb = static_cast<char*>(pa) + b_off;
         PackPair pp{{PackOp{a, lda, stride_a, a_rows, a_cols, pa, a_rows_p, a_cols_p},
                      PackOp{b, ldb, stride_b, b_rows, b_cols, pb, b_rows_p, b_cols_p}}};
@@ -320,8 +407,35 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
             h.c = c;
             h.ldc = ldc;
             h.sc = stride_c;
-            return ab_dtype == MLXHIP_DTYPE_BF16 ? gemm16_bf16(c_dtype, ta, tb, h, batch, cfg, s)
-                                                 : gemm16_f16(c_dtype, ta, tb, h, batch, cfg, s);
+            // Split over K when 128x128 tiles leave most CUs idle: the
+            // smallest power of two giving one workgroup per CU, at most 8,
+            // keeping at least 256 k (8 K tiles) per split. The 1000 x 777 x
+            // 1531 product (56 tiles) runs 4 splits of 384 k on 224 CUs.
+            int sp = 1;
+            if (cfg == 1 && path == 0)
+                while (sp < 8 && mid_tiles * sp < 256 && k / (2 * sp) >= 256) sp *= 2;
+            // MLXHIP_GEMM16_SPLITS=s forces the split factor (1..8; tuning).
+            if (const char* e = getenv("MLXHIP_GEMM16_SPLITS")) {
+                const int v = atoi(e);
+                if (v >= 1 && v <= 8) sp = v;
+            }
+            if (sp == 1)
+                return ab_dtype == MLXHIP_DTYPE_BF16 ? gemm16_bf16(c_dtype, ta, tb, h, batch, cfg, s)
+                                                     : gemm16_f16(c_dtype, ta, tb, h, batch, cfg, s);
+            // f32 partials [batch][split][m][ldw] (rows padded to 16 bytes for
+            // the vector stores), summed in split order into C.
+            h.k_chunk = ceil_div(ceil_div(k, sp), 32) * 32;
+            h.splits = (int)ceil_div(k, h.k_chunk);
+            const int64_t ldw = ceil_div(n, 4) * 4;
+            void* part = nullptr;
+            MLXHIP_TRY(take_workspace(fs, s, WS_SPLITK, (size_t)(batch * h.splits * m * ldw) * sizeof(float), &part));
+            h.c = part;
+            h.ldc = ldw;
+            h.sc = m * ldw;
+            MLXHIP_TRY(ab_dtype == MLXHIP_DTYPE_BF16 ? gemm16_bf16(MLXHIP_DTYPE_F32, ta, tb, h, batch, cfg, s)
+                                                     : gemm16_f16(MLXHIP_DTYPE_F32, ta, tb, h, batch, cfg, s));
+            return splitk_reduce(c_dtype, static_cast<const float*>(part), c, m, n, ldw, ldc, stride_c, h.splits,
+                                 batch, s);
         }
     }
     // General kernel. f32 operands (measured on MI355X): 256x256 blocks from
@@ -396,30 +510,15 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     if (splits == 1) return run(g, c_dtype);
     g.k_chunk = ceil_div(ceil_div(k, splits), bk) * bk;
     g.splits = (int)ceil_div(k, g.k_chunk);
-    StreamBuf ws(s);
     void* part = nullptr;
-    MLXHIP_TRY(take_workspace(fs, ws, (size_t)(batch * g.splits * m * n) * sizeof(float), &part));
-    gemm_detail::GemmArgs gp = g;
-    gp.c = part;
-    gp.ldc = n;
-    gp.sc = m * n;
-    MLXHIP_TRY(run(gp, MLXHIP_DTYPE_F32));
-    const dim3 grid = elem_grid(m * n, batch);
-    switch (c_dtype) {
-        case MLXHIP_DTYPE_F32:
-            hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_F32>, grid, dim3(256), 0, s,
-                               static_cast<const float*>(part), c, m, n, ldc, stride_c, g.splits);
-            break;
-        case MLXHIP_DTYPE_BF16:
-            hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_BF16>, grid, dim3(256), 0, s,
-                               static_cast<const float*>(part), c, m, n, ldc, stride_c, g.splits);
-            break;
-        default:
-            hipLaunchKernelGGL(splitk_reduce_kernel<MLXHIP_DTYPE_F16>, grid, dim3(256), 0, s,
-                               static_cast<const float*>(part), c, m, n, ldc, stride_c, g.splits);
-            break;
-    }
-    return launch_check("splitk_reduce_kernel");
+    MLXHIP_TRY(take_workspace(fs, s, WS_SPLITK, (size_t)(batch * g.splits * m * n) * sizeof(float), &part));
+    g.ws = static_cast<float*>(part);
+    // Partials, then their sum in split order (deterministic). (Reducing in
+    // the GEMM kernel's last workgroup per tile needs a device-scope release
+    // per workgroup, which on this part writes back the whole L2 of the XCD:
+    // measured 4-6x slower.)
+    MLXHIP_TRY(run(g, c_dtype));
+    return splitk_reduce(c_dtype, static_cast<const float*>(part), c, m, n, n, ldc, stride_c, g.splits, batch, s);
 }
 }  // namespace
 

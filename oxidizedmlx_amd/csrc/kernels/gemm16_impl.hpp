@@ -99,6 +99,13 @@ struct Args {
     int64_t ldc, sc;
     uint32_t a_bytes, b_bytes;  // byte extent of one batch slice (descriptor range)
     int tiles_m, tiles_n;
+    // Split-K (splits > 1): gridDim.y = batch * splits; split s of batch b
+    // covers k in [s * k_chunk, min(k, (s + 1) * k_chunk)) and writes its
+    // f32 partial to c + (b * splits + s) * sc (the kernel is instantiated
+    // with an f32 C; c / ldc / sc describe the workspace); a second kernel
+    // sums the partials in split order.
+    int splits = 1;
+    int64_t k_chunk = 0;
 };
 
 template <int N>
@@ -305,8 +312,9 @@ void gemm16_kernel(Args g) {
     const int64_t total = (int64_t)nwg * gridDim.y;
     int64_t lin = (int64_t)blockIdx.y * nwg + blockIdx.x;
     if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
-    const int64_t batch = lin / nwg;
-    const int id = (int)(lin - batch * nwg);
+    const int64_t slice = lin / nwg;  // batch * splits + split
+    const int id = (int)(lin - slice * nwg);
+    const int64_t batch = slice / g.splits, split = slice - batch * g.splits;
     constexpr int GROUP_M = 4;
     const int in_group = GROUP_M * g.tiles_n;
     const int first_m = (id / in_group) * GROUP_M;
@@ -315,16 +323,23 @@ void gemm16_kernel(Args g) {
     const int tn = (id % in_group) / gsz;
     const int64_t m0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
 
-    const char* A = static_cast<const char*>(g.a) + batch * g.sa * 2;
-    const char* B = static_cast<const char*>(g.b) + batch * g.sb * 2;
-    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)g.a_bytes, BUF_FLAGS);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)g.b_bytes, BUF_FLAGS);
+    // A split starts k_chunk * split into K: its operands are the slices'
+    // sub-matrices from that k on (descriptor ranges shortened to match).
+    const int64_t kb = split * g.k_chunk;
+    const int64_t klen = g.splits > 1 ? min(g.k - kb, g.k_chunk) : g.k;
+    const int64_t a_koff = (KCA ? kb : kb * g.lda) * 2, b_koff = (KCB ? kb : kb * g.ldb) * 2;
+    const char* A = static_cast<const char*>(g.a) + batch * g.sa * 2 + a_koff;
+    const char* B = static_cast<const char*>(g.b) + batch * g.sb * 2 + b_koff;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)(g.a_bytes - (uint32_t)a_koff), BUF_FLAGS);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)(g.b_bytes - (uint32_t)b_koff), BUF_FLAGS);
 
     constexpr int ROWB_A = C::BM * 2, ROWB_B = C::BN * 2;
     Loader<KCA, C::BM, WAVES> la;
     Loader<KCB, C::BN, WAVES> lb;
-    la.init(tid, m0, g.m, g.lda, g.k);
-    lb.init(tid, n0, g.n, g.ldb, g.k);
+    la.init(tid, m0, g.m, g.lda, klen);
+    lb.init(tid, n0, g.n, g.ldb, klen);
     FragAddr<KCA, TM, ROWB_A> fa;
     FragAddr<KCB, TN, ROWB_B> fb;
     fa.init(lane, 32 * TM * wm);
@@ -338,7 +353,7 @@ void gemm16_kernel(Args g) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    const int nk = (int)((g.k + BK - 1) / BK);
+    const int nk = (int)((klen + BK - 1) / BK);
     constexpr int LA = C::LA, LB = C::LB, LPT = LA + LB;
     constexpr int B_OFF = C::A_BYTES;  // stage layout: A block, then B block
 
@@ -425,7 +440,7 @@ void gemm16_kernel(Args g) {
     constexpr int ROWS_PER_READ = 64 / LANES_PER_ROW;
     static_assert(LANES_PER_ROW <= 64 && 64 % LANES_PER_ROW == 0, "epilogue read shape");
     MLXHIP_LDS char* region = smem + wave * PASS_ROWS * PITCH;
-    char* Cp = static_cast<char*>(g.c) + batch * g.sc * ES;
+    char* Cp = static_cast<char*>(g.c) + slice * g.sc * ES;
     const int64_t row0 = m0 + 32 * TM * wm, col0 = n0 + 32 * TN * wn;
     const bool vec_ok = (g.ldc * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(Cp) % 16) == 0;
 #pragma unroll
@@ -508,7 +523,7 @@ int launch(const Args& a0, int64_t batch, hipStream_t s) {
     Args a = a0;
     a.tiles_m = (int)ceil_div(a.m, C::BM);
     a.tiles_n = (int)ceil_div(a.n, C::BN);
-    dim3 grid((unsigned)(a.tiles_m * a.tiles_n), (unsigned)batch);
+    dim3 grid((unsigned)(a.tiles_m * a.tiles_n), (unsigned)(batch * a.splits));
     hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, C, true>), grid, dim3(C::THREADS), 0, s, a);
     return launch_check("gemm16_kernel");
 }

@@ -51,9 +51,11 @@ struct GemmArgs {
     int tiles_m, tiles_n;
     // Split-K: blockIdx.y = batch * splits + split; split s covers
     // k in [s * k_chunk, min(k, (s + 1) * k_chunk)) and writes its f32
-    // partial product to C + blockIdx.y * sc (a workspace the host reduces).
+    // partial product to ws + blockIdx.y * m * n (row pitch n); a second
+    // kernel sums the partials in split order.
     int splits = 1;
     int64_t k_chunk = 0;
+    float* ws = nullptr;
 };
 
 template <int DT>
@@ -312,8 +314,24 @@ void gemm_kernel(GemmArgs g) {
     }
 
     // Epilogue: accumulator element v of lane l is C[8*(v/4) + 4*(l/32) + v%4][l%32].
+    if (g.splits > 1) {
+        // f32 partial of this split into its workspace slice.
+        float* P = g.ws + by * g.m * g.n;
+#pragma unroll
+        for (int i = 0; i < WTM; ++i)
+#pragma unroll
+            for (int j = 0; j < WTN; ++j) {
+                const int64_t col = n0 + wn * 32 * WTN + j * 32 + lrow;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t row = m0 + wm * 32 * WTM + i * 32 + 8 * (v >> 2) + 4 * lgrp + (v & 3);
+                    if (row < g.m && col < g.n) P[row * g.n + col] = acc[i][j][v];
+                }
+            }
+        return;
+    }
     void* C = g.c;
-    const int64_t cbase = by * g.sc;
+    const int64_t cbase = batch * g.sc;
 #pragma unroll
     for (int i = 0; i < WTM; ++i)
 #pragma unroll

@@ -79,3 +79,40 @@ def test_graph_errors():
         L.mlxhip_graph_free(None)
     finally:
         hb.destroy_stream(s)
+
+
+def test_workspace_first_grown_under_capture():
+    # A fresh stream has no cached workspace yet: the split-K GEMM, the
+    # 16-bit split-K GEMM with packed operands and their tile counters are
+    # first allocated while the stream is being recorded. Every replay must
+    # match the eager result computed on another stream.
+    n1, mo, no, ko = 512, 1000, 777, 1531
+    A1 = hb.DeviceBuffer.from_array(synth.normal(11, (n1, n1)))
+    B1 = hb.DeviceBuffer.from_array(synth.normal(12, (n1, n1)))
+    Ao = hb.DeviceBuffer.from_array(synth.bf16_bits(synth.normal(13, (mo, ko))))
+    Bo = hb.DeviceBuffer.from_array(synth.bf16_bits(synth.normal(14, (ko, no))))
+    C1, Co = hb.DeviceBuffer(n1 * n1 * 4), hb.DeviceBuffer(mo * no * 4)
+
+    def seq(st):
+        hb.gemm(abi.F32, abi.F32, False, False, n1, n1, n1, A1, n1, B1, n1, C1, n1, stream=st)
+        hb.gemm(abi.BF16, abi.F32, False, False, mo, no, ko, Ao, ko, Bo, no, Co, no, stream=st)
+
+    e = hb.create_stream()
+    s = hb.create_stream()
+    try:
+        seq(e)
+        hb.synchronize(e)
+        eager = [C1.download(np.float32, n1 * n1), Co.download(np.float32, mo * no)]
+        with hb.Graph(s) as g:
+            seq(s)
+        for rep in range(3):
+            C1.upload(np.full(n1 * n1, np.nan, np.float32))
+            Co.upload(np.full(mo * no, np.nan, np.float32))
+            g.launch()
+            hb.synchronize(s)
+            np.testing.assert_array_equal(C1.download(np.float32, n1 * n1), eager[0], err_msg=f"replay {rep}")
+            np.testing.assert_array_equal(Co.download(np.float32, mo * no), eager[1], err_msg=f"replay {rep}")
+        g.close()
+    finally:
+        hb.destroy_stream(s)
+        hb.destroy_stream(e)
