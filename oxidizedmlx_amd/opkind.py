@@ -54,9 +54,13 @@ class Op:
         return KIND[self.name]
 
     def to_c(self) -> Tuple[abi.mlxhip_op_t, list]:
-        """The C form (and the arrays it points into); cached per value, the
-        C side only reads it."""
-        return _op_to_c(self)
+        """The C form (and the arrays it points into); built once per Op
+        object (kept on it) and per value (shared), the C side only reads it."""
+        c = self.__dict__.get("_c")
+        if c is None:
+            c = _op_to_c(self)
+            object.__setattr__(self, "_c", c)
+        return c
 
     def _build_c(self) -> Tuple[abi.mlxhip_op_t, list]:
         keep: list = []
@@ -89,6 +93,21 @@ class Op:
 
     def __repr__(self) -> str:  # compact, Rust-like
         return f"OpKind::{self.name}"
+
+
+_ops: dict = {}
+
+
+def _interned(name: str, **kw) -> Op:
+    """One Op object per (variant, payload), so its C form is built once
+    (graph building asks for the same reshapes and transposes every step)."""
+    key = (name, tuple(sorted(kw.items())))
+    op = _ops.get(key)
+    if op is None:
+        if len(_ops) > 4096:
+            _ops.clear()
+        op = _ops[key] = Op(name, **kw)
+    return op
 
 
 class OpKind:
@@ -125,11 +144,11 @@ class OpKind:
 
     @staticmethod
     def Reshape(new_shape: Sequence[int]) -> Op:
-        return Op("Reshape", shape=tuple(int(d) for d in new_shape))
+        return _interned("Reshape", shape=tuple(map(int, new_shape)))
 
     @staticmethod
     def Transpose(axes: Optional[Sequence[int]] = None) -> Op:
-        return Op("Transpose", axes=None if axes is None else tuple(int(a) for a in axes))
+        return _interned("Transpose", axes=None if axes is None else tuple(map(int, axes)))
 
     @staticmethod
     def Softmax(axis: int) -> Op:
@@ -149,7 +168,7 @@ class OpKind:
 
     @staticmethod
     def Broadcast(target_shape: Sequence[int]) -> Op:
-        return Op("Broadcast", shape=tuple(int(d) for d in target_shape))
+        return _interned("Broadcast", shape=tuple(map(int, target_shape)))
 
     @staticmethod
     def ScaledMaskedSoftmax(scale: float, causal: bool) -> Op:
@@ -198,8 +217,13 @@ class TensorMeta:
         return n
 
     def to_c(self) -> Tuple[abi.mlxhip_meta_t, list]:
-        """The C form (cached per value, read-only on the C side)."""
-        return _meta_to_c(self)
+        """The C form (built once per object and per value, read-only on the
+        C side)."""
+        c = self.__dict__.get("_c")
+        if c is None:
+            c = _meta_to_c(self)
+            object.__setattr__(self, "_c", c)
+        return c
 
     def _build_c(self) -> Tuple[abi.mlxhip_meta_t, list]:
         arr = abi.int64_array(self.shape)

@@ -33,7 +33,21 @@ from .opkind import Op, OpKind, TensorMeta
 
 
 def _shape(dims) -> Tuple[int, ...]:
-    return tuple(int(d) for d in dims)
+    return tuple(map(int, dims))
+
+
+_metas: dict = {}
+
+
+def _meta(shape: Tuple[int, ...], dtype: int) -> TensorMeta:
+    """One TensorMeta per (shape, dtype), so its C form is built once."""
+    key = (shape, dtype)
+    m = _metas.get(key)
+    if m is None:
+        if len(_metas) > 4096:
+            _metas.clear()
+        m = _metas[key] = TensorMeta(shape, dtype)
+    return m
 
 
 def _numel(shape: Sequence[int]) -> int:
@@ -104,7 +118,7 @@ class Tensor:
         if d.size != _numel(shape):
             raise abi.InvalidArgument(
                 f"data length {d.size} does not match shape {list(shape)} (expected {_numel(shape)})")
-        return cls(stream, stream.add_constant(d, TensorMeta(shape, dtype)), shape, dtype)
+        return cls(stream, stream.add_constant(d, _meta(shape, dtype)), shape, dtype)
 
     @classmethod
     def from_f32(cls, data, shape: Sequence[int], stream=None) -> "Tensor":
@@ -133,15 +147,16 @@ class Tensor:
         default stream when none is given)."""
         shape = _shape(shape)
         stream = stream if stream is not None else default_stream()
-        return cls(stream, stream.add_constant_dev(ptr, TensorMeta(shape, dtype)), shape, dtype)
+        return cls(stream, stream.add_constant_dev(ptr, _meta(shape, dtype)), shape, dtype)
 
     def _lazy(self, op: Op, inputs: Sequence["Tensor"], shape: Sequence[int]) -> "Tensor":
         shape = _shape(shape)
+        st = self.stream
         for t in inputs:
-            if t.stream is not self.stream:
+            if t.stream is not st:
                 raise abi.InvalidArgument("tensors on different streams cannot be combined")
-        nid = self.stream.add_op(op, [t.node for t in inputs], TensorMeta(shape, self.dtype))
-        return Tensor(self.stream, nid, shape, self.dtype)
+        nid = st.add_op(op, [t.node for t in inputs], _meta(shape, self.dtype))
+        return Tensor(st, nid, shape, self.dtype)
 
     # ── elementwise (tensor.rs:167-238): equal shapes only ───────────────
     def _binary(self, op: Op, rhs: "Tensor") -> "Tensor":
