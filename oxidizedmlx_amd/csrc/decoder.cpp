@@ -62,14 +62,18 @@ struct mlxhip_decoder_t {
     std::vector<size_t> off_layer;  // per layer: wqkv, bqkv, wo, bo, w1, b1, w2, b2 (8 entries)
     std::vector<uint8_t> set;       // which parameters were loaded
 
-    // activations and state
-    float *x = nullptr, *q = nullptr, *o = nullptr, *u = nullptr;
+    // activations and state: the residual stream x (f32 and its bf16
+    // planes xs), q, and the planes of the attention output (os) and of the
+    // SiLU output (us); planes are [3][DEC_MAX_BATCH][width]
+    float *x = nullptr, *q = nullptr;
+    uint16_t *xs = nullptr, *os = nullptr, *us = nullptr;
     float *kc = nullptr, *vc = nullptr;  // [L][max_batch][H][hd][max_seq], [L][max_batch][H][max_seq][hd]
     int* tokens = nullptr;               // [(max_seq + 1)][batch]
     int* argmax = nullptr;               // [max_seq][batch]
     int* tctr = nullptr;
     uint64_t* part = nullptr;
     int part_capacity = 0;
+
     float* logits = nullptr;             // [batch][steps][vocab], grown on demand
     size_t logits_cap = 0;
 
@@ -94,7 +98,7 @@ struct mlxhip_decoder_t {
         (void)hipSetDevice(device);
         if (stream) (void)hipStreamSynchronize(stream);
         drop_graphs();
-        for (void* p : {(void*)w, (void*)x, (void*)q, (void*)o, (void*)u, (void*)kc, (void*)vc, (void*)tokens,
+        for (void* p : {(void*)w, (void*)x, (void*)q, (void*)xs, (void*)os, (void*)us, (void*)kc, (void*)vc, (void*)tokens,
                         (void*)argmax, (void*)tctr, (void*)part, (void*)logits})
             if (p) (void)hipFree(p);
         if (ev0) (void)hipEventDestroy(ev0);
@@ -125,51 +129,51 @@ struct mlxhip_decoder_t {
             g.eps = c.eps;
             g.tctr = tctr;
             // q | k | v = rms_norm(x) Wqkv^T + bqkv
-            g.w = lw(l, 0); g.ldw = d; g.bias = lw(l, 1);
-            g.x = x; g.ldx = d; g.n = 3 * d; g.k = d;
+            g.w = lw(l, 0); g.bias = lw(l, 1);
+            g.xs = xs; g.ldxs = d; g.n = 3 * d; g.k = d;
             g.out = q; g.ldo = d;
             g.kc = kcl; g.vc = vcl; g.dmodel = d; g.heads = H; g.head_dim = hd; g.tmax = c.max_seq;
             MLXHIP_TRY(dec_gemv(DEC_EPI_QKV, true, g, s));
-            MLXHIP_TRY(dec_attention(q, kcl, vcl, o, batch, H, hd, c.max_seq, scale, tctr, s));
+            MLXHIP_TRY(dec_attention(q, kcl, vcl, os, batch, H, hd, c.max_seq, scale, tctr, s));
             // x = x + (o Wo^T + bo)
             g = DecGemv();
             g.batch = batch; g.tctr = tctr;
-            g.w = lw(l, 2); g.ldw = d; g.bias = lw(l, 3);
-            g.x = o; g.ldx = d; g.n = d; g.k = d;
-            g.out = x; g.ldo = d;
+            g.w = lw(l, 2); g.bias = lw(l, 3);
+            g.xs = os; g.ldxs = d; g.n = d; g.k = d;
+            g.out = x; g.ldo = d; g.outs = xs; g.ldos = d;
             MLXHIP_TRY(dec_gemv(DEC_EPI_RESID, false, g, s));
             // u = silu(rms_norm(x) W1^T + b1)
             g = DecGemv();
             g.batch = batch; g.tctr = tctr; g.eps = c.eps;
-            g.w = lw(l, 4); g.ldw = d; g.bias = lw(l, 5);
-            g.x = x; g.ldx = d; g.n = c.hidden; g.k = d;
-            g.out = u; g.ldo = c.hidden;
+            g.w = lw(l, 4); g.bias = lw(l, 5);
+            g.xs = xs; g.ldxs = d; g.n = c.hidden; g.k = d;
+            g.outs = us; g.ldos = c.hidden;
             MLXHIP_TRY(dec_gemv(DEC_EPI_SILU, true, g, s));
             // x = x + (u W2^T + b2)
             g = DecGemv();
             g.batch = batch; g.tctr = tctr;
-            g.w = lw(l, 6); g.ldw = c.hidden; g.bias = lw(l, 7);
-            g.x = u; g.ldx = c.hidden; g.n = d; g.k = c.hidden;
-            g.out = x; g.ldo = d;
+            g.w = lw(l, 6); g.bias = lw(l, 7);
+            g.xs = us; g.ldxs = c.hidden; g.n = d; g.k = c.hidden;
+            g.out = x; g.ldo = d; g.outs = xs; g.ldos = d;
             MLXHIP_TRY(dec_gemv(DEC_EPI_RESID, false, g, s));
         }
         // logits = rms_norm(x) Wlm^T, argmax per workgroup
         DecGemv g;
         g.batch = batch; g.tctr = tctr; g.eps = c.eps;
-        g.w = w + off_lm; g.ldw = d;
-        g.x = x; g.ldx = d; g.n = c.vocab; g.k = d;
+        g.w = w + off_lm;
+        g.xs = xs; g.ldxs = d; g.n = c.vocab; g.k = d;
         g.out = want_logits ? logits : nullptr;
         g.ldo = (int64_t)steps_total * c.vocab;
         g.part = part; g.part_capacity = part_capacity;
         MLXHIP_TRY(dec_gemv(DEC_EPI_ARGMAX, true, g, s));
-        return dec_finish(part, dec_gemv_groups(c.vocab, d), tokens, argmax, w + off_emb, x, d, c.vocab, batch,
+        return dec_finish(part, dec_gemv_groups(c.vocab, d), tokens, argmax, w + off_emb, x, xs, d, c.vocab, batch,
                           prompt_len, tctr, s);
     }
 
     // Position counter to 0, x = embedding of token 0.
     int enqueue_start(int batch, hipStream_t s) {
         MLXHIP_TRY(dec_set_counter(tctr, 0, s));
-        return dec_embed(w + off_emb, tokens, x, cfg.d_model, cfg.vocab, batch, tctr, s);
+        return dec_embed(w + off_emb, tokens, x, xs, cfg.d_model, cfg.vocab, batch, tctr, s);
     }
 };
 
@@ -191,8 +195,8 @@ int validate_config(const mlxhip_decoder_config_t& c) {
                     hd);
     if (c.d_model % 32 || c.hidden % 32)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decoder config: d_model and hidden must be multiples of 32");
-    // d_model feeds the RMS-normalising GEMVs (Q/K/V, up, LM head), hidden the
-    // down projection; both must fit the GEMV's LDS staging.
+    // d_model feeds the RMS-normalising GEMVs (Q/K/V, up, LM head), whose
+    // LDS holds the squares of the activation.
     if (dec_gemv_lds_bytes(c.d_model, 16, 1, true, true) > (size_t)DEC_LDS_LIMIT ||
         dec_gemv_lds_bytes(c.hidden, 16, 1, false, false) > (size_t)DEC_LDS_LIMIT)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decoder config: d_model %d / hidden %d exceed the GEMV's LDS staging",
@@ -219,7 +223,7 @@ int init_decoder(mlxhip_decoder_t* D) {
     const size_t d = c.d_model, V = c.vocab, Hd = c.hidden;
     size_t off = 0;
     D->off_emb = off; off += align_elems(V * d);
-    D->off_lm = off; off += align_elems(V * d);
+    D->off_lm = off; off += align_elems((size_t)ceil_div(V, 16) * 16 * d);  // rows padded to the 16-row tile
     D->off_layer.resize((size_t)c.n_layers * 8);
     const size_t sizes[8] = {3 * d * d, 3 * d, d * d, d, Hd * d, Hd, d * Hd, d};
     for (int l = 0; l < c.n_layers; ++l)
@@ -233,8 +237,16 @@ int init_decoder(mlxhip_decoder_t* D) {
     const size_t B = c.max_batch, S = c.max_seq, H = c.n_heads;
     MLXHIP_TRY(dev_alloc(&D->x, B * d));
     MLXHIP_TRY(dev_alloc(&D->q, B * d));
-    MLXHIP_TRY(dev_alloc(&D->o, B * d));
-    MLXHIP_TRY(dev_alloc(&D->u, B * Hd));
+    // Planes are allocated for DEC_MAX_BATCH rows (the GEMV's MFMA reads all
+    // of them; rows of absent sequences only feed discarded columns) and
+    // cleared, so every row holds finite values.
+    const size_t planes = 3 * (size_t)DEC_MAX_BATCH;
+    MLXHIP_TRY(dev_alloc(&D->xs, planes * d));
+    MLXHIP_TRY(dev_alloc(&D->os, planes * d));
+    MLXHIP_TRY(dev_alloc(&D->us, planes * Hd));
+    MLXHIP_HIP(hipMemsetAsync(D->xs, 0, planes * d * 2, D->stream));
+    MLXHIP_HIP(hipMemsetAsync(D->os, 0, planes * d * 2, D->stream));
+    MLXHIP_HIP(hipMemsetAsync(D->us, 0, planes * Hd * 2, D->stream));
     const size_t kv = (size_t)c.n_layers * B * H * D->head_dim * S;
     MLXHIP_TRY(dev_alloc(&D->kc, kv));
     MLXHIP_TRY(dev_alloc(&D->vc, kv));
@@ -365,11 +377,28 @@ int mlxhip_decoder_set_param(mlxhip_decoder_t* D, int32_t layer, int32_t which, 
     }
     if (len != want)
         return fail_shape({(int64_t)want}, {(int64_t)len}, "decoder_set_param");
-    std::vector<uint16_t> h(len);
-    for (size_t i = 0; i < len; ++i) h[i] = bf16_rne_host(values[i]);
+    // GEMV weights go in the GEMV's fragment order (the LM head's rows padded
+    // with zeros to whole 16-row tiles); the embedding and biases stay plain.
+    size_t cols = 0;
+    switch (which) {
+        case MLXHIP_DEC_LM_HEAD: case MLXHIP_DEC_WQ: case MLXHIP_DEC_WK: case MLXHIP_DEC_WV: case MLXHIP_DEC_WO:
+        case MLXHIP_DEC_W1: cols = d; break;
+        case MLXHIP_DEC_W2: cols = Hd; break;
+        default: break;
+    }
+    std::vector<uint16_t> h;
+    if (cols) {
+        const size_t rows = len / cols;
+        h.assign((size_t)ceil_div((int64_t)rows, 16) * 16 * cols, 0);
+        for (size_t n = 0; n < rows; ++n)
+            for (size_t k = 0; k < cols; ++k) h[dec_tiled_index(n, k, cols)] = bf16_rne_host(values[n * cols + k]);
+    } else {
+        h.resize(len);
+        for (size_t i = 0; i < len; ++i) h[i] = bf16_rne_host(values[i]);
+    }
     std::lock_guard<std::mutex> g(D->mu);
     MLXHIP_HIP(hipSetDevice(D->device));
-    MLXHIP_HIP(hipMemcpyAsync(D->w + off, h.data(), len * 2, hipMemcpyHostToDevice, D->stream));
+    MLXHIP_HIP(hipMemcpyAsync(D->w + off, h.data(), h.size() * 2, hipMemcpyHostToDevice, D->stream));
     MLXHIP_HIP(hipStreamSynchronize(D->stream));
     D->set[D->param_index(layer, which)] = 1;
     return MLXHIP_OK;

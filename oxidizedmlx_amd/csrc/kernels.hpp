@@ -72,23 +72,26 @@ int fill(float* y, float v, int64_t n, hipStream_t s);
 constexpr int DEC_MAX_BATCH = 8;          // sequences per decode step
 constexpr int DEC_LDS_LIMIT = 159 * 1024; // dynamic LDS (a CDNA4 CU has 160 KiB; 1 KiB kept for static LDS)
 enum DecEpilogue {
-    DEC_EPI_STORE = 0,   // out[b][n] = y
     DEC_EPI_QKV = 1,     // q -> out, k / v -> KV cache at position t
-    DEC_EPI_RESID = 2,   // out[b][n] += y (residual stream)
-    DEC_EPI_SILU = 3,    // out[b][n] = silu(y)
+    DEC_EPI_RESID = 2,   // out[b][n] += y (residual stream), and its planes
+    DEC_EPI_SILU = 3,    // silu(y) -> planes (and out when set)
     DEC_EPI_ARGMAX = 4,  // logits history (optional) + per-workgroup argmax keys
 };
-// Y[b][n] = sum_k X[b][k] W[n][k] (+ bias[n]), W bf16 [N, ldw], X f32 [B, ldx].
+// Y[b][n] = sum_k X[b][k] W[n][k] (+ bias[n]). W is bf16 in MFMA fragment
+// order (dec_tiled_index) with its rows padded to a multiple of 16. X is read as
+// its three bf16 planes xs[3][DEC_MAX_BATCH][ldxs] (hi, mid, lo; row b of a
+// plane is sequence b; hi + mid + lo is the f32 value).
 struct DecGemv {
-    const uint16_t* w = nullptr;
-    int64_t ldw = 0;
+    const uint16_t* w = nullptr;     // fragment-ordered [ceil(N/16)*16][K]
     const uint16_t* bias = nullptr;  // bf16 [N] or null
-    const float* x = nullptr;
-    int64_t ldx = 0;
-    float eps = 0.0f;                // RMS-norm eps of the prologue
+    const uint16_t* xs = nullptr;    // X planes
+    int64_t ldxs = 0;
+    float eps = 0.0f;                // RMS-norm eps
     int n = 0, k = 0, batch = 0;
-    float* out = nullptr;            // STORE/SILU/RESID: [B, ldo]; QKV: q [B, ldo];
+    float* out = nullptr;            // SILU (optional)/RESID: [B, ldo]; QKV: q [B, ldo];
     int64_t ldo = 0;                 // ARGMAX: logits[b*ldo + t*n + n'] (may be null)
+    uint16_t* outs = nullptr;        // SILU/RESID: planes of the output [3][DEC_MAX_BATCH][ldos]
+    int64_t ldos = 0;
     float* kc = nullptr;             // QKV: K^T cache [B][H][hd][tmax]
     float* vc = nullptr;             // QKV: V cache   [B][H][tmax][hd]
     int dmodel = 0, heads = 0, head_dim = 0, tmax = 0;
@@ -99,16 +102,22 @@ struct DecGemv {
 int dec_prepare();
 int dec_gemv(int epi, bool norm, const DecGemv& p, hipStream_t s);
 int dec_gemv_groups(int n, int k);
+// Position of W[n][k] of a [N][K] weight in the GEMV's fragment order: 16-row
+// tiles, each a run of 32-k steps of 64 lanes x 8 bf16 (lane = n%16 +
+// 16*((k%32)/8)), so one step's A fragments are 1 KB of consecutive memory.
+size_t dec_tiled_index(int64_t n, int64_t k, int64_t K);
 size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax, bool norm);
 size_t dec_attn_lds_bytes(int hd, int tmax);
-int dec_attention(const float* q, const float* kc, const float* vc, float* o, int batch, int heads, int hd,
+// o of every (sequence, head) into the planes os[3][DEC_MAX_BATCH][heads*hd].
+int dec_attention(const float* q, const float* kc, const float* vc, uint16_t* os, int batch, int heads, int hd,
                   int tmax, float scale, const int* tctr, hipStream_t s);
-int dec_embed(const uint16_t* emb, const int* tokens, float* x, int d, int vocab, int batch, const int* tctr,
-              hipStream_t s);
+// x [batch][d] and its planes xs[3][DEC_MAX_BATCH][d] = embedding of the tokens at position t.
+int dec_embed(const uint16_t* emb, const int* tokens, float* x, uint16_t* xs, int d, int vocab, int batch,
+              const int* tctr, hipStream_t s);
 // argmax over the LM head's partial maxima, next token (prompt or argmax),
-// its embedding into x [batch][d], t += 1.
+// its embedding into x [batch][d] and its planes, t += 1.
 int dec_finish(const uint64_t* part, int groups, int* tokens, int* argmax_out, const uint16_t* emb, float* x,
-               int d, int vocab, int batch, int prompt_len, int* tctr, hipStream_t s);
+               uint16_t* xs, int d, int vocab, int batch, int prompt_len, int* tctr, hipStream_t s);
 int dec_set_counter(int* p, int v, hipStream_t s);
 
 // ── attention.hip (fused scaled, masked attention of a batch of heads) ────

@@ -22,13 +22,24 @@
 //
 // The GEMV (Y[B,N] = X[B,K]·W[N,K]^T) is HBM-bound on W. It runs on MFMA
 // (v_mfma_f32_16x16x32_bf16) without rounding the f32 activations to bf16:
-// each activation is split into three bf16 terms x = hi + mid + lo (each term
+// each activation is kept as three bf16 terms x = hi + mid + lo (each term
 // the round-to-nearest-even bf16 of what the previous ones left; the
 // differences are exact in f32), so hi/mid/lo carry 24 significant bits
 // between them and bf16·bf16 products are exact in the f32 accumulator. The
 // 24 columns [hi b0..7 | mid b0..7 | lo b0..7] fill two 16-column MFMA tiles
 // (the last 8 columns are zero) and y = hi + (mid + lo) per (row, b).
+//
+// Split activations: whatever produces an activation that a GEMV consumes
+// (the residual updates, the SiLU, the attention, the embedding lookups)
+// also writes it as three bf16 planes Xs[3][DEC_MAX_BATCH][ld] (plane 0 hi,
+// 1 mid, 2 lo; row b of a plane is sequence b). The consuming GEMV loads its
+// MFMA B operand straight from those planes, so no workgroup re-splits or
+// stages X. RMS normalisation is a per-sequence scale: the GEMV runs on the
+// raw activation and divides the dot product by the row's RMS, which it
+// sums from the f32 activation while the MFMAs run.
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 
 #include "../common.hpp"
 #include "../kernels.hpp"
@@ -51,12 +62,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int WAVE = 64;
 constexpr int KSTEP = 32;                 // k per MFMA
-constexpr int KPASS = 256;                // k per wave per pass
-constexpr int NSTEP = KPASS / KSTEP;      // MFMA steps per pass
-constexpr int XPAD = 8;                   // bf16 padding of each LDS row
-constexpr int XROWS = 3 * DEC_MAX_BATCH;  // hi, mid, lo rows of the batch
+constexpr int NSTEP = 6;                  // MFMA steps per pass (W and X fragments of a pass held in registers)
+constexpr int KPASS = NSTEP * KSTEP;      // k per wave per pass
 constexpr int TILE_N = 16;                // output features per wave tile
 constexpr int MAX_WAVES = 16;
+constexpr int XN = 4;                     // X units (8 k of 3 planes) per thread per round
+constexpr int XPAD = 8;                   // bf16 padding of each LDS plane row (spreads rows over the banks)
+constexpr int XROWS = 3 * DEC_MAX_BATCH;  // hi, mid, lo rows of the batch
+constexpr int WSS_FLOATS = 2 * DEC_MAX_BATCH;  // rms, 1/rms
 
 __device__ inline uint32_t bf16_rne(float f) {
     uint32_t u = __float_as_uint(f);
@@ -64,6 +77,32 @@ __device__ inline uint32_t bf16_rne(float f) {
     return u >> 16;
 }
 __device__ inline float bf16_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Writes v as its hi/mid/lo bf16 terms into the planes of `xs` (row b, column n).
+__device__ inline void store_split(uint16_t* xs, int64_t ld, int b, int64_t n, float v) {
+    const uint32_t h = bf16_rne(v);
+    const float r1 = v - bf16_f32(h);
+    const uint32_t m = bf16_rne(r1);
+    const float r2 = r1 - bf16_f32(m);
+    xs[(int64_t)b * ld + n] = (uint16_t)h;
+    xs[(int64_t)(DEC_MAX_BATCH + b) * ld + n] = (uint16_t)m;
+    xs[(int64_t)(2 * DEC_MAX_BATCH + b) * ld + n] = (uint16_t)bf16_rne(r2);
+}
+
+// Row b of x (and its planes) = f32 of the bf16 embedding row `src`, 8
+// values per unit (the planes: hi = the bf16 value, mid = lo = 0).
+__device__ inline void store_embedding_unit(const uint4 e, float* x, uint16_t* xs, int64_t ld, int b, int k) {
+    float* xr = x + (int64_t)b * ld + k;
+    const uint32_t w[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        reinterpret_cast<float4*>(xr)[j] =
+            make_float4(bf16_f32(w[2 * j] & 0xFFFFu), bf16_f32(w[2 * j] >> 16), bf16_f32(w[2 * j + 1] & 0xFFFFu),
+                        bf16_f32(w[2 * j + 1] >> 16));
+    *reinterpret_cast<uint4*>(xs + (int64_t)b * ld + k) = e;
+    *reinterpret_cast<uint4*>(xs + (int64_t)(DEC_MAX_BATCH + b) * ld + k) = make_uint4(0u, 0u, 0u, 0u);
+    *reinterpret_cast<uint4*>(xs + (int64_t)(2 * DEC_MAX_BATCH + b) * ld + k) = make_uint4(0u, 0u, 0u, 0u);
+}
 
 __device__ inline uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
@@ -89,42 +128,80 @@ __device__ inline uint32_t order_key(float f) {
 // [s*kw, (s+1)*kw). Partials of the KS slices are summed in slice order
 // (deterministic).
 //
+// The workgroup first stages the X planes (rows of the B <= 8 sequences) in
+// LDS with contiguous 16-byte loads, one (sequence, 8-k unit) of all three
+// planes per thread, so each load instruction covers 1 KB of consecutive
+// memory; the MFMA B operands are then read from LDS. Loading them straight
+// from memory in MFMA layout (16 rows x 64 bytes per instruction, repeated
+// by every row tile of the workgroup) measured 1-5 us slower per launch.
+// With NORM the same thread also sums the squares of its unit's values
+// (hi + mid + lo reproduces the f32 value exactly), and wave b (mod waves)
+// adds the units of row b in k order, then across lanes, for the RMS of
+// sequence b; the GEMV runs on the raw activation and its dot products are
+// divided by the RMS.
+//
 // The kernel is latency-bound at decode sizes (a few MB per launch), so every
 // global load whose address does not depend on this kernel's own results is
-// issued at the start, before the first wait: the step position, the
-// epilogue's bias and residual values, the X rows and the W fragments. Each
-// thread then normalises and splits at most XU float4s of X (a workgroup has
-// at least 8*K/4/XU threads): the split costs ~25 VALU operations per value,
-// so it is spread over every thread of the workgroup. The RMS of row b is
-// summed by wave b (mod waves), lane by lane in k order, then across lanes.
+// issued at the start, before the first wait: the X units, the W fragments
+// of the first pass, the step position and the epilogue's bias and residual
+// values.
 //
 // ARGMAX (the LM head) publishes each workgroup's per-sequence maximum key
 // for decode_finish.
-constexpr int XU = 8;  // float4s of X per thread, at most
-
 template <int EPI, bool NORM>
 __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks, int r_tiles, int kw) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int K = p.k, N = p.n, B = p.batch;
-    const int pitch = K + XPAD;
     constexpr int TB = TILE_N * DEC_MAX_BATCH;  // outputs of one row tile
-    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-    float* red = reinterpret_cast<float*>(smem + (size_t)XROWS * pitch * 2);
-    float* wss = red + r_tiles * ks * TB;                                 // [2][8]: rms, 1/rms
-    uint64_t* keys = reinterpret_cast<uint64_t*>(wss + MAX_WAVES * DEC_MAX_BATCH);  // [r_tiles * TB]
-    float* psum = reinterpret_cast<float*>(keys + (EPI == DEC_EPI_ARGMAX ? r_tiles * TB : 0));  // NORM: [8 * K/4]
+    const int pitch = K + XPAD;                 // bf16 per LDS plane row
+    uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                                    // [24][pitch]
+    float* red = reinterpret_cast<float*>(smem + (size_t)XROWS * pitch * 2);            // [r_tiles * ks][TB]
+    float* wss = red + r_tiles * ks * TB;                                                // [2][8]: rms, 1/rms
+    uint64_t* keys = reinterpret_cast<uint64_t*>(wss + WSS_FLOATS);                     // ARGMAX: [r_tiles * TB]
+    float* psum = reinterpret_cast<float*>(keys + (EPI == DEC_EPI_ARGMAX ? r_tiles * TB : 0));  // NORM: [8][K/8]
 
     const int tid = threadIdx.x, nthr = blockDim.x;
     const int wave = tid / WAVE, lane = tid % WAVE;
     const int nwaves = nthr / WAVE;
     const int ksl = wave % ks, rl = wave / ks;
-    const int n0 = (blockIdx.x * r_tiles + rl) * TILE_N;
+    const int tile0 = blockIdx.x * r_tiles;
+    const int n0 = (tile0 + rl) * TILE_N;
     const int kb = ksl * kw;
     const int ke = min(K, kb + kw);
     const bool active = n0 < N && kb < K;
     const int nitems = r_tiles * TB;
 
     // ── loads issued up front ───────────────────────────────────────────────
+    // X unit u (u < B*K/8): sequence u / (K/8), k = 8 * (u % (K/8)), three planes.
+    const int k8 = K / 8, nunits = B * k8;
+    u32x4 xu[XN][3];
+    auto load_units = [&](int u0) {
+#pragma unroll
+        for (int i = 0; i < XN; ++i) {
+            const int u = u0 + tid + i * nthr;
+            if (u < nunits) {
+                const int b = u / k8, k = 8 * (u - b * k8);
+#pragma unroll
+                for (int q = 0; q < 3; ++q)
+                    xu[i][q] = *reinterpret_cast<const u32x4*>(p.xs + (int64_t)(q * DEC_MAX_BATCH + b) * p.ldxs + k);
+            }
+        }
+    };
+    load_units(0);
+    // A operand (W, stored in fragment order): lane l's 8 k of feature
+    // n0 + l%16 at k block l/16 are 16 consecutive bytes, and the 64 lanes'
+    // fragments of one 32-k step are 1 KB of consecutive memory.
+    const int col = lane & 15, kg = lane >> 4;
+    const uint16_t* wp = p.w + ((int64_t)(n0 / TILE_N) * (K / KSTEP) * WAVE + lane) * 8;
+    u32x4 a[NSTEP];
+    auto load_pass = [&](int k0) {
+        const int steps = active ? min(NSTEP, (ke - k0) / KSTEP) : 0;
+#pragma unroll
+        for (int s = 0; s < NSTEP; ++s)
+            if (s < steps) a[s] = *reinterpret_cast<const u32x4*>(wp + (int64_t)(k0 / KSTEP + s) * WAVE * 8);
+    };
+    load_pass(kb);
+
     const int t = p.tctr ? *p.tctr : 0;
     float pre_bias[2] = {0.0f, 0.0f}, pre_res[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -132,58 +209,51 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
         const int i = tid + e * nthr;
         if (i < nitems) {
             const int rr = i / TB, row = (i % TB) / DEC_MAX_BATCH, b = i % DEC_MAX_BATCH;
-            const int n = (blockIdx.x * r_tiles + rr) * TILE_N + row;
+            const int n = (tile0 + rr) * TILE_N + row;
             if (n < N && b < B) {
                 if (p.bias) pre_bias[e] = bf16_f32(p.bias[n]);
                 if constexpr (EPI == DEC_EPI_RESID) pre_res[e] = p.out[(int64_t)b * p.ldo + n];
             }
         }
     }
-    // X unit u = tid + i*nthr is float4 column u % (K/4) of row u / (K/4).
-    const int k4 = K / 4, nunits = DEC_MAX_BATCH * k4;
-    float4 xv[XU];
-#pragma unroll
-    for (int i = 0; i < XU; ++i) {
-        const int u = tid + i * nthr;
-        const int b = u / k4;
-        xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (u < nunits && b < B) xv[i] = *reinterpret_cast<const float4*>(p.x + (int64_t)b * p.ldx + 4 * (u - b * k4));
-    }
-    // Lane l reads 8 consecutive k of feature n0 + l%16 (MFMA A-operand layout:
-    // row l%16, k block l/16). Rows past N read row N-1 (discarded).
-    const int frow = min(n0 + (lane & 15), N - 1);
-    const uint16_t* wp = p.w + (int64_t)frow * p.ldw + 8 * (lane >> 4);
-    u32x4 a[NSTEP];
-    auto load_pass = [&](int k0) {
-        const int steps = active ? min(NSTEP, (ke - k0) / KSTEP) : 0;
-#pragma unroll
-        for (int s = 0; s < NSTEP; ++s)
-            if (s < steps) a[s] = *reinterpret_cast<const u32x4*>(wp + k0 + s * KSTEP);
-    };
-    load_pass(kb);
 
-    // ── prologue: X (optionally RMS-normalised) split into hi/mid/lo bf16 rows
-    if constexpr (NORM) {
-        // rms_norm, cpu_kernels.rs:647-669: sqrt(sum(x*x)/d + eps), y = x / rms.
-        // The squares come from the X units already in registers (no second
-        // read of X, which would also wait behind the W loads): each unit's
-        // sum goes to LDS, then wave b (mod waves) adds row b's in k order.
+    // ── X planes into LDS (and the squares of X) ───────────────────────────
+    auto store_units = [&](int u0) {
 #pragma unroll
-        for (int i = 0; i < XU; ++i) {
-            const int u = tid + i * nthr;
+        for (int i = 0; i < XN; ++i) {
+            const int u = u0 + tid + i * nthr;
             if (u < nunits) {
-                const float4 v = xv[i];
-                float q = v.x * v.x;
-                q += v.y * v.y;
-                q += v.z * v.z;
-                q += v.w * v.w;
-                psum[u] = q;
+                const int b = u / k8, c = u - b * k8;
+#pragma unroll
+                for (int q = 0; q < 3; ++q)
+                    *reinterpret_cast<u32x4*>(xl + (q * DEC_MAX_BATCH + b) * pitch + 8 * c) = xu[i][q];
+                if constexpr (NORM) {
+                    // rms_norm, cpu_kernels.rs:647-669: sqrt(sum(x*x)/d + eps), y = x / rms.
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int w32 = j / 2, sh = (j & 1) * 16;
+                        const float x = bf16_f32((xu[i][0][w32] >> sh) & 0xFFFFu) +
+                                        (bf16_f32((xu[i][1][w32] >> sh) & 0xFFFFu) +
+                                         bf16_f32((xu[i][2][w32] >> sh) & 0xFFFFu));
+                        ss += x * x;
+                    }
+                    psum[u] = ss;
+                }
             }
         }
-        __syncthreads();
+    };
+    store_units(0);
+    // Rows wider than XN * nthr units (not met at decode sizes) take more rounds.
+    for (int u0 = XN * nthr; u0 < nunits; u0 += XN * nthr) {
+        load_units(u0);
+        store_units(u0);
+    }
+    __syncthreads();
+    if constexpr (NORM) {
         for (int b = wave; b < B; b += nwaves) {
             float ss = 0.0f;
-            for (int c = lane; c < k4; c += WAVE) ss += psum[b * k4 + c];
+            for (int c = lane; c < k8; c += WAVE) ss += psum[b * k8 + c];
             ss = wave_sum(ss);
             if (lane == 0) {
                 float rms = sqrtf(ss / (float)K + p.eps), r;
@@ -192,48 +262,17 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
                 wss[DEC_MAX_BATCH + b] = r;
             }
         }
-        __syncthreads();
     }
-#pragma unroll
-    for (int i = 0; i < XU; ++i) {
-        const int u = tid + i * nthr;
-        if (u < nunits) {
-            const int b = u / k4, k = 4 * (u - b * k4);
-            float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-            if constexpr (NORM) {
-                if (b < B) {
-                    const float d = wss[b], r = wss[DEC_MAX_BATCH + b];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) v[j] = div_by(v[j], d, r);
-                }
-            }
-            uint32_t h[4], m[4], l[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                h[j] = bf16_rne(v[j]);
-                const float r1 = v[j] - bf16_f32(h[j]);
-                m[j] = bf16_rne(r1);
-                const float r2 = r1 - bf16_f32(m[j]);
-                l[j] = bf16_rne(r2);
-            }
-            *reinterpret_cast<uint2*>(xs + (0 * DEC_MAX_BATCH + b) * pitch + k) =
-                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-            *reinterpret_cast<uint2*>(xs + (1 * DEC_MAX_BATCH + b) * pitch + k) =
-                make_uint2(m[0] | (m[1] << 16), m[2] | (m[3] << 16));
-            *reinterpret_cast<uint2*>(xs + (2 * DEC_MAX_BATCH + b) * pitch + k) =
-                make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
-        }
-    }
-    __syncthreads();
 
     // ── main loop: 2 MFMAs per 16 features x 32 k ───────────────────────────
-    // B operand (X columns): lane l holds column l%16, k block l/16. Tile 0
-    // columns are hi(b0..7), mid(b0..7); tile 1 columns are lo(b0..7), zero.
-    const int col = lane & 15, kg = lane >> 4;
-    const uint16_t* x0 = xs + col * pitch + 8 * kg;
-    const uint16_t* x1 = xs + (2 * DEC_MAX_BATCH + (col & 7)) * pitch + 8 * kg;
+    // B operand (X) from LDS: lane l holds column l%16, k block l/16. Tile 0
+    // column c is plane c/8 (hi, mid) of sequence c%8, tile 1 column c < 8
+    // the lo plane of sequence c; columns 8..15 of tile 1 are zero.
+    const uint16_t* x0 = xl + col * pitch + 8 * kg;
+    const uint16_t* x1 = xl + (2 * DEC_MAX_BATCH + (col & 7)) * pitch + 8 * kg;
     const bool zero1 = col >= 8;
     f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
     for (int k0 = kb; k0 < ke; k0 += KPASS) {
         if (k0 != kb) load_pass(k0);
         const int steps = active ? min(NSTEP, (ke - k0) / KSTEP) : 0;
@@ -242,8 +281,8 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
             if (s < steps) {
                 const int ko = k0 + s * KSTEP;
                 const u32x4 b0 = *reinterpret_cast<const u32x4*>(x0 + ko);
-                u32x4 b1 = {0u, 0u, 0u, 0u};
-                if (!zero1) b1 = *reinterpret_cast<const u32x4*>(x1 + ko);
+                u32x4 b1 = *reinterpret_cast<const u32x4*>(x1 + ko);
+                b1 = zero1 ? zero4 : b1;
                 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[s]),
                                                                __builtin_bit_cast(bf16x8, b0), acc0, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[s]),
@@ -264,24 +303,33 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     }
     __syncthreads();
 
-    // ── epilogue: sum the k-slices in order, bias, then the op ─────────────
+    // ── epilogue: sum the k-slices in order, 1/rms, bias, then the op ──────
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int i = tid + e * nthr;
         if (i >= nitems) continue;
         const int rr = i / TB, ei = i % TB;
         const int row = ei / DEC_MAX_BATCH, b = ei % DEC_MAX_BATCH;
-        const int n = (blockIdx.x * r_tiles + rr) * TILE_N + row;
+        const int n = (tile0 + rr) * TILE_N + row;
         float v = red[(rr * ks) * TB + ei];
         for (int s = 1; s < ks; ++s) v += red[(rr * ks + s) * TB + ei];
         const bool valid = n < N && b < B;
+        if constexpr (NORM) {
+            if (b < B) v = div_by(v, wss[b], wss[DEC_MAX_BATCH + b]);
+        }
         if (p.bias) v = v + pre_bias[e];
-        if constexpr (EPI == DEC_EPI_STORE) {
-            if (valid) p.out[(int64_t)b * p.ldo + n] = v;
-        } else if constexpr (EPI == DEC_EPI_SILU) {
-            if (valid) p.out[(int64_t)b * p.ldo + n] = v * sigmoid_ref(v);
+        if constexpr (EPI == DEC_EPI_SILU) {
+            if (valid) {
+                const float y = v * sigmoid_ref(v);
+                if (p.out) p.out[(int64_t)b * p.ldo + n] = y;
+                store_split(p.outs, p.ldos, b, n, y);
+            }
         } else if constexpr (EPI == DEC_EPI_RESID) {
-            if (valid) p.out[(int64_t)b * p.ldo + n] = pre_res[e] + v;
+            if (valid) {
+                const float y = pre_res[e] + v;
+                p.out[(int64_t)b * p.ldo + n] = y;
+                store_split(p.outs, p.ldos, b, n, y);
+            }
         } else if constexpr (EPI == DEC_EPI_QKV) {
             if (valid) {
                 const int d = p.dmodel, seg = n / d, nn = n - seg * d;
@@ -315,14 +363,17 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
 // then lanes with equal i % 8 and the 8 waves combine theirs. Equal logits
 // resolve to the lowest index (the key's low word is 0xFFFFFFFF - index). The
 // next token is the prompt's while t+1 < prompt_len, else the argmax; its
-// embedding row becomes the residual stream x of the next step.
+// embedding row becomes the residual stream x (and its planes) of the next
+// step, 8 values per thread and unit, every unit's load issued before the
+// first store.
 constexpr int FIN_BLOCK = DEC_MAX_BATCH * WAVE;
 constexpr int FIN_KEYS = 8;  // keys per thread loaded at once
+constexpr int FIN_UNITS = 4; // embedding units (8 bf16) per thread loaded at once
 
 __global__ __launch_bounds__(FIN_BLOCK) void decode_finish_kernel(
     const uint64_t* __restrict__ part, int groups, int* __restrict__ tokens, int* __restrict__ argmax_out,
-    const uint16_t* __restrict__ emb, float* __restrict__ x, int d, int vocab, int batch, int prompt_len,
-    int* __restrict__ tctr) {
+    const uint16_t* __restrict__ emb, float* __restrict__ x, uint16_t* __restrict__ xs, int d, int vocab,
+    int batch, int prompt_len, int* __restrict__ tctr) {
     __shared__ uint64_t s_max[FIN_BLOCK / WAVE][DEC_MAX_BATCH];
     __shared__ int s_tok[DEC_MAX_BATCH];
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
@@ -363,9 +414,25 @@ __global__ __launch_bounds__(FIN_BLOCK) void decode_finish_kernel(
         s_tok[tid] = next < 0 ? 0 : (next > vocab - 1 ? vocab - 1 : next);
     }
     __syncthreads();
-    for (int i = tid; i < batch * d; i += FIN_BLOCK) {
-        const int bb = i / d, k = i - bb * d;
-        x[(int64_t)bb * d + k] = bf16_f32(emb[(int64_t)s_tok[bb] * d + k]);
+    const int d8 = d / 8, units = batch * d8;
+    for (int u0 = tid; u0 < units; u0 += FIN_UNITS * FIN_BLOCK) {
+        uint4 e[FIN_UNITS];
+#pragma unroll
+        for (int j = 0; j < FIN_UNITS; ++j) {
+            const int u = u0 + j * FIN_BLOCK;
+            if (u < units) {
+                const int bb = u / d8;
+                e[j] = *reinterpret_cast<const uint4*>(emb + (int64_t)s_tok[bb] * d + 8 * (u - bb * d8));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FIN_UNITS; ++j) {
+            const int u = u0 + j * FIN_BLOCK;
+            if (u < units) {
+                const int bb = u / d8;
+                store_embedding_unit(e[j], x, xs, d, bb, 8 * (u - bb * d8));
+            }
+        }
     }
     if (tid == 0) *tctr = t + 1;
 }
@@ -398,7 +465,7 @@ template <int HD>
 __global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __restrict__ q,
                                                                 const float* __restrict__ kc,
                                                                 const float* __restrict__ vc,
-                                                                float* __restrict__ o, int heads,
+                                                                uint16_t* __restrict__ os, int heads,
                                                                 int tmax, float scale,
                                                                 const int* __restrict__ tctr) {
     extern __shared__ __attribute__((aligned(16))) float sm[];
@@ -485,58 +552,74 @@ __global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __r
     if (tid < HD) {
         float r = part[tid];
         for (int gg = 1; gg < G; ++gg) r += part[gg * HD + tid];
-        o[(int64_t)b * d + h * HD + tid] = r;
+        store_split(os, d, b, h * HD + tid, r);
     }
 }
 
-// ── embedding of the step's tokens ────────────────────────────────────────
+// ── embedding of the step's tokens (x and its planes) ──────────────────────
 __global__ __launch_bounds__(256) void decode_embed_kernel(const uint16_t* __restrict__ emb,
                                                            const int* __restrict__ tokens,
-                                                           float* __restrict__ x, int d, int vocab,
-                                                           int batch, const int* __restrict__ tctr) {
+                                                           float* __restrict__ x, uint16_t* __restrict__ xs,
+                                                           int d, int vocab, int batch,
+                                                           const int* __restrict__ tctr) {
     const int b = blockIdx.x;
     const int t = *tctr;
     int tok = tokens[(int64_t)t * batch + b];
     tok = tok < 0 ? 0 : (tok > vocab - 1 ? vocab - 1 : tok);
     const uint16_t* src = emb + (int64_t)tok * d;
-    for (int k = threadIdx.x; k < d; k += blockDim.x) x[(int64_t)b * d + k] = bf16_f32(src[k]);
+    for (int u = threadIdx.x; u < d / 8; u += blockDim.x)
+        store_embedding_unit(*reinterpret_cast<const uint4*>(src + 8 * u), x, xs, d, b, 8 * u);
 }
 
 __global__ void decode_set_kernel(int* __restrict__ p, int v) { *p = v; }
 
-// Launch shape: a problem with fewer than 512 row tiles splits K into
-// slices of ~64 (up to 16 waves), so the workgroup has threads enough to
-// split X quickly and its W loads spread over many waves; a wide problem
-// (the LM head) uses 256-k slices and up to 16/KS row tiles per workgroup
-// while that still leaves >= 256 workgroups, so fewer workgroups repeat the
-// prologue.
-void gemv_shape(int n, int k, int& ks, int& r, int& kw, int& grid) {
+// Launch shape: a problem with fewer than 512 row tiles gives each
+// workgroup one row tile and splits K into slices of ~64 (up to 16 waves),
+// so its W and X loads spread over many waves; a wide problem (the LM head)
+// uses slices of up to KPASS and up to 16/KS row tiles per workgroup while
+// that still leaves >= 256 workgroups (the row tiles of a workgroup share
+// their X fragments in the L1 cache). MLXHIP_DEC_WIDE="ks,r" overrides the
+// wide shape (tuning).
+//
+// K is not split across workgroups: adding partial sums of several
+// workgroups takes a device-scope fence per workgroup (an L2 write-back and
+// invalidate of its XCD), measured at 15-20 us per launch over 300-400
+// workgroups of a decode step, where a whole GEMV takes 5-12 us.
+struct GemvShape {
+    int ks, r, kw, grid;
+};
+
+GemvShape gemv_shape(int n, int k) {
+    GemvShape g{1, 1, 0, 0};
     const int ntiles = (int)ceil_div(n, TILE_N);
-    r = 1;
     if (ntiles >= 512) {
-        ks = std::min(MAX_WAVES, (int)ceil_div(k, KPASS));
-        while ((r * 2) * ks <= MAX_WAVES && ceil_div(ntiles, r * 2) >= 256) r *= 2;
+        g.ks = std::min(MAX_WAVES, (int)ceil_div(k, KPASS));
+        while ((g.r * 2) * g.ks <= MAX_WAVES && ceil_div(ntiles, g.r * 2) >= 256) g.r *= 2;
+        static const char* env = std::getenv("MLXHIP_DEC_WIDE");
+        int eks = 0, er = 0;
+        if (env && std::sscanf(env, "%d,%d", &eks, &er) == 2 && eks >= 1 && er >= 1 && eks * er <= MAX_WAVES) {
+            g.ks = eks;
+            g.r = er;
+        }
     } else {
-        ks = std::max(1, std::min(MAX_WAVES, (int)ceil_div(k, 64)));
+        g.ks = std::max(1, std::min(MAX_WAVES, (int)ceil_div(k, 64)));
     }
-    kw = (int)ceil_div(ceil_div(k, ks), KSTEP) * KSTEP;
-    grid = (int)ceil_div(ntiles, r);
+    g.kw = (int)ceil_div(ceil_div(k, g.ks), KSTEP) * KSTEP;
+    g.grid = (int)ceil_div(ntiles, g.r);
+    return g;
 }
 
 template <int EPI, bool NORM>
 int launch_gemv(const DecGemv& p, hipStream_t s) {
-    int ks, r, kw, grid;
-    gemv_shape(p.n, p.k, ks, r, kw, grid);
-    if (ceil_div((int64_t)DEC_MAX_BATCH * (p.k / 4), (int64_t)r * ks * WAVE) > XU)
-        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: K = %d too wide for one workgroup", p.k);
-    const size_t lds = dec_gemv_lds_bytes(p.k, ks, r, EPI == DEC_EPI_ARGMAX, NORM);
+    const GemvShape g = gemv_shape(p.n, p.k);
+    const size_t lds = dec_gemv_lds_bytes(p.k, g.ks, g.r, EPI == DEC_EPI_ARGMAX, NORM);
     if (lds > DEC_LDS_LIMIT)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: K = %d needs %zu bytes of LDS (limit %d)", p.k,
                     lds, DEC_LDS_LIMIT);
-    if (EPI == DEC_EPI_ARGMAX && grid > p.part_capacity)
+    if (EPI == DEC_EPI_ARGMAX && g.grid > p.part_capacity)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: %d workgroups exceed the partial-max buffer (%d)",
-                    grid, p.part_capacity);
-    hipLaunchKernelGGL((gemv_kernel<EPI, NORM>), dim3(grid), dim3(r * ks * WAVE), lds, s, p, ks, r, kw);
+                    g.grid, p.part_capacity);
+    hipLaunchKernelGGL((gemv_kernel<EPI, NORM>), dim3(g.grid), dim3(g.r * g.ks * WAVE), lds, s, p, g.ks, g.r, g.kw);
     return launch_check("decode gemv_kernel");
 }
 
@@ -550,18 +633,20 @@ int set_lds_attr() {
 }  // namespace
 
 size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax, bool norm) {
-    size_t b = (size_t)XROWS * (k + XPAD) * 2;                    // hi/mid/lo rows
-    b += (size_t)r * ks * TILE_N * DEC_MAX_BATCH * sizeof(float);  // k-slice partials
-    b += MAX_WAVES * DEC_MAX_BATCH * sizeof(float);               // row rms and 1 / rms
+    size_t b = (size_t)XROWS * (k + XPAD) * 2;                           // X planes
+    b += (size_t)r * ks * TILE_N * DEC_MAX_BATCH * sizeof(float);        // k-slice partials
+    b += WSS_FLOATS * sizeof(float);                                     // row rms and 1 / rms
     if (argmax) b += (size_t)r * TILE_N * DEC_MAX_BATCH * sizeof(uint64_t);
-    if (norm) b += (size_t)DEC_MAX_BATCH * (k / 4) * sizeof(float);  // squares of the X units
+    if (norm) b += (size_t)DEC_MAX_BATCH * (k / 8) * sizeof(float);      // squares of the X units
     return b;
 }
 
-int dec_gemv_groups(int n, int k) {
-    int ks, r, kw, grid;
-    gemv_shape(n, k, ks, r, kw, grid);
-    return grid;
+int dec_gemv_groups(int n, int k) { return gemv_shape(n, k).grid; }
+
+size_t dec_tiled_index(int64_t n, int64_t k, int64_t K) {
+    const int64_t tile = n / TILE_N, step = k / KSTEP;
+    const int64_t lane = (n % TILE_N) + TILE_N * ((k % KSTEP) / 8);
+    return (size_t)(((tile * (K / KSTEP) + step) * WAVE + lane) * 8 + k % 8);
 }
 
 int dec_prepare() {
@@ -569,22 +654,20 @@ int dec_prepare() {
     MLXHIP_TRY((set_lds_attr<DEC_EPI_RESID, false>()));
     MLXHIP_TRY((set_lds_attr<DEC_EPI_SILU, true>()));
     MLXHIP_TRY((set_lds_attr<DEC_EPI_ARGMAX, true>()));
-    MLXHIP_TRY((set_lds_attr<DEC_EPI_STORE, false>()));
-    MLXHIP_TRY((set_lds_attr<DEC_EPI_STORE, true>()));
     return MLXHIP_OK;
 }
 
 int dec_gemv(int epi, bool norm, const DecGemv& p, hipStream_t s) {
-    if (p.k <= 0 || p.k % KSTEP || p.n <= 0 || p.batch <= 0 || p.batch > DEC_MAX_BATCH || p.ldw % 8 ||
-        p.ldx % 4)
+    if (p.k <= 0 || p.k % KSTEP || p.n <= 0 || p.batch <= 0 || p.batch > DEC_MAX_BATCH || p.ldxs % 8 ||
+        p.ldxs < p.k || !p.xs)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: unsupported shape n=%d k=%d batch=%d", p.n, p.k,
                     p.batch);
+    if ((epi == DEC_EPI_RESID || epi == DEC_EPI_SILU) && (!p.outs || p.ldos < p.n))
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: epilogue %d needs the output planes", epi);
     if (epi == DEC_EPI_QKV && norm) return launch_gemv<DEC_EPI_QKV, true>(p, s);
     if (epi == DEC_EPI_RESID && !norm) return launch_gemv<DEC_EPI_RESID, false>(p, s);
     if (epi == DEC_EPI_SILU && norm) return launch_gemv<DEC_EPI_SILU, true>(p, s);
     if (epi == DEC_EPI_ARGMAX && norm) return launch_gemv<DEC_EPI_ARGMAX, true>(p, s);
-    if (epi == DEC_EPI_STORE && !norm) return launch_gemv<DEC_EPI_STORE, false>(p, s);
-    if (epi == DEC_EPI_STORE && norm) return launch_gemv<DEC_EPI_STORE, true>(p, s);
     return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: no kernel for epilogue %d (norm=%d)", epi, (int)norm);
 }
 
@@ -592,7 +675,7 @@ size_t dec_attn_lds_bytes(int hd, int tmax) {
     return ((size_t)tmax + hd + ATT_PART + ATT_BLOCK / WAVE) * sizeof(float);
 }
 
-int dec_attention(const float* q, const float* kc, const float* vc, float* o, int batch, int heads, int hd,
+int dec_attention(const float* q, const float* kc, const float* vc, uint16_t* os, int batch, int heads, int hd,
                   int tmax, float scale, const int* tctr, hipStream_t s) {
     if (batch <= 0 || heads <= 0 || tmax <= 0)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode attention: empty problem");
@@ -600,29 +683,31 @@ int dec_attention(const float* q, const float* kc, const float* vc, float* o, in
     if (lds > 64 * 1024) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode attention: max_seq %d too long", tmax);
     const dim3 grid(batch * heads), block(ATT_BLOCK);
     switch (hd) {
-        case 8: hipLaunchKernelGGL(decode_attn_kernel<8>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
-        case 16: hipLaunchKernelGGL(decode_attn_kernel<16>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
-        case 32: hipLaunchKernelGGL(decode_attn_kernel<32>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
-        case 64: hipLaunchKernelGGL(decode_attn_kernel<64>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
-        case 128: hipLaunchKernelGGL(decode_attn_kernel<128>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
-        case 256: hipLaunchKernelGGL(decode_attn_kernel<256>, grid, block, lds, s, q, kc, vc, o, heads, tmax, scale, tctr); break;
+        case 8: hipLaunchKernelGGL(decode_attn_kernel<8>, grid, block, lds, s, q, kc, vc, os, heads, tmax, scale, tctr); break;
+        case 16: hipLaunchKernelGGL(decode_attn_kernel<16>, grid, block, lds, s, q, kc, vc, os, heads, tmax, scale, tctr); break;
+        case 32: hipLaunchKernelGGL(decode_attn_kernel<32>, grid, block, lds, s, q, kc, vc, os, heads, tmax, scale, tctr); break;
+        case 64: hipLaunchKernelGGL(decode_attn_kernel<64>, grid, block, lds, s, q, kc, vc, os, heads, tmax, scale, tctr); break;
+        case 128: hipLaunchKernelGGL(decode_attn_kernel<128>, grid, block, lds, s, q, kc, vc, os, heads, tmax, scale, tctr); break;
+        case 256: hipLaunchKernelGGL(decode_attn_kernel<256>, grid, block, lds, s, q, kc, vc, os, heads, tmax, scale, tctr); break;
         default: return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode attention: head_dim %d not in {8, 16, ..., 256}", hd);
     }
     return launch_check("decode_attn_kernel");
 }
 
-int dec_embed(const uint16_t* emb, const int* tokens, float* x, int d, int vocab, int batch, const int* tctr,
-              hipStream_t s) {
-    hipLaunchKernelGGL(decode_embed_kernel, dim3(batch), dim3(256), 0, s, emb, tokens, x, d, vocab, batch, tctr);
+int dec_embed(const uint16_t* emb, const int* tokens, float* x, uint16_t* xs, int d, int vocab, int batch,
+              const int* tctr, hipStream_t s) {
+    if (d % 8) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode embed: d_model %d is not a multiple of 8", d);
+    hipLaunchKernelGGL(decode_embed_kernel, dim3(batch), dim3(256), 0, s, emb, tokens, x, xs, d, vocab, batch, tctr);
     return launch_check("decode_embed_kernel");
 }
 
 int dec_finish(const uint64_t* part, int groups, int* tokens, int* argmax_out, const uint16_t* emb, float* x,
-               int d, int vocab, int batch, int prompt_len, int* tctr, hipStream_t s) {
+               uint16_t* xs, int d, int vocab, int batch, int prompt_len, int* tctr, hipStream_t s) {
     if (batch <= 0 || batch > DEC_MAX_BATCH)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode finish: batch %d outside [1, %d]", batch, DEC_MAX_BATCH);
+    if (d % 8) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode finish: d_model %d is not a multiple of 8", d);
     hipLaunchKernelGGL(decode_finish_kernel, dim3(1), dim3(FIN_BLOCK), 0, s, part, groups, tokens, argmax_out, emb,
-                       x, d, vocab, batch, prompt_len, tctr);
+                       x, xs, d, vocab, batch, prompt_len, tctr);
     return launch_check("decode_finish_kernel");
 }
 
