@@ -157,6 +157,16 @@ int mlxhip_last_status(void);
 int mlxhip_last_shape_mismatch(int64_t* expected, size_t* expected_ndim,
                                int64_t* got, size_t* got_ndim, size_t cap);
 
+/* Allocation-failure hook for error-path tests (no counterpart in the
+ * reference, whose tests force failures through bad shapes and parameters
+ * only: crates/mlx-core/tests/attention_golden.rs:259-302). After `after`
+ * more successful device allocations, every device allocation the library
+ * makes (stream buffers and scratch, GEMM workspaces, mlxhip_buffer_alloc,
+ * decoders) fails with MLXHIP_ERR_FFI_FAILED until the hook is reset with
+ * after < 0. Cached blocks count as allocations. The environment variable
+ * MLXHIP_FAIL_ALLOC_AFTER=n sets it at the first allocation. Returns MLXHIP_OK. */
+int mlxhip_debug_fail_allocations(int64_t after);
+
 /* Number of visible HIP devices (0 when no GPU; never fails). */
 int mlxhip_device_count(void);
 

@@ -18,15 +18,19 @@ from oxidizedmlx_amd import abi
 from oxidizedmlx_amd.opkind import NodeInput, Op, TensorMeta, inputs_to_c
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "libmlx_cpu_ref.so")
+# MLXHIP_ORACLE_LIB selects another build of the same sources (the sanitized
+# one, oracle/_sanitize/libmlx_cpu_ref.so).
+LIB = os.environ.get("MLXHIP_ORACLE_LIB") or os.path.join(HERE, "libmlx_cpu_ref.so")
+SAN_LIB = os.path.join(HERE, "_sanitize", "libmlx_cpu_ref.so")
 
 _lib = None
 _lock = threading.Lock()
 
 
-def build() -> None:
-    """Compiles the oracle with its Makefile (gcc, -ffp-contract=off)."""
-    subprocess.run(["make", "-s", "-C", HERE, "-B"], check=True)
+def build(sanitize: bool = False) -> None:
+    """Compiles the oracle with its Makefile (gcc, -ffp-contract=off); with
+    ``sanitize`` the ASan + UBSan build (clang) into oracle/_sanitize."""
+    subprocess.run(["make", "-s", "-C", HERE, "-B"] + (["sanitize"] if sanitize else []), check=True)
 
 
 def load() -> C.CDLL:

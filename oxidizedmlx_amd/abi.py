@@ -164,6 +164,7 @@ PROTOTYPES = {
     "mlxhip_last_status": (_i, []),
     "mlxhip_last_shape_mismatch": (_i, [C.POINTER(_i64), C.POINTER(_sz), C.POINTER(_i64),
                                         C.POINTER(_sz), _sz]),
+    "mlxhip_debug_fail_allocations": (_i, [_i64]),
     "mlxhip_device_count": (_i, []),
     "mlxhip_init": (_i, [_i]),
     "mlxhip_synchronize": (_i, [_vp]),

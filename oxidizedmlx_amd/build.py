@@ -17,6 +17,24 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmlxhip.so")
+# Host code built with AddressSanitizer and UndefinedBehaviorSanitizer (device
+# code unchanged). Load it with MLXHIP_LIB and the sanitizer runtime preloaded
+# (SANITIZER_RUNTIME); tests/test_sanitizers.py does so.
+SAN_BUILD = os.path.join(HERE, "_sanitize", "obj")
+SAN_LIB = os.path.join(HERE, "_sanitize", "libmlxhip.so")
+SANITIZE = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer",
+            "-Xarch_host", "-g"]
+
+
+def sanitizer_runtime() -> str:
+    """The shared ASan runtime of the ROCm clang that compiled the host code
+    (it also carries the UBSan handlers)."""
+    import glob
+    hits = sorted(glob.glob("/opt/rocm/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not hits:
+        raise RuntimeError("libclang_rt.asan-x86_64.so not found under /opt/rocm/llvm")
+    return hits[-1]
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -52,12 +70,13 @@ EXTRA = {
 }
 
 
-def _compile(src: str) -> tuple[str, float]:
+def _compile(src: str, sanitize: bool = False) -> tuple[str, float]:
     path = os.path.join(CSRC, src)
-    obj = os.path.join(BUILD, src.replace("/", "_") + ".o")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, *EXTRA.get(src, []), "-c", path, "-o", obj]
+    obj = os.path.join(SAN_BUILD if sanitize else BUILD, src.replace("/", "_") + ".o")
+    extra = SANITIZE if sanitize else []
+    cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, *extra, *EXTRA.get(src, []), "-c", path, "-o", obj]
     if src.endswith(".cpp"):
-        cmd = [HIPCC, "-x", "hip", f"--offload-arch={ARCH}", *COMMON, "-c", path, "-o", obj]
+        cmd = [HIPCC, "-x", "hip", f"--offload-arch={ARCH}", *COMMON, *extra, "-c", path, "-o", obj]
     t = time.time()
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -65,28 +84,31 @@ def _compile(src: str) -> tuple[str, float]:
     return obj, time.time() - t
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> str:
-    """Compiles every source (always, no staleness check) and links the library."""
+def build(jobs: int | None = None, verbose: bool = True, sanitize: bool = False) -> str:
+    """Compiles every source (always, no staleness check) and links the
+    library; with ``sanitize`` the host code is instrumented (ASan + UBSan)
+    and the library goes to ``_sanitize/libmlxhip.so``."""
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    os.makedirs(BUILD, exist_ok=True)
+    os.makedirs(SAN_BUILD if sanitize else BUILD, exist_ok=True)
     jobs = jobs or min(len(SOURCES), max(1, (os.cpu_count() or 4)))
     t0 = time.time()
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = []
-        for src, (obj, dt) in zip(SOURCES, ex.map(_compile, SOURCES)):
+        for src, (obj, dt) in zip(SOURCES, ex.map(lambda f: _compile(f, sanitize), SOURCES)):
             objs.append(obj)
             if verbose:
-                print(f"  compiled {src} in {dt:.1f}s", flush=True)
-    tmp = LIB + ".tmp"
+                print(f"  compiled {src}{' (sanitized host code)' if sanitize else ''} in {dt:.1f}s", flush=True)
+    lib_path = SAN_LIB if sanitize else LIB
+    tmp = lib_path + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-6000:]}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"  built {LIB} in {time.time() - t0:.1f}s", flush=True)
-    return LIB
+        print(f"  built {lib_path} in {time.time() - t0:.1f}s", flush=True)
+    return lib_path
 
 
 def clean() -> None:
@@ -96,5 +118,5 @@ def clean() -> None:
 
 
 if __name__ == "__main__":
-    build()
+    build(sanitize="--sanitize" in sys.argv[1:])
     sys.exit(0)

@@ -10,6 +10,7 @@
 #include "backend.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -146,7 +147,34 @@ size_t round_size(size_t b) {
 }
 }  // namespace
 
+namespace {
+// Successful device allocations left before every further one fails: -1 off,
+// -2 not yet read from MLXHIP_FAIL_ALLOC_AFTER.
+std::atomic<int64_t> g_alloc_budget{-2};
+}  // namespace
+
+bool forced_alloc_failure() {
+    int64_t b = g_alloc_budget.load();
+    if (b == -2) {
+        const char* e = std::getenv("MLXHIP_FAIL_ALLOC_AFTER");
+        int64_t v = -1;
+        if (e && *e) {
+            char* end = nullptr;
+            const long long n = std::strtoll(e, &end, 10);
+            if (end && *end == '\0' && n >= 0) v = n;
+        }
+        g_alloc_budget.compare_exchange_strong(b, v);
+        b = g_alloc_budget.load();
+    }
+    while (b >= 0) {
+        if (b == 0) return true;
+        if (g_alloc_budget.compare_exchange_weak(b, b - 1)) return false;
+    }
+    return false;
+}
+
 void* pool_alloc(size_t bytes) {
+    if (forced_alloc_failure()) return nullptr;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
     const size_t sz = round_size(bytes);
@@ -672,6 +700,11 @@ extern "C" {
 
 int mlxhip_abi_version(void) { return MLXHIP_ABI_VERSION; }
 
+int mlxhip_debug_fail_allocations(int64_t after) {
+    g_alloc_budget.store(after < 0 ? -1 : after);
+    return MLXHIP_OK;
+}
+
 const char* mlxhip_last_error(void) { return last_error().c_str(); }
 
 int mlxhip_last_status(void) { return t_last_status; }
@@ -745,6 +778,10 @@ int mlxhip_eval_node(const mlxhip_op_t* op, const mlxhip_input_t* inputs, size_t
 mlxhip_buffer_t* mlxhip_buffer_alloc(size_t bytes) {
     if (ensure_device() != MLXHIP_OK) return nullptr;
     void* p = nullptr;
+    if (bytes && forced_alloc_failure()) {
+        fail(MLXHIP_ERR_FFI_FAILED, "hipMalloc(%zu) failed (forced by the allocation-failure hook)", bytes);
+        return nullptr;
+    }
     if (bytes && hipMalloc(&p, bytes) != hipSuccess) {
         (void)hipGetLastError();  // not to be reported by a later launch check
         fail(MLXHIP_ERR_FFI_FAILED, "hipMalloc(%zu) failed", bytes);

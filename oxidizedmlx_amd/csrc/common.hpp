@@ -42,6 +42,12 @@ int hip_fail(hipError_t e, const char* what);
         if (rc_ != MLXHIP_OK) return rc_; \
     } while (0)
 
+// Allocation-failure hook (mlxhip_debug_fail_allocations, or the
+// environment variable MLXHIP_FAIL_ALLOC_AFTER=n read at the first device
+// allocation): true when the device allocation about to be made must fail.
+// Every device allocation of the library asks first.
+bool forced_alloc_failure();
+
 // Makes sure the calling thread has an initialised device (device 0 unless
 // mlxhip_init chose another). Returns MLXHIP_ERR_BACKEND_UNAVAILABLE without
 // a GPU.

@@ -209,6 +209,9 @@ int validate_config(const mlxhip_decoder_config_t& c) {
 
 template <class T>
 int dev_alloc(T** p, size_t count) {
+    if (forced_alloc_failure())
+        return fail(MLXHIP_ERR_FFI_FAILED, "decoder: device allocation of %zu bytes failed (forced)",
+                    std::max<size_t>(count, 1) * sizeof(T));
     MLXHIP_HIP(hipMalloc(reinterpret_cast<void**>(p), std::max<size_t>(count, 1) * sizeof(T)));
     return MLXHIP_OK;
 }

@@ -153,8 +153,7 @@ struct mlxhip_stream_t {
     // on this stream).
     int add_constant(const float* data, size_t len, const mlxhip::MetaVal& mv, bool device_src, uint64_t* id) {
         if ((int64_t)len != mv.numel())
-            return mlxhip::fail(MLXHIP_ERR_SHAPE_MISMATCH, "stream_add_constant: %zu values for %lld elements", len,
-                        (long long)mv.numel());
+            return mlxhip::fail_shape({mv.numel()}, {(int64_t)len}, "stream_add_constant");
         float* p = static_cast<float*>(mlxhip::pool_alloc((len ? len : 1) * sizeof(float)));
         if (!p) return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: device allocation failed");
         if (len && hipMemcpyAsync(p, data, len * sizeof(float),
