@@ -243,6 +243,41 @@ def test_hip_block_grads_match_oracle():
 
 
 @pytest.mark.gpu
+@pytest.mark.usefixtures("hip", "oracle_lib")
+def test_hip_block_config4_prefix_matches_oracle():
+    """Config 4 at full size (d_model 1024, 16 heads, seq 512, batch 4) on
+    the GPU against the oracle. The loss weights gy are zero except on the
+    first P positions of sequence 0, so the loss, every weight gradient and
+    the x gradient depend only on that causal prefix (attention at position i
+    sees positions <= i; the norms and the MLP act row by row): the oracle
+    runs the same block on x[0:P] with gy[0:P] (batch 1, seq P), and the GPU's
+    x gradient is exactly zero on every other row (their cotangents are zero
+    and masked attention probabilities are exactly zero)."""
+    cfg = nn.BlockConfig()
+    P = 64
+    arrs, x, gy = block_arrays(cfg, seed=31)
+    gy_masked = np.zeros_like(gy)
+    gy_masked[:P] = gy[:P]  # rows are [batch][seq]: rows 0..P-1 are sequence 0, positions 0..P-1
+    print(f"config 4 on the GPU, loss on the first {P} positions of sequence 0", flush=True)
+    loss_h, gh = block_grads(hip_stream(), cfg, arrs, x, gy_masked)
+    cfg_p = nn.BlockConfig(d_model=cfg.d_model, n_heads=cfg.n_heads, seq=P, batch=1, eps=cfg.eps)
+    print(f"oracle on the {P}-position prefix", flush=True)
+    loss_o, go = block_grads(OracleStream(), cfg_p, arrs, x[:P], gy[:P])
+    assert abs(loss_h - loss_o) <= 1e-4 * max(1.0, abs(loss_o)), (loss_h, loss_o)
+    assert not gh["x"][P:].any(), "x gradient outside the prefix is not zero"
+    gh = dict(gh, x=gh["x"][:P])
+    top = max(float(np.abs(g).max()) for g in go.values())
+    bad = []
+    for k in go:
+        scale = max(float(np.abs(go[k]).max()), 1e-3 * top)  # see the config-4 test against torch
+        err = float(np.abs(gh[k].astype(np.float64) - go[k]).max())
+        print(f"  {k}: max abs err {err:.3e} (scale {scale:.3e})", flush=True)
+        if err > 1e-4 * scale:
+            bad.append(f"{k}: max abs err {err:.3e} (scale {scale:.3e})")
+    assert not bad, "; ".join(bad)
+
+
+@pytest.mark.gpu
 @pytest.mark.usefixtures("hip")
 def test_hip_block_fusion_off_matches_on():
     from oxidizedmlx_amd.backend import HipStream

@@ -168,3 +168,21 @@ def test_config5_matches_stream_forward():
     clear, total = check_logits_and_argmax(lg, am, ref, "config 5")
     print(f"  config 5: {clear} of {total} argmax decisions with a clear margin", flush=True)
     assert clear >= total * 0.9
+
+
+def test_config5_full_size_matches_oracle():
+    """Config 5 at full size (12 layers, d_model 768, 12 heads, vocab 32000,
+    batch 8, prompt 16) for 8 new tokens, teacher-forced against the oracle's
+    mlx-nn decoder on sequences 0 and 5 (23 positions each): every logit
+    and every clear-margin argmax decision."""
+    cfg = nn.DecoderConfig()
+    P = nn.decoder_params(cfg, 77)
+    dec = HipDecoder(cfg)
+    dec.load(P)
+    prompt = np.random.default_rng(23).integers(0, cfg.vocab, size=(8, 16))
+    toks, am, lg = dec.generate(prompt, 8, argmax=True, logits=True)
+    seq = np.concatenate([prompt, toks[:, :-1]], axis=1)
+    for b in (0, 5):
+        print(f"config 5, oracle on sequence {b}", flush=True)
+        ref = oracle_logits(cfg, P, seq[b:b + 1])
+        check_logits_and_argmax(lg[b:b + 1], am[b:b + 1], ref, f"config 5 sequence {b}")
