@@ -441,25 +441,18 @@ __global__ __launch_bounds__(FIN_BLOCK) void decode_finish_kernel(
 //
 // Block = 256 threads for one (b, h). Scores s_j = (q·k_j)·scale summed over
 // the head dimension in order (as cpu_matmul_raw), softmax as
-// cpu_kernels.rs:790-806 (max, exp(x - max), sum, divide), then
-// o = sum_j p_j v_j. The cache is K^T [hd][tmax] (thread j reads column j:
-// consecutive threads, consecutive addresses) and V [tmax][hd] (a thread
-// reads float4s of a row). Every thread issues a whole chunk of its loads
-// before using any of them, so each phase costs about one memory round trip.
+// cpu_kernels.rs:790-806 (max, exp(x - max), sum, divide), o = sum_j p_j v_j.
+// The cache is K^T [hd][tmax] (thread j reads column j: consecutive threads,
+// consecutive addresses) and V [tmax][hd] (a thread reads float4s of a row).
+// The V rows of the P·V phase and the K columns of the thread's first
+// position are loaded before anything is used and q (the same for the whole
+// block) through the scalar cache, so the loads cost about one memory round
+// trip. Each wave takes exp(s_j - m_w) against its own maximum m_w and sums
+// them; one exchange of the waves' (m_w, l_w) gives the block maximum m and
+// the sum l = sum_w l_w e^(m_w - m); the P·V phase accumulates
+// e_j e^(m_w - m) v_j and divides by l at the end. Two barriers in all.
 constexpr int ATT_BLOCK = 256;
-constexpr int ATT_PART = 4 * ATT_BLOCK;  // partial sums of the P·V phase
-
-__device__ inline float block_reduce(float v, float* buf, bool is_max) {
-    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
-    v = is_max ? wave_max(v) : wave_sum(v);
-    __syncthreads();
-    if (lane == 0) buf[wave] = v;
-    __syncthreads();
-    float r = buf[0];
-#pragma unroll
-    for (int w = 1; w < ATT_BLOCK / WAVE; ++w) r = is_max ? fmaxf(r, buf[w]) : r + buf[w];
-    return r;
-}
+constexpr int ATT_WAVES = ATT_BLOCK / WAVE;
 
 template <int HD>
 __global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __restrict__ q,
@@ -468,33 +461,34 @@ __global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __r
                                                                 uint16_t* __restrict__ os, int heads,
                                                                 int tmax, float scale,
                                                                 const int* __restrict__ tctr) {
+    constexpr int C4 = HD / 4, G = ATT_BLOCK / C4, VCH = 16;
     extern __shared__ __attribute__((aligned(16))) float sm[];
-    float* s = sm;                  // [tmax]
-    float* qs = s + tmax;           // [HD]
-    float* part = qs + HD;          // [ATT_PART]
-    float* buf = part + ATT_PART;   // [ATT_BLOCK / WAVE]
+    float* s = sm;                  // [tmax] scores
+    float* part = s + ((tmax + 3) & ~3);  // [G][HD] P·V partials (16-byte aligned)
+    float* slot = part + G * HD;    // [ATT_WAVES][2] (max, sum) of each wave
     const int bh = blockIdx.x, b = bh / heads, h = bh % heads;
     const int d = heads * HD;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE;
     const float* kT = kc + (int64_t)bh * HD * tmax;
     const float* vv = vc + (int64_t)bh * tmax * HD;
+    const float* qp = q + (int64_t)b * d + h * HD;
     const int T = *tctr + 1;
-    for (int i = tid; i < HD; i += ATT_BLOCK) qs[i] = q[(int64_t)b * d + h * HD + i];
 
     // P·V mapping: thread (c, g) owns columns 4c..4c+3 over positions
-    // j = g (mod G). Its first VCH rows of V are loaded together with K.
-    constexpr int C4 = HD / 4, G = ATT_BLOCK / C4, VCH = 16;
+    // j = g (mod G). Its first VCH rows of V are loaded first. Rows past the
+    // last position load row T-1 instead (no branch around the loads, which
+    // would make the compiler wait for each one) and get probability 0.
     const int c = tid % C4, g = tid / C4;
     float4 vr[VCH];
 #pragma unroll
     for (int u = 0; u < VCH; ++u) {
-        const int j = g + u * G;
-        vr[u] = j < T ? *reinterpret_cast<const float4*>(vv + (int64_t)j * HD + 4 * c)
-                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const int j = min(g + u * G, T - 1);
+        vr[u] = *reinterpret_cast<const float4*>(vv + (int64_t)j * HD + 4 * c);
     }
-    constexpr int KCH = HD < 64 ? HD : 64;  // K loads in flight per thread
-    __syncthreads();                         // qs
 
+    // Scores of positions j = tid (mod 256), K loaded KCH values at a time.
+    constexpr int KCH = HD < 64 ? HD : 64;
+    float mloc = -INFINITY;
     for (int j = tid; j < T; j += ATT_BLOCK) {
         float acc = 0.0f;
 #pragma unroll
@@ -503,28 +497,49 @@ __global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __r
 #pragma unroll
             for (int u = 0; u < KCH; ++u) kv[u] = kT[(int64_t)(d0 + u) * tmax + j];
 #pragma unroll
-            for (int u = 0; u < KCH; ++u) acc += qs[d0 + u] * kv[u];
+            for (int u = 0; u < KCH; ++u) acc += qp[d0 + u] * kv[u];
         }
-        s[j] = acc * scale;
+        const float sc = acc * scale;
+        s[j] = sc;
+        mloc = fmaxf(mloc, sc);
     }
-    float m = -INFINITY;
-    for (int j = tid; j < T; j += ATT_BLOCK) m = fmaxf(m, s[j]);
-    m = block_reduce(m, buf, true);
-    float sum = 0.0f;
+    // e_j = exp(s_j - m_w) against the maximum m_w of the wave that owns
+    // position j (wave (j % 256) / 64), and the wave's sum l_w of them.
+    const float mw = wave_max(mloc);
+    float lloc = 0.0f;
     for (int j = tid; j < T; j += ATT_BLOCK) {
-        const float e = expf(s[j] - m);
+        const float e = expf(s[j] - mw);
         s[j] = e;
-        sum += e;
+        lloc += e;
     }
-    sum = block_reduce(sum, buf, false);
-    for (int j = tid; j < T; j += ATT_BLOCK) s[j] = s[j] / sum;
-    __syncthreads();
+    const float lw = wave_sum(lloc);
+    if (lane == 0) {
+        slot[2 * wave] = mw;
+        slot[2 * wave + 1] = lw;
+    }
+    __syncthreads();  // e_j and the waves' (max, sum)
+    // Block maximum m, factors f_w = exp(m_w - m) (0 for a wave without
+    // positions), sum l = sum_w l_w f_w.
+    float m = slot[0];
+#pragma unroll
+    for (int w = 1; w < ATT_WAVES; ++w) m = fmaxf(m, slot[2 * w]);
+    float f[ATT_WAVES], l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) {
+        f[w] = slot[2 * w] == -INFINITY ? 0.0f : expf(slot[2 * w] - m);
+        l += slot[2 * w + 1] * f[w];
+    }
+    static_assert(ATT_WAVES == 4, "factor select below");
+    auto prob = [&](int j) {
+        const int w = (j >> 6) & 3;
+        const float fw = w == 0 ? f[0] : (w == 1 ? f[1] : (w == 2 ? f[2] : f[3]));
+        return j < T ? s[j] * fw : 0.0f;
+    };
 
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int u = 0; u < VCH; ++u) {
-        const int j = g + u * G;
-        const float pj = j < T ? s[j] : 0.0f;
+        const float pj = prob(g + u * G);
         acc.x += pj * vr[u].x;
         acc.y += pj * vr[u].y;
         acc.z += pj * vr[u].z;
@@ -533,14 +548,12 @@ __global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __r
     for (int j0 = g + VCH * G; j0 < T; j0 += G * VCH) {
 #pragma unroll
         for (int u = 0; u < VCH; ++u) {
-            const int j = j0 + u * G;
-            vr[u] = j < T ? *reinterpret_cast<const float4*>(vv + (int64_t)j * HD + 4 * c)
-                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const int j = min(j0 + u * G, T - 1);
+            vr[u] = *reinterpret_cast<const float4*>(vv + (int64_t)j * HD + 4 * c);
         }
 #pragma unroll
         for (int u = 0; u < VCH; ++u) {
-            const int j = j0 + u * G;
-            const float pj = j < T ? s[j] : 0.0f;
+            const float pj = prob(j0 + u * G);
             acc.x += pj * vr[u].x;
             acc.y += pj * vr[u].y;
             acc.z += pj * vr[u].z;
@@ -552,7 +565,7 @@ __global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __r
     if (tid < HD) {
         float r = part[tid];
         for (int gg = 1; gg < G; ++gg) r += part[gg * HD + tid];
-        store_split(os, d, b, h * HD + tid, r);
+        store_split(os, d, b, h * HD + tid, r / l);
     }
 }
 
@@ -672,7 +685,8 @@ int dec_gemv(int epi, bool norm, const DecGemv& p, hipStream_t s) {
 }
 
 size_t dec_attn_lds_bytes(int hd, int tmax) {
-    return ((size_t)tmax + hd + ATT_PART + ATT_BLOCK / WAVE) * sizeof(float);
+    const size_t g = ATT_BLOCK / (hd / 4);  // P·V position groups
+    return ((size_t)ceil_div(tmax, 4) * 4 + g * hd + 2 * ATT_WAVES) * sizeof(float);
 }
 
 int dec_attention(const float* q, const float* kc, const float* vc, uint16_t* os, int batch, int heads, int hd,
