@@ -254,6 +254,17 @@ uint64_t mlxhip_stream_launch_count(const mlxhip_stream_t* s);
 /* Enables (1, default) or disables (0) look-ahead fusion of single-consumer
  * elementwise chains and of Transpose into MatMul operand layouts. */
 int mlxhip_stream_set_fusion(mlxhip_stream_t* s, int enabled);
+/* Asynchronous evaluation (0 = off, the default): eval and eval_many return
+ * once the stream's kernels are enqueued instead of after they finish, so
+ * the caller can build its next graph while the GPU works. Results are the
+ * same bit for bit. get_buffer, mlxhip_stream_synchronize and stream_free
+ * wait for the work; an error a kernel meets after its launch is reported
+ * there. No reference counterpart: the reference's Stream::eval returns
+ * computed values (backend.rs:85-159); a caller that only reads results
+ * through get_buffer sees the same values. Turning it off synchronizes. */
+int mlxhip_stream_set_async(mlxhip_stream_t* s, int enabled);
+/* Waits for every kernel of the stream (see mlxhip_stream_set_async). */
+int mlxhip_stream_synchronize(mlxhip_stream_t* s);
 /* Stream::eval over several outputs at once (Graph::topo_sort takes a slice
  * of outputs, crates/mlx-core/src/graph.rs:268-294): one topological order
  * and one fusion plan for all of them, one synchronisation at the end. Every
@@ -261,7 +272,8 @@ int mlxhip_stream_set_fusion(mlxhip_stream_t* s, int enabled);
 int mlxhip_stream_eval_many(mlxhip_stream_t* s, const uint64_t* nodes, size_t n);
 /* As mlxhip_stream_add_constant with `data` a device address: the values are
  * copied device-to-device on the stream's queue, so `data` must stay
- * unchanged until the next mlxhip_stream_eval* call on `s` returns. No
+ * unchanged until the next mlxhip_stream_eval* call on `s` returns (with
+ * asynchronous evaluation: until the stream is next synchronized). No
  * reference counterpart (the reference's constants always come from host
  * vectors, backend.rs:59-71); for callers whose inputs already live in HBM. */
 uint64_t mlxhip_stream_add_constant_dev(mlxhip_stream_t* s, const float* data, size_t len,

@@ -60,7 +60,7 @@ class HipBackend:
 class HipStream:
     """Stream bound to mlx-hip: lazy graph, CSE, memoised HBM-resident buffers."""
 
-    def __init__(self, fusion: bool = True):
+    def __init__(self, fusion: bool = True, async_eval: bool = False):
         L = lib()
         self._L = L
         self._s = L.mlxhip_stream_new()
@@ -69,6 +69,8 @@ class HipStream:
         self.metas: dict[int, TensorMeta] = {}
         if not fusion:
             self.set_fusion(False)
+        if async_eval:
+            self.set_async(True)
 
     def close(self) -> None:
         if getattr(self, "_s", None):
@@ -80,6 +82,14 @@ class HipStream:
 
     def set_fusion(self, enabled: bool) -> None:
         abi.check(self._L.mlxhip_stream_set_fusion(self._s, 1 if enabled else 0), self._L)
+
+    def set_async(self, enabled: bool) -> None:
+        """Asynchronous evaluation: eval returns once the kernels are queued;
+        get_buffer / synchronize / close wait for them."""
+        abi.check(self._L.mlxhip_stream_set_async(self._s, 1 if enabled else 0), self._L)
+
+    def synchronize(self) -> None:
+        abi.check(self._L.mlxhip_stream_synchronize(self._s), self._L)
 
     def add_constant(self, data, m: TensorMeta) -> int:
         d = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)

@@ -321,7 +321,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             eval_calls += nodes_in_chain.size();
             launches += 1;
             if (rc != MLXHIP_OK) {
-                pool_release(out);
+                release_later(out);
                 buffers.erase(id);
                 break;
             }
@@ -371,12 +371,17 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         launches += 1;
         rc = eval_node_device(op, ins.data(), ins.size(), meta, out, hs, scratch, hint);
         if (rc != MLXHIP_OK) {
-            pool_release(out);
+            release_later(out);
             buffers.erase(id);
             break;
         }
     }
     // Scratch may only return to the pool after the kernels using it finish.
+    if (async_eval) {
+        pending.insert(pending.end(), scratch.blocks.begin(), scratch.blocks.end());
+        scratch.blocks.clear();
+        return rc;
+    }
     hipError_t e = hipStreamSynchronize(hs);
     if (rc == MLXHIP_OK && e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
     return rc;
@@ -474,8 +479,7 @@ int mlxhip_stream_get_buffer(mlxhip_stream_t* s, uint64_t node, float* out, size
     if (!len) return MLXHIP_OK;
     MLXHIP_HIP(hipSetDevice(s->device));
     MLXHIP_HIP(hipMemcpyAsync(out, it->second.ptr, len * sizeof(float), hipMemcpyDeviceToHost, s->hs));
-    MLXHIP_HIP(hipStreamSynchronize(s->hs));
-    return MLXHIP_OK;
+    return s->drain();
 }
 
 uint64_t mlxhip_stream_eval_count(const mlxhip_stream_t* s) { return s ? s->eval_calls.load() : 0; }
@@ -488,6 +492,22 @@ size_t mlxhip_stream_cache_len(const mlxhip_stream_t* s) {
 }
 
 uint64_t mlxhip_stream_launch_count(const mlxhip_stream_t* s) { return s ? s->launches.load() : 0; }
+
+int mlxhip_stream_set_async(mlxhip_stream_t* s, int enabled) {
+    if (!s) return fail(MLXHIP_ERR_NULL_PTR, "stream_set_async: null stream");
+    std::lock_guard<std::mutex> g(s->mu);
+    MLXHIP_HIP(hipSetDevice(s->device));
+    if (!enabled && s->async_eval) MLXHIP_TRY(s->drain());
+    s->async_eval = enabled != 0;
+    return MLXHIP_OK;
+}
+
+int mlxhip_stream_synchronize(mlxhip_stream_t* s) {
+    if (!s) return fail(MLXHIP_ERR_NULL_PTR, "stream_synchronize: null stream");
+    std::lock_guard<std::mutex> g(s->mu);
+    MLXHIP_HIP(hipSetDevice(s->device));
+    return s->drain();
+}
 
 int mlxhip_stream_set_fusion(mlxhip_stream_t* s, int enabled) {
     if (!s) return fail(MLXHIP_ERR_NULL_PTR, "stream_set_fusion: null stream");

@@ -78,14 +78,37 @@ struct mlxhip_stream_t {
     std::atomic<uint64_t> eval_calls{0};
     std::atomic<uint64_t> launches{0};
     bool fusion = true;
+    // Asynchronous evaluation (mlxhip_stream_set_async): eval returns once
+    // its kernels are enqueued; blocks its kernels may still use wait in
+    // `pending` until the stream drains (get_buffer, synchronize, free).
+    bool async_eval = false;
+    std::vector<void*> pending;
     hipStream_t hs = nullptr;
     int device = 0;
 
     ~mlxhip_stream_t() {
         if (hs) (void)hipStreamSynchronize(hs);
+        for (void* p : pending) mlxhip::pool_release(p);
         for (auto& kv : buffers)
             if (kv.second.owned) mlxhip::pool_release(kv.second.ptr);
         if (hs) (void)hipStreamDestroy(hs);
+    }
+
+    // Waits for every kernel of this stream, then returns the blocks of
+    // earlier asynchronous evaluations to the pool.
+    int drain() {
+        const hipError_t e = hipStreamSynchronize(hs);
+        for (void* p : pending) mlxhip::pool_release(p);
+        pending.clear();
+        return e == hipSuccess ? MLXHIP_OK : mlxhip::hip_fail(e, "hipStreamSynchronize");
+    }
+
+    // A block a kernel of this stream may still use goes back to the pool
+    // now (synchronous evaluation: the stream is drained before eval
+    // returns) or when the stream drains.
+    void release_later(void* p) {
+        if (async_eval) pending.push_back(p);
+        else mlxhip::pool_release(p);
     }
 
     uint64_t add_node(const mlxhip::OpVal& op, std::vector<uint64_t> inputs, const mlxhip::MetaVal& meta, bool cse_ok) {
@@ -156,13 +179,22 @@ struct mlxhip_stream_t {
             return mlxhip::fail_shape({mv.numel()}, {(int64_t)len}, "stream_add_constant");
         float* p = static_cast<float*>(mlxhip::pool_alloc((len ? len : 1) * sizeof(float)));
         if (!p) return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: device allocation failed");
-        if (len && hipMemcpyAsync(p, data, len * sizeof(float),
-                                  device_src ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, hs) != hipSuccess) {
-            mlxhip::pool_release(p);
-            return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: copy failed");
+        // Device data: copied on this stream, ordered before its later kernels.
+        // Host data (which the caller may free as soon as the call returns):
+        // copied by a blocking hipMemcpy, which does not wait for this
+        // (non-blocking) stream's queued work. The block is fresh from the
+        // pool, where blocks only return once no kernel uses them, so nothing
+        // queued touches it, and the kernels that read it are enqueued after
+        // the copy has finished.
+        if (len) {
+            const hipError_t e = device_src ? hipMemcpyAsync(p, data, len * sizeof(float), hipMemcpyDeviceToDevice, hs)
+                                            : hipMemcpy(p, data, len * sizeof(float), hipMemcpyHostToDevice);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                mlxhip::pool_release(p);
+                return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: copy failed");
+            }
         }
-        // Host data may be freed by the caller right after the call returns.
-        if (!device_src && len) (void)hipStreamSynchronize(hs);
         mlxhip_op_t op{};
         op.kind = MLXHIP_OP_CONSTANT;
         *id = add_node(mlxhip::OpVal::from(op), {}, mv, false);

@@ -279,6 +279,33 @@ def test_hip_block_config4_prefix_matches_oracle():
 
 @pytest.mark.gpu
 @pytest.mark.usefixtures("hip")
+def test_hip_block_async_eval_matches_sync():
+    """Asynchronous evaluation (mlxhip_stream_set_async) changes no result:
+    three block steps queued on one asynchronous stream without reading
+    anything in between (each step's host constants copied while earlier
+    steps still run), then every gradient of every step read, bit for bit
+    against a synchronous stream."""
+    from oxidizedmlx_amd.backend import HipStream
+    arrs, x, gy = block_arrays(SMALL, seed=13)
+    _, want = block_grads(HipStream(), SMALL, arrs, x, gy)
+    st = HipStream(async_eval=True)
+    steps = []
+    for _ in range(3):
+        loss, params, xt = block_loss(st, SMALL, arrs, x, gy)
+        names = list(params)
+        _, gs = value_and_grad(loss, [params[k] for k in names] + [xt])
+        st.eval_many([g.node for g in gs])
+        steps.append(dict(zip(names + ["x"], gs)))
+    for got in steps:
+        for k, g in got.items():
+            np.testing.assert_array_equal(g.to_numpy(), want[k], err_msg=k)
+    st.synchronize()
+    st.set_async(False)
+    st.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip")
 def test_hip_block_fusion_off_matches_on():
     from oxidizedmlx_amd.backend import HipStream
     arrs, x, gy = block_arrays(SMALL, seed=11)

@@ -439,3 +439,36 @@ def test_transpose_rewrites_match_unfused(fusion):
         res.append([s.get_buffer(t) for t in (y, dx, dw)])
     for got, want in zip(*res):
         assert_allclose(got, want, 1e-5, 1e-5, "transpose rewrites")
+
+
+def test_async_eval_stream_semantics():
+    """mlxhip_stream_set_async: evaluations return before their kernels
+    finish; a host constant added while kernels still run, a chain of
+    evaluations that read each other's results, get_buffer (which waits),
+    synchronize and turning the mode off all give the synchronous values."""
+    rng = np.random.default_rng(21)
+    a = rng.standard_normal((256, 384)).astype(np.float32)
+    b = rng.standard_normal((384, 128)).astype(np.float32)
+    c = rng.standard_normal((256, 128)).astype(np.float32)
+
+    def run(asyn):
+        s = HipStream(async_eval=asyn)
+        ai = s.add_constant(a, meta([256, 384]))
+        bi = s.add_constant(b, meta([384, 128]))
+        mm = s.add_op(OpKind.MatMul, [ai, bi], meta([256, 128]))
+        s.eval(mm)
+        ci = s.add_constant(c, meta([256, 128]))  # copied while the GEMM may still run
+        sm = s.add_op(OpKind.Softmax(1), [mm], meta([256, 128]))
+        out = s.add_op(OpKind.Add, [sm, ci], meta([256, 128]))
+        s.eval(out)
+        second = s.add_op(OpKind.Mul, [out, mm], meta([256, 128]))
+        s.eval_many([second])
+        res = [s.get_buffer(n) for n in (mm, out, second)]
+        if asyn:
+            s.synchronize()
+            s.set_async(False)
+        s.close()
+        return res
+
+    for x, y in zip(run(False), run(True)):
+        np.testing.assert_array_equal(x, y)
