@@ -261,8 +261,8 @@ def main() -> int:
     # asynchronous stream (mlxhip_stream_set_async): eval_many returns once a
     # step's kernels are queued, so the host builds the next step's graph
     # while the GPU runs this one; the kernels still run one after another on
-    # one queue. Every 16 steps the stream is closed (which waits for its work
-    # and frees its buffers) and replaced, so HBM use stays bounded.
+    # one queue. After its eval a step's nodes are cleared (mlxhip_stream_clear):
+    # the next step's buffers reuse their HBM in queue order.
     from oxidizedmlx_amd import nn as mnn
     bcfg = mnn.BlockConfig()
     blk_host = {name: synth.normal(0x5EED0100 + i, shp, 0.0, 0.02)
@@ -272,22 +272,20 @@ def main() -> int:
     blk_dev = {k: hb.DeviceBuffer.from_array(v) for k, v in blk_host.items()}
     del blk_host
 
-    blk = {"stream": None, "steps": 0}
+    blk = {"stream": None}
 
     def block_step() -> None:
         from oxidizedmlx_amd.tensor import Tensor, value_and_grad
-        if blk["stream"] is None or blk["steps"] == 16:
-            if blk["stream"] is not None:
-                blk["stream"].close()
-            blk["stream"], blk["steps"] = hb.HipStream(async_eval=True), 0
+        if blk["stream"] is None:
+            blk["stream"] = hb.HipStream(async_eval=True)
         st = blk["stream"]
-        blk["steps"] += 1
         t = {k: Tensor.from_device(b.ptr, (bcfg.rows, bcfg.d_model) if k in ("x", "gy")
                                    else bcfg.param_shapes()[k], st) for k, b in blk_dev.items()}
         params = {k: t[k] for k in bcfg.param_shapes()}
         loss = mnn.TransformerBlock(bcfg, params)(t["x"]).mul(t["gy"]).sum_all()
         _, grads = value_and_grad(loss, list(params.values()) + [t["x"]])
         st.eval_many([g.node for g in grads])
+        st.clear()
 
     # Config 5: greedy decoding with a 12-layer decoder (d_model 768, 12
     # heads, vocab 32000, 4x SiLU MLP), bf16 weights N(0, 0.02^2), batch 8,

@@ -265,6 +265,14 @@ int mlxhip_stream_set_fusion(mlxhip_stream_t* s, int enabled);
 int mlxhip_stream_set_async(mlxhip_stream_t* s, int enabled);
 /* Waits for every kernel of the stream (see mlxhip_stream_set_async). */
 int mlxhip_stream_synchronize(mlxhip_stream_t* s);
+/* Forgets every node of the stream, as if it were new (node ids are not
+ * reused; using an old one is MLXHIP_ERR_INVALID_ARGUMENT). Their HBM
+ * returns to the library: with asynchronous evaluation the stream's later
+ * work may reuse it at once, in queue order, without waiting for the
+ * kernels already queued. No reference counterpart (a reference Stream keeps
+ * every node until it is dropped, backend.rs:37-185); for a loop that builds
+ * a new graph every step on one stream. */
+int mlxhip_stream_clear(mlxhip_stream_t* s);
 /* Stream::eval over several outputs at once (Graph::topo_sort takes a slice
  * of outputs, crates/mlx-core/src/graph.rs:268-294): one topological order
  * and one fusion plan for all of them, one synchronisation at the end. Every

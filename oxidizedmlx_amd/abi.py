@@ -191,6 +191,7 @@ PROTOTYPES = {
     "mlxhip_stream_set_fusion": (_i, [_vp, _i]),
     "mlxhip_stream_set_async": (_i, [_vp, _i]),
     "mlxhip_stream_synchronize": (_i, [_vp]),
+    "mlxhip_stream_clear": (_i, [_vp]),
     "mlxhip_stream_eval_many": (_i, [_vp, C.POINTER(_u64), _sz]),
     "mlxhip_stream_add_constant_dev": (_u64, [_vp, _vp, _sz, C.POINTER(mlxhip_meta_t)]),
     "mlxhip_stream_grad": (_i, [_vp, _u64, C.POINTER(_u64), _sz, C.POINTER(_u64)]),

@@ -91,6 +91,12 @@ class HipStream:
     def synchronize(self) -> None:
         abi.check(self._L.mlxhip_stream_synchronize(self._s), self._L)
 
+    def clear(self) -> None:
+        """Forgets every node (their HBM is reused by this stream's later
+        work); node ids handed out before are no longer valid."""
+        abi.check(self._L.mlxhip_stream_clear(self._s), self._L)
+        self.metas.clear()
+
     def add_constant(self, data, m: TensorMeta) -> int:
         d = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
         cm, keep = m.to_c()

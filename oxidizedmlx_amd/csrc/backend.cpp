@@ -220,6 +220,15 @@ void* pool_alloc(size_t bytes) {
     return p;
 }
 
+size_t pool_round(size_t bytes) { return round_size(bytes); }
+
+size_t pool_block_size(void* p) {
+    Pool& P = pool();
+    std::lock_guard<std::mutex> g(P.mu);
+    auto it = P.owned.find(p);
+    return it == P.owned.end() ? 0 : it->second.second;
+}
+
 void pool_release(void* p) {
     if (!p) return;
     Pool& P = pool();

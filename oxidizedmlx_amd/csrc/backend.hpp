@@ -18,6 +18,10 @@ namespace mlxhip {
 // synchronise their stream first).
 void* pool_alloc(size_t bytes);
 void pool_release(void* p);
+// The size pool_alloc rounds a request of `bytes` to, and the size of a block
+// it handed out (0 for a pointer it does not own).
+size_t pool_round(size_t bytes);
+size_t pool_block_size(void* p);
 
 // Temporary device buffers of one node evaluation, handed back to the pool
 // by the owner after its stream has been synchronised.

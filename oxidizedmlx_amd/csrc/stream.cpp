@@ -378,7 +378,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     }
     // Scratch may only return to the pool after the kernels using it finish.
     if (async_eval) {
-        pending.insert(pending.end(), scratch.blocks.begin(), scratch.blocks.end());
+        for (void* p : scratch.blocks) release_later(p);
         scratch.blocks.clear();
         return rc;
     }
@@ -500,6 +500,13 @@ int mlxhip_stream_set_async(mlxhip_stream_t* s, int enabled) {
     if (!enabled && s->async_eval) MLXHIP_TRY(s->drain());
     s->async_eval = enabled != 0;
     return MLXHIP_OK;
+}
+
+int mlxhip_stream_clear(mlxhip_stream_t* s) {
+    if (!s) return fail(MLXHIP_ERR_NULL_PTR, "stream_clear: null stream");
+    std::lock_guard<std::mutex> g(s->mu);
+    MLXHIP_HIP(hipSetDevice(s->device));
+    return s->clear();
 }
 
 int mlxhip_stream_synchronize(mlxhip_stream_t* s) {

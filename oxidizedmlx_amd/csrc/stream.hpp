@@ -79,16 +79,18 @@ struct mlxhip_stream_t {
     std::atomic<uint64_t> launches{0};
     bool fusion = true;
     // Asynchronous evaluation (mlxhip_stream_set_async): eval returns once
-    // its kernels are enqueued; blocks its kernels may still use wait in
-    // `pending` until the stream drains (get_buffer, synchronize, free).
+    // its kernels are enqueued. Blocks released while queued kernels may
+    // still use them wait in `pending` (size, block) until the stream drains
+    // (get_buffer, synchronize, free); meanwhile later work of this stream may
+    // take them at once (stream_alloc), since the stream runs in order.
     bool async_eval = false;
-    std::vector<void*> pending;
+    std::vector<std::pair<size_t, void*>> pending;
     hipStream_t hs = nullptr;
     int device = 0;
 
     ~mlxhip_stream_t() {
         if (hs) (void)hipStreamSynchronize(hs);
-        for (void* p : pending) mlxhip::pool_release(p);
+        for (auto& b : pending) mlxhip::pool_release(b.second);
         for (auto& kv : buffers)
             if (kv.second.owned) mlxhip::pool_release(kv.second.ptr);
         if (hs) (void)hipStreamDestroy(hs);
@@ -98,7 +100,7 @@ struct mlxhip_stream_t {
     // earlier asynchronous evaluations to the pool.
     int drain() {
         const hipError_t e = hipStreamSynchronize(hs);
-        for (void* p : pending) mlxhip::pool_release(p);
+        for (auto& b : pending) mlxhip::pool_release(b.second);
         pending.clear();
         return e == hipSuccess ? MLXHIP_OK : mlxhip::hip_fail(e, "hipStreamSynchronize");
     }
@@ -107,8 +109,48 @@ struct mlxhip_stream_t {
     // now (synchronous evaluation: the stream is drained before eval
     // returns) or when the stream drains.
     void release_later(void* p) {
-        if (async_eval) pending.push_back(p);
+        if (async_eval) pending.emplace_back(mlxhip::pool_block_size(p), p);
         else mlxhip::pool_release(p);
+    }
+
+    // A block for memory that only this stream's queue writes and reads: a
+    // pending block of fitting size (the smallest in [size, 1.5 size], as the
+    // pool chooses) if there is one, else one from the pool.
+    void* stream_alloc(size_t bytes) {
+        const size_t sz = mlxhip::pool_round(bytes);
+        size_t best = 0;
+        bool found = false;
+        for (size_t i = 0; i < pending.size(); ++i) {
+            const size_t b = pending[i].first;
+            if (b >= sz && b <= sz + sz / 2 && (!found || b < pending[best].first)) {
+                best = i;
+                found = true;
+            }
+        }
+        if (found) {
+            void* p = pending[best].second;
+            pending[best] = pending.back();
+            pending.pop_back();
+            return p;
+        }
+        return mlxhip::pool_alloc(bytes);
+    }
+
+    // Forgets every node (mlxhip_stream_clear); their blocks go back through
+    // release_later. Node ids are never reused.
+    int clear() {
+        if (!async_eval) {
+            // Queued device-to-device constant copies may still write them.
+            const hipError_t e = hipStreamSynchronize(hs);
+            if (e != hipSuccess) return mlxhip::hip_fail(e, "hipStreamSynchronize");
+        }
+        for (auto& kv : buffers)
+            if (kv.second.owned) release_later(kv.second.ptr);
+        buffers.clear();
+        nodes.clear();
+        cse.clear();
+        consumers.clear();
+        return MLXHIP_OK;
     }
 
     uint64_t add_node(const mlxhip::OpVal& op, std::vector<uint64_t> inputs, const mlxhip::MetaVal& meta, bool cse_ok) {
@@ -177,7 +219,11 @@ struct mlxhip_stream_t {
     int add_constant(const float* data, size_t len, const mlxhip::MetaVal& mv, bool device_src, uint64_t* id) {
         if ((int64_t)len != mv.numel())
             return mlxhip::fail_shape({mv.numel()}, {(int64_t)len}, "stream_add_constant");
-        float* p = static_cast<float*>(mlxhip::pool_alloc((len ? len : 1) * sizeof(float)));
+        // Device data is copied on this stream's queue, so the block may be
+        // one the stream still has queued work on; host data is copied
+        // outside the queue and needs a block no queued kernel uses.
+        const size_t bytes = (len ? len : 1) * sizeof(float);
+        float* p = static_cast<float*>(device_src ? stream_alloc(bytes) : mlxhip::pool_alloc(bytes));
         if (!p) return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: device allocation failed");
         // Device data: copied on this stream, ordered before its later kernels.
         // Host data (which the caller may free as soon as the call returns):
@@ -191,7 +237,7 @@ struct mlxhip_stream_t {
                                             : hipMemcpy(p, data, len * sizeof(float), hipMemcpyHostToDevice);
             if (e != hipSuccess) {
                 (void)hipGetLastError();
-                mlxhip::pool_release(p);
+                release_later(p);
                 return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream_add_constant: copy failed");
             }
         }
@@ -205,7 +251,7 @@ struct mlxhip_stream_t {
     int alloc_out(uint64_t id, float** out) {
         const mlxhip::Node& n = nodes.at(id);
         const size_t len = (size_t)n.meta.numel();
-        float* p = static_cast<float*>(mlxhip::pool_alloc((len ? len : 1) * sizeof(float)));
+        float* p = static_cast<float*>(stream_alloc((len ? len : 1) * sizeof(float)));
         if (!p) return mlxhip::fail(MLXHIP_ERR_FFI_FAILED, "stream: device allocation of %zu floats failed", len);
         buffers[id] = mlxhip::DevBuf{p, len};
         *out = p;

@@ -306,6 +306,34 @@ def test_hip_block_async_eval_matches_sync():
 
 @pytest.mark.gpu
 @pytest.mark.usefixtures("hip")
+def test_hip_block_steps_with_clear_reuse_memory():
+    """Block steps on one asynchronous stream, each cleared after its eval
+    (mlxhip_stream_clear) so the next step's buffers reuse its HBM while its
+    kernels may still be queued: four steps queued back to back, then the
+    last one's gradients read, bit for bit against a synchronous stream; an
+    old node id is rejected after a clear."""
+    from oxidizedmlx_amd.backend import HipStream
+    arrs, x, gy = block_arrays(SMALL, seed=17)
+    _, want = block_grads(HipStream(), SMALL, arrs, x, gy)
+    st = HipStream(async_eval=True)
+    for step in range(4):
+        loss, params, xt = block_loss(st, SMALL, arrs, x, gy)
+        names = list(params)
+        _, gs = value_and_grad(loss, [params[k] for k in names] + [xt])
+        st.eval_many([g.node for g in gs])
+        if step < 3:
+            old = gs[0].node
+            st.clear()
+    got = {k: g.to_numpy() for k, g in zip(names + ["x"], gs)}
+    for k in want:
+        np.testing.assert_array_equal(got[k], want[k], err_msg=k)
+    with pytest.raises(abi.InvalidArgument):
+        st.eval(old)
+    st.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip")
 def test_hip_block_fusion_off_matches_on():
     from oxidizedmlx_amd.backend import HipStream
     arrs, x, gy = block_arrays(SMALL, seed=11)
