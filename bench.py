@@ -256,7 +256,7 @@ def main() -> int:
     # seq 512, batch 4, 4x SiLU MLP), f32, forward and backward through the
     # Stream's autograd. Weights N(0, 0.02^2), x N(0, 1); the loss is
     # sum(block(x) * gy) with gy N(0, 1). Inputs stay in HBM; each step builds
-    # the whole graph again from them (device-to-device constants), runs the
+    # the whole graph again from them (constants that read them in place), runs the
     # autograd and evaluates every gradient. Consecutive steps share one
     # asynchronous stream (mlxhip_stream_set_async): eval_many returns once a
     # step's kernels are queued, so the host builds the next step's graph
@@ -279,7 +279,7 @@ def main() -> int:
         if blk["stream"] is None:
             blk["stream"] = hb.HipStream(async_eval=True)
         st = blk["stream"]
-        t = {k: Tensor.from_device(b.ptr, (bcfg.rows, bcfg.d_model) if k in ("x", "gy")
+        t = {k: Tensor.view_device(b.ptr, (bcfg.rows, bcfg.d_model) if k in ("x", "gy")
                                    else bcfg.param_shapes()[k], st) for k, b in blk_dev.items()}
         params = {k: t[k] for k in bcfg.param_shapes()}
         loss = mnn.TransformerBlock(bcfg, params)(t["x"]).mul(t["gy"]).sum_all()

@@ -286,6 +286,14 @@ int mlxhip_stream_eval_many(mlxhip_stream_t* s, const uint64_t* nodes, size_t n)
  * vectors, backend.rs:59-71); for callers whose inputs already live in HBM. */
 uint64_t mlxhip_stream_add_constant_dev(mlxhip_stream_t* s, const float* data, size_t len,
                                         const mlxhip_meta_t* meta);
+/* As mlxhip_stream_add_constant_dev without the copy: the node reads `data`
+ * (256-byte-aligned device memory of the caller) in place, so `data` must
+ * stay valid and unchanged for as long as the node exists (until the stream
+ * is cleared or freed); the stream never writes or frees it. No reference
+ * counterpart; for inputs that already live in HBM, such as a model's
+ * weights read by every step. */
+uint64_t mlxhip_stream_add_constant_view(mlxhip_stream_t* s, const float* data, size_t len,
+                                         const mlxhip_meta_t* meta);
 /* value_and_grad / backward (crates/mlx-autograd/src/lib.rs:30-107) with the
  * VJP table of crates/mlx-autograd/src/vjp.rs:8-178: `loss` must have one
  * element (else MLXHIP_ERR_INVALID_ARGUMENT "grad requires scalar loss"); it

@@ -194,6 +194,7 @@ PROTOTYPES = {
     "mlxhip_stream_clear": (_i, [_vp]),
     "mlxhip_stream_eval_many": (_i, [_vp, C.POINTER(_u64), _sz]),
     "mlxhip_stream_add_constant_dev": (_u64, [_vp, _vp, _sz, C.POINTER(mlxhip_meta_t)]),
+    "mlxhip_stream_add_constant_view": (_u64, [_vp, _vp, _sz, C.POINTER(mlxhip_meta_t)]),
     "mlxhip_stream_grad": (_i, [_vp, _u64, C.POINTER(_u64), _sz, C.POINTER(_u64)]),
     "mlxhip_gemm": (_i, [_i32, _i32, _i32, _i32, _i64, _i64, _i64, _i64,
                          _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp]),

@@ -133,6 +133,17 @@ class HipStream:
         self.metas[nid] = m
         return nid
 
+    def add_constant_view(self, ptr: int, m: TensorMeta) -> int:
+        """Constant that reads numel(m) floats at device address ``ptr``
+        (256-byte aligned) in place; the memory must stay valid and unchanged
+        while the node exists (until clear / close)."""
+        cm, keep = m.to_c()
+        nid = self._L.mlxhip_stream_add_constant_view(self._s, ptr, m.numel(), C.byref(cm))
+        if nid == 0:
+            abi.check(self._L.mlxhip_last_status() or abi.ERR_FFI_FAILED, self._L)
+        self.metas[nid] = m
+        return nid
+
     def grad(self, loss: int, wrt: Sequence[int]) -> list[int]:
         """value_and_grad's backward pass (mlx-autograd lib.rs:30-107) for
         several wrt nodes: returns the (unevaluated) gradient node ids."""

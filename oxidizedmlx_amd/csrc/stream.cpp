@@ -136,9 +136,11 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     std::unordered_map<uint64_t, std::vector<uint64_t>> chain_of;   // chain end -> nodes
     std::unordered_map<uint64_t, int> acc_input;                    // node -> index of its acc input
     std::unordered_set<uint64_t> interior;                          // fused, not materialised
-    // Broadcasts that only tile their source and whose every consumer is an
-    // elementwise node of this evaluation: the chain kernel reads the source
-    // periodically and the broadcast is never materialised.
+    // Broadcasts that only tile their source and whose every consumer in this
+    // evaluation is elementwise: the chain kernel reads the source
+    // periodically and the broadcast is not materialised. (A consumer already
+    // evaluated needs nothing more; one evaluated later finds no buffer and
+    // plans the broadcast again.)
     std::unordered_map<uint64_t, int64_t> virtual_bcast;            // node -> period (elements)
     if (fusion) {
         std::unordered_map<uint64_t, std::vector<uint64_t>> users;
@@ -151,7 +153,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             const int64_t per = tiling_period(nodes.at(n.inputs[0]).meta.shape, n.meta.shape);
             if (per <= 0 || per != nodes.at(n.inputs[0]).meta.numel()) continue;
             const std::vector<uint64_t>& u = users[id];
-            if (u.empty() || u.size() != consumers[id]) continue;
+            if (u.empty()) continue;
             bool ok = true;
             for (uint64_t c : u) {
                 const Node& cn = nodes.at(c);
@@ -432,6 +434,22 @@ static uint64_t add_constant(mlxhip_stream_t* s, const float* data, size_t len, 
 
 uint64_t mlxhip_stream_add_constant(mlxhip_stream_t* s, const float* data, size_t len, const mlxhip_meta_t* meta) {
     return add_constant(s, data, len, meta, false);
+}
+
+uint64_t mlxhip_stream_add_constant_view(mlxhip_stream_t* s, const float* data, size_t len,
+                                         const mlxhip_meta_t* meta) {
+    if (!s || !meta || (len && !data)) {
+        fail(MLXHIP_ERR_NULL_PTR, "stream_add_constant_view: null argument");
+        return 0;
+    }
+    if (meta->ndim && !meta->shape) {
+        fail(MLXHIP_ERR_NULL_PTR, "stream_add_constant_view: null shape");
+        return 0;
+    }
+    std::lock_guard<std::mutex> g(s->mu);
+    uint64_t id = 0;
+    if (s->add_constant_view(data, len, meta_from(meta), &id) != MLXHIP_OK) return 0;
+    return id;
 }
 
 uint64_t mlxhip_stream_add_constant_dev(mlxhip_stream_t* s, const float* data, size_t len,

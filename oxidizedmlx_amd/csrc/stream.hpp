@@ -248,6 +248,21 @@ struct mlxhip_stream_t {
         return MLXHIP_OK;
     }
 
+    // A Constant node that reads `data`, device memory the caller owns, in
+    // place (no copy; the node does not own the memory, so clear and free
+    // leave it alone). Kernels only ever read a node's inputs.
+    int add_constant_view(const float* data, size_t len, const mlxhip::MetaVal& mv, uint64_t* id) {
+        if ((int64_t)len != mv.numel()) return mlxhip::fail_shape({mv.numel()}, {(int64_t)len}, "stream_add_constant_view");
+        if (reinterpret_cast<uintptr_t>(data) % 256)
+            return mlxhip::fail(MLXHIP_ERR_INVALID_ARGUMENT,
+                                "stream_add_constant_view: data must be 256-byte aligned (as pool blocks are)");
+        mlxhip_op_t op{};
+        op.kind = MLXHIP_OP_CONSTANT;
+        *id = add_node(mlxhip::OpVal::from(op), {}, mv, false);
+        buffers[*id] = mlxhip::DevBuf{const_cast<float*>(data), len, false};
+        return MLXHIP_OK;
+    }
+
     int alloc_out(uint64_t id, float** out) {
         const mlxhip::Node& n = nodes.at(id);
         const size_t len = (size_t)n.meta.numel();

@@ -149,6 +149,14 @@ class Tensor:
         stream = stream if stream is not None else default_stream()
         return cls(stream, stream.add_constant_dev(ptr, _meta(shape, dtype)), shape, dtype)
 
+    @classmethod
+    def view_device(cls, ptr: int, shape: Sequence[int], stream=None, dtype: int = abi.F32) -> "Tensor":
+        """Constant that reads f32 device memory in place (HipStream only):
+        256-byte aligned, valid and unchanged while the node exists."""
+        shape = _shape(shape)
+        stream = stream if stream is not None else default_stream()
+        return cls(stream, stream.add_constant_view(ptr, _meta(shape, dtype)), shape, dtype)
+
     def _lazy(self, op: Op, inputs: Sequence["Tensor"], shape: Sequence[int]) -> "Tensor":
         shape = _shape(shape)
         st = self.stream

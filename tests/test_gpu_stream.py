@@ -472,3 +472,35 @@ def test_async_eval_stream_semantics():
 
     for x, y in zip(run(False), run(True)):
         np.testing.assert_array_equal(x, y)
+
+
+def test_constant_views_read_device_memory_in_place():
+    """mlxhip_stream_add_constant_view: a node that reads caller-owned device
+    memory without a copy gives the copied constant's results bit for bit,
+    leaves the memory untouched through evaluation, clear and close, and
+    rejects memory that is not 256-byte aligned."""
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((64, 96)).astype(np.float32)
+    b = rng.standard_normal((96, 32)).astype(np.float32)
+    from oxidizedmlx_amd.backend import DeviceBuffer
+    A, B = DeviceBuffer.from_array(a), DeviceBuffer.from_array(b)
+
+    def run(view):
+        s = HipStream(async_eval=view)
+        add = s.add_constant_view if view else s.add_constant_dev
+        ai, bi = add(A.ptr, meta([64, 96])), add(B.ptr, meta([96, 32]))
+        mm = s.add_op(OpKind.MatMul, [ai, bi], meta([64, 32]))
+        sm = s.add_op(OpKind.Softmax(1), [mm], meta([64, 32]))
+        s.eval(sm)
+        out = s.get_buffer(sm)
+        s.clear()
+        s.close()
+        return out
+
+    np.testing.assert_array_equal(run(True), run(False))
+    np.testing.assert_array_equal(A.download(), a.reshape(-1))
+    np.testing.assert_array_equal(B.download(), b.reshape(-1))
+    s = HipStream()
+    with pytest.raises(abi.InvalidArgument, match="aligned"):
+        s.add_constant_view(A.ptr + 4, meta([4]))
+    s.close()
