@@ -260,6 +260,37 @@ __global__ __launch_bounds__(BLOCK) void broadcast_kernel(const float* __restric
     }
 }
 
+// ── gathers with 32-bit index arithmetic ────────────────────────────────
+// out[u] = in[src(u)] over units of VEC floats: src is the sum over the
+// output's axes of (coordinate of u on that axis) x (input stride of that
+// axis, in units). The coordinates come from multiply-high division by
+// invariant divisors (Granlund and Montgomery, PLDI 1994): for a divisor
+// d >= 2 with l = ceil(log2 d), p = 31 + l and mul = ceil(2^p / d) < 2^32,
+// floor(n / d) = umulhi(n, mul) >> (p - 32) for every 0 <= n < 2^31; d = 1 is
+// taken as is. Used when every unit index and source offset fits 31 bits,
+// in place of 64-bit divisions (tens of instructions each per axis).
+struct Gather32 {
+    int ndim;
+    uint32_t dim[MAXD], mul[MAXD], shr[MAXD], stride[MAXD];
+};
+
+template <int VEC>
+__global__ __launch_bounds__(BLOCK) void gather32_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                         Gather32 g, uint32_t total) {
+    for (uint32_t u = blockIdx.x * BLOCK + threadIdx.x; u < total; u += gridDim.x * BLOCK) {
+        uint32_t rem = u, src = 0;
+        for (int d = g.ndim - 1; d >= 0; --d) {
+            const uint32_t q = g.dim[d] == 1 ? rem : (__umulhi(rem, g.mul[d]) >> g.shr[d]);
+            src += (rem - q * g.dim[d]) * g.stride[d];
+            rem = q;
+        }
+        if constexpr (VEC == 4)
+            reinterpret_cast<float4*>(y)[u] = reinterpret_cast<const float4*>(x)[src];
+        else
+            y[u] = x[src];
+    }
+}
+
 // One thread per output element; sequential fold in the reference's order
 // (reduce_along_axis, cpu_kernels.rs:166-195; Sum folds from -0.0), so the
 // result is bit-identical to the CPU's. The fold is a chain of dependent
@@ -564,6 +595,44 @@ int transpose2d(const float* x, float* y, int64_t rows, int64_t cols, hipStream_
     return launch_check("transpose2d_kernel");
 }
 
+// Host side of gather32_kernel: `dims` the output shape, `stride` each output
+// axis's input stride (elements). Returns false (nothing launched) when the
+// 32-bit form does not apply.
+bool gather32(const float* x, float* y, const int64_t* dims, const int64_t* stride, int ndim, int64_t total,
+              hipStream_t s, int* rc) {
+    // float4 units when the innermost output axis is contiguous in the input
+    // and holds a multiple of 4 elements, and both pointers are 16-byte aligned.
+    const bool vec = ndim > 0 && stride[ndim - 1] == 1 && dims[ndim - 1] % 4 == 0 &&
+                     (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16 == 0;
+    const int64_t unit = vec ? 4 : 1;
+    const int64_t units = total / unit;
+    if (units >= (int64_t(1) << 31)) return false;
+    Gather32 g{};
+    g.ndim = ndim;
+    int64_t max_src = 0;
+    for (int d = 0; d < ndim; ++d) {
+        const int64_t n = d == ndim - 1 ? dims[d] / unit : dims[d];
+        const int64_t st = d == ndim - 1 ? stride[d] : stride[d] / unit;
+        if (d < ndim - 1 && stride[d] % unit) return false;
+        max_src += (n - 1) * st;
+        g.dim[d] = (uint32_t)n;
+        g.stride[d] = (uint32_t)st;
+        if (n >= 2) {
+            int l = 0;
+            while ((int64_t(1) << l) < n) ++l;
+            const int p = 31 + l;
+            g.mul[d] = (uint32_t)(((uint64_t(1) << p) + (uint64_t)n - 1) / (uint64_t)n);
+            g.shr[d] = (uint32_t)(p - 32);
+        }
+    }
+    if (max_src >= (int64_t(1) << 31)) return false;
+    const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(units, BLOCK), MAX_GRID);
+    if (vec) hipLaunchKernelGGL(gather32_kernel<4>, dim3(grid), dim3(BLOCK), 0, s, x, y, g, (uint32_t)units);
+    else hipLaunchKernelGGL(gather32_kernel<1>, dim3(grid), dim3(BLOCK), 0, s, x, y, g, (uint32_t)units);
+    *rc = launch_check("gather32_kernel");
+    return true;
+}
+
 int permute(const float* x, float* y, const int64_t* shape, const int64_t* perm, int ndim,
             hipStream_t s) {
     if (ndim > MAXD) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "permute: rank %d > %d", ndim, MAXD);
@@ -585,6 +654,8 @@ int permute(const float* x, float* y, const int64_t* shape, const int64_t* perm,
         ns.v[i] = shape[perm[i]];
         st.v[i] = old_stride[perm[i]];
     }
+    int rc = MLXHIP_OK;
+    if (gather32(x, y, ns.v, st.v, ndim, total, s, &rc)) return rc;
     hipLaunchKernelGGL(permute_kernel, dim3(grid_for(total)), dim3(BLOCK), 0, s, x, y, ns, st, ndim,
                        total);
     return launch_check("permute_kernel");
@@ -613,6 +684,8 @@ int broadcast(const float* x, float* y, const int64_t* in_shape, int in_ndim,
             st.v[d] = 0;
         }
     }
+    int rc = MLXHIP_OK;
+    if (gather32(x, y, os.v, st.v, out_ndim, total, s, &rc)) return rc;
     hipLaunchKernelGGL(broadcast_kernel, dim3(grid_for(total)), dim3(BLOCK), 0, s, x, y, os, st,
                        out_ndim, total);
     return launch_check("broadcast_kernel");

@@ -65,3 +65,17 @@ def test_axis_sum_beyond_one_grid_stride():
     hb.eval_node_dev(OpKind.Sum(1), [(xb, (rows, 2))], meta([rows]), yb)
     hb.synchronize()
     np.testing.assert_array_equal(yb.download(count=rows), x[:, 0] + x[:, 1])
+
+
+def test_broadcast_beyond_32bit_indices():
+    # 2^31 + 4096 output elements (8 GiB): past what the 32-bit gather
+    # indexes, so the broadcast takes the 64-bit kernel. Rows on either side
+    # of element 2^31 and the last row are checked.
+    rows, cols = (1 << 19) + 1, 4096
+    x = np.random.default_rng(15).standard_normal(cols, dtype=np.float32)
+    xb, yb = hb.DeviceBuffer.from_array(x), hb.DeviceBuffer(4 * rows * cols)
+    print(f"broadcast [1, {cols}] -> [{rows}, {cols}]", flush=True)
+    hb.eval_node_dev(OpKind.Broadcast((rows, cols)), [(xb, (1, cols))], meta([rows, cols]), yb)
+    hb.synchronize()
+    for r in (0, rows - 2, rows - 1):
+        np.testing.assert_array_equal(yb.download(count=cols, offset=4 * r * cols), x)

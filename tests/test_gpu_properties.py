@@ -79,8 +79,33 @@ def test_transpose_any_rank(sp):
 
 
 @st.composite
+def shape_and_perm_keeping_inner(draw):
+    """Up to 8 axes, the innermost kept in place and a multiple of 4 long: the
+    layouts the gather moves in 16-byte units."""
+    inner = 4 * draw(st.integers(1, 40))
+    outer = tuple(draw(st.lists(st.integers(1, 5), min_size=1, max_size=7)))
+    perm = tuple(draw(st.permutations(range(len(outer))))) + (len(outer),)
+    return outer + (inner,), perm
+
+
+@settings(max_examples=60, deadline=None, derandomize=True, suppress_health_check=list(HealthCheck))
+@given(sp=shape_and_perm_keeping_inner())
+def test_transpose_keeping_inner_axis(sp):
+    shape, perm = sp
+    print(f"transpose {shape} by {perm}", flush=True)
+    x = synth.normal(len(shape) * 211 + sum(shape), shape)
+    xb, yb = hb.DeviceBuffer.from_array(x), hb.DeviceBuffer(x.nbytes)
+    out_shape = [shape[p] for p in perm]
+    hb.eval_node_dev(OpKind.Transpose(perm), [(xb, shape)], meta(out_shape), yb)
+    hb.synchronize()
+    np.testing.assert_array_equal(yb.download(count=x.size).reshape(out_shape), x.transpose(perm))
+
+
+@st.composite
 def broadcastable(draw):
     out = draw(st.lists(st.integers(1, 6), min_size=1, max_size=4))
+    if draw(st.booleans()):
+        out.append(4 * draw(st.integers(1, 16)))  # an innermost axis the gather moves 16 bytes at a time
     keep = draw(st.integers(0, len(out)))  # the input is a suffix of the output shape
     src = [d if draw(st.booleans()) else 1 for d in out[len(out) - keep:]]
     return tuple(src), tuple(out)
