@@ -17,6 +17,7 @@
 #include "device_math.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 #pragma clang fp contract(off)
 
@@ -340,6 +341,118 @@ __global__ __launch_bounds__(RED_BLOCK) void reduce_axis_kernel(const float* __r
         for (int64_t d = full; d < dim; ++d) v = fold<KIND>(v, p[d * inner]);
         if (KIND == 1) v = v / (float)dim;
         y[f] = v;
+    }
+}
+
+// The same sequential fold for reductions over a long axis with few
+// outputs (the bias gradients of a block: Sum over 2048 rows of [2048, N]).
+// One thread per output leaves most CUs idle and each busy CU streaming its
+// columns at the rate one CU can keep cache lines in flight. Here a
+// workgroup owns COLS outputs of one outer index: its 256 threads copy
+// chunks of RC_CH rows x COLS columns straight from memory into a ring of
+// LDS slots (buffer loads with the LDS flag, 16 bytes per lane, RC_P chunks
+// ahead), and COLS lanes of wave 0 fold each chunk in row order while the
+// next ones arrive. Rows past the end read as zero (out of the buffer's
+// range) and are never folded; columns past the end are never stored.
+// Needs inner % 4 == 0, a 16-byte aligned x and a slab of under 2^32 bytes.
+constexpr int RC_BLOCK = 256;
+
+#define MLXHIP_LDS_AS __attribute__((address_space(3)))
+
+// 16 bytes per lane from buffer offset `voff` into LDS at dst + 16 * lane.
+// Inline assembly, so the compiler does not wait for these loads before
+// every LDS read; the kernel waits for them itself (vmcnt, then a barrier).
+__device__ inline void rc_lds_load16(__amdgpu_buffer_rsrc_t rsrc, MLXHIP_LDS_AS char* dst, uint32_t voff) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(m0) : "memory");
+}
+
+template <int KIND, int COLS, int RC_CH, int RC_P, int FB>
+__global__ __launch_bounds__(RC_BLOCK) void reduce_cols_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                               int64_t dim, int64_t inner, int64_t col_blocks) {
+    constexpr int TPR = COLS / 4;                       // lanes per row
+    constexpr int RPI = 64 / TPR;                       // rows per wave instruction (1 KiB)
+    constexpr int RC_NB = RC_P + 1;
+    constexpr int CHUNK_BYTES = RC_CH * COLS * 4;
+    constexpr int L = CHUNK_BYTES / (RC_BLOCK * 16);    // loads per thread per chunk
+    static_assert(L * RC_BLOCK * 16 == CHUNK_BYTES, "whole 1 KiB blocks per wave");
+    // The ring; the vmcnt below assumes these loads are the only vector
+    // memory operations in flight.
+    __shared__ __align__(16) float ring[RC_NB][RC_CH * COLS];
+    const int64_t o = blockIdx.x / col_blocks;
+    const int64_t c0 = (blockIdx.x % col_blocks) * COLS;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const float* slab = x + o * dim * inner;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)slab, (short)0, (int)(uint32_t)(dim * inner * 4), 0x00020000);
+    // Load l of a chunk: wave instruction q = l * 4 + wave covers rows
+    // q * RPI .. q * RPI + RPI - 1 of the chunk; the lane's 16 bytes are
+    // row lane / TPR, columns c0 + 4 * (lane % TPR) .. + 3.
+    uint32_t voff[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const int64_t row = (int64_t)(l * 4 + wave) * RPI + lane / TPR;
+        voff[l] = (uint32_t)((row * inner + c0 + 4 * (lane % TPR)) * 4);
+    }
+    const uint32_t chunk_step = (uint32_t)(RC_CH * inner * 4);
+    auto issue = [&](int ch) {
+        MLXHIP_LDS_AS char* slot = (MLXHIP_LDS_AS char*)&ring[ch % RC_NB][0];
+#pragma unroll
+        for (int l = 0; l < L; ++l)
+            rc_lds_load16(rsrc, slot + (l * 4 + wave) * 1024, voff[l] + (uint32_t)ch * chunk_step);
+    };
+    const int nch = (int)((dim + RC_CH - 1) / RC_CH);
+    float v = KIND == 2 ? -INFINITY : -0.0f;
+    for (int ch = 0; ch < RC_P; ++ch) issue(ch);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L * (RC_P - 1)) : "memory");
+    __syncthreads();
+    for (int c = 0; c < nch; ++c) {
+        // Slot (c + P) % NB was folded in the previous pass, before the barrier.
+        // Chunks past the end are issued too (every row out of range), so the
+        // count of younger loads below is always L * (P - 1).
+        issue(c + RC_P);
+        if (tid < COLS) {
+            const float* b = &ring[c % RC_NB][tid];
+            const int rows = (int)std::min<int64_t>(RC_CH, dim - (int64_t)c * RC_CH);
+            if (rows == RC_CH) {
+                // Two register batches of FB rows in turn: batch B's LDS
+                // reads are in flight while batch A is folded (the scheduling
+                // barriers keep the compiler from sinking the reads to their
+                // adds, which would expose the LDS latency on every pair).
+                float a[FB], bb[FB];
+#pragma unroll
+                for (int i = 0; i < FB; ++i) a[i] = b[i * COLS];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int r = 0; r < RC_CH; r += 2 * FB) {
+#pragma unroll
+                    for (int i = 0; i < FB; ++i) bb[i] = b[(r + FB + i) * COLS];
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < FB; ++i) v = fold<KIND>(v, a[i]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (r + 2 * FB < RC_CH) {
+#pragma unroll
+                        for (int i = 0; i < FB; ++i) a[i] = b[(r + 2 * FB + i) * COLS];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < FB; ++i) v = fold<KIND>(v, bb[i]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                for (int i = 0; i < rows; ++i) v = fold<KIND>(v, b[i * COLS]);
+            }
+        }
+        // This thread's loads of chunk c + 1 are done, then everyone's.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L * (RC_P - 1)) : "memory");
+        __syncthreads();
+    }
+    // Drain the loads past the end before the workgroup exits.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (tid < COLS && c0 + tid < inner) {
+        if (KIND == 1) v = v / (float)dim;
+        y[o * inner + c0 + tid] = v;
     }
 }
 
@@ -695,6 +808,25 @@ int reduce_axis(int kind, const float* x, float* y, int64_t outer, int64_t dim, 
                 hipStream_t s) {
     const int64_t n = outer * inner;
     if (n == 0) return MLXHIP_OK;
+    // Long axes over float4-aligned rows: the chunked LDS fold (same order).
+    // Chunks of 256 rows, 4 in flight, folded from 32-row register batches:
+    // the fastest of the chunk / prefetch / batch sizes measured on Sum over
+    // 2048 rows of 1024 and 4096 columns (11.1 and 16.4 us, against 25.8 and
+    // 26.3 us for one thread per output). Offsets up to P + 1 chunks past
+    // the last row stay below 2^32.
+    constexpr int CH = 256, PF = 4, FB = 32, COLS = 16;
+    if (dim >= 2 * CH && inner % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+        (dim + (PF + 1) * CH) * inner * 4 < (int64_t(1) << 32) && outer * ceil_div(inner, COLS) < (int64_t(1) << 31)) {
+        const int64_t cb = ceil_div(inner, COLS);
+        const dim3 g((unsigned)(outer * cb));
+        if (kind == 0)
+            hipLaunchKernelGGL((reduce_cols_kernel<0, COLS, CH, PF, FB>), g, dim3(RC_BLOCK), 0, s, x, y, dim, inner, cb);
+        else if (kind == 1)
+            hipLaunchKernelGGL((reduce_cols_kernel<1, COLS, CH, PF, FB>), g, dim3(RC_BLOCK), 0, s, x, y, dim, inner, cb);
+        else
+            hipLaunchKernelGGL((reduce_cols_kernel<2, COLS, CH, PF, FB>), g, dim3(RC_BLOCK), 0, s, x, y, dim, inner, cb);
+        return launch_check("reduce_cols_kernel");
+    }
     const dim3 grid((unsigned)std::min<int64_t>(ceil_div(n, RED_BLOCK), MAX_GRID));
     if (kind == 0) hipLaunchKernelGGL(reduce_axis_kernel<0>, grid, dim3(RED_BLOCK), 0, s, x, y, outer, dim, inner);
     else if (kind == 1) hipLaunchKernelGGL(reduce_axis_kernel<1>, grid, dim3(RED_BLOCK), 0, s, x, y, outer, dim, inner);

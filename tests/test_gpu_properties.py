@@ -144,6 +144,24 @@ def test_axis_reduction_any_shape(sa, kind):
     np.testing.assert_array_equal(yb.download(count=int(np.prod(out_shape))), oracle_reduce(op, x, out_shape))
 
 
+@pytest.mark.parametrize("shape,axis", [
+    ((2048, 1024), 0), ((2048, 4096), 0), ((512, 16), 0), ((600, 20), 0), ((2049, 1028), 0),
+    ((3, 700, 36), 1), ((2, 1000, 8), -2), ((1279, 4), 0), ((2, 3, 640, 12), 2)])
+@pytest.mark.parametrize("kind", ["sum", "mean", "max"])
+def test_long_axis_reduction(shape, axis, kind):
+    """Axes of 512 elements and more over float4-aligned rows take the
+    chunked LDS fold: ragged last chunks, column blocks that run past the
+    row, several outer slices; bit for bit against the oracle's fold."""
+    print(f"{kind} over axis {axis} of {shape}", flush=True)
+    op = {"sum": OpKind.Sum(axis), "mean": OpKind.Mean(axis), "max": OpKind.Max(axis)}[kind]
+    x = synth.normal(sum(shape) * 31 + len(shape), shape, 0.0, 3.0)
+    out_shape = [d for i, d in enumerate(shape) if i != axis % len(shape)]
+    xb, yb = hb.DeviceBuffer.from_array(x), hb.DeviceBuffer(4 * int(np.prod(out_shape)))
+    hb.eval_node_dev(op, [(xb, shape)], meta(out_shape), yb)
+    hb.synchronize()
+    np.testing.assert_array_equal(yb.download(count=int(np.prod(out_shape))), oracle_reduce(op, x, out_shape))
+
+
 def oracle_reduce(op, x, out_shape):
     from oracle.cpu_ref import CpuRefBackend
     from oxidizedmlx_amd.opkind import NodeInput
