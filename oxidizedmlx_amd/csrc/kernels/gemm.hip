@@ -37,9 +37,9 @@ int elem_size(int dt) { return dt == MLXHIP_DTYPE_F32 ? 4 : 2; }
 
 // Sum of the split-K partials in split order (deterministic), converted to C.
 // ws holds batch * splits slices of [m, n] f32 with row pitch ldw, slice
-// (b, s) at (b*splits+s)*m*ldw. Thread (row, 4-column group) of a 2-D grid:
-// blockIdx.x walks rows of RED_COLS x RED_ROWS work items, blockIdx.y the
-// batch; no 64-bit division. VEC: ldw and the partials are 16-byte aligned,
+// (b, s) at (b*splits+s)*m*ldw. Thread (row, 4-column group): a block holds
+// RED_ROWS rows x RED_COLS groups, blockIdx.x enumerates (row block, column
+// block) pairs and strides over the row blocks, blockIdx.y the batch. VEC: ldw and the partials are 16-byte aligned,
 // so each split contributes one float4 load per thread.
 constexpr int RED_COLS = 64;  // 4-column groups per row of work items
 constexpr int RED_ROWS = 4;
@@ -52,9 +52,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     const int64_t groups = (n + 3) / 4;
     const int gx = threadIdx.x % RED_COLS, gy = threadIdx.x / RED_COLS;
     const int64_t slice = m * ldw;
-    for (int64_t row = (int64_t)blockIdx.x * RED_ROWS + gy; row < m; row += (int64_t)gridDim.x * RED_ROWS) {
+    // blockIdx.x = row block * col_blocks + column block: every thread owns
+    // one 4-column group, so all of a thread's loads are in flight at once.
+    const int64_t col_blocks = (groups + RED_COLS - 1) / RED_COLS;
+    const int64_t rblocks = gridDim.x / col_blocks;
+    const int64_t g = (blockIdx.x % col_blocks) * RED_COLS + gx;
+    if (g >= groups) return;
+    for (int64_t row = (int64_t)(blockIdx.x / col_blocks) * RED_ROWS + gy; row < m; row += rblocks * RED_ROWS) {
         const float* pr = ws + b * splits * slice + row * ldw;
-        for (int64_t g = gx; g < groups; g += RED_COLS) {
+        {
             const int64_t col = 4 * g;
             // Every split's values are loaded before the first add (one memory
             // latency, not one per split), then summed in split order.
@@ -68,7 +74,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
                     v[s][0] = t.x, v[s][1] = t.y, v[s][2] = t.z, v[s][3] = t.w;
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[s][e] = col + e < n ? p[e] : 0.0f;
+                    for (int e = 0; e < 4; ++e) v[s][e] = p[std::min<int64_t>(e, n - 1 - col)];  // clamped, unguarded
                 }
             }
             float acc[4] = {v[0][0], v[0][1], v[0][2], v[0][3]};
@@ -90,7 +96,12 @@ int splitk_reduce(int c_dtype, const float* ws, void* c, int64_t m, int64_t n, i
     // VEC: every float4 read stays inside a row of the partials (ldw a
     // multiple of 4; reads past n up to ldw stay in the row padding).
     const bool vec = ldw % 4 == 0 && reinterpret_cast<uintptr_t>(ws) % 16 == 0 && ceil_div(n, 4) * 4 <= ldw;
-    const dim3 grid((unsigned)std::min<int64_t>(ceil_div(m, RED_ROWS), 65535), (unsigned)batch);
+    if (m == 0 || n == 0) return MLXHIP_OK;
+    const int64_t col_blocks = ceil_div(ceil_div(n, 4), RED_COLS);
+    if (col_blocks > (int64_t(1) << 22)) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "splitk_reduce: rows too long");
+    const int64_t row_blocks = std::max<int64_t>(
+        1, std::min<int64_t>({ceil_div(m, RED_ROWS), 65535, (int64_t(1) << 22) / col_blocks}));
+    const dim3 grid((unsigned)(row_blocks * col_blocks), (unsigned)batch);
 #define MLXHIP_RED(CT)                                                                                       \
     do {                                                                                                    \
         if (vec) hipLaunchKernelGGL((splitk_reduce_kernel<CT, true>), grid, dim3(256), 0, s, ws, c, m, n, ldw, \
@@ -119,16 +130,36 @@ struct PackPair {
     PackOp op[2];
 };
 
+// One 16-byte chunk of a destination row: columns c0 .. c0 + CH - 1 of
+// source row r, zero outside rows x cols. Every element is loaded, from a
+// row and column clamped into range, before any is selected: a guarded load
+// per element compiles to a branch that waits for its own load.
+template <typename T, int CH>
+__device__ inline uint4 pack_chunk(const T* sb, int64_t ld, int64_t rows, int64_t cols, int64_t r, int64_t c0) {
+    union {
+        uint4 v;
+        T e[CH];
+    } u;
+    const T* src = sb + (r < rows ? r : rows - 1) * ld;
+    T t[CH];
+#pragma unroll
+    for (int e = 0; e < CH; ++e) t[e] = src[c0 + e < cols ? c0 + e : cols - 1];
+#pragma unroll
+    for (int e = 0; e < CH; ++e) u.e[e] = (r < rows && c0 + e < cols) ? t[e] : T(0);
+    return u.v;
+}
+
 // Both operands of one GEMM in one launch (blockIdx.z picks the operand,
 // blockIdx.y the batch slice). Each thread writes one 16-byte chunk of a
 // destination row (cols_p is a multiple of the chunk and the destination is
 // 16-byte aligned); the source, whose rows need not be aligned, is read
-// element by element.
+// element by element. An empty source (no rows or no columns) packs zeros.
 template <typename T>
 __global__ __launch_bounds__(256) void pack_kernel(PackPair pp) {
     constexpr int CH = 16 / sizeof(T);
     const PackOp& p = pp.op[blockIdx.z];
     const int64_t b = blockIdx.y;
+    const bool empty = p.rows <= 0 || p.cols <= 0;
     const int chunks = (int)(p.cols_p / CH);  // per destination row (host-checked to fit 32 bits)
     const T* sb = static_cast<const T*>(p.src) + b * p.sstride;
     uint4* db = reinterpret_cast<uint4*>(static_cast<T*>(p.dst) + b * p.rows_p * p.cols_p);
@@ -139,30 +170,12 @@ __global__ __launch_bounds__(256) void pack_kernel(PackPair pp) {
     if (chunks <= 256) {
         const int rloc = t / chunks, q = t - rloc * chunks;
         if (rloc >= per_block) return;
-        for (int64_t r = (int64_t)blockIdx.x * per_block + rloc; r < p.rows_p; r += (int64_t)gridDim.x * per_block) {
-            const int c0 = q * CH;
-            union {
-                uint4 v;
-                T e[CH];
-            } u;
-            const T* src = sb + r * p.ld;
-#pragma unroll
-            for (int e = 0; e < CH; ++e) u.e[e] = (r < p.rows && c0 + e < p.cols) ? src[c0 + e] : T(0);
-            db[r * chunks + q] = u.v;
-        }
+        for (int64_t r = (int64_t)blockIdx.x * per_block + rloc; r < p.rows_p; r += (int64_t)gridDim.x * per_block)
+            db[r * chunks + q] = empty ? make_uint4(0, 0, 0, 0) : pack_chunk<T, CH>(sb, p.ld, p.rows, p.cols, r, q * CH);
     } else {
         for (int64_t r = blockIdx.x; r < p.rows_p; r += gridDim.x) {
-            const T* src = sb + r * p.ld;
-            for (int q = t; q < chunks; q += 256) {
-                const int c0 = q * CH;
-                union {
-                    uint4 v;
-                    T e[CH];
-                } u;
-#pragma unroll
-                for (int e = 0; e < CH; ++e) u.e[e] = (r < p.rows && c0 + e < p.cols) ? src[c0 + e] : T(0);
-                db[r * chunks + q] = u.v;
-            }
+            for (int q = t; q < chunks; q += 256)
+                db[r * chunks + q] = empty ? make_uint4(0, 0, 0, 0) : pack_chunk<T, CH>(sb, p.ld, p.rows, p.cols, r, q * CH);
         }
     }
 }
