@@ -263,10 +263,15 @@ int vjp(Builder& b, uint64_t id, const Node& n, uint64_t g, const std::vector<bo
         case MLXHIP_OP_SOFTMAX: {
             if (!arity(1)) return MLXHIP_ERR_INVALID_ARGUMENT;
             if (need[0]) {
-                // Recompute softmax from the forward input (CSE returns the
-                // forward node), then SoftmaxVjp [grad, softmax output].
-                mlxhip_op_t so = Builder::op(MLXHIP_OP_SOFTMAX);
-                so.axis = n.op.op.axis;
+                // The forward node's own op over its own input: CSE returns
+                // the forward node (an op differing in any field, such as
+                // has_axis, would make a second Softmax that evaluates again),
+                // then SoftmaxVjp [grad, softmax output].
+                mlxhip_op_t so = n.op.op;
+                so.shape = nullptr;
+                so.shape_len = 0;
+                so.axes = nullptr;
+                so.axes_len = 0;
                 const uint64_t sm = b.node(so, {in[0]}, b.shape(in[0]), b.meta(in[0]).dtype);
                 mlxhip_op_t o = Builder::op(MLXHIP_OP_SOFTMAX_VJP);
                 o.axis = n.op.op.axis;

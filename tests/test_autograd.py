@@ -306,6 +306,36 @@ def test_hip_block_async_eval_matches_sync():
 
 @pytest.mark.gpu
 @pytest.mark.usefixtures("hip")
+def test_hip_softmax_vjp_reuses_forward_softmax():
+    """The Softmax VJP takes the forward Softmax node itself (CSE over the
+    same op and input) as its output operand, so a gradient evaluated after
+    the forward evaluates no second softmax: evaluating y and then dx costs
+    exactly the nodes of evaluating dx alone on a fresh stream (a second
+    Softmax node would add one), and both give the same dx."""
+    from oxidizedmlx_amd.backend import HipStream
+    x0, w0 = synth.normal(71, (6, 37)), synth.normal(72, (6, 37))
+
+    def build(st):
+        x = Tensor.from_f32_on_stream(x0.reshape(-1), x0.shape, st)
+        w = Tensor.from_f32_on_stream(w0.reshape(-1), w0.shape, st)
+        y = x.softmax(-1)
+        _, gs = value_and_grad(y.mul(w).sum_all(), [x])
+        return y, gs[0]
+
+    a, b = HipStream(fusion=False), HipStream(fusion=False)
+    ya, ga = build(a)
+    a.eval_many([ya.node])
+    a.eval_many([ga.node])
+    _, gb = build(b)
+    b.eval_many([gb.node])
+    assert a.eval_count() == b.eval_count()
+    np.testing.assert_array_equal(ga.to_numpy(), gb.to_numpy())
+    a.close()
+    b.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip")
 def test_hip_block_steps_with_clear_reuse_memory():
     """Block steps on one asynchronous stream, each cleared after its eval
     (mlxhip_stream_clear) so the next step's buffers reuse its HBM while its
