@@ -222,8 +222,10 @@ def main() -> int:
     dA = [hb.DeviceBuffer.from_array(A) for _ in range(SETS)]
     dB = [hb.DeviceBuffer.from_array(B) for _ in range(SETS)]
     dC = [hb.DeviceBuffer(n * n * 2) for _ in range(SETS)]
-    # Config 1: f32 512^3. Config 3: batched [32,1024,1024]^2 bf16/f16 (f32 C),
-    # the transposed-B case, and the odd 1000 x 777 x 1531 (edge tiles).
+    # Config 1: f32 512^3. Config 3: batched [32,1024,1024]^2 bf16/f16, the
+    # transposed-B case, and the odd 1000 x 777 x 1531 (edge tiles), each with
+    # f32 accumulation and C in the operands' dtype: the reference's matmul
+    # gives its result the left operand's dtype (tensor.rs:274-294).
     A1 = hb.DeviceBuffer.from_array(synth.normal(0x5EED0001, (512, 512)))
     B1 = hb.DeviceBuffer.from_array(synth.normal(0x5EED0002, (512, 512)))
     C1 = hb.DeviceBuffer(512 * 512 * 4)
@@ -234,13 +236,13 @@ def main() -> int:
     Bb16 = [hb.DeviceBuffer.from_array(synth.bf16_bits(Bb)) for _ in range(SETS)]
     Abh = [hb.DeviceBuffer.from_array(synth.f16_bits(Ab)) for _ in range(SETS)]
     Bbh = [hb.DeviceBuffer.from_array(synth.f16_bits(Bb)) for _ in range(SETS)]
-    Cb = [hb.DeviceBuffer(bt * nb * nb * 4) for _ in range(SETS)]
+    Cb = [hb.DeviceBuffer(bt * nb * nb * 2) for _ in range(SETS)]
     mo, no, ko = 1000, 777, 1531
     # The config-1 and odd-shape operands (a few MiB) stay cache-resident
     # whatever the rotation; they get one buffer set.
     Ao = hb.DeviceBuffer.from_array(synth.bf16_bits(synth.normal(0x5EED000A, (mo, ko))))
     Bo = hb.DeviceBuffer.from_array(synth.bf16_bits(synth.normal(0x5EED000B, (ko, no))))
-    Co = hb.DeviceBuffer(mo * no * 4)
+    Co = hb.DeviceBuffer(mo * no * 2)
     del Ab, Bb
     x = synth.normal(SEEDS["x"], (n, n), 0.0, 2.0)
     w = synth.uniform(SEEDS["w"], (n, n), -1.0, 1.0)
@@ -324,11 +326,11 @@ def main() -> int:
         # one replay of the K calls recorded with mlxhip_graph_*; measured on
         # this stack, replays were not faster than the eager calls.)
         "gemm_f32_512_cfg1": dict(flops=2.0 * 512 ** 3, bytes=3 * 512 * 512 * 4, peak=157.3),
-        "gemm_bf16_batched_32x1024_cfg3": dict(flops=2.0 * bt * nb ** 3, bytes=bt * nb * nb * 8),
-        "gemm_f16_batched_32x1024_cfg3": dict(flops=2.0 * bt * nb ** 3, bytes=bt * nb * nb * 8),
-        "gemm_bf16_batched_32x1024_nt_cfg3": dict(flops=2.0 * bt * nb ** 3, bytes=bt * nb * nb * 8),
+        "gemm_bf16_batched_32x1024_cfg3": dict(flops=2.0 * bt * nb ** 3, bytes=bt * nb * nb * 6),
+        "gemm_f16_batched_32x1024_cfg3": dict(flops=2.0 * bt * nb ** 3, bytes=bt * nb * nb * 6),
+        "gemm_bf16_batched_32x1024_nt_cfg3": dict(flops=2.0 * bt * nb ** 3, bytes=bt * nb * nb * 6),
         "gemm_bf16_odd_1000x777x1531_cfg3": dict(flops=2.0 * mo * no * ko,
-                                                  bytes=(mo * ko + ko * no) * 2 + mo * no * 4),
+                                                  bytes=(mo * ko + ko * no + mo * no) * 2),
         "softmax_4096x4096": dict(bytes=2 * n * n * 4),
         "layernorm_4096x4096": dict(bytes=2 * n * n * 4),
         "rmsnorm_4096x4096": dict(bytes=2 * n * n * 4),
@@ -368,11 +370,12 @@ def main() -> int:
                     stream=stream)
         elif name.startswith("gemm_") and "batched" in name:
             f16 = name.startswith("gemm_f16_")
-            hb.gemm(abi.F16 if f16 else abi.BF16, abi.F32, False, "_nt_" in name, nb, nb, nb,
+            dt16 = abi.F16 if f16 else abi.BF16
+            hb.gemm(dt16, dt16, False, "_nt_" in name, nb, nb, nb,
                     (Abh if f16 else Ab16)[j], nb, (Bbh if f16 else Bb16)[j], nb, Cb[j], nb, batch=bt,
                     stride_a=nb * nb, stride_b=nb * nb, stride_c=nb * nb, stream=stream)
         elif name == "gemm_bf16_odd_1000x777x1531_cfg3":
-            hb.gemm(abi.BF16, abi.F32, False, False, mo, no, ko, Ao, ko, Bo, no, Co, no,
+            hb.gemm(abi.BF16, abi.BF16, False, False, mo, no, ko, Ao, ko, Bo, no, Co, no,
                     stream=stream)
         elif name == "copy_64MiB":
             hb.ew_chain([], [xs["chain"][j]], ys["chain"][j], n * n, stream=stream)
@@ -481,13 +484,15 @@ def main() -> int:
             # rerun this one into set 0 before reading it.
             launch(k, 0)
             hb.synchronize(stream)
-            c = Cb[0].download(np.float32, bt * nb * nb).reshape(bt, nb, nb)
+            bits = Cb[0].download(np.uint16, bt * nb * nb)
+            c = (bits.view(np.float16).astype(np.float32) if f16 else synth.bf16_to_f32(bits)).reshape(bt, nb, nb)
             outs[k] = dict(kind="batched", a=a, b=b, c=c, rows=np.array([0, 300, 700, 1023]), rtol=1e-2)
         if "gemm_bf16_odd_1000x777x1531_cfg3" in res:
             outs["gemm_bf16_odd_1000x777x1531_cfg3"] = dict(
                 kind="gemm", a=synth.round_bf16(synth.normal(0x5EED000A, (mo, ko))),
                 b=synth.round_bf16(synth.normal(0x5EED000B, (ko, no))),
-                c=Co.download(np.float32, mo * no).reshape(mo, no), rows=np.arange(0, mo, 40), rtol=1e-2)
+                c=synth.bf16_to_f32(Co.download(np.uint16, mo * no)).reshape(mo, no), rows=np.arange(0, mo, 40),
+                rtol=1e-2)
         rsel = np.arange(0, n, 64)
         for op, k in (("softmax", "softmax_4096x4096"), ("layernorm", "layernorm_4096x4096"),
                       ("rmsnorm", "rmsnorm_4096x4096")):

@@ -84,6 +84,25 @@ def causal_mask(seq: int) -> np.ndarray:
     return m
 
 
+_DEVICE_CONSTANTS: Dict[tuple, object] = {}
+
+
+def _fixed_constant(key: tuple, values: np.ndarray, shape, st) -> Tensor:
+    """A constant that is the same in every graph (the attention scale, the
+    causal mask). On a stream that reads device memory in place (HipStream)
+    it is uploaded once per process and each graph takes a view of it, so a
+    training step copies nothing from the host; other streams take it as an
+    ordinary constant."""
+    if not hasattr(st, "add_constant_view"):
+        return Tensor.from_f32_on_stream(values, shape, st)
+    buf = _DEVICE_CONSTANTS.get(key)
+    if buf is None:
+        from .backend import DeviceBuffer
+        buf = DeviceBuffer.from_array(np.ascontiguousarray(values, dtype=np.float32).reshape(-1))
+        _DEVICE_CONSTANTS[key] = buf
+    return Tensor.view_device(buf.ptr, shape, st)
+
+
 class CausalSelfAttention:
     """Causal multi-head self-attention over x [batch*seq, d_model] (rows
     ordered batch-major), with Q/K/V/output projections as Linear layers."""
@@ -108,8 +127,9 @@ class CausalSelfAttention:
         q, k, v = self._heads(self.wq(x)), self._heads(self.wk(x)), self._heads(self.wv(x))
         scores = q.matmul(k.transpose((0, 2, 1)))                      # [B*H, S, S]
         st = x.stream
-        scale = Tensor.from_f32_on_stream([1.0 / math.sqrt(dh)], (), st).broadcast_to(scores.shape)
-        mask = Tensor.from_f32_on_stream(causal_mask(self.s), (self.s, self.s), st).broadcast_to(scores.shape)
+        scale = _fixed_constant(("scale", dh), np.array([1.0 / math.sqrt(dh)], np.float32), (), st)
+        mask = _fixed_constant(("causal", self.s), causal_mask(self.s), (self.s, self.s), st)
+        scale, mask = scale.broadcast_to(scores.shape), mask.broadcast_to(scores.shape)
         p = scores.mul(scale).add(mask).softmax(-1)
         o = p.matmul(v)                                                 # [B*H, S, Dh]
         o = o.reshape((self.b, self.h, self.s, dh)).transpose((0, 2, 1, 3)).reshape((bs, d))
