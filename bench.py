@@ -22,6 +22,7 @@ kernels, single-threaded) timed on a bounded sample on this host.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import platform
@@ -276,7 +277,12 @@ def main() -> int:
 
     blk = {"stream": None}
 
-    def block_step() -> None:
+    # The same step with the attention through the fused HeadAttention op:
+    # one kernel for the forward of every head, two for its gradient, instead
+    # of the [64, 512, 512] score, probability and gradient tensors.
+    bcfg_fused = dataclasses.replace(bcfg, fused_attention=True)
+
+    def block_step(fused: bool = False) -> None:
         from oxidizedmlx_amd.tensor import Tensor, value_and_grad
         if blk["stream"] is None:
             blk["stream"] = hb.HipStream(async_eval=True)
@@ -284,7 +290,7 @@ def main() -> int:
         t = {k: Tensor.view_device(b.ptr, (bcfg.rows, bcfg.d_model) if k in ("x", "gy")
                                    else bcfg.param_shapes()[k], st) for k, b in blk_dev.items()}
         params = {k: t[k] for k in bcfg.param_shapes()}
-        loss = mnn.TransformerBlock(bcfg, params)(t["x"]).mul(t["gy"]).sum_all()
+        loss = mnn.TransformerBlock(bcfg_fused if fused else bcfg, params)(t["x"]).mul(t["gy"]).sum_all()
         _, grads = value_and_grad(loss, list(params.values()) + [t["x"]])
         st.eval_many([g.node for g in grads])
         st.clear()
@@ -340,6 +346,8 @@ def main() -> int:
         # not by events.
         "transformer_block_fwd_bwd_cfg4": dict(flops=3.0 * bcfg.forward_flops(), bytes=0, peak=157.3,
                                                wall=True),
+        "transformer_block_fwd_bwd_cfg4_fused_attention": dict(flops=3.0 * bcfg.forward_flops(), bytes=0,
+                                                               peak=157.3, wall=True),
         "decode_cfg5": dict(bytes=dcfg.decode_bytes(d_batch, d_prompt, d_new), decoder=True),
         "attention_fused_cfg4": dict(flops=at_flops, bytes=4 * at_bh * at_t * at_dh * 4, peak=157.3),
     }
@@ -357,6 +365,8 @@ def main() -> int:
             dec_ms.append(dec.last_timing()[0])
         elif name == "transformer_block_fwd_bwd_cfg4":
             block_step()
+        elif name == "transformer_block_fwd_bwd_cfg4_fused_attention":
+            block_step(fused=True)
         elif name == "gemm_bf16_4096":
             hb.gemm(abi.BF16, abi.BF16, False, False, n, n, n, dA[j], n, dB[j], n, dC[j], n, stream=stream)
         elif name == "softmax_4096x4096":

@@ -87,7 +87,18 @@ typedef enum {
     MLXHIP_OP_ROPE_MLX = 31,              /* OpKind::RoPE: base, offset, traditional */
     MLXHIP_OP_NARROW = 32,                /* axis, start, length */
     MLXHIP_OP_CONCATENATE = 33,           /* axis */
-    MLXHIP_OP_COUNT_ = 34
+    /* No reference counterpart (extensions for training through fused
+     * attention; the reference's Attention is 2-D and has no VJP,
+     * crates/mlx-autograd/src/vjp.rs:173-176):
+     * HeadAttention: inputs Q, K, V [heads, t, dh], output [heads, t, dh]:
+     * per head the Attention op's arithmetic (cpu_attention,
+     * crates/mlx-core/src/cpu_kernels.rs:738-812) through mlxhip_attention.
+     * Differentiable: its VJP is one HeadAttentionVjp node.
+     * HeadAttentionVjp: inputs Q, K, V, O (the forward output), dO; output
+     * [3, heads, t, dh] = dQ, dK, dV (mlxhip_attention_vjp). */
+    MLXHIP_OP_HEAD_ATTENTION = 34,        /* scale, causal */
+    MLXHIP_OP_HEAD_ATTENTION_VJP = 35,    /* scale, causal */
+    MLXHIP_OP_COUNT_ = 36
 } mlxhip_op_kind_t;
 
 /* One OpKind value with its parameters. Fields an op does not use are
@@ -426,6 +437,20 @@ int mlxhip_ew_chain(const mlxhip_ew_instr_t* prog, size_t n_instr,
 int mlxhip_attention(const float* q, const float* k, const float* v, float* o,
                      int64_t batch, int64_t tq, int64_t tk, int64_t dh,
                      float scale, int32_t causal, void* stream);
+
+/* Gradient of mlxhip_attention for `batch` packed heads of t queries and t
+ * keys (dh = 64, t a multiple of 64): given Q, K, V, the forward output O
+ * and its cotangent dO ([batch][t][dh] f32 each), writes dQ, dK and dV of the
+ * same shape. No reference counterpart: the reference's Attention op has no
+ * VJP (crates/mlx-autograd/src/vjp.rs:173-176); this is the standard one
+ * (P = softmax(scale Q K^T) under the causal mask, dS = P o (dO V^T - rowsum(dO o O)),
+ * dQ = scale dS K, dK = scale dS^T Q, dV = P^T dO), streamed over blocks of
+ * 64 keys / queries with f32 matrix-core products; nothing of size t x t is
+ * stored. Operands 16-byte aligned; any other shape MLXHIP_ERR_INVALID_ARGUMENT.
+ * Row statistics go to a per-stream workspace. */
+int mlxhip_attention_vjp(const float* q, const float* k, const float* v, const float* o,
+                         const float* dout, float* dq, float* dk, float* dv, int64_t batch,
+                         int64_t t, int64_t dh, float scale, int32_t causal, void* stream);
 
 /* 2-D transpose y[cols, rows] = x[rows, cols]^T of 4-byte elements
  * (transpose, cpu_kernels.rs:232-274, axes = None on rank 2). Bit-exact. */

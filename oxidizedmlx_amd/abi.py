@@ -211,6 +211,7 @@ PROTOTYPES = {
     "mlxhip_ew_chain": (_i, [C.POINTER(mlxhip_ew_instr_t), _sz, C.POINTER(_vp), _sz,
                              _fp, _i64, _vp]),
     "mlxhip_attention": (_i, [_fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64, _f, _i32, _vp]),
+    "mlxhip_attention_vjp": (_i, [_fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64, _f, _i32, _vp]),
     "mlxhip_transpose2d": (_i, [_fp, _fp, _i64, _i64, _vp]),
     "mlxhip_cast": (_i, [_vp, _i32, _vp, _i32, _i64, _vp]),
     "mlxhip_decoder_new": (_vp, [C.POINTER(mlxhip_decoder_config_t)]),

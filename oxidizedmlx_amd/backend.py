@@ -311,6 +311,13 @@ def attention(q, k, v, o, batch: int, tq: int, tk: int, dh: int, scale: float, c
     abi.check(lib().mlxhip_attention(_p(q), _p(k), _p(v), _p(o), batch, tq, tk, dh, scale, int(causal), stream))
 
 
+def attention_vjp(q, k, v, o, do, dq, dk, dv, batch: int, t: int, dh: int, scale: float, causal: bool,
+                  stream=None) -> None:
+    """dQ, dK, dV of fused attention for `batch` packed heads (device buffers)."""
+    abi.check(lib().mlxhip_attention_vjp(_p(q), _p(k), _p(v), _p(o), _p(do), _p(dq), _p(dk), _p(dv), batch, t, dh,
+                                         scale, int(causal), stream))
+
+
 def transpose2d(x, y, rows: int, cols: int, stream=None) -> None:
     abi.check(lib().mlxhip_transpose2d(_p(x), _p(y), rows, cols, stream))
 

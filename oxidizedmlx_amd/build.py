@@ -59,6 +59,7 @@ SOURCES = [
     "kernels/gemm16_f16.hip",
     "kernels/decode.hip",
     "kernels/attention.hip",
+    "kernels/attention_bwd.hip",
 ]
 
 

@@ -48,7 +48,8 @@ const char* op_name(int k) {
         "Constant", "Parameter", "Add", "Sub", "Mul", "Div", "Neg", "Exp", "Log", "Sum", "Mean", "Max",
         "MatMul", "Reshape", "Transpose", "Softmax", "Silu", "Gelu", "LayerNorm", "RmsNorm", "Rope",
         "Broadcast", "Embedding", "ScaledMaskedSoftmax", "Attention", "LayerNormVjp", "RmsNormVjp",
-        "SoftmaxVjp", "SiluVjp", "GeluVjp", "Sqrt", "RoPE", "Narrow", "Concatenate"};
+        "SoftmaxVjp", "SiluVjp", "GeluVjp", "Sqrt", "RoPE", "Narrow", "Concatenate", "HeadAttention",
+        "HeadAttentionVjp"};
     return (k >= 0 && k < MLXHIP_OP_COUNT_) ? names[k] : "?";
 }
 
@@ -276,6 +277,32 @@ int vjp(Builder& b, uint64_t id, const Node& n, uint64_t g, const std::vector<bo
                 mlxhip_op_t o = Builder::op(MLXHIP_OP_SOFTMAX_VJP);
                 o.axis = n.op.op.axis;
                 MLXHIP_SET(0, b.vjp_op(o, g, sm));
+            }
+            return MLXHIP_OK;
+        }
+        case MLXHIP_OP_HEAD_ATTENTION: {
+            // One HeadAttentionVjp node [q, k, v, o = this node, g] gives
+            // [3, heads, t, dh]; input i's gradient is its slice i (a Narrow
+            // along the leading axis, which the stream reads in place).
+            if (!arity(3)) return MLXHIP_ERR_INVALID_ARGUMENT;
+            if (!b.same_shape(g, id, "HeadAttention")) return recorded_status();
+            const std::vector<int64_t> sh = b.shape(id);
+            std::vector<int64_t> vsh{3};
+            vsh.insert(vsh.end(), sh.begin(), sh.end());
+            mlxhip_op_t vo = Builder::op(MLXHIP_OP_HEAD_ATTENTION_VJP);
+            vo.scale = n.op.op.scale;
+            vo.causal = n.op.op.causal;
+            const uint64_t all = b.node(vo, {in[0], in[1], in[2], id, g}, vsh, b.meta(id).dtype);
+            if (!all) return recorded_status();
+            std::vector<int64_t> one{1};
+            one.insert(one.end(), sh.begin(), sh.end());
+            for (int i = 0; i < 3; ++i) {
+                mlxhip_op_t no = Builder::op(MLXHIP_OP_NARROW);
+                no.axis = 0;
+                no.has_axis = 1;
+                no.start = i;
+                no.length = 1;
+                MLXHIP_SET(i, b.reshape(b.node(no, {all}, one, b.meta(id).dtype), sh));
             }
             return MLXHIP_OK;
         }

@@ -451,6 +451,58 @@ int eval_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inp
                 dh, 0, s);
 }
 
+// HeadAttention: the Attention op's arithmetic for every head of
+// [heads, t, dh] operands, in one fused launch when the shape and alignment
+// allow it, else head by head through eval_attention.
+int eval_head_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,
+                        const mlxhip_meta_t& meta, float* out, hipStream_t s, Scratch& scratch) {
+    if (n_inputs != 3) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttention requires exactly 3 inputs [Q, K, V]");
+    const mlxhip_input_t &q = in[0], &k = in[1], &v = in[2];
+    if (q.ndim != 3 || k.ndim != 3 || v.ndim != 3)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttention inputs must be 3-D [heads, t, dh]");
+    const int64_t h = q.shape[0], tq = q.shape[1], dh = q.shape[2], tk = k.shape[1];
+    if (k.shape[0] != h || v.shape[0] != h || k.shape[2] != dh || v.shape[1] != tk || v.shape[2] != dh)
+        return fail_shape({h, tk, dh}, {k.shape[0], k.shape[1], k.shape[2]}, "HeadAttention");
+    MLXHIP_TRY(expect_len(h * tq * dh, numel_of(meta.shape, meta.ndim), "HeadAttention"));
+    if (h * tq * dh == 0) return MLXHIP_OK;
+    if (tk == 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttention: no keys");
+    const uintptr_t al = reinterpret_cast<uintptr_t>(q.data) | reinterpret_cast<uintptr_t>(k.data) |
+                         reinterpret_cast<uintptr_t>(v.data) | reinterpret_cast<uintptr_t>(out);
+    if (attention_fused_supported(dh, tq, tk) && al % 16 == 0 && dh % 4 == 0)
+        return attention_fused(q.data, k.data, v.data, out, h, tq, tk, dh, tq * dh, tk * dh, tk * dh, tq * dh,
+                               op.scale, op.causal, s);
+    const int64_t qs[2] = {tq, dh}, ks[2] = {tk, dh};
+    for (int64_t i = 0; i < h; ++i) {
+        mlxhip_input_t hi[3] = {{q.data + i * tq * dh, (size_t)(tq * dh), qs, 2, q.dtype},
+                                {k.data + i * tk * dh, (size_t)(tk * dh), ks, 2, k.dtype},
+                                {v.data + i * tk * dh, (size_t)(tk * dh), ks, 2, v.dtype}};
+        mlxhip_meta_t m = meta;
+        m.shape = qs;
+        m.ndim = 2;
+        MLXHIP_TRY(eval_attention(op, hi, 3, m, out + i * tq * dh, s, scratch));
+    }
+    return MLXHIP_OK;
+}
+
+// HeadAttentionVjp: [Q, K, V, O, dO] -> [3, heads, t, dh] = dQ, dK, dV.
+int eval_head_attention_vjp(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,
+                            const mlxhip_meta_t& meta, float* out, hipStream_t s) {
+    if (n_inputs != 5)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttentionVjp requires exactly 5 inputs [Q, K, V, O, dO]");
+    const mlxhip_input_t& q = in[0];
+    if (q.ndim != 3) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttentionVjp inputs must be 3-D [heads, t, dh]");
+    for (size_t i = 1; i < 5; ++i)
+        if (in[i].ndim != 3 || in[i].shape[0] != q.shape[0] || in[i].shape[1] != q.shape[1] ||
+            in[i].shape[2] != q.shape[2])
+            return fail_shape(std::vector<int64_t>(q.shape, q.shape + 3),
+                              std::vector<int64_t>(in[i].shape, in[i].shape + in[i].ndim), "HeadAttentionVjp");
+    const int64_t h = q.shape[0], t = q.shape[1], dh = q.shape[2], n = h * t * dh;
+    MLXHIP_TRY(expect_len(3 * n, numel_of(meta.shape, meta.ndim), "HeadAttentionVjp"));
+    if (n == 0) return MLXHIP_OK;
+    return attention_vjp(in[0].data, in[1].data, in[2].data, in[3].data, in[4].data, out, out + n, out + 2 * n, h,
+                         t, dh, op.scale, op.causal, s);
+}
+
 }  // namespace
 
 int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,
@@ -619,6 +671,8 @@ int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_i
                           op.causal, s);
         }
         case MLXHIP_OP_ATTENTION: return eval_attention(op, in, n_inputs, meta, out, s, scratch);
+        case MLXHIP_OP_HEAD_ATTENTION: return eval_head_attention(op, in, n_inputs, meta, out, s, scratch);
+        case MLXHIP_OP_HEAD_ATTENTION_VJP: return eval_head_attention_vjp(op, in, n_inputs, meta, out, s);
         case MLXHIP_OP_LAYER_NORM_VJP:
         case MLXHIP_OP_RMS_NORM_VJP: {
             REQUIRE(0);
@@ -937,6 +991,17 @@ int mlxhip_attention(const float* q, const float* k, const float* v, float* o, i
     if (tk == 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: no keys");
     return attention_fused(q, k, v, o, batch, tq, tk, dh, tq * dh, tk * dh, tk * dh, tq * dh, scale, causal,
                            as_stream(stream));
+}
+
+int mlxhip_attention_vjp(const float* q, const float* k, const float* v, const float* o, const float* dout,
+                         float* dq, float* dk, float* dv, int64_t batch, int64_t t, int64_t dh, float scale,
+                         int32_t causal, void* stream) {
+    MLXHIP_TRY(ensure_device());
+    if (batch < 0 || t < 0 || dh < 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention vjp: negative size");
+    if (batch == 0 || t == 0 || dh == 0) return MLXHIP_OK;
+    if (!q || !k || !v || !o || !dout || !dq || !dk || !dv)
+        return fail(MLXHIP_ERR_NULL_PTR, "attention vjp: null operand");
+    return attention_vjp(q, k, v, o, dout, dq, dk, dv, batch, t, dh, scale, causal, as_stream(stream));
 }
 
 int mlxhip_transpose2d(const float* x, float* y, int64_t rows, int64_t cols, void* stream) {

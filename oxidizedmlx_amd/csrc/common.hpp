@@ -73,7 +73,7 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // outgrown is retired, not freed (a HIP graph recorded earlier may still name
 // it); retired and live blocks are released by release_stream_workspaces(s)
 // after `s` has drained. Calls on different streams use different blocks.
-enum WsSlot { WS_PACK = 0, WS_SPLITK = 1, WS_REDUCE = 2 };
+enum WsSlot { WS_PACK = 0, WS_SPLITK = 1, WS_REDUCE = 2, WS_ATTN = 3 };
 int stream_workspace(hipStream_t s, int slot, size_t bytes, void** out);
 void release_stream_workspaces(hipStream_t s);
 

@@ -129,6 +129,15 @@ int attention_fused(const float* q, const float* k, const float* v, float* o, in
                     int64_t tk, int64_t dh, int64_t sq, int64_t sk, int64_t sv, int64_t so, float scale,
                     int causal, hipStream_t s);
 
+// ── attention_bwd.hip (gradient of fused attention, dQ / dK / dV) ──────────
+// dh == 64, tq == tk a multiple of 64; operands [batch][t][dh], contiguous,
+// 16-byte aligned. Scratch (row log-sum-exp and dO.O) comes from the
+// stream's WS_ATTN workspace.
+bool attention_vjp_supported(int64_t dh, int64_t tq, int64_t tk);
+int attention_vjp(const float* q, const float* k, const float* v, const float* o, const float* dout, float* dq,
+                  float* dk, float* dv, int64_t batch, int64_t t, int64_t dh, float scale, int causal,
+                  hipStream_t s);
+
 // ── gemm.hip ──────────────────────────────────────────────────────────────
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,

@@ -339,6 +339,27 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
                 continue;
             }
         }
+        // Narrow along an axis with only size-1 axes before it takes a
+        // contiguous range of its input: the node aliases that range (node
+        // buffers live until the stream is cleared, like Reshape's).
+        if (n.op.op.kind == MLXHIP_OP_NARROW && n.inputs.size() == 1) {
+            auto src = buffers.find(n.inputs[0]);
+            const std::vector<int64_t>& ish = nodes.at(n.inputs[0]).meta.shape;
+            int64_t ax = n.op.op.axis;
+            if (ax < 0) ax += (int64_t)ish.size();
+            if (src != buffers.end() && ax >= 0 && ax < (int64_t)ish.size()) {
+                int64_t outer = 1, inner = 1;
+                for (int64_t d = 0; d < ax; ++d) outer *= ish[d];
+                for (int64_t d = ax + 1; d < (int64_t)ish.size(); ++d) inner *= ish[d];
+                const int64_t st = n.op.op.start, ln = n.op.op.length;
+                if (outer == 1 && st >= 0 && ln >= 0 && st + ln <= ish[ax] &&
+                    (int64_t)src->second.len == ish[ax] * inner && ln * inner == n.meta.numel()) {
+                    buffers[id] = DevBuf{src->second.ptr + st * inner, (size_t)(ln * inner), false};
+                    eval_calls += 1;
+                    continue;
+                }
+            }
+        }
         // Single node through HipBackend::eval_node. A MatMul operand that is
         // a folded Transpose (or a chain of them) is read from the source
         // with the operand layout flipped once per Transpose; a swapped

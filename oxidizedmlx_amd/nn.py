@@ -107,9 +107,15 @@ class CausalSelfAttention:
     """Causal multi-head self-attention over x [batch*seq, d_model] (rows
     ordered batch-major), with Q/K/V/output projections as Linear layers."""
 
-    def __init__(self, wq: Linear, wk: Linear, wv: Linear, wo: Linear, n_heads: int, batch: int, seq: int):
+    def __init__(self, wq: Linear, wk: Linear, wv: Linear, wo: Linear, n_heads: int, batch: int, seq: int,
+                 fused: bool = False):
         self.wq, self.wk, self.wv, self.wo = wq, wk, wv, wo
         self.h, self.b, self.s = n_heads, batch, seq
+        # fused: the scores, mask, softmax and P.V of every head as one
+        # HeadAttention op (fused forward kernel, fused backward through its
+        # VJP) instead of MatMul, Mul, Add, Softmax, MatMul. Same function;
+        # needs a HIP stream (the oracle has no such op).
+        self.fused = fused
 
     def _heads(self, t: Tensor) -> Tensor:
         # [B*S, D] -> [B, S, H, Dh] -> [B, H, S, Dh] -> [B*H, S, Dh]
@@ -125,6 +131,10 @@ class CausalSelfAttention:
                                       f"batch {self.b} x seq {self.s}, {self.h} heads")
         dh = d // self.h
         q, k, v = self._heads(self.wq(x)), self._heads(self.wk(x)), self._heads(self.wv(x))
+        if self.fused:
+            o = q.head_attention(k, v, 1.0 / math.sqrt(dh), True)        # [B*H, S, Dh]
+            o = o.reshape((self.b, self.h, self.s, dh)).transpose((0, 2, 1, 3)).reshape((bs, d))
+            return self.wo(o)
         scores = q.matmul(k.transpose((0, 2, 1)))                      # [B*H, S, S]
         st = x.stream
         scale = _fixed_constant(("scale", dh), np.array([1.0 / math.sqrt(dh)], np.float32), (), st)
@@ -190,6 +200,9 @@ class BlockConfig:
     batch: int = 4
     mlp_ratio: int = 4
     eps: float = 1e-5
+    # Attention through the fused HeadAttention op (forward and VJP kernels)
+    # instead of the composed MatMul / Softmax graph; HIP streams only.
+    fused_attention: bool = False
 
     @property
     def hidden(self) -> int:
@@ -223,7 +236,7 @@ class TransformerBlock:
         self.norm2 = RmsNorm(cfg.d_model, cfg.eps)
         self.attn = CausalSelfAttention(Linear(p["wq"], p["bq"]), Linear(p["wk"], p["bk"]),
                                         Linear(p["wv"], p["bv"]), Linear(p["wo"], p["bo"]),
-                                        cfg.n_heads, cfg.batch, cfg.seq)
+                                        cfg.n_heads, cfg.batch, cfg.seq, fused=cfg.fused_attention)
         self.mlp = Mlp(Linear(p["w1"], p["b1"]), Linear(p["w2"], p["b2"]))
 
     def forward(self, x: Tensor) -> Tensor:

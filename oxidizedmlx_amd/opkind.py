@@ -24,7 +24,7 @@ KIND = {
     "RmsNorm": 19, "Rope": 20, "Broadcast": 21, "Embedding": 22,
     "ScaledMaskedSoftmax": 23, "Attention": 24, "LayerNormVjp": 25, "RmsNormVjp": 26,
     "SoftmaxVjp": 27, "SiluVjp": 28, "GeluVjp": 29, "Sqrt": 30, "RoPE": 31,
-    "Narrow": 32, "Concatenate": 33,
+    "Narrow": 32, "Concatenate": 33, "HeadAttention": 34, "HeadAttentionVjp": 35,
 }
 NAME = {v: k for k, v in KIND.items()}
 
@@ -177,6 +177,16 @@ class OpKind:
     @staticmethod
     def Attention(scale: float, causal: bool) -> Op:
         return Op("Attention", scale=scale, causal=causal)
+
+    @staticmethod
+    def HeadAttention(scale: float, causal: bool) -> Op:
+        """Attention of every head of Q, K, V [heads, t, dh] (no reference
+        counterpart; differentiable on a HIP stream)."""
+        return Op("HeadAttention", scale=scale, causal=causal)
+
+    @staticmethod
+    def HeadAttentionVjp(scale: float, causal: bool) -> Op:
+        return Op("HeadAttentionVjp", scale=scale, causal=causal)
 
     @staticmethod
     def LayerNormVjp(eps: float) -> Op:

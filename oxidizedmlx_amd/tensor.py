@@ -310,6 +310,20 @@ class Tensor:
         return self._lazy(OpKind.Attention(scale, causal), [self, k, v], self.shape)
 
     # ── row ops (tensor.rs:379-435) ──────────────────────────────────────
+    def head_attention(self, k: "Tensor", v: "Tensor", scale: float, causal: bool) -> "Tensor":
+        """Attention of every head: Q [H, Tq, Dh], K/V [H, Tk, Dh] -> [H, Tq, Dh],
+        per head the arithmetic of ``attention``. No reference counterpart;
+        unlike ``attention`` it has a VJP (one fused backward op) on a HIP
+        stream, so a block can train through the fused kernels."""
+        if len(self.shape) != 3 or len(k.shape) != 3 or len(v.shape) != 3:
+            raise abi.InvalidArgument("head_attention requires 3D tensors [heads, seq, head_dim]")
+        if k.shape[0] != self.shape[0] or k.shape[2] != self.shape[2]:
+            raise abi.ShapeMismatch(f"expected {list(self.shape)}, got {list(k.shape)}",
+                                    list(self.shape), list(k.shape))
+        if v.shape != k.shape:
+            raise abi.ShapeMismatch(f"expected {list(k.shape)}, got {list(v.shape)}", list(k.shape), list(v.shape))
+        return self._lazy(OpKind.HeadAttention(scale, causal), [self, k, v], self.shape)
+
     def softmax(self, axis: int) -> "Tensor":
         nd = len(self.shape)
         ax = axis + nd if axis < 0 else axis

@@ -277,6 +277,54 @@ def test_hip_block_config4_prefix_matches_oracle():
     assert not bad, "; ".join(bad)
 
 
+def compare_block_grads(gh, go, loss_h, loss_o):
+    assert abs(loss_h - loss_o) <= 1e-4 * max(1.0, abs(loss_o)), (loss_h, loss_o)
+    top = max(float(np.abs(g).max()) for g in go.values())
+    bad = []
+    for k in go:
+        scale = max(float(np.abs(go[k]).max()), 1e-3 * top)
+        err = float(np.abs(gh[k].astype(np.float64) - go[k]).max())
+        print(f"  {k}: max abs err {err:.3e} (scale {scale:.3e})", flush=True)
+        if err > 1e-4 * scale:
+            bad.append(f"{k}: max abs err {err:.3e} (scale {scale:.3e})")
+    assert not bad, "; ".join(bad)
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip", "oracle_lib")
+def test_hip_block_fused_attention_matches_oracle():
+    """The block with its attention as one HeadAttention op (fused forward,
+    fused VJP) against the oracle's autograd of the composed graph (MatMul,
+    scale, -1e9 mask, Softmax, MatMul): same loss and gradients within the
+    block tests' tolerance. Head dim 64, two 64-position blocks."""
+    import dataclasses
+    cfg = nn.BlockConfig(d_model=128, n_heads=2, seq=128, batch=2)
+    arrs, x, gy = block_arrays(cfg, seed=17)
+    loss_h, gh = block_grads(hip_stream(), dataclasses.replace(cfg, fused_attention=True), arrs, x, gy)
+    loss_o, go = block_grads(OracleStream(), cfg, arrs, x, gy)
+    compare_block_grads(gh, go, loss_h, loss_o)
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip", "oracle_lib")
+def test_hip_block_fused_attention_config4_prefix_matches_oracle():
+    """Config 4 at full size with fused attention on the GPU against the
+    oracle's composed block on the causal prefix (as in the composed
+    config-4 test above): the x gradient is exactly zero past the prefix."""
+    import dataclasses
+    cfg = nn.BlockConfig()
+    P = 64
+    arrs, x, gy = block_arrays(cfg, seed=31)
+    gy_masked = np.zeros_like(gy)
+    gy_masked[:P] = gy[:P]
+    print(f"config 4 with fused attention on the GPU, loss on the first {P} positions of sequence 0", flush=True)
+    loss_h, gh = block_grads(hip_stream(), dataclasses.replace(cfg, fused_attention=True), arrs, x, gy_masked)
+    cfg_p = nn.BlockConfig(d_model=cfg.d_model, n_heads=cfg.n_heads, seq=P, batch=1, eps=cfg.eps)
+    loss_o, go = block_grads(OracleStream(), cfg_p, arrs, x[:P], gy[:P])
+    assert not gh["x"][P:].any(), "x gradient outside the prefix is not zero"
+    compare_block_grads(dict(gh, x=gh["x"][:P]), go, loss_h, loss_o)
+
+
 @pytest.mark.gpu
 @pytest.mark.usefixtures("hip")
 def test_hip_block_async_eval_matches_sync():
