@@ -112,6 +112,30 @@ __device__ inline void block_store(float* lds, int tid, const f32x4 (&r)[4]) {
     }
 }
 
+// Workgroup id -> (head, block). Under the causal mask a block's work grows
+// with its index (dQ: key blocks 0..qb) or shrinks (dK/dV: query blocks
+// kb..nb-1). Two workgroups run on each CU at once, and the dispatcher fills
+// one slot on every CU with the first half of the ids before the second
+// slot: ids i and i + half are paired as blocks b and nb - 1 - b of one
+// head, so every CU gets the same work. `heavy_high`: block nb - 1 is the
+// heaviest (dQ) rather than block 0 (dK/dV).
+__device__ inline void block_of(int id, int heads, int nb, bool heavy_high, int* head, int* blk) {
+    const int hp = nb / 2, half = heads * hp;
+    int b;
+    if (id < half) {                 // the heavier block of each pair
+        *head = id / hp;
+        b = nb - 1 - id % hp;
+    } else if (id < 2 * half) {      // its partner
+        const int j = id - half;
+        *head = j / hp;
+        b = j % hp;
+    } else {                         // odd nb: the middle block of each head
+        *head = id - 2 * half;
+        b = hp;
+    }
+    *blk = heavy_high ? b : nb - 1 - b;
+}
+
 // ── dQ, L, D ───────────────────────────────────────────────────────────────
 // S^T tile = K Q^T (rows keys, columns queries): the lane's column is query
 // q = qb*64 + 32 qh + c, so L_q and D_q are per-lane scalars.
@@ -126,8 +150,9 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     float* Ks = smem;
     float* Vs = smem + BT * PITCH;
     const int nqb = T / BT;
-    const int64_t head = blockIdx.x / nqb;
-    const int qb = blockIdx.x % nqb;
+    int head_i, qb;
+    block_of((int)blockIdx.x, (int)(gridDim.x / nqb), nqb, true, &head_i, &qb);
+    const int64_t head = head_i;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int qh = wave & 1, kh = wave >> 1, c = lane & 31, h = lane >> 5;
     const int64_t hoff = head * (int64_t)T * DH;
@@ -153,21 +178,25 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     // query, and the two waves of a query half different key halves: their
     // (m, l) pairs are combined in a fixed order (lanes, then kh 0 before
     // kh 1), so both waves get the same L_q.
-    // Each block's loads are issued while the previous block is computed.
+    // Blocks are staged without prefetch: two workgroups share each CU and
+    // one computes while the other waits for its loads (registers for a
+    // prefetch would leave room for only one).
     float m = -INFINITY, l = 0.0f;
-    block_load(Kh, 0, tid, kc);
     for (int kb = 0; kb < nkb; ++kb) {
+        block_load(Kh, kb * BT, tid, kc);
         __syncthreads();  // the previous block's readers are done
         block_store(Ks, tid, kc);
         __syncthreads();
-        // The next block, or pass 2's first one (block 0) after the last.
-        block_load(Kh, (kb + 1 < nkb ? kb + 1 : 0) * BT, tid, kc);
-        f32x16 sa = zero16();
+        // Two independent accumulator chains (step s feeds chain s % 2),
+        // summed in chain order: one chain of dependent MFMAs runs at about
+        // half the matrix pipe's rate. Pass 2 sums S the same way.
+        f32x16 s2[2] = {zero16(), zero16()};
         float kr[32];
         lds_row32(Ks + (32 * kh + c) * PITCH + 32 * h, kr);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < 32; ++s) mfma(kr[s], qr[s], sa);  // the same chain as pass 2
+        for (int s = 0; s < 32; ++s) mfma(kr[s], qr[s], s2[s & 1]);
+        const f32x16 sa = s2[0] + s2[1];
         float x[16], mt = -INFINITY;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -211,28 +240,37 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
 
     // Pass 2: dQ^T (rows d, columns queries) += K^T dS^T over the wave's keys.
-    block_load(Vh, 0, tid, vc);
     f32x16 dq0 = zero16(), dq1 = zero16();
     for (int kb = 0; kb < nkb; ++kb) {
+        block_load(Kh, kb * BT, tid, kc);
+        block_load(Vh, kb * BT, tid, vc);
         __syncthreads();
         block_store(Ks, tid, kc);
         block_store(Vs, tid, vc);
         __syncthreads();
-        // Unconditional (the last block reloads itself): no load sits under a
-        // branch, so the register arrays stay in registers.
-        const int nb = kb + 1 < nkb ? kb + 1 : kb;
-        block_load(Kh, nb * BT, tid, kc);
-        block_load(Vh, nb * BT, tid, vc);
-        f32x16 sa = zero16(), pa = zero16();
-        float kr[32], vr[32];
-        lds_row32(Ks + (32 * kh + c) * PITCH + 32 * h, kr);
-        lds_row32(Vs + (32 * kh + c) * PITCH + 32 * h, vr);
-        __builtin_amdgcn_sched_barrier(0);
+        f32x16 s2[2] = {zero16(), zero16()}, p2[2] = {zero16(), zero16()};
+        // Two halves of 16 steps, each half's LDS reads issued before its MFMAs.
 #pragma unroll
-        for (int s = 0; s < 32; ++s) {
-            mfma(kr[s], qr[s], sa);   // S^T
-            mfma(vr[s], dor[s], pa);  // dP^T = V dO^T
+        for (int s0 = 0; s0 < 32; s0 += 16) {
+            float kr[16], vr[16];
+            const f32x4* kp = reinterpret_cast<const f32x4*>(Ks + (32 * kh + c) * PITCH + 32 * h + s0);
+            const f32x4* vp = reinterpret_cast<const f32x4*>(Vs + (32 * kh + c) * PITCH + 32 * h + s0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 a = kp[i], b = vp[i];
+                kr[4 * i] = a[0], kr[4 * i + 1] = a[1], kr[4 * i + 2] = a[2], kr[4 * i + 3] = a[3];
+                vr[4 * i] = b[0], vr[4 * i + 1] = b[1], vr[4 * i + 2] = b[2], vr[4 * i + 3] = b[3];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                mfma(kr[i], qr[s0 + i], s2[i & 1]);     // S^T, as in pass 1
+                mfma(vr[i], dor[s0 + i], p2[i & 1]);    // dP^T = V dO^T
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+        const f32x16 sa = s2[0] + s2[1];
+        const f32x16 pa = p2[0] + p2[1];
         float ds[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -301,8 +339,9 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     float* Qs = smem;
     float* dOs = smem + BT * PITCH;
     const int nkb = T / BT;
-    const int64_t head = blockIdx.x / nkb;
-    const int kb = blockIdx.x % nkb;
+    int head_i, kb;
+    block_of((int)blockIdx.x, (int)(gridDim.x / nkb), nkb, false, &head_i, &kb);
+    const int64_t head = head_i;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int qh = wave & 1, kh = wave >> 1, c = lane & 31, h = lane >> 5;
     const int64_t hoff = head * (int64_t)T * DH;
@@ -313,14 +352,14 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     load_row_half(Kh, j, h, kr);
     load_row_half(Vh, j, h, vr);
     f32x16 dk0 = zero16(), dk1 = zero16(), dv0 = zero16(), dv1 = zero16();
-    // Each query block's loads are issued while the previous one is computed.
+    // Blocks staged without prefetch (two workgroups per CU, as in the dQ kernel).
     f32x4 qc[4], oc[4];
     const int qb0 = causal ? kb : 0, nqb = T / BT;
     const int lrow = tid < BT ? tid : 0;
-    block_load(Qh, qb0 * BT, tid, qc);
-    block_load(dOh, qb0 * BT, tid, oc);
-    float lv = lse[head * T + qb0 * BT + lrow], dv = dd[head * T + qb0 * BT + lrow];
     for (int qb = qb0; qb < nqb; ++qb) {
+        block_load(Qh, qb * BT, tid, qc);
+        block_load(dOh, qb * BT, tid, oc);
+        const float lv = lse[head * T + qb * BT + lrow], dv = dd[head * T + qb * BT + lrow];
         __syncthreads();
         block_store(Qs, tid, qc);
         block_store(dOs, tid, oc);
@@ -329,21 +368,29 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
             Ds[tid] = dv;
         }
         __syncthreads();
-        const int nb = qb + 1 < nqb ? qb + 1 : qb;  // the last block reloads itself
-        block_load(Qh, nb * BT, tid, qc);
-        block_load(dOh, nb * BT, tid, oc);
-        lv = lse[head * T + nb * BT + lrow];
-        dv = dd[head * T + nb * BT + lrow];
-        f32x16 sa = zero16(), pa = zero16();
-        float qrow[32], orow[32];
-        lds_row32(Qs + (32 * qh + c) * PITCH + 32 * h, qrow);
-        lds_row32(dOs + (32 * qh + c) * PITCH + 32 * h, orow);
-        __builtin_amdgcn_sched_barrier(0);
+        f32x16 s2[2] = {zero16(), zero16()}, p2[2] = {zero16(), zero16()};
+        // Two halves of 16 steps, each half's LDS reads issued before its MFMAs.
 #pragma unroll
-        for (int s = 0; s < 32; ++s) {
-            mfma(qrow[s], kr[s], sa);  // S = Q K^T
-            mfma(orow[s], vr[s], pa);  // dP = dO V^T
+        for (int s0 = 0; s0 < 32; s0 += 16) {
+            float qrow[16], orow[16];
+            const f32x4* qp = reinterpret_cast<const f32x4*>(Qs + (32 * qh + c) * PITCH + 32 * h + s0);
+            const f32x4* op = reinterpret_cast<const f32x4*>(dOs + (32 * qh + c) * PITCH + 32 * h + s0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 a = qp[i], b = op[i];
+                qrow[4 * i] = a[0], qrow[4 * i + 1] = a[1], qrow[4 * i + 2] = a[2], qrow[4 * i + 3] = a[3];
+                orow[4 * i] = b[0], orow[4 * i + 1] = b[1], orow[4 * i + 2] = b[2], orow[4 * i + 3] = b[3];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                mfma(qrow[i], kr[s0 + i], s2[i & 1]);  // S = Q K^T (chains as in the dQ kernel)
+                mfma(orow[i], vr[s0 + i], p2[i & 1]);  // dP = dO V^T
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+        const f32x16 sa = s2[0] + s2[1];
+        const f32x16 pa = p2[0] + p2[1];
         float p[16], ds[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -354,22 +401,27 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
         }
         // dV^T (rows d, columns keys) += dO^T P, dK^T += Q^T dS; slot (s, h)
         // is query 32 qh + crow(s, h): this lane's p[s] and ds[s].
-        float oa[16], ob[16], qa[16], qb2[16];
+        // Two halves of 8 steps, each half's LDS reads issued before its MFMAs.
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const int qi = 32 * qh + crow(s, h);
-            oa[s] = dOs[qi * PITCH + c];
-            ob[s] = dOs[qi * PITCH + 32 + c];
-            qa[s] = Qs[qi * PITCH + c];
-            qb2[s] = Qs[qi * PITCH + 32 + c];
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        for (int s0 = 0; s0 < 16; s0 += 8) {
+            float oa[8], ob[8], qa[8], qb2[8];
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            mfma(oa[s], p[s], dv0);
-            mfma(ob[s], p[s], dv1);
-            mfma(qa[s], ds[s], dk0);
-            mfma(qb2[s], ds[s], dk1);
+            for (int i = 0; i < 8; ++i) {
+                const int qi = 32 * qh + crow(s0 + i, h);
+                oa[i] = dOs[qi * PITCH + c];
+                ob[i] = dOs[qi * PITCH + 32 + c];
+                qa[i] = Qs[qi * PITCH + c];
+                qb2[i] = Qs[qi * PITCH + 32 + c];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                mfma(oa[i], p[s0 + i], dv0);
+                mfma(ob[i], p[s0 + i], dv1);
+                mfma(qa[i], ds[s0 + i], dk0);
+                mfma(qb2[i], ds[s0 + i], dk1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     // Add the qh = 1 partials into the qh = 0 waves, then write dK and dV.
