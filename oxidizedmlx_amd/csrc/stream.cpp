@@ -392,12 +392,26 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         const mlxhip_meta_t meta = n.meta.c();
         eval_calls += covered;
         launches += 1;
-        rc = eval_node_device(op, ins.data(), ins.size(), meta, out, hs, scratch, hint);
+        // A leaf axis reduction over a long axis runs on the side queue.
+        hipStream_t q = hs;
+        const int kind = en.op.op.kind;
+        if ((kind == MLXHIP_OP_SUM || kind == MLXHIP_OP_MEAN || kind == MLXHIP_OP_MAX) && en.op.op.has_axis &&
+            !swapped && consumers[id] == 0 && ins.size() == 1 && ins[0].ndim >= 1) {
+            int64_t ax = en.op.op.axis;
+            if (ax < 0) ax += (int64_t)ins[0].ndim;
+            if (ax >= 0 && ax < (int64_t)ins[0].ndim && ins[0].shape[ax] >= 512 && (rc = fork_side(&q)) != MLXHIP_OK)
+                break;
+        }
+        rc = eval_node_device(op, ins.data(), ins.size(), meta, out, q, scratch, hint);
         if (rc != MLXHIP_OK) {
             release_later(out);
             buffers.erase(id);
             break;
         }
+    }
+    {
+        const int jr = join_side();
+        if (rc == MLXHIP_OK) rc = jr;
     }
     // Scratch may only return to the pool after the kernels using it finish.
     if (async_eval) {

@@ -87,13 +87,50 @@ struct mlxhip_stream_t {
     std::vector<std::pair<size_t, void*>> pending;
     hipStream_t hs = nullptr;
     int device = 0;
+    // A second queue for leaf reductions (created on first use): an axis
+    // reduction that no node consumes is a long chain of dependent adds on a
+    // few CUs (the bias gradients of a block), and runs beside the rest of
+    // the evaluation instead of between its kernels. It starts after
+    // everything queued on hs before it (fork event), and hs waits for it
+    // at the end of the evaluation (join event), so to every later user the
+    // two queues are one. Default priority, like hs.
+    hipStream_t side = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+    bool side_pending = false;
 
     ~mlxhip_stream_t() {
+        if (side) (void)hipStreamSynchronize(side);
         if (hs) (void)hipStreamSynchronize(hs);
         for (auto& b : pending) mlxhip::pool_release(b.second);
         for (auto& kv : buffers)
             if (kv.second.owned) mlxhip::pool_release(kv.second.ptr);
+        if (fork_ev) (void)hipEventDestroy(fork_ev);
+        if (join_ev) (void)hipEventDestroy(join_ev);
+        if (side) (void)hipStreamDestroy(side);
         if (hs) (void)hipStreamDestroy(hs);
+    }
+
+    // The side queue, ready to start after all work queued so far on hs.
+    int fork_side(hipStream_t* out) {
+        if (!side) {
+            MLXHIP_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+            MLXHIP_HIP(hipEventCreateWithFlags(&fork_ev, hipEventDisableTiming));
+            MLXHIP_HIP(hipEventCreateWithFlags(&join_ev, hipEventDisableTiming));
+        }
+        MLXHIP_HIP(hipEventRecord(fork_ev, hs));
+        MLXHIP_HIP(hipStreamWaitEvent(side, fork_ev, 0));
+        side_pending = true;
+        *out = side;
+        return MLXHIP_OK;
+    }
+
+    // hs waits for the side queue's work (end of an evaluation).
+    int join_side() {
+        if (!side_pending) return MLXHIP_OK;
+        side_pending = false;
+        MLXHIP_HIP(hipEventRecord(join_ev, side));
+        MLXHIP_HIP(hipStreamWaitEvent(hs, join_ev, 0));
+        return MLXHIP_OK;
     }
 
     // Waits for every kernel of this stream, then returns the blocks of

@@ -416,6 +416,33 @@ def test_sum_axis_matches_sequential_fold_bitwise(shape, axis, kind):
     np.testing.assert_array_equal(res[0], res[1])
 
 
+@pytest.mark.parametrize("async_eval", [False, True])
+def test_leaf_reductions_beside_other_work(async_eval):
+    """Axis reductions over long axes that no node consumes (a block's bias
+    gradients) run on the stream's second queue beside the other kernels:
+    several of them, read right after the evaluation, equal the oracle bit
+    for bit, and so does the work they overlapped."""
+    x0, w0 = synth.normal(541, (1024, 256)), synth.normal(542, (256, 512))
+    res = []
+    for s in ((HipStream(async_eval=True) if async_eval else HipStream()), cpu_ref_stream()):
+        x = s.add_constant(x0, meta((1024, 256)))
+        w = s.add_constant(w0, meta((256, 512)))
+        y = s.add_op(OpKind.MatMul, [x, w], meta((1024, 512)))
+        outs = [y, s.add_op(OpKind.Sum(0), [y], meta((512,))), s.add_op(OpKind.Mean(0), [x], meta((256,))),
+                s.add_op(OpKind.Max(-2), [y], meta((512,))), s.add_op(OpKind.Neg, [y], meta((1024, 512)))]
+        s.eval_many(outs)
+        res.append([s.get_buffer(o) for o in outs])
+    for i, (a, b) in enumerate(zip(*res)):
+        if i in (0, 4):
+            assert_allclose(a, b, 1e-5 * float(np.abs(b).max()), 1e-5, f"output {i}")
+        else:
+            # the fold of the GPU's own product equals the oracle's fold of it
+            src = res[0][0].reshape(1024, 512) if i != 2 else x0
+            want = {1: np.add.accumulate(src, axis=0)[-1], 2: (np.add.accumulate(src, axis=0)[-1] / np.float32(1024)),
+                    3: src.max(axis=0)}[i]
+            np.testing.assert_array_equal(a, want.astype(np.float32), err_msg=f"output {i}")
+
+
 @pytest.mark.parametrize("fusion", [False, True])
 def test_transpose_rewrites_match_unfused(fusion):
     # transpose(transpose(W)) read by a MatMul folds to W itself; a Transpose
