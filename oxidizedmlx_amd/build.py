@@ -57,6 +57,7 @@ SOURCES = [
     "kernels/gemm_f32.hip",
     "kernels/gemm16_bf16.hip",
     "kernels/gemm16_f16.hip",
+    "kernels/gemm16_x6.hip",
     "kernels/decode.hip",
     "kernels/attention.hip",
     "kernels/attention_bwd.hip",

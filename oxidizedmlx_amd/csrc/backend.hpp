@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "../../include/mlxhip.h"
+#include "kernels.hpp"
 
 namespace mlxhip {
 
@@ -27,6 +28,15 @@ size_t pool_block_size(void* p);
 // by the owner after its stream has been synchronised.
 struct Scratch {
     std::vector<void*> blocks;
+    // Split-f32 planes of the evaluation's f32 products, in blocks of this
+    // scratch (they live exactly as long).
+    PlaneCache planes;
+    Scratch() {
+        planes.alloc = [](void* ctx, size_t bytes) { return static_cast<Scratch*>(ctx)->get_bytes(bytes); };
+        planes.ctx = this;
+    }
+    Scratch(const Scratch&) = delete;
+    Scratch& operator=(const Scratch&) = delete;
     float* get(size_t n_floats);
     void* get_bytes(size_t bytes);
     void release_all();

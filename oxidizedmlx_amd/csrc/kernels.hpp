@@ -7,6 +7,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 #include "../../include/mlxhip.h"
 
@@ -139,9 +140,26 @@ int attention_vjp(const float* q, const float* k, const float* v, const float* o
                   hipStream_t s);
 
 // ── gemm.hip ──────────────────────────────────────────────────────────────
+// bf16 planes of f32 operands (the split-f32 GEMM) made during one graph
+// evaluation, kept for its later products of the same stored matrices: a
+// node's buffer is written once and not again while the evaluation runs.
+// Blocks come from alloc(ctx, bytes) and must outlive the evaluation's
+// kernels (the evaluation's Scratch).
+struct PlaneCache {
+    struct Entry {
+        const void* src;
+        int64_t ld, stride, rows, cols, batch;
+        uint16_t* planes;  // three planes of batch * rows_p * cols_p, then the flag word
+        uint32_t* flag;
+        uint32_t gen;
+    };
+    std::vector<Entry> entries;
+    void* (*alloc)(void* ctx, size_t bytes) = nullptr;
+    void* ctx = nullptr;
+};
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
-         int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s);
+         int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, PlaneCache* planes = nullptr);
 // gemm_small.hip: f32 products small enough for one or two rounds of 32 x 32
 // tiles with K <= 512, one launch, no workspace, any alignment.
 bool gemm_small_f32_fits(int64_t m, int64_t n, int64_t k, int64_t batch);

@@ -6,6 +6,7 @@
 #include "gemm16_impl.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -199,8 +200,9 @@ int pack2(int dt, const PackPair& pp, int64_t batch, hipStream_t s) {
 
 // MLXHIP_GEMM_PATH: unset/"auto" = choose by shape, "general" = always the
 // general kernel, "lds16" = the direct-to-LDS 16-bit kernel whenever the
-// operands allow it ("lds16_256" / "lds16_128": with that block size). Read
-// on every call so one process (the tests) can cover every kernel.
+// operands allow it ("lds16_256" / "lds16_128": with that block size),
+// "x6" = every f32 product through the split-f32 kernel. Read on every call
+// so one process (the tests) can cover every kernel.
 int gemm_path() {
     const char* e = getenv("MLXHIP_GEMM_PATH");
     if (!e) return 0;
@@ -208,6 +210,7 @@ int gemm_path() {
     if (!strcmp(e, "lds16")) return 2;
     if (!strcmp(e, "lds16_256")) return 3;
     if (!strcmp(e, "lds16_128")) return 4;
+    if (!strcmp(e, "x6")) return 5;
     return 0;
 }
 
@@ -287,14 +290,207 @@ int fixed_scratch(void** out) {
 int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
               int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
               int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, bool padded,
-              FixedScratch* fs);
+              FixedScratch* fs, PlaneCache* cache = nullptr);
+
+// Generation numbers of split-f32 products: each call's flag value.
+std::atomic<uint32_t> g_x6_gen{0};
+
+// f32 product through the bf16 planes (gemm16_x6.hip): one launch splits
+// the operands (those `cache` does not already hold), one runs the plane
+// products (and, when split over K, one sums the partials). Sets *ran =
+// false, doing nothing, when the planes would not fit the kernel's 32-bit
+// buffer offsets.
+//
+// Planes hold the operand as stored ([rows][cols] per batch slice) with both
+// extents padded with zeros to multiples of 32, which serves it in either
+// role and either orientation: K, whichever extent it is, becomes whole K
+// tiles, and the padded M / N rows only feed C elements that are not stored.
+int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const float* a, int64_t lda,
+            int64_t stride_a, const float* b, int64_t ldb, int64_t stride_b, float* c, int64_t ldc,
+            int64_t stride_c, hipStream_t s, PlaneCache* cache, bool* ran) {
+    *ran = false;
+    const int64_t kp = ceil_div(k, 32) * 32;  // segment length: whole K tiles
+    struct Operand {
+        X6SplitOp op;
+        bool fresh;  // to be split by this call
+    };
+    Operand opd[2];
+    const float* srcs[2] = {a, b};
+    const int64_t lds[2] = {lda, ldb}, strides[2] = {stride_a, stride_b};
+    const int64_t rows[2] = {ta ? k : m, tb ? n : k}, cols[2] = {ta ? m : k, tb ? k : n};
+    for (int i = 0; i < 2; ++i) {
+        X6SplitOp& o = opd[i].op;
+        o = X6SplitOp{};
+        o.src = srcs[i];
+        o.ld = lds[i];
+        o.stride = batch > 1 ? strides[i] : 0;
+        o.rows = rows[i];
+        o.cols = cols[i];
+        o.rows_p = ceil_div(rows[i], 32) * 32;
+        o.cols_p = ceil_div(cols[i], 32) * 32;
+        o.plane = batch * o.rows_p * o.cols_p;
+        o.chunks = o.plane / 8;
+        // The descriptor of one slice spans two whole planes plus the slice.
+        if (o.chunks >= ((int64_t)1 << 31) ||
+            (2 * o.plane + o.rows_p * o.cols_p) * 2 >= (int64_t)gemm16::OOB - 4096)
+            return MLXHIP_OK;
+        opd[i].fresh = true;
+    }
+    auto same = [](const X6SplitOp& x, const X6SplitOp& y) {
+        return x.src == y.src && x.ld == y.ld && x.stride == y.stride && x.rows == y.rows && x.cols == y.cols;
+    };
+    auto new_gen = [] {
+        uint32_t g = 0;
+        while (g == 0) g = ++g_x6_gen;
+        return g;
+    };
+    const size_t flag_room = 256;
+    auto plane_bytes = [](const X6SplitOp& o) { return ((size_t)(3 * o.plane * 2) + 255) & ~size_t(255); };
+    if (cache && cache->alloc) {
+        for (int i = 0; i < 2; ++i) {
+            X6SplitOp& o = opd[i].op;
+            for (const PlaneCache::Entry& e : cache->entries)
+                if (e.src == o.src && e.ld == o.ld && e.stride == o.stride && e.rows == o.rows && e.cols == o.cols &&
+                    e.batch == batch) {
+                    o.dst = e.planes;
+                    o.flag = e.flag;
+                    o.gen = e.gen;
+                    opd[i].fresh = false;
+                    break;
+                }
+            if (!opd[i].fresh) continue;
+            if (i == 1 && same(o, opd[0].op)) {  // A and B are one matrix, split above
+                o.dst = opd[0].op.dst;
+                o.flag = opd[0].op.flag;
+                o.gen = opd[0].op.gen;
+                opd[i].fresh = false;
+                continue;
+            }
+            const size_t pb = plane_bytes(o);
+            char* blk = static_cast<char*>(cache->alloc(cache->ctx, pb + flag_room));
+            if (!blk) return fail(MLXHIP_ERR_FFI_FAILED, "gemm: device allocation of %zu bytes failed", pb + flag_room);
+            o.dst = reinterpret_cast<uint16_t*>(blk);
+            o.flag = reinterpret_cast<uint32_t*>(blk + pb);
+            o.gen = new_gen();
+            cache->entries.push_back(PlaneCache::Entry{o.src, o.ld, o.stride, o.rows, o.cols, batch, o.dst, o.flag,
+                                                       o.gen});
+        }
+    } else {
+        const bool one = same(opd[0].op, opd[1].op);
+        const size_t pa = plane_bytes(opd[0].op), pb = one ? 0 : plane_bytes(opd[1].op);
+        void* ws = nullptr;
+        MLXHIP_TRY(stream_workspace(s, WS_PACK, pa + pb + 2 * flag_room, &ws));
+        char* base = static_cast<char*>(ws);
+        opd[0].op.dst = reinterpret_cast<uint16_t*>(base);
+        opd[0].op.flag = reinterpret_cast<uint32_t*>(base + pa + pb);
+        opd[0].op.gen = new_gen();
+        if (one) {
+            opd[1].op.dst = opd[0].op.dst;
+            opd[1].op.flag = opd[0].op.flag;
+            opd[1].op.gen = opd[0].op.gen;
+            opd[1].fresh = false;
+        } else {
+            opd[1].op.dst = reinterpret_cast<uint16_t*>(base + pa);
+            opd[1].op.flag = reinterpret_cast<uint32_t*>(base + pa + pb + flag_room);
+            opd[1].op.gen = new_gen();
+        }
+    }
+    X6SplitPair sp{};
+    for (int i = 0; i < 2; ++i)
+        if (opd[i].fresh) sp.op[sp.n++] = opd[i].op;
+    const X6SplitOp &oa = opd[0].op, &ob = opd[1].op;
+
+    gemm16::Args h{};
+    h.m = m;
+    h.n = n;
+    h.k = kp;
+    h.a = oa.dst;
+    h.lda = oa.cols_p;
+    h.sa = oa.rows_p * oa.cols_p;
+    h.b = ob.dst;
+    h.ldb = ob.cols_p;
+    h.sb = ob.rows_p * ob.cols_p;
+    h.c = c;
+    h.ldc = ldc;
+    h.sc = stride_c;
+    h.a_bytes = (uint32_t)((2 * oa.plane + h.sa) * 2);
+    h.b_bytes = (uint32_t)((2 * ob.plane + h.sb) * 2);
+    h.plane_a = (uint32_t)(oa.plane * 2);
+    h.plane_b = (uint32_t)(ob.plane * 2);
+    h.fa = a;
+    h.flda = lda;
+    h.fsa = stride_a;
+    h.fb = b;
+    h.fldb = ldb;
+    h.fsb = stride_b;
+    h.fk = k;
+    h.flag_a = oa.flag;
+    h.gen_a = oa.gen;
+    h.flag_b = ob.flag;
+    h.gen_b = ob.gen;
+
+    // Block tile and split over the 6 k segments of depth kp (measured on
+    // the config-4 shapes, split included): 256x256 blocks split over K to
+    // one workgroup per CU when each split keeps at least 3072 k (96 K
+    // tiles: 2048x4096x1024 125 us split 2 against 141 us unsplit and 150 us
+    // with 128x128 blocks; 4096x1024x2048 126 us split 4 against 141 us with
+    // 128x128 blocks split 2); otherwise 128x128 blocks split to about one
+    // workgroup per CU (2048x1024x1024: 51 us split 2, 69 us unsplit).
+    // MLXHIP_X6="cfg,splits" forces them (tuning).
+    const int64_t kv = gemm16::X6_SEGS * kp;
+    const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256) * batch;
+    const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * batch;
+    int sp_big = 1;
+    while (sp_big < 8 && big_tiles * sp_big < 256) sp_big *= 2;
+    int cfg = 0, sp_k = sp_big;
+    if (big_tiles * sp_big < 256 || kv / sp_big < 3072) {
+        cfg = 1;
+        sp_k = 1;
+        while (sp_k < 8 && mid_tiles * sp_k < 256 && kv / (2 * sp_k) >= 256) sp_k *= 2;
+    }
+    if (const char* e = getenv("MLXHIP_X6")) {
+        int cf = 0, v = 0;
+        if (sscanf(e, "%d,%d", &cf, &v) == 2 && (cf == 0 || cf == 1) && v >= 1 && v <= 8) {
+            cfg = cf;
+            sp_k = v;
+        }
+    }
+    if (batch * sp_k > 65535) sp_k = 1;
+    if (sp.n) MLXHIP_TRY(x6_split(sp, s));
+    if (sp_k == 1) {
+        MLXHIP_TRY(gemm16_x6(ta, tb, h, batch, cfg, s));
+        *ran = true;
+        return MLXHIP_OK;
+    }
+    h.k_chunk = ceil_div(ceil_div(kv, sp_k), 32) * 32;
+    h.splits = (int)ceil_div(kv, h.k_chunk);
+    const int64_t ldw = ceil_div(n, 4) * 4;
+    void* part = nullptr;
+    MLXHIP_TRY(stream_workspace(s, WS_SPLITK, (size_t)(batch * h.splits * m * ldw) * sizeof(float), &part));
+    h.c = part;
+    h.ldc = ldw;
+    h.sc = m * ldw;
+    MLXHIP_TRY(gemm16_x6(ta, tb, h, batch, cfg, s));
+    MLXHIP_TRY(splitk_reduce(MLXHIP_DTYPE_F32, static_cast<const float*>(part), c, m, n, ldw, ldc, stride_c,
+                             h.splits, batch, s));
+    *ran = true;
+    return MLXHIP_OK;
+}
+
+// Whether an f32 product goes through the split-f32 kernel (path 0: by
+// shape).
+bool use_x6(int path, int64_t m, int64_t n, int64_t k, int64_t batch) {
+    if (path == 5) return true;
+    if (path != 0) return false;
+    return m >= 256 && n >= 256 && k >= 256 && (double)m * (double)n * (double)k * (double)batch >= 2147483648.0;
+}
 }  // namespace
 
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
-         int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s) {
+         int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, PlaneCache* planes) {
     return gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
-                     ldc, stride_c, s, false, nullptr);
+                     ldc, stride_c, s, false, nullptr, planes);
 }
 
 int gemm_noalloc(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
@@ -314,7 +510,7 @@ namespace {
 int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
               int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
               int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, bool padded,
-              FixedScratch* fs) {
+              FixedScratch* fs, PlaneCache* cache) {
     if (ab_dtype != MLXHIP_DTYPE_F32 && ab_dtype != MLXHIP_DTYPE_BF16 && ab_dtype != MLXHIP_DTYPE_F16)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: input dtype %d unsupported", ab_dtype);
     if (c_dtype != MLXHIP_DTYPE_F32 && c_dtype != MLXHIP_DTYPE_BF16 && c_dtype != MLXHIP_DTYPE_F16)
@@ -337,6 +533,17 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     if (ldb < b_cols) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: ldb %lld < %lld", (long long)ldb, (long long)b_cols);
     if (ceil_div(m, 64) * ceil_div(n, 64) > INT32_MAX)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: too many tiles");
+
+    // Large f32 products: bf16 planes on the 16-bit matrix cores (not in
+    // the fixed-scratch entry point: the planes would not fit it).
+    if (ab_dtype == MLXHIP_DTYPE_F32 && c_dtype == MLXHIP_DTYPE_F32 && !fs && !padded &&
+        use_x6(gemm_path(), m, n, k, batch)) {
+        bool ran = false;
+        MLXHIP_TRY(gemm_x6(trans_a, trans_b, m, n, k, batch, static_cast<const float*>(a), lda, stride_a,
+                           static_cast<const float*>(b), ldb, stride_b, static_cast<float*>(c), ldc, stride_c, s,
+                           cache, &ran));
+        if (ran) return MLXHIP_OK;
+    }
 
     // Small f32 products (config 1's 512^3): one launch of 32 x 32 tiles with
     // K split across the workgroup's waves, instead of split-K partials and

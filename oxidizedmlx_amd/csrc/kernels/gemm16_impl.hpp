@@ -106,6 +106,59 @@ struct Args {
     // sums the partials in split order.
     int splits = 1;
     int64_t k_chunk = 0;
+    // Split-f32 mode (kernel template X6): a and b each hold three bf16
+    // planes (hi, mid, lo with hi + mid + lo == the f32 value) plane_a /
+    // plane_b bytes apart, in the layout a plain bf16 operand would have;
+    // k is the (padded) K of one plane. The product runs over 6 k segments,
+    // one per plane pair (see seg_plane_a / seg_plane_b); k_chunk and the
+    // split ranges count k over those 6 segments. When *flag == gen the
+    // split found a value that is not finite (or rounds out of range) and
+    // the kernel instead forms C from the f32 operands fa / fb directly
+    // (flag_a / gen_a: A's split, flag_b / gen_b: B's).
+    uint32_t plane_a = 0, plane_b = 0;
+    const float* fa = nullptr;
+    const float* fb = nullptr;
+    int64_t flda = 0, fsa = 0, fldb = 0, fsb = 0, fk = 0;
+    const uint32_t* flag_a = nullptr;
+    const uint32_t* flag_b = nullptr;
+    uint32_t gen_a = 0, gen_b = 0;
+};
+
+// Plane pairs of the 6 k segments, smallest products first so the f32
+// accumulators add the large hi*hi terms last: (mid, mid), (lo, hi),
+// (hi, lo), (mid, hi), (hi, mid), (hi, hi); plane 0 = hi, 1 = mid, 2 = lo.
+// With the planes rounded to nearest, |mid| <= 2^-8 |x| and |lo| <= 2^-16 |x|,
+// so the three dropped pairs (mid*lo, lo*mid, lo*lo) add up to at most about
+// 2^-23 of |a b| (one f32 rounding of the product is 2^-24 of it).
+__host__ __device__ constexpr int seg_plane_a(int seg) { return (0x001021 >> (4 * seg)) & 3; }
+__host__ __device__ constexpr int seg_plane_b(int seg) { return (0x010201 >> (4 * seg)) & 3; }
+constexpr int X6_SEGS = 6;
+
+// Position of the next K tile in split-f32 mode: segment, k inside it, and
+// how many tiles of the workgroup's range are left (this one included).
+struct SegCursor {
+    int seg, kin, left;
+    __device__ inline void init(int64_t vtile0, int tiles_per_seg, int ntiles) {
+        seg = (int)(vtile0 / tiles_per_seg);
+        kin = (int)(vtile0 - (int64_t)seg * tiles_per_seg) * BK;
+        left = ntiles;
+    }
+    __device__ inline void next(int seg_k) {
+        kin += BK;
+        if (kin >= seg_k) {
+            kin = 0;
+            ++seg;
+        }
+        --left;
+    }
+    // k to hand the loaders: past the range, one no chunk accepts.
+    __device__ inline int k() const { return left > 0 ? kin : INT32_MAX; }
+    __device__ inline uint32_t base_a(uint32_t plane) const {
+        return left > 0 ? (uint32_t)seg_plane_a(seg) * plane : 0u;
+    }
+    __device__ inline uint32_t base_b(uint32_t plane) const {
+        return left > 0 ? (uint32_t)seg_plane_b(seg) * plane : 0u;
+    }
 };
 
 template <int N>
@@ -176,16 +229,18 @@ struct Loader {
     }
 
     // Load i (0 .. L-1) of the tile starting at k0.
+    // `base`: byte offset added to every in-range chunk (split-f32 mode:
+    // the plane of the tile's segment).
     __device__ inline void issue_one(__amdgpu_buffer_rsrc_t rsrc, MLXHIP_LDS char* stage_op, int wave,
-                                     int k0, int i) const {
-        const uint32_t v = k0 < lim[i] ? off[i] + (uint32_t)k0 * k_stride_bytes : OOB;
+                                     int k0, int i, uint32_t base = 0) const {
+        const uint32_t v = k0 < lim[i] ? off[i] + base + (uint32_t)k0 * k_stride_bytes : OOB;
         lds_load16(rsrc, stage_op + (i * WAVES + wave) * 1024, v);
     }
 
     __device__ inline void issue(__amdgpu_buffer_rsrc_t rsrc, MLXHIP_LDS char* stage_op, int wave,
-                                 int k0) const {
+                                 int k0, uint32_t base = 0) const {
 #pragma unroll
-        for (int i = 0; i < L; ++i) issue_one(rsrc, stage_op, wave, k0, i);
+        for (int i = 0; i < L; ++i) issue_one(rsrc, stage_op, wave, k0, i, base);
     }
 };
 
@@ -281,10 +336,33 @@ constexpr int pass_rows(int budget) {
     return r;
 }
 
-template <int DT, int CT, int TA, int TB, class C, bool SPREAD>
+// Split-f32 mode, inputs flagged as not finite: the workgroup's tile of C
+// (f32) straight from the f32 operands, one FMA chain per element over the
+// whole K, so infinities and NaNs combine as in an f32 product. Split 0 of a
+// split-K launch holds the product, the other splits zeros.
+template <int TA, int TB, class C>
+__device__ void x6_direct(const Args& g, int64_t batch, int64_t split, int64_t slice, int64_t m0, int64_t n0,
+                          int tid) {
+    const float* A = g.fa + batch * g.fsa;
+    const float* B = g.fb + batch * g.fsb;
+    float* Cp = static_cast<float*>(g.c) + slice * g.sc;
+    for (int e = tid; e < C::BM * C::BN; e += C::THREADS) {
+        const int64_t m = m0 + e / C::BN, n = n0 + e % C::BN;
+        if (m >= g.m || n >= g.n) continue;
+        float acc = 0.0f;
+        if (split == 0)
+            for (int64_t k = 0; k < g.fk; ++k)
+                acc = fmaf(TA ? A[k * g.flda + m] : A[m * g.flda + k], TB ? B[n * g.fldb + k] : B[k * g.fldb + n],
+                           acc);
+        Cp[m * g.ldc + n] = acc;
+    }
+}
+
+template <int DT, int CT, int TA, int TB, class C, bool SPREAD, bool X6 = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
                           amdgpu_waves_per_eu(C::WPE, C::WPE)))
 void gemm16_kernel(Args g) {
+    static_assert(!X6 || (DT == MLXHIP_DTYPE_BF16 && CT == MLXHIP_DTYPE_F32), "split-f32 mode: bf16 planes, f32 C");
     constexpr bool KCA = (TA == 0);  // A stored [M][K]
     constexpr bool KCB = (TB == 1);  // B stored [N][K]
     constexpr int STAGES = C::STAGES, TM = C::TM, TN = C::TN, WAVES = C::WAVES;
@@ -323,11 +401,23 @@ void gemm16_kernel(Args g) {
     const int tn = (id % in_group) / gsz;
     const int64_t m0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
 
+    if constexpr (X6) {
+        if (__atomic_load_n(g.flag_a, __ATOMIC_RELAXED) == g.gen_a ||
+            __atomic_load_n(g.flag_b, __ATOMIC_RELAXED) == g.gen_b) {
+            x6_direct<TA, TB, C>(g, batch, split, slice, m0, n0, tid);
+            return;
+        }
+    }
+
     // A split starts k_chunk * split into K: its operands are the slices'
     // sub-matrices from that k on (descriptor ranges shortened to match).
+    // Split-f32 mode: K counts over the 6 segments; the tiles find their
+    // segment's planes through a SegCursor and the descriptors start at the
+    // slice.
     const int64_t kb = split * g.k_chunk;
-    const int64_t klen = g.splits > 1 ? min(g.k - kb, g.k_chunk) : g.k;
-    const int64_t a_koff = (KCA ? kb : kb * g.lda) * 2, b_koff = (KCB ? kb : kb * g.ldb) * 2;
+    const int64_t kv = X6 ? X6_SEGS * g.k : g.k;
+    const int64_t klen = g.splits > 1 ? min(kv - kb, g.k_chunk) : kv;
+    const int64_t a_koff = X6 ? 0 : (KCA ? kb : kb * g.lda) * 2, b_koff = X6 ? 0 : (KCB ? kb : kb * g.ldb) * 2;
     const char* A = static_cast<const char*>(g.a) + batch * g.sa * 2 + a_koff;
     const char* B = static_cast<const char*>(g.b) + batch * g.sb * 2 + b_koff;
     const __amdgpu_buffer_rsrc_t ra =
@@ -338,8 +428,8 @@ void gemm16_kernel(Args g) {
     constexpr int ROWB_A = C::BM * 2, ROWB_B = C::BN * 2;
     Loader<KCA, C::BM, WAVES> la;
     Loader<KCB, C::BN, WAVES> lb;
-    la.init(tid, m0, g.m, g.lda, klen);
-    lb.init(tid, n0, g.n, g.ldb, klen);
+    la.init(tid, m0, g.m, g.lda, X6 ? g.k : klen);
+    lb.init(tid, n0, g.n, g.ldb, X6 ? g.k : klen);
     FragAddr<KCA, TM, ROWB_A> fa;
     FragAddr<KCB, TN, ROWB_B> fb;
     fa.init(lane, 32 * TM * wm);
@@ -362,11 +452,23 @@ void gemm16_kernel(Args g) {
     // iteration t+1 instead (spread over its MFMAs) and the prologue leaves
     // out B of tile STAGES-1; the count of loads younger than any tile is
     // unchanged.
+    // Split-f32 mode: ca walks the tiles A (and, without SPREAD, B) loads
+    // next, cb the tiles of B's spread loads (one tile behind).
+    SegCursor ca{}, cb{};
+    const int seg_k = (int)g.k;
+    if constexpr (X6) ca.init(kb / BK, seg_k / BK, nk);
 #pragma unroll
     for (int t = 0; t < STAGES; ++t) {
         MLXHIP_LDS char* st = smem + t * C::STAGE_BYTES;
-        la.issue(ra, st, wave, t * BK);
-        if (!SPREAD || t < STAGES - 1) lb.issue(rb, st + B_OFF, wave, t * BK);
+        if constexpr (X6) {
+            if (t == STAGES - 1) cb = ca;
+            la.issue(ra, st, wave, ca.k(), ca.base_a(g.plane_a));
+            if (!SPREAD || t < STAGES - 1) lb.issue(rb, st + B_OFF, wave, ca.k(), ca.base_b(g.plane_b));
+            ca.next(seg_k);
+        } else {
+            la.issue(ra, st, wave, t * BK);
+            if (!SPREAD || t < STAGES - 1) lb.issue(rb, st + B_OFF, wave, t * BK);
+        }
     }
     if constexpr (SPREAD) wait_vmcnt<(STAGES - 2) * LPT + LA>();
     else wait_vmcnt<(STAGES - 1) * LPT>();
@@ -387,6 +489,16 @@ void gemm16_kernel(Args g) {
         const int cur = kt % STAGES;
         const MLXHIP_LDS char* st = smem + cur * C::STAGE_BYTES;
         MLXHIP_LDS char* spread_dst = smem + ((kt + STAGES - 1) % STAGES) * C::STAGE_BYTES + B_OFF;
+        // k and plane offsets of the loads of this iteration: B's spread
+        // loads (tile kt-1+STAGES), then A's and B's (tile kt+STAGES).
+        const int k_sp = X6 ? cb.k() : (kt - 1 + STAGES) * BK;
+        const uint32_t base_sp = X6 ? cb.base_b(g.plane_b) : 0u;
+        const int k_ld = X6 ? ca.k() : (kt + STAGES) * BK;
+        const uint32_t base_la = X6 ? ca.base_a(g.plane_a) : 0u, base_lb = X6 ? ca.base_b(g.plane_b) : 0u;
+        if constexpr (X6) {
+            cb.next(seg_k);
+            ca.next(seg_k);
+        }
         // First half: MFMAs of k-step 0, reads of k-step 1 of this tile.
 #pragma unroll
         for (int q = 0; q < NM; ++q) {
@@ -399,7 +511,7 @@ void gemm16_kernel(Args g) {
             if constexpr (SPREAD) {
                 // B of tile kt-1+STAGES into the stage released in iteration kt-1.
                 if (((q + 1) * LB) / NM > (q * LB) / NM)
-                    lb.issue_one(rb, spread_dst, wave, (kt - 1 + STAGES) * BK, (q * LB) / NM);
+                    lb.issue_one(rb, spread_dst, wave, k_sp, (q * LB) / NM, base_sp);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -408,7 +520,6 @@ void gemm16_kernel(Args g) {
         wait_vmcnt<(STAGES - 2) * LPT>();
         lds_barrier();
         MLXHIP_LDS char* dst = smem + cur * C::STAGE_BYTES;
-        const int k0 = (kt + STAGES) * BK;
         const MLXHIP_LDS char* nx = smem + ((kt + 1) % STAGES) * C::STAGE_BYTES;
         // Second half: MFMAs of k-step 1; the k-step 0 reads of tile kt+1
         // and the loads of tile kt+STAGES.
@@ -420,8 +531,8 @@ void gemm16_kernel(Args g) {
                 // Reads first: the next tile's first MFMAs consume them.
                 if (o < NA) read_one<KCA, TM, ROWB_A>(nx, fa, 0, o, af[0]);
                 else if (o < NR) read_one<KCB, TN, ROWB_B>(nx + B_OFF, fb, 0, o - NA, bf[0]);
-                else if (o < NR + LA) la.issue_one(ra, dst, wave, k0, o - NR);
-                else if (!SPREAD) lb.issue_one(rb, dst + B_OFF, wave, k0, o - NR - LA);
+                else if (o < NR + LA) la.issue_one(ra, dst, wave, k_ld, o - NR, base_la);
+                else if (!SPREAD) lb.issue_one(rb, dst + B_OFF, wave, k_ld, o - NR - LA, base_lb);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -518,35 +629,58 @@ inline bool supported(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t b
     return true;
 }
 
-template <int DT, int CT, int TA, int TB, class C>
+template <int DT, int CT, int TA, int TB, class C, bool X6 = false>
 int launch(const Args& a0, int64_t batch, hipStream_t s) {
     Args a = a0;
     a.tiles_m = (int)ceil_div(a.m, C::BM);
     a.tiles_n = (int)ceil_div(a.n, C::BN);
     dim3 grid((unsigned)(a.tiles_m * a.tiles_n), (unsigned)(batch * a.splits));
-    hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, C, true>), grid, dim3(C::THREADS), 0, s, a);
+    hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, C, true, X6>), grid, dim3(C::THREADS), 0, s, a);
     return launch_check("gemm16_kernel");
 }
 
-template <int DT, int CT, class C>
+template <int DT, int CT, class C, bool X6 = false>
 int dispatch_layout(const Args& a, int64_t batch, int ta, int tb, hipStream_t s) {
-    if (!ta && !tb) return launch<DT, CT, 0, 0, C>(a, batch, s);
-    if (!ta && tb) return launch<DT, CT, 0, 1, C>(a, batch, s);
-    if (ta && !tb) return launch<DT, CT, 1, 0, C>(a, batch, s);
-    return launch<DT, CT, 1, 1, C>(a, batch, s);
+    if (!ta && !tb) return launch<DT, CT, 0, 0, C, X6>(a, batch, s);
+    if (!ta && tb) return launch<DT, CT, 0, 1, C, X6>(a, batch, s);
+    if (ta && !tb) return launch<DT, CT, 1, 0, C, X6>(a, batch, s);
+    return launch<DT, CT, 1, 1, C, X6>(a, batch, s);
 }
 
 // cfg: 0 = CfgLarge, 1 = CfgMid.
-template <int DT, int CT>
+template <int DT, int CT, bool X6 = false>
 int dispatch(const Args& a, int64_t batch, int ta, int tb, int cfg, hipStream_t s) {
-    if (cfg == 0) return dispatch_layout<DT, CT, CfgLarge>(a, batch, ta, tb, s);
-    return dispatch_layout<DT, CT, CfgMid>(a, batch, ta, tb, s);
+    if (cfg == 0) return dispatch_layout<DT, CT, CfgLarge, X6>(a, batch, ta, tb, s);
+    return dispatch_layout<DT, CT, CfgMid, X6>(a, batch, ta, tb, s);
 }
 
 }  // namespace gemm16
 
-// Per-dtype entry points (gemm16_bf16.hip, gemm16_f16.hip).
+// Per-dtype entry points (gemm16_bf16.hip, gemm16_f16.hip), and the
+// split-f32 mode (gemm16_x6.hip; f32 C).
 int gemm16_bf16(int c_dtype, int ta, int tb, const gemm16::Args& a, int64_t batch, int cfg, hipStream_t s);
 int gemm16_f16(int c_dtype, int ta, int tb, const gemm16::Args& a, int64_t batch, int cfg, hipStream_t s);
+int gemm16_x6(int ta, int tb, const gemm16::Args& a, int64_t batch, int cfg, hipStream_t s);
+
+// One f32 operand's split into three bf16 planes (gemm16_x6.hip). Each plane
+// is [batch][rows_p][cols_p] with zeros beyond [rows][cols], so a plane
+// product over the padded extents adds nothing for them.
+struct X6SplitOp {
+    const float* src;
+    int64_t ld, stride;      // source row pitch and batch stride (elements)
+    int64_t rows, cols;      // source extent of one batch slice
+    int64_t rows_p, cols_p;  // plane extent of one slice; cols_p % 8 == 0
+    uint16_t* dst;           // plane 0 (16-byte aligned); plane p at dst + p * plane
+    int64_t plane;           // elements per plane: batch * rows_p * cols_p
+    int64_t chunks;          // plane / 8, below 2^31
+    uint32_t* flag;          // receives gen if a value is not finite or its
+    uint32_t gen;            // hi plane rounds out of range
+};
+// Up to two operands in one launch (gridDim.y = n).
+struct X6SplitPair {
+    X6SplitOp op[2];
+    int n;
+};
+int x6_split(const X6SplitPair& sp, hipStream_t s);
 
 }  // namespace mlxhip

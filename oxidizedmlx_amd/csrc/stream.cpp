@@ -417,6 +417,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     if (async_eval) {
         for (void* p : scratch.blocks) release_later(p);
         scratch.blocks.clear();
+        scratch.planes.entries.clear();
         return rc;
     }
     hipError_t e = hipStreamSynchronize(hs);

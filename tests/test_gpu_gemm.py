@@ -179,9 +179,12 @@ def test_gemm_argument_errors():
     (1000, 1100, 700, 0, 1),    # 128x128 blocks with edge tiles, split 2
     (1024, 3072, 2048, 1, 0),   # 192 tiles of 128x128: K split 4 (a power of two)
 ])
-def test_f32_block_and_split_choices(m, n, k, ta, tb):
+def test_f32_block_and_split_choices(monkeypatch, m, n, k, ta, tb):
     # The f32 shapes of the config-4 block pick 128x128 or 256x256 blocks
-    # and split K; sampled rows against the oracle.
+    # and split K in the general kernel (which the automatic choice gives
+    # the split-f32 kernel instead for the larger ones); sampled rows
+    # against the oracle.
+    monkeypatch.setenv("MLXHIP_GEMM_PATH", "general")
     check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), seed=m + n + k, rows=sample_rows(m, 10))
 
 
