@@ -327,7 +327,7 @@ void* Scratch::get_bytes(size_t bytes) {
 void Scratch::release_all() {
     for (void* p : blocks) pool_release(p);
     blocks.clear();
-    planes.entries.clear();
+    own_planes.entries.clear();
 }
 
 // ── eval_node on device operands ──────────────────────────────────────────
@@ -421,7 +421,7 @@ int eval_matmul(const mlxhip_input_t* in, size_t n_inputs, const mlxhip_meta_t& 
     // here too. The 16-bit MFMA path (operands held as bf16/f16) is the
     // explicit mlxhip_gemm with ab_dtype BF16/F16.
     return gemm(MLXHIP_DTYPE_F32, MLXHIP_DTYPE_F32, ta, tb, m, n, k, batch, a.data, lda, m * k, b.data, ldb,
-                k * n, out, n, m * n, s, &scratch.planes);
+                k * n, out, n, m * n, s, scratch.planes);
 }
 
 int eval_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,

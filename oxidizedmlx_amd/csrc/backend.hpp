@@ -28,12 +28,14 @@ size_t pool_block_size(void* p);
 // by the owner after its stream has been synchronised.
 struct Scratch {
     std::vector<void*> blocks;
-    // Split-f32 planes of the evaluation's f32 products, in blocks of this
-    // scratch (they live exactly as long).
-    PlaneCache planes;
+    // Split-f32 planes of the f32 products: by default kept in blocks of this
+    // scratch (as long as it lives); a Stream points `planes` at its own
+    // cache, which lives until the stream is cleared.
+    PlaneCache own_planes;
+    PlaneCache* planes = &own_planes;
     Scratch() {
-        planes.alloc = [](void* ctx, size_t bytes) { return static_cast<Scratch*>(ctx)->get_bytes(bytes); };
-        planes.ctx = this;
+        own_planes.alloc = [](void* ctx, size_t bytes) { return static_cast<Scratch*>(ctx)->get_bytes(bytes); };
+        own_planes.ctx = this;
     }
     Scratch(const Scratch&) = delete;
     Scratch& operator=(const Scratch&) = delete;

@@ -442,15 +442,21 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
     const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * batch;
     int sp_big = 1;
     while (sp_big < 8 && big_tiles * sp_big < 256) sp_big *= 2;
+    // 256x128 blocks when they alone come to about one per CU
+    // (2048x4096x1024: 120 us against 124 us for 256x256 split 2).
+    const int64_t wide_tiles = ceil_div(m, 256) * ceil_div(n, 128) * batch;
     int cfg = 0, sp_k = sp_big;
-    if (big_tiles * sp_big < 256 || kv / sp_big < 3072) {
+    if (big_tiles < 224 && wide_tiles >= 224 && wide_tiles <= 256) {
+        cfg = 2;
+        sp_k = 1;
+    } else if (big_tiles * sp_big < 256 || kv / sp_big < 3072) {
         cfg = 1;
         sp_k = 1;
         while (sp_k < 8 && mid_tiles * sp_k < 256 && kv / (2 * sp_k) >= 256) sp_k *= 2;
     }
     if (const char* e = getenv("MLXHIP_X6")) {
         int cf = 0, v = 0;
-        if (sscanf(e, "%d,%d", &cf, &v) == 2 && (cf == 0 || cf == 1) && v >= 1 && v <= 8) {
+        if (sscanf(e, "%d,%d", &cf, &v) == 2 && cf >= 0 && cf <= 2 && v >= 1 && v <= 8) {
             cfg = cf;
             sp_k = v;
         }

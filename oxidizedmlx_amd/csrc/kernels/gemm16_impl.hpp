@@ -88,6 +88,9 @@ using CfgLarge = Cfg<2, 4, 4, 2, 4, 2>;
 // 128 x 128 block, 4 waves of 64 x 64 (two workgroups per CU): problems
 // with too few 256 x 256 tiles to occupy the chip.
 using CfgMid = Cfg<2, 2, 2, 2, 4, 2>;
+// 256 x 128 block, 8 waves of 64 x 64 (two waves per SIMD): one workgroup
+// per CU for problems with 256 such tiles.
+using CfgWide = Cfg<4, 2, 2, 2, 4, 2>;
 
 struct Args {
     int64_t m, n, k;
@@ -647,10 +650,12 @@ int dispatch_layout(const Args& a, int64_t batch, int ta, int tb, hipStream_t s)
     return launch<DT, CT, 1, 1, C, X6>(a, batch, s);
 }
 
-// cfg: 0 = CfgLarge, 1 = CfgMid.
+// cfg: 0 = CfgLarge, 1 = CfgMid, 2 = CfgWide (split-f32 mode only).
 template <int DT, int CT, bool X6 = false>
 int dispatch(const Args& a, int64_t batch, int ta, int tb, int cfg, hipStream_t s) {
     if (cfg == 0) return dispatch_layout<DT, CT, CfgLarge, X6>(a, batch, ta, tb, s);
+    if constexpr (X6)
+        if (cfg == 2) return dispatch_layout<DT, CT, CfgWide, X6>(a, batch, ta, tb, s);
     return dispatch_layout<DT, CT, CfgMid, X6>(a, batch, ta, tb, s);
 }
 

@@ -175,8 +175,10 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             if (buffers.count(id) || requested.count(id)) continue;
             const Node& t = nodes.at(id);
             if (!is_matrix_swap(t) || t.inputs.empty()) continue;
+            // Consumers outside this evaluation either hold their buffers
+            // already or will plan this Transpose again when they run.
             const std::vector<uint64_t>& u = users[id];
-            if (u.empty() || u.size() != consumers[id]) continue;
+            if (u.empty()) continue;
             bool ok = true;
             for (uint64_t c : u) {
                 if (buffers.count(c) || folded_transpose.count(c)) continue;
@@ -258,6 +260,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     // ── evaluation ────────────────────────────────────────────────────────
     std::unordered_set<uint64_t> counted_virtual, counted_folded;  // eval_count covers each once
     Scratch scratch;
+    scratch.planes = &planes;
     int rc = MLXHIP_OK;
     for (uint64_t id : order) {
         if (buffers.count(id) || folded_transpose.count(id) || interior.count(id) || virtual_bcast.count(id) ||
@@ -417,7 +420,6 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     if (async_eval) {
         for (void* p : scratch.blocks) release_later(p);
         scratch.blocks.clear();
-        scratch.planes.entries.clear();
         return rc;
     }
     hipError_t e = hipStreamSynchronize(hs);

@@ -97,6 +97,26 @@ struct mlxhip_stream_t {
     hipStream_t side = nullptr;
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     bool side_pending = false;
+    // bf16 planes of the f32 operands of this stream's split-f32 products,
+    // kept until clear() so products in later evaluations reuse them (the
+    // forward's weights and activations in the gradient's evaluation). A
+    // node's buffer is never written again while the node exists (view
+    // constants by the contract of add_constant_view), and a block released
+    // before clear() drops the planes made from it (release_later).
+    mlxhip::PlaneCache planes;
+    std::vector<void*> plane_blocks;
+
+    mlxhip_stream_t() {
+        planes.alloc = [](void* ctx, size_t bytes) {
+            auto* self = static_cast<mlxhip_stream_t*>(ctx);
+            void* p = self->stream_alloc(bytes);
+            if (p) self->plane_blocks.push_back(p);
+            return p;
+        };
+        planes.ctx = this;
+    }
+    mlxhip_stream_t(const mlxhip_stream_t&) = delete;
+    mlxhip_stream_t& operator=(const mlxhip_stream_t&) = delete;
 
     ~mlxhip_stream_t() {
         if (side) (void)hipStreamSynchronize(side);
@@ -104,6 +124,7 @@ struct mlxhip_stream_t {
         for (auto& b : pending) mlxhip::pool_release(b.second);
         for (auto& kv : buffers)
             if (kv.second.owned) mlxhip::pool_release(kv.second.ptr);
+        for (void* p : plane_blocks) mlxhip::pool_release(p);
         if (fork_ev) (void)hipEventDestroy(fork_ev);
         if (join_ev) (void)hipEventDestroy(join_ev);
         if (side) (void)hipStreamDestroy(side);
@@ -146,7 +167,21 @@ struct mlxhip_stream_t {
     // now (synchronous evaluation: the stream is drained before eval
     // returns) or when the stream drains.
     void release_later(void* p) {
-        if (async_eval) pending.emplace_back(mlxhip::pool_block_size(p), p);
+        const size_t sz = mlxhip::pool_block_size(p);
+        if (!planes.entries.empty()) {
+            const char* lo = static_cast<const char*>(p);
+            auto& e = planes.entries;
+            for (size_t i = 0; i < e.size();) {
+                const char* src = static_cast<const char*>(e[i].src);
+                if (src >= lo && src < lo + sz) {
+                    e[i] = e.back();
+                    e.pop_back();
+                } else {
+                    ++i;
+                }
+            }
+        }
+        if (async_eval) pending.emplace_back(sz, p);
         else mlxhip::pool_release(p);
     }
 
@@ -181,6 +216,9 @@ struct mlxhip_stream_t {
             const hipError_t e = hipStreamSynchronize(hs);
             if (e != hipSuccess) return mlxhip::hip_fail(e, "hipStreamSynchronize");
         }
+        planes.entries.clear();
+        for (void* p : plane_blocks) release_later(p);
+        plane_blocks.clear();
         for (auto& kv : buffers)
             if (kv.second.owned) release_later(kv.second.ptr);
         buffers.clear();

@@ -80,9 +80,9 @@ def test_x6_batched_and_padded(ta, tb):
 
 @pytest.mark.gpu
 @pytest.mark.usefixtures("hip", "oracle_lib", "x6")
-@pytest.mark.parametrize("setting", ["0,1", "0,3", "1,1", "1,2", "1,5", "1,8"])
+@pytest.mark.parametrize("setting", ["0,1", "0,3", "1,1", "1,2", "1,5", "1,8", "2,1", "2,3"])
 def test_x6_block_and_split_settings(monkeypatch, setting):
-    """Both block tiles, and split-K ranges that start and end inside a
+    """Every block tile, and split-K ranges that start and end inside a
     segment (5 splits of 6 segments) or cover less than one."""
     monkeypatch.setenv("MLXHIP_X6", setting)
     check_gemm(520, 300, 352, F32, F32, ta=False, tb=True, seed=5, full=True)

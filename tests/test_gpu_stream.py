@@ -531,3 +531,61 @@ def test_constant_views_read_device_memory_in_place():
     with pytest.raises(abi.InvalidArgument, match="aligned"):
         s.add_constant_view(A.ptr + 4, meta([4]))
     s.close()
+
+
+@pytest.mark.parametrize("fusion", [False, True])
+def test_transpose_rewrites_across_evaluations(fusion):
+    # The forward product is evaluated first (as grad does with the loss),
+    # then the gradient products: transpose(transpose(W)) still folds to W
+    # although the inner Transpose's other consumer ran in the earlier
+    # evaluation, so the second evaluation runs its two products only.
+    x0, w0 = synth.normal(541, (40, 24)), synth.normal(542, (24, 24))
+    g0 = synth.normal(543, (40, 24))
+    res, launches = [], []
+    for s in (HipStream(fusion=fusion), cpu_ref_stream()):
+        x = s.add_constant(x0, meta((40, 24)))
+        w = s.add_constant(w0, meta((24, 24)))
+        g = s.add_constant(g0, meta((40, 24)))
+        wt = s.add_op(OpKind.Transpose(None), [w], meta((24, 24)))
+        y = s.add_op(OpKind.MatMul, [x, wt], meta((40, 24)))                 # x W^T
+        s.eval(y)
+        wtt = s.add_op(OpKind.Transpose(None), [wt], meta((24, 24)))
+        dx = s.add_op(OpKind.MatMul, [g, wtt], meta((40, 24)))               # g W
+        xt = s.add_op(OpKind.Transpose(None), [x], meta((24, 40)))
+        dw = s.add_op(OpKind.MatMul, [xt, g], meta((24, 24)))                # x^T g
+        before = s.launch_count() if isinstance(s, HipStream) else 0
+        s.eval_many([dx, dw])
+        if isinstance(s, HipStream):
+            launches.append(s.launch_count() - before)
+        res.append([s.get_buffer(t) for t in (y, dx, dw)])
+    for got, want in zip(*res):
+        assert_allclose(got, want, 1e-5, 1e-5, "transpose rewrites across evaluations")
+    if fusion:
+        assert launches == [2]
+
+
+def test_split_f32_planes_reused_across_evaluations_and_dropped_at_clear():
+    # Products large enough for the split-f32 GEMM: W's planes, made by the
+    # first evaluation, serve the second one's g W; after clear() a view
+    # constant over the same device memory holding new values gets new
+    # planes (every result against float64 with the f32 accumulation bound).
+    from oxidizedmlx_amd.backend import DeviceBuffer
+    from parity import gemm_full_check
+    T, I, O = 1024, 2048, 1024
+    x0, g0 = synth.normal(551, (T, I)), synth.normal(553, (T, O))
+    wbuf = DeviceBuffer(O * I * 4)
+    s = HipStream()
+    for rnd, seed in enumerate((552, 554)):
+        w0 = synth.normal(seed, (O, I))
+        wbuf.upload(w0)
+        x = s.add_constant(x0, meta((T, I)))
+        w = s.add_constant_view(wbuf.ptr, meta((O, I)))
+        wt = s.add_op(OpKind.Transpose(None), [w], meta((I, O)))
+        y = s.add_op(OpKind.MatMul, [x, wt], meta((T, O)))                   # x W^T
+        s.eval(y)
+        g = s.add_constant(g0, meta((T, O)))
+        dx = s.add_op(OpKind.MatMul, [g, w], meta((T, I)))                   # g W
+        s.eval(dx)
+        gemm_full_check(s.get_buffer(y).reshape(T, O), x0, w0.T, "f32", f"x W^T, round {rnd}")
+        gemm_full_check(s.get_buffer(dx).reshape(T, I), g0, w0, "f32", f"g W, round {rnd}")
+        s.clear()
