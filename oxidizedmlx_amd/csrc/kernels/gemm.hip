@@ -429,34 +429,27 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
     h.flag_b = ob.flag;
     h.gen_b = ob.gen;
 
-    // Block tile and split over the 6 k segments of depth kp (measured on
-    // the config-4 shapes, split included): 256x256 blocks split over K to
-    // one workgroup per CU when each split keeps at least 3072 k (96 K
-    // tiles: 2048x4096x1024 125 us split 2 against 141 us unsplit and 150 us
-    // with 128x128 blocks; 4096x1024x2048 126 us split 4 against 141 us with
-    // 128x128 blocks split 2); otherwise 128x128 blocks split to about one
-    // workgroup per CU (2048x1024x1024: 51 us split 2, 69 us unsplit).
-    // MLXHIP_X6="cfg,splits" forces them (tuning).
+    // Block tile and split (measured on the config-4 shapes, split and
+    // partial sums included): the interleaved kernel, whose 144 KiB of LDS
+    // stages allow one workgroup per CU; 256x128 blocks when they alone come
+    // to about one per CU (2048x4096x1024: 94 us, against 123 us for the
+    // segment-by-segment kernel), else 128x128 blocks split over K to one
+    // workgroup per CU (2048x1024x1024 split 2: 41 us against 54 us;
+    // 1024x1024x2048 split 4: 42 us against 55 us; 4096x1024x2048 unsplit:
+    // 104 us against 124 us). MLXHIP_X6="cfg,splits" forces them (tuning;
+    // cfg 0-2 the segment-by-segment kernel with 256x256, 128x128 and
+    // 256x128 blocks, 3-4 the interleaved one with 256x128 and 128x128).
     const int64_t kv = gemm16::X6_SEGS * kp;
-    const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256) * batch;
-    const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * batch;
-    int sp_big = 1;
-    while (sp_big < 8 && big_tiles * sp_big < 256) sp_big *= 2;
-    // 256x128 blocks when they alone come to about one per CU
-    // (2048x4096x1024: 120 us against 124 us for 256x256 split 2).
     const int64_t wide_tiles = ceil_div(m, 256) * ceil_div(n, 128) * batch;
-    int cfg = 0, sp_k = sp_big;
-    if (big_tiles < 224 && wide_tiles >= 224 && wide_tiles <= 256) {
-        cfg = 2;
-        sp_k = 1;
-    } else if (big_tiles * sp_big < 256 || kv / sp_big < 3072) {
-        cfg = 1;
-        sp_k = 1;
-        while (sp_k < 8 && mid_tiles * sp_k < 256 && kv / (2 * sp_k) >= 256) sp_k *= 2;
+    const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * batch;
+    int cfg = 3, sp_k = 1;
+    if (wide_tiles < 224) {
+        cfg = 4;
+        while (sp_k < 8 && mid_tiles * sp_k < 256 && kp / (2 * sp_k) >= 128) sp_k *= 2;
     }
     if (const char* e = getenv("MLXHIP_X6")) {
         int cf = 0, v = 0;
-        if (sscanf(e, "%d,%d", &cf, &v) == 2 && cf >= 0 && cf <= 2 && v >= 1 && v <= 8) {
+        if (sscanf(e, "%d,%d", &cf, &v) == 2 && cf >= 0 && cf <= 4 && v >= 1 && v <= 8) {
             cfg = cf;
             sp_k = v;
         }
@@ -468,8 +461,11 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
         *ran = true;
         return MLXHIP_OK;
     }
-    h.k_chunk = ceil_div(ceil_div(kv, sp_k), 32) * 32;
-    h.splits = (int)ceil_div(kv, h.k_chunk);
+    // The interleaved kernel (cfg 3 / 4) runs all six products per K tile:
+    // its splits divide the planes' K, the other kernel's the 6 segments.
+    const int64_t kspan = cfg >= 3 ? kp : kv;
+    h.k_chunk = ceil_div(ceil_div(kspan, sp_k), 32) * 32;
+    h.splits = (int)ceil_div(kspan, h.k_chunk);
     const int64_t ldw = ceil_div(n, 4) * 4;
     void* part = nullptr;
     MLXHIP_TRY(stream_workspace(s, WS_SPLITK, (size_t)(batch * h.splits * m * ldw) * sizeof(float), &part));

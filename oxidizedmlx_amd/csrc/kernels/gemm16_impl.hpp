@@ -339,6 +339,120 @@ constexpr int pass_rows(int budget) {
     return r;
 }
 
+// The workgroup's C tile. XCD-aware order over the whole grid (every tile
+// of every batch slice): the hardware hands consecutive workgroup ids (x
+// fastest) to the 8 XCDs round-robin; give each XCD a contiguous range of
+// (slice, tile) ids so the tiles of a slice share one L2, then order a
+// slice's tiles in groups of 4 tile rows so neighbours share A rows / B
+// columns.
+struct TileId {
+    int64_t slice, batch, split;  // slice = batch * splits + split
+    int64_t m0, n0;
+};
+template <class C>
+__device__ inline TileId tile_of(const Args& g) {
+    const int nwg = g.tiles_m * g.tiles_n;
+    const int64_t total = (int64_t)nwg * gridDim.y;
+    int64_t lin = (int64_t)blockIdx.y * nwg + blockIdx.x;
+    if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+    TileId t;
+    t.slice = lin / nwg;
+    const int id = (int)(lin - t.slice * nwg);
+    t.batch = t.slice / g.splits;
+    t.split = t.slice - t.batch * g.splits;
+    constexpr int GROUP_M = 4;
+    const int in_group = GROUP_M * g.tiles_n;
+    const int first_m = (id / in_group) * GROUP_M;
+    const int gsz = min(g.tiles_m - first_m, GROUP_M);
+    const int tm = first_m + (id % in_group) % gsz;
+    const int tn = (id % in_group) / gsz;
+    t.m0 = (int64_t)tm * C::BM;
+    t.n0 = (int64_t)tn * C::BN;
+    return t;
+}
+
+// Epilogue of the kernels below (C tile of one workgroup, after its last
+// MFMA), through the first bytes of the operand stages' LDS.
+template <int CT, class C, int PIPE_BYTES>
+__device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN], MLXHIP_LDS char* smem, int64_t slice,
+                               int64_t m0, int64_t n0, int wave, int lane) {
+    // Through LDS. acc[i][j][v] = C[m][n] with m = WR wm + 32 i +
+    // lane % 32 and n = WC wn + 32 j + 8 (v / 4) + 4 (lane / 32) + v % 4
+    // inside the tile (WR x WC: the wave's sub-tile). Each wave converts its
+    // sub-tile into padded LDS rows (PITCH = row bytes + 16: consecutive rows
+    // fall in distinct bank groups for the 8/16-byte writes) and reads it
+    // back row by row, so every global store instruction writes whole row
+    // segments instead of 16-byte pieces of 32 rows.
+    constexpr int TM = C::TM, TN = C::TN;
+    constexpr int ES = CT == MLXHIP_DTYPE_F32 ? 4 : 2;
+    constexpr int PASS_ROWS = pass_rows<C, ES>(PIPE_BYTES);
+    constexpr int ROW_BYTES = 32 * TN * ES;  // one wave sub-tile row
+    constexpr int PITCH = ROW_BYTES + 16;
+    const int wm = wave / C::WN, wn = wave % C::WN;
+    wait_vmcnt<0>();
+    lds_barrier();  // every wave is done with the operand stages
+    constexpr int LANES_PER_ROW = ROW_BYTES / 16;
+    constexpr int ROWS_PER_READ = 64 / LANES_PER_ROW;
+    static_assert(LANES_PER_ROW <= 64 && 64 % LANES_PER_ROW == 0, "epilogue read shape");
+    MLXHIP_LDS char* region = smem + wave * PASS_ROWS * PITCH;
+    char* Cp = static_cast<char*>(g.c) + slice * g.sc * ES;
+    const int64_t row0 = m0 + 32 * TM * wm, col0 = n0 + 32 * TN * wn;
+    const bool vec_ok = (g.ldc * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(Cp) % 16) == 0;
+#pragma unroll
+    for (int pass = 0; pass < 32 * TM / PASS_ROWS; ++pass) {
+#pragma unroll
+        for (int i = 0; i < PASS_ROWS / 32; ++i) {
+            const int ii = pass * (PASS_ROWS / 32) + i;
+            const int r = 32 * i + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int c = 32 * j + 8 * q + 4 * (lane >> 5);
+                    MLXHIP_LDS char* p = region + r * PITCH + c * ES;
+                    const f32x16& a = acc[ii][j];
+                    if constexpr (ES == 4) {
+                        *(MLXHIP_LDS f32x4*)p = f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+                    } else {
+                        *(MLXHIP_LDS u32x2*)p =
+                            u32x2{pack2<CT>(a[4 * q], a[4 * q + 1]), pack2<CT>(a[4 * q + 2], a[4 * q + 3])};
+                    }
+                }
+        }
+        // The staged rows are read back by the same wave: LDS accesses of one
+        // wave complete in order, so no barrier is needed.
+#pragma unroll 4
+        for (int rr = 0; rr < PASS_ROWS; rr += ROWS_PER_READ) {
+            const int r = rr + lane / LANES_PER_ROW;
+            const int cb = (lane % LANES_PER_ROW) * 16;  // byte offset inside the row
+            const u32x4 v = *(const MLXHIP_LDS u32x4*)(region + r * PITCH + cb);
+            const int64_t m = row0 + pass * PASS_ROWS + r;
+            const int64_t n = col0 + cb / ES;
+            if (m >= g.m || n >= g.n) continue;
+            char* dst = Cp + (m * g.ldc + n) * ES;
+            if (vec_ok && n + 16 / ES <= g.n) {
+                *reinterpret_cast<u32x4*>(dst) = v;
+            } else {
+                // Row end or unaligned C: element stores.
+#pragma unroll
+                for (int e = 0; e < 16 / ES; ++e) {
+                    if (n + e >= g.n) break;
+                    const uint32_t w = v[(e * ES) / 4];
+                    if constexpr (ES == 4) reinterpret_cast<uint32_t*>(dst)[e] = w;
+                    else reinterpret_cast<uint16_t*>(dst)[e] = (uint16_t)(w >> (16 * (e & 1)));
+                }
+            }
+        }
+    }
+}
+
+// LDS bytes the epilogue stages (it reuses the operand stages' LDS).
+template <int CT, class C, int PIPE_BYTES>
+constexpr int epi_bytes() {
+    constexpr int ES = CT == MLXHIP_DTYPE_F32 ? 4 : 2;
+    return C::WAVES * pass_rows<C, ES>(PIPE_BYTES) * (32 * C::TN * ES + 16);
+}
+
 // Split-f32 mode, inputs flagged as not finite: the workgroup's tile of C
 // (f32) straight from the f32 operands, one FMA chain per element over the
 // whole K, so infinities and NaNs combine as in an f32 product. Split 0 of a
@@ -369,12 +483,8 @@ void gemm16_kernel(Args g) {
     constexpr bool KCA = (TA == 0);  // A stored [M][K]
     constexpr bool KCB = (TB == 1);  // B stored [N][K]
     constexpr int STAGES = C::STAGES, TM = C::TM, TN = C::TN, WAVES = C::WAVES;
-    constexpr int ES = CT == MLXHIP_DTYPE_F32 ? 4 : 2;
     constexpr int PIPE_BYTES = STAGES * C::STAGE_BYTES;
-    constexpr int PASS_ROWS = pass_rows<C, ES>(PIPE_BYTES);
-    constexpr int ROW_BYTES = 32 * TN * ES;  // one wave sub-tile row in the epilogue
-    constexpr int PITCH = ROW_BYTES + 16;
-    constexpr int EPI_BYTES = WAVES * PASS_ROWS * PITCH;
+    constexpr int EPI_BYTES = epi_bytes<CT, C, PIPE_BYTES>();
     constexpr int SMEM_BYTES = PIPE_BYTES > EPI_BYTES ? PIPE_BYTES : EPI_BYTES;
     __shared__ __attribute__((aligned(1024))) char smem_raw[SMEM_BYTES];
     MLXHIP_LDS char* smem = (MLXHIP_LDS char*)smem_raw;
@@ -384,25 +494,8 @@ void gemm16_kernel(Args g) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / C::WN, wn = wave % C::WN;
 
-    // XCD-aware order over the whole grid (every tile of every batch slice):
-    // the hardware hands consecutive workgroup ids (x fastest) to the 8 XCDs
-    // round-robin; give each XCD a contiguous range of (slice, tile) ids so
-    // the tiles of a slice share one L2, then order a slice's tiles in groups
-    // of 4 tile rows so neighbours share A rows / B columns.
-    const int nwg = g.tiles_m * g.tiles_n;
-    const int64_t total = (int64_t)nwg * gridDim.y;
-    int64_t lin = (int64_t)blockIdx.y * nwg + blockIdx.x;
-    if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
-    const int64_t slice = lin / nwg;  // batch * splits + split
-    const int id = (int)(lin - slice * nwg);
-    const int64_t batch = slice / g.splits, split = slice - batch * g.splits;
-    constexpr int GROUP_M = 4;
-    const int in_group = GROUP_M * g.tiles_n;
-    const int first_m = (id / in_group) * GROUP_M;
-    const int gsz = min(g.tiles_m - first_m, GROUP_M);
-    const int tm = first_m + (id % in_group) % gsz;
-    const int tn = (id % in_group) / gsz;
-    const int64_t m0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
+    const TileId tl = tile_of<C>(g);
+    const int64_t slice = tl.slice, batch = tl.batch, split = tl.split, m0 = tl.m0, n0 = tl.n0;
 
     if constexpr (X6) {
         if (__atomic_load_n(g.flag_a, __ATOMIC_RELAXED) == g.gen_a ||
@@ -541,68 +634,7 @@ void gemm16_kernel(Args g) {
         }
     }
 
-    // Epilogue through LDS. acc[i][j][v] = C[m][n] with m = WR wm + 32 i +
-    // lane % 32 and n = WC wn + 32 j + 8 (v / 4) + 4 (lane / 32) + v % 4
-    // inside the tile (WR x WC: the wave's sub-tile). Each wave converts its
-    // sub-tile into padded LDS rows (PITCH = row bytes + 16: consecutive rows
-    // fall in distinct bank groups for the 8/16-byte writes) and reads it
-    // back row by row, so every global store instruction writes whole row
-    // segments instead of 16-byte pieces of 32 rows.
-    wait_vmcnt<0>();
-    lds_barrier();  // every wave is done with the operand stages
-    constexpr int LANES_PER_ROW = ROW_BYTES / 16;
-    constexpr int ROWS_PER_READ = 64 / LANES_PER_ROW;
-    static_assert(LANES_PER_ROW <= 64 && 64 % LANES_PER_ROW == 0, "epilogue read shape");
-    MLXHIP_LDS char* region = smem + wave * PASS_ROWS * PITCH;
-    char* Cp = static_cast<char*>(g.c) + slice * g.sc * ES;
-    const int64_t row0 = m0 + 32 * TM * wm, col0 = n0 + 32 * TN * wn;
-    const bool vec_ok = (g.ldc * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(Cp) % 16) == 0;
-#pragma unroll
-    for (int pass = 0; pass < 32 * TM / PASS_ROWS; ++pass) {
-#pragma unroll
-        for (int i = 0; i < PASS_ROWS / 32; ++i) {
-            const int ii = pass * (PASS_ROWS / 32) + i;
-            const int r = 32 * i + (lane & 31);
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int c = 32 * j + 8 * q + 4 * (lane >> 5);
-                    MLXHIP_LDS char* p = region + r * PITCH + c * ES;
-                    const f32x16& a = acc[ii][j];
-                    if constexpr (ES == 4) {
-                        *(MLXHIP_LDS f32x4*)p = f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
-                    } else {
-                        *(MLXHIP_LDS u32x2*)p =
-                            u32x2{pack2<CT>(a[4 * q], a[4 * q + 1]), pack2<CT>(a[4 * q + 2], a[4 * q + 3])};
-                    }
-                }
-        }
-        // The staged rows are read back by the same wave: LDS accesses of one
-        // wave complete in order, so no barrier is needed.
-#pragma unroll 4
-        for (int rr = 0; rr < PASS_ROWS; rr += ROWS_PER_READ) {
-            const int r = rr + lane / LANES_PER_ROW;
-            const int cb = (lane % LANES_PER_ROW) * 16;  // byte offset inside the row
-            const u32x4 v = *(const MLXHIP_LDS u32x4*)(region + r * PITCH + cb);
-            const int64_t m = row0 + pass * PASS_ROWS + r;
-            const int64_t n = col0 + cb / ES;
-            if (m >= g.m || n >= g.n) continue;
-            char* dst = Cp + (m * g.ldc + n) * ES;
-            if (vec_ok && n + 16 / ES <= g.n) {
-                *reinterpret_cast<u32x4*>(dst) = v;
-            } else {
-                // Row end or unaligned C: element stores.
-#pragma unroll
-                for (int e = 0; e < 16 / ES; ++e) {
-                    if (n + e >= g.n) break;
-                    const uint32_t w = v[(e * ES) / 4];
-                    if constexpr (ES == 4) reinterpret_cast<uint32_t*>(dst)[e] = w;
-                    else reinterpret_cast<uint16_t*>(dst)[e] = (uint16_t)(w >> (16 * (e & 1)));
-                }
-            }
-        }
-    }
+    store_c<CT, C, PIPE_BYTES>(g, acc, smem, slice, m0, n0, wave, lane);
 }
 
 // Host-side check of what the kernel assumes about its operands; returns

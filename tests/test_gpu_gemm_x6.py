@@ -73,6 +73,16 @@ def test_x6_layouts_full(ta, tb, m, n, k):
 
 @pytest.mark.gpu
 @pytest.mark.usefixtures("hip", "oracle_lib", "x6")
+@pytest.mark.parametrize("setting", ["3,1", "4,2"])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("m,n,k", [(67, 45, 93), (300, 200, 520)])
+def test_x6_interleaved_layouts_full(monkeypatch, setting, ta, tb, m, n, k):
+    monkeypatch.setenv("MLXHIP_X6", setting)
+    check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), seed=5 * m + k, full=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip", "oracle_lib", "x6")
 @pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0)])
 def test_x6_batched_and_padded(ta, tb):
     check_gemm(200, 136, 160, F32, F32, ta=bool(ta), tb=bool(tb), batch=3, seed=11, ld_pad=5, full=True)
@@ -80,9 +90,11 @@ def test_x6_batched_and_padded(ta, tb):
 
 @pytest.mark.gpu
 @pytest.mark.usefixtures("hip", "oracle_lib", "x6")
-@pytest.mark.parametrize("setting", ["0,1", "0,3", "1,1", "1,2", "1,5", "1,8", "2,1", "2,3"])
+@pytest.mark.parametrize("setting", ["0,1", "0,3", "1,1", "1,2", "1,5", "1,8", "2,1", "2,3", "3,1", "3,3", "4,1",
+                                     "4,2"])
 def test_x6_block_and_split_settings(monkeypatch, setting):
-    """Every block tile, and split-K ranges that start and end inside a
+    """Every block tile of both kernels (segment by segment: 0-2,
+    interleaved: 3-4), and split-K ranges that start and end inside a
     segment (5 splits of 6 segments) or cover less than one."""
     monkeypatch.setenv("MLXHIP_X6", setting)
     check_gemm(520, 300, 352, F32, F32, ta=False, tb=True, seed=5, full=True)
