@@ -325,7 +325,10 @@ int mlxhip_stream_grad(mlxhip_stream_t* s, uint64_t loss, const uint64_t* wrt, s
  * op(A) = A [M,K] (trans_a = 0, row pitch lda) or A^T with A stored [K,M]
  * (trans_a = 1); op(B) = B [K,N] (trans_b = 0, row pitch ldb) or B^T with B
  * stored [N,K] (trans_b = 1). A_b = a + b*stride_a elements (likewise B, C).
- * ab_dtype: F32 (f32 MFMA), BF16 or F16 (16-bit MFMA); both operands share it.
+ * ab_dtype: F32, BF16 or F16 (16-bit MFMA); both operands share it. F32
+ * products with m, n, k >= 256 and m*n*k*batch >= 2^31 run as six bf16
+ * products of an exact three-plane split of each operand (f32 accuracy;
+ * inf/NaN inputs take an exact f32 path), smaller ones on the f32 MFMA.
  * c_dtype: F32, or BF16/F16 (round-to-nearest-even of the f32 accumulator).
  * Replaces matmul (crates/mlx-core/src/cpu_kernels.rs:197-230) and the Metal
  * tiled_gemm_f32 (crates/mlx-metal/src/kernels/gemm.metal:32-77), adding the
@@ -343,7 +346,8 @@ int mlxhip_gemm(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t tran
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). No
  * counterpart in the reference. Same arguments, kernels, split-K plan and
  * results (bit for bit) as mlxhip_gemm, but its workspace (split-K partials,
- * zero-padded copies of unaligned operands) comes from one fixed device array
+ * zero-padded copies of unaligned operands, the bf16 planes of large f32
+ * products) comes from one fixed device array
  * of mlxhip_gemm_noalloc_scratch_bytes() bytes (64 MiB) per device, held
  * until the process ends; it calls no hipMalloc/hipFree and no allocating
  * library routine. A product whose workspace exceeds that array returns

@@ -230,8 +230,9 @@ bool general_override(int* wt, int* splits) {
 }  // namespace
 
 // ── Fixed device scratch of gemm_noalloc ─────────────────────────────────
-// The split-K partials and the zero-padded operand copies of gemm_noalloc
-// live in this array instead of stream-ordered allocations. Each device that
+// The split-K partials, the zero-padded operand copies and the split-f32
+// planes of gemm_noalloc live in this array instead of stream-ordered
+// allocations. Each device that
 // loads the library holds its own copy until the process ends. In host code
 // `scratch` names a host-side stand-in, never the device memory: the device
 // address comes from hipGetSymbolAddress, once per device, and only that
@@ -243,8 +244,10 @@ namespace {
 // Bump allocator over one call's share of the fixed scratch (nullptr in the
 // allocating path). Every region it hands out is written in full by the
 // kernel that uses it before any kernel reads it (each split-K slice covers
-// all of [m, n]; a packed copy writes its zero padding too), so nothing is
-// cleared between calls.
+// all of [m, n]; a packed copy writes its zero padding too, and so does the
+// split into planes), so nothing is cleared between calls. The one word
+// that is not (a split's non-finite flag) is compared with a number no
+// earlier call used.
 struct FixedScratch {
     char* base;
     size_t cap;
@@ -297,9 +300,10 @@ std::atomic<uint32_t> g_x6_gen{0};
 
 // f32 product through the bf16 planes (gemm16_x6.hip): one launch splits
 // the operands (those `cache` does not already hold), one runs the plane
-// products (and, when split over K, one sums the partials). Sets *ran =
-// false, doing nothing, when the planes would not fit the kernel's 32-bit
-// buffer offsets.
+// products (and, when split over K, one sums the partials). Planes and
+// partials come from the stream's workspaces, or from the fixed scratch
+// (fs, no cache). Sets *ran = false, doing nothing, when the planes would
+// not fit the kernel's 32-bit buffer offsets.
 //
 // Planes hold the operand as stored ([rows][cols] per batch slice) with both
 // extents padded with zeros to multiples of 32, which serves it in either
@@ -307,7 +311,7 @@ std::atomic<uint32_t> g_x6_gen{0};
 // tiles, and the padded M / N rows only feed C elements that are not stored.
 int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const float* a, int64_t lda,
             int64_t stride_a, const float* b, int64_t ldb, int64_t stride_b, float* c, int64_t ldc,
-            int64_t stride_c, hipStream_t s, PlaneCache* cache, bool* ran) {
+            int64_t stride_c, hipStream_t s, PlaneCache* cache, FixedScratch* fs, bool* ran) {
     *ran = false;
     const int64_t kp = ceil_div(k, 32) * 32;  // segment length: whole K tiles
     struct Operand {
@@ -346,7 +350,7 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
     };
     const size_t flag_room = 256;
     auto plane_bytes = [](const X6SplitOp& o) { return ((size_t)(3 * o.plane * 2) + 255) & ~size_t(255); };
-    if (cache && cache->alloc) {
+    if (cache && cache->alloc && !fs) {
         for (int i = 0; i < 2; ++i) {
             X6SplitOp& o = opd[i].op;
             for (const PlaneCache::Entry& e : cache->entries)
@@ -379,7 +383,7 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
         const bool one = same(opd[0].op, opd[1].op);
         const size_t pa = plane_bytes(opd[0].op), pb = one ? 0 : plane_bytes(opd[1].op);
         void* ws = nullptr;
-        MLXHIP_TRY(stream_workspace(s, WS_PACK, pa + pb + 2 * flag_room, &ws));
+        MLXHIP_TRY(take_workspace(fs, s, WS_PACK, pa + pb + 2 * flag_room, &ws));
         char* base = static_cast<char*>(ws);
         opd[0].op.dst = reinterpret_cast<uint16_t*>(base);
         opd[0].op.flag = reinterpret_cast<uint32_t*>(base + pa + pb);
@@ -468,7 +472,7 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
     h.splits = (int)ceil_div(kspan, h.k_chunk);
     const int64_t ldw = ceil_div(n, 4) * 4;
     void* part = nullptr;
-    MLXHIP_TRY(stream_workspace(s, WS_SPLITK, (size_t)(batch * h.splits * m * ldw) * sizeof(float), &part));
+    MLXHIP_TRY(take_workspace(fs, s, WS_SPLITK, (size_t)(batch * h.splits * m * ldw) * sizeof(float), &part));
     h.c = part;
     h.ldc = ldw;
     h.sc = m * ldw;
@@ -536,14 +540,13 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     if (ceil_div(m, 64) * ceil_div(n, 64) > INT32_MAX)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: too many tiles");
 
-    // Large f32 products: bf16 planes on the 16-bit matrix cores (not in
-    // the fixed-scratch entry point: the planes would not fit it).
-    if (ab_dtype == MLXHIP_DTYPE_F32 && c_dtype == MLXHIP_DTYPE_F32 && !fs && !padded &&
+    // Large f32 products: bf16 planes on the 16-bit matrix cores.
+    if (ab_dtype == MLXHIP_DTYPE_F32 && c_dtype == MLXHIP_DTYPE_F32 && !padded &&
         use_x6(gemm_path(), m, n, k, batch)) {
         bool ran = false;
         MLXHIP_TRY(gemm_x6(trans_a, trans_b, m, n, k, batch, static_cast<const float*>(a), lda, stride_a,
                            static_cast<const float*>(b), ldb, stride_b, static_cast<float*>(c), ldc, stride_c, s,
-                           cache, &ran));
+                           cache, fs, &ran));
         if (ran) return MLXHIP_OK;
     }
 
