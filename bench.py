@@ -230,6 +230,14 @@ def main() -> int:
     A1 = hb.DeviceBuffer.from_array(synth.normal(0x5EED0001, (512, 512)))
     B1 = hb.DeviceBuffer.from_array(synth.normal(0x5EED0002, (512, 512)))
     C1 = hb.DeviceBuffer(512 * 512 * 4)
+    # The headline shape in f32, the reference's own arithmetic (its
+    # matmul is f32, cpu_kernels.rs:197-230): N(0,1) operands, one set
+    # (the split-f32 path reads bf16 planes made each call).
+    A32 = synth.normal(SEEDS["A"], (n, n)) if want("gemm_f32_4096") else None
+    B32 = synth.normal(SEEDS["B"], (n, n)) if want("gemm_f32_4096") else None
+    dA32 = hb.DeviceBuffer.from_array(A32) if want("gemm_f32_4096") else None
+    dB32 = hb.DeviceBuffer.from_array(B32) if want("gemm_f32_4096") else None
+    dC32 = hb.DeviceBuffer(n * n * 4) if want("gemm_f32_4096") else None
     nb, bt = 1024, 32
     Ab = synth.normal(0x5EED0008, (bt, nb, nb))
     Bb = synth.normal(0x5EED0009, (bt, nb, nb))
@@ -332,6 +340,9 @@ def main() -> int:
         # one replay of the K calls recorded with mlxhip_graph_*; measured on
         # this stack, replays were not faster than the eager calls.)
         "gemm_f32_512_cfg1": dict(flops=2.0 * 512 ** 3, bytes=3 * 512 * 512 * 4, peak=157.3),
+        # f32 FLOP/s; the product runs as six bf16 MFMA products of a
+        # three-plane split, so its ceiling is the bf16 peak / 6.
+        "gemm_f32_4096": dict(flops=2.0 * n ** 3, bytes=0, peak=BF16_PEAK_TFLOPS / 6.0),
         "gemm_bf16_batched_32x1024_cfg3": dict(flops=2.0 * bt * nb ** 3, bytes=bt * nb * nb * 6),
         "gemm_f16_batched_32x1024_cfg3": dict(flops=2.0 * bt * nb ** 3, bytes=bt * nb * nb * 6),
         "gemm_bf16_batched_32x1024_nt_cfg3": dict(flops=2.0 * bt * nb ** 3, bytes=bt * nb * nb * 6),
@@ -375,6 +386,8 @@ def main() -> int:
             hb.layernorm_rows(xs["layernorm"][j], ys["layernorm"][j], n, n, 1e-5, stream=stream)
         elif name == "rmsnorm_4096x4096":
             hb.rmsnorm_rows(xs["rmsnorm"][j], ys["rmsnorm"][j], n, n, 1e-5, stream=stream)
+        elif name == "gemm_f32_4096":
+            hb.gemm(abi.F32, abi.F32, False, False, n, n, n, dA32, n, dB32, n, dC32, n, stream=stream)
         elif name == "gemm_f32_512_cfg1":
             hb.gemm(abi.F32, abi.F32, False, False, 512, 512, 512, A1, 512, B1, 512, C1, 512,
                     stream=stream)
@@ -396,16 +409,18 @@ def main() -> int:
              if ((k in only) if kernels[k].get("calibration") else want(k))]
     ev = {k: (hb.Event(), hb.Event()) for k in names}
 
-    log(f"bench: warmup {args.warmup} steps")
-    for k in names:
-        for i in range(args.warmup):
-            launch(k, i)
-    hb.synchronize(stream)
-    log(f"bench: timing {args.steps} steps")
+    # Each workload's warmup steps run right before its timed steps, so no
+    # workload is timed on a chip that another one's warmup has just heated
+    # (the headline GEMM measured 1045 TFLOP/s after the f32 4096^3 warmups
+    # against 1170 TFLOP/s after its own).
+    log(f"bench: {args.warmup} warmup + {args.steps} timed steps per workload")
     t0 = time.perf_counter()
     wall_ms = {}
     graphs = []
     for k in names:
+        for i in range(args.warmup):
+            launch(k, i)
+        hb.synchronize(None)
         if kernels[k].get("decoder"):
             dec_ms.clear()
             for i in range(args.steps):
@@ -435,6 +450,7 @@ def main() -> int:
         for i in range(args.steps):
             launch(k, i)
         e1.record(stream)
+        hb.synchronize(stream)
     hb.synchronize(stream)
     wall = time.perf_counter() - t0
     if blk["stream"] is not None:
@@ -476,6 +492,9 @@ def main() -> int:
             c = synth.bf16_to_f32(dC[0].download(np.uint16, n * n)).reshape(n, n)
             outs["gemm_bf16_4096"] = dict(kind="gemm", a=synth.bf16_to_f32(A), b=synth.bf16_to_f32(B),
                                           c=c, rows=grows, rtol=1e-2)
+        if "gemm_f32_4096" in res:
+            outs["gemm_f32_4096"] = dict(kind="gemm", a=A32, b=B32, c=dC32.download(np.float32, n * n).reshape(n, n),
+                                         rows=grows, rtol=1e-5)
         if "gemm_f32_512_cfg1" in res:
             outs["gemm_f32_512_cfg1"] = dict(
                 kind="gemm", a=synth.normal(0x5EED0001, (512, 512)), b=synth.normal(0x5EED0002, (512, 512)),
