@@ -93,11 +93,14 @@ typedef enum {
      * HeadAttention: inputs Q, K, V [heads, t, dh], output [heads, t, dh]:
      * per head the Attention op's arithmetic (cpu_attention,
      * crates/mlx-core/src/cpu_kernels.rs:738-812) through mlxhip_attention.
+     * With has_axis, axis = H: inputs and output [groups, t, H*dh], H heads
+     * side by side in each row (a [batch*t, d_model] projection viewed as
+     * [batch, t, d_model]); head h of group b is columns h*dh .. h*dh+dh-1.
      * Differentiable: its VJP is one HeadAttentionVjp node.
-     * HeadAttentionVjp: inputs Q, K, V, O (the forward output), dO; output
-     * [3, heads, t, dh] = dQ, dK, dV (mlxhip_attention_vjp). */
-    MLXHIP_OP_HEAD_ATTENTION = 34,        /* scale, causal */
-    MLXHIP_OP_HEAD_ATTENTION_VJP = 35,    /* scale, causal */
+     * HeadAttentionVjp: inputs Q, K, V, O (the forward output), dO, the same
+     * axis; output [3, <input shape>] = dQ, dK, dV (mlxhip_attention_vjp). */
+    MLXHIP_OP_HEAD_ATTENTION = 34,        /* scale, causal, axis (heads per row, if has_axis) */
+    MLXHIP_OP_HEAD_ATTENTION_VJP = 35,    /* scale, causal, axis (heads per row, if has_axis) */
     MLXHIP_OP_COUNT_ = 36
 } mlxhip_op_kind_t;
 

@@ -282,7 +282,7 @@ int vjp(Builder& b, uint64_t id, const Node& n, uint64_t g, const std::vector<bo
         }
         case MLXHIP_OP_HEAD_ATTENTION: {
             // One HeadAttentionVjp node [q, k, v, o = this node, g] gives
-            // [3, heads, t, dh]; input i's gradient is its slice i (a Narrow
+            // [3, <input shape>]; input i's gradient is its slice i (a Narrow
             // along the leading axis, which the stream reads in place).
             if (!arity(3)) return MLXHIP_ERR_INVALID_ARGUMENT;
             if (!b.same_shape(g, id, "HeadAttention")) return recorded_status();
@@ -292,6 +292,8 @@ int vjp(Builder& b, uint64_t id, const Node& n, uint64_t g, const std::vector<bo
             mlxhip_op_t vo = Builder::op(MLXHIP_OP_HEAD_ATTENTION_VJP);
             vo.scale = n.op.op.scale;
             vo.causal = n.op.op.causal;
+            vo.axis = n.op.op.axis;  // heads per row, as the forward's
+            vo.has_axis = n.op.op.has_axis;
             const uint64_t all = b.node(vo, {in[0], in[1], in[2], id, g}, vsh, b.meta(id).dtype);
             if (!all) return recorded_status();
             std::vector<int64_t> one{1};

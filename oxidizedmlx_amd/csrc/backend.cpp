@@ -454,23 +454,37 @@ int eval_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inp
 // HeadAttention: the Attention op's arithmetic for every head of
 // [heads, t, dh] operands, in one fused launch when the shape and alignment
 // allow it, else head by head through eval_attention.
+// HeadAttention: heads of Q [.., tq, ..], K / V [.., tk, ..]. Without an
+// axis: [heads, t, dh], one head per leading index. With axis = H (has_axis):
+// [groups, t, H * dh], H heads side by side in each row (the layout of a
+// [batch * t, d_model] projection viewed as [batch, t, d_model]); the output
+// takes the inputs' layout.
 int eval_head_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,
                         const mlxhip_meta_t& meta, float* out, hipStream_t s, Scratch& scratch) {
     if (n_inputs != 3) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttention requires exactly 3 inputs [Q, K, V]");
     const mlxhip_input_t &q = in[0], &k = in[1], &v = in[2];
     if (q.ndim != 3 || k.ndim != 3 || v.ndim != 3)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttention inputs must be 3-D [heads, t, dh]");
-    const int64_t h = q.shape[0], tq = q.shape[1], dh = q.shape[2], tk = k.shape[1];
-    if (k.shape[0] != h || v.shape[0] != h || k.shape[2] != dh || v.shape[1] != tk || v.shape[2] != dh)
-        return fail_shape({h, tk, dh}, {k.shape[0], k.shape[1], k.shape[2]}, "HeadAttention");
-    MLXHIP_TRY(expect_len(h * tq * dh, numel_of(meta.shape, meta.ndim), "HeadAttention"));
-    if (h * tq * dh == 0) return MLXHIP_OK;
+    const int64_t g = q.shape[0], tq = q.shape[1], w = q.shape[2], tk = k.shape[1];
+    if (k.shape[0] != g || v.shape[0] != g || k.shape[2] != w || v.shape[1] != tk || v.shape[2] != w)
+        return fail_shape({g, tk, w}, {k.shape[0], k.shape[1], k.shape[2]}, "HeadAttention");
+    const int64_t hg = op.has_axis ? op.axis : 1;
+    if (hg < 1 || w % hg)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttention: %lld heads per row of %lld values", (long long)hg,
+                    (long long)w);
+    const int64_t h = g * hg, dh = w / hg;
+    MLXHIP_TRY(expect_len(g * tq * w, numel_of(meta.shape, meta.ndim), "HeadAttention"));
+    if (g * tq * w == 0) return MLXHIP_OK;
     if (tk == 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttention: no keys");
     const uintptr_t al = reinterpret_cast<uintptr_t>(q.data) | reinterpret_cast<uintptr_t>(k.data) |
                          reinterpret_cast<uintptr_t>(v.data) | reinterpret_cast<uintptr_t>(out);
-    if (attention_fused_supported(dh, tq, tk) && al % 16 == 0 && dh % 4 == 0)
-        return attention_fused(q.data, k.data, v.data, out, h, tq, tk, dh, tq * dh, tk * dh, tk * dh, tq * dh,
-                               op.scale, op.causal, s);
+    if (attention_fused_supported(dh, tq, tk) && al % 16 == 0 && dh % 4 == 0 && w % 4 == 0)
+        return attention_fused(q.data, k.data, v.data, out, h, tq, tk, dh, tq * w, tk * w, tk * w, tq * w,
+                               op.scale, op.causal, s, hg, w);
+    if (hg > 1)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT,
+                    "HeadAttention with heads side by side in rows needs the fused kernel (dh 16, 32, 64 or 128, "
+                    "16-byte aligned rows): dh=%lld", (long long)dh);
     const int64_t qs[2] = {tq, dh}, ks[2] = {tk, dh};
     for (int64_t i = 0; i < h; ++i) {
         mlxhip_input_t hi[3] = {{q.data + i * tq * dh, (size_t)(tq * dh), qs, 2, q.dtype},
@@ -484,7 +498,8 @@ int eval_head_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t 
     return MLXHIP_OK;
 }
 
-// HeadAttentionVjp: [Q, K, V, O, dO] -> [3, heads, t, dh] = dQ, dK, dV.
+// HeadAttentionVjp: [Q, K, V, O, dO] -> [3, ...] = dQ, dK, dV, each in the
+// inputs' layout (axis as for HeadAttention).
 int eval_head_attention_vjp(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,
                             const mlxhip_meta_t& meta, float* out, hipStream_t s) {
     if (n_inputs != 5)
@@ -496,11 +511,15 @@ int eval_head_attention_vjp(const mlxhip_op_t& op, const mlxhip_input_t* in, siz
             in[i].shape[2] != q.shape[2])
             return fail_shape(std::vector<int64_t>(q.shape, q.shape + 3),
                               std::vector<int64_t>(in[i].shape, in[i].shape + in[i].ndim), "HeadAttentionVjp");
-    const int64_t h = q.shape[0], t = q.shape[1], dh = q.shape[2], n = h * t * dh;
+    const int64_t g = q.shape[0], t = q.shape[1], w = q.shape[2], n = g * t * w;
+    const int64_t hg = op.has_axis ? op.axis : 1;
+    if (hg < 1 || w % hg)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "HeadAttentionVjp: %lld heads per row of %lld values",
+                    (long long)hg, (long long)w);
     MLXHIP_TRY(expect_len(3 * n, numel_of(meta.shape, meta.ndim), "HeadAttentionVjp"));
     if (n == 0) return MLXHIP_OK;
-    return attention_vjp(in[0].data, in[1].data, in[2].data, in[3].data, in[4].data, out, out + n, out + 2 * n, h,
-                         t, dh, op.scale, op.causal, s);
+    return attention_vjp(in[0].data, in[1].data, in[2].data, in[3].data, in[4].data, out, out + n, out + 2 * n,
+                         g * hg, t, w / hg, op.scale, op.causal, s, hg, w);
 }
 
 }  // namespace

@@ -126,18 +126,23 @@ int dec_set_counter(int* p, int v, hipStream_t s);
 bool attention_fused_supported(int64_t dh, int64_t tq, int64_t tk);
 // Q [batch][tq][dh], K/V [batch][tk][dh], O [batch][tq][dh], row-major with
 // batch strides sq/sk/sv/so (elements); Q, K, V and O 16-byte aligned.
+// With hg > 1, heads sit side by side in rows: head i is columns
+// (i % hg) * dh .. +dh of row group i / hg (groups s* floats apart, rows
+// rs floats apart; rs = 0 means dh), as in a [groups][t][hg * dh] tensor.
 int attention_fused(const float* q, const float* k, const float* v, float* o, int64_t batch, int64_t tq,
                     int64_t tk, int64_t dh, int64_t sq, int64_t sk, int64_t sv, int64_t so, float scale,
-                    int causal, hipStream_t s);
+                    int causal, hipStream_t s, int64_t hg = 1, int64_t rs = 0);
 
 // ── attention_bwd.hip (gradient of fused attention, dQ / dK / dV) ──────────
 // dh == 64, tq == tk a multiple of 64; operands [batch][t][dh], contiguous,
 // 16-byte aligned. Scratch (row log-sum-exp and dO.O) comes from the
 // stream's WS_ATTN workspace.
 bool attention_vjp_supported(int64_t dh, int64_t tq, int64_t tk);
+// hg > 1: heads side by side in rows of rs floats, as for attention_fused
+// (every operand [batch / hg][t][rs]).
 int attention_vjp(const float* q, const float* k, const float* v, const float* o, const float* dout, float* dq,
                   float* dk, float* dv, int64_t batch, int64_t t, int64_t dh, float scale, int causal,
-                  hipStream_t s);
+                  hipStream_t s, int64_t hg = 1, int64_t rs = 0);
 
 // ── gemm.hip ──────────────────────────────────────────────────────────────
 // bf16 planes of f32 operands (the split-f32 GEMM) made during one graph

@@ -155,7 +155,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_fused_kernel(const float* __
                                                                  float* __restrict__ o, int tq, int tk,
                                                                  int64_t sq, int64_t sk, int64_t sv,
                                                                  int64_t so, float scale, int causal,
-                                                                 int npairs, int nblk) {
+                                                                 int npairs, int nblk, int hg, int rs) {
     using T = Tile<DH>;
     constexpr int NS = T::NS, CT = T::CT;
     __shared__ __attribute__((aligned(16))) char lds[T::STAGES * T::STAGE];
@@ -165,11 +165,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_fused_kernel(const float* __
     // heads, so a head's K and V are fetched into one L2.
     const unsigned L = blockIdx.x, N = gridDim.x;
     const unsigned logical = N % XCDS == 0 ? (L % XCDS) * (N / XCDS) + L / XCDS : L;
+    // Head bh is head bh % hg of row group bh / hg: its rows are rs floats
+    // apart, its columns start at (bh % hg) * DH (hg = 1, rs = DH: one
+    // [t, DH] block per head, s* floats apart).
     const int bh = (int)(logical / (unsigned)npairs), pair = (int)(logical % (unsigned)npairs);
-    q += bh * sq;
-    k += bh * sk;
-    v += bh * sv;
-    o += bh * so;
+    const int64_t grp = bh / hg, hcol = (int64_t)(bh % hg) * DH;
+    q += grp * sq + hcol;
+    k += grp * sk + hcol;
+    v += grp * sv + hcol;
+    o += grp * so + hcol;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int li = lane & 15, lg = lane >> 4;
     const int g = wave & 3, h = wave >> 2;
@@ -194,7 +198,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_fused_kernel(const float* __
         const int kb_ = (it) * 2 * KT;                                                       \
         _Pragma("unroll") for (int j = 0; j < T::LU; ++j) {                                  \
             _Pragma("unroll") for (int e = 0; e < 2; ++e) {                                  \
-                const int64_t o_ = (int64_t)min(kb_ + ukey[j] + e, tk - 1) * DH + ucol[j];   \
+                const int64_t o_ = (int64_t)min(kb_ + ukey[j] + e, tk - 1) * rs + ucol[j];   \
                 kr[j][e] = *reinterpret_cast<const float4*>(k + o_);                         \
                 vr[j][e] = *reinterpret_cast<const float4*>(v + o_);                         \
             }                                                                                \
@@ -251,7 +255,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_fused_kernel(const float* __
         // columns 32s + 8lg .. +7 (zero past dh).
         u32x4 qb[NS][3];
         {
-            const float* qr = q + (int64_t)min(qw + li, tq - 1) * DH;
+            const float* qr = q + (int64_t)min(qw + li, tq - 1) * rs;
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
                 float x[8];
@@ -403,7 +407,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_fused_kernel(const float* __
             shared_divisor(l, rl);
             const int row = qw + li;
             if (row < tq) {
-                float* orow = o + (int64_t)row * DH + 4 * lg;
+                float* orow = o + (int64_t)row * rs + 4 * lg;
 #pragma unroll
                 for (int c = 0; c < CT; ++c) {
                     float4 w;
@@ -425,11 +429,12 @@ int64_t pairs_of(int64_t tq) { return (blocks_of(tq) + 1) / 2; }
 
 template <int DH>
 int launch(const float* q, const float* k, const float* v, float* o, int64_t batch, int64_t tq, int64_t tk,
-           int64_t sq, int64_t sk, int64_t sv, int64_t so, float scale, int causal, hipStream_t s) {
+           int64_t sq, int64_t sk, int64_t sv, int64_t so, float scale, int causal, int hg, int rs,
+           hipStream_t s) {
     const int64_t npairs = pairs_of(tq);
     const dim3 grid((unsigned)(npairs * batch));
     hipLaunchKernelGGL(attn_fused_kernel<DH>, grid, dim3(ATT_THREADS), 0, s, q, k, v, o, (int)tq, (int)tk, sq, sk,
-                       sv, so, scale, causal, (int)npairs, (int)blocks_of(tq));
+                       sv, so, scale, causal, (int)npairs, (int)blocks_of(tq), hg, rs);
     return launch_check("attn_fused_kernel");
 }
 
@@ -442,8 +447,12 @@ bool attention_fused_supported(int64_t dh, int64_t tq, int64_t tk) {
 
 int attention_fused(const float* q, const float* k, const float* v, float* o, int64_t batch, int64_t tq,
                     int64_t tk, int64_t dh, int64_t sq, int64_t sk, int64_t sv, int64_t so, float scale,
-                    int causal, hipStream_t s) {
+                    int causal, hipStream_t s, int64_t hg, int64_t rs) {
     if (batch <= 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: batch %lld", (long long)batch);
+    if (rs == 0) rs = dh;
+    if (hg < 1 || batch % hg || rs < hg * dh || rs % 4 || rs > INT32_MAX || hg > INT32_MAX)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: %lld heads per row of %lld floats (dh %lld, batch %lld)",
+                    (long long)hg, (long long)rs, (long long)dh, (long long)batch);
     if (!attention_fused_supported(dh, tq, tk))
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: fused kernel unsupported for dh=%lld tq=%lld tk=%lld",
                     (long long)dh, (long long)tq, (long long)tk);
@@ -457,16 +466,19 @@ int attention_fused(const float* q, const float* k, const float* v, float* o, in
                          reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
     if (al % 16 || (sq | sk | sv | so) % 4)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: Q, K, V and O need 16-byte aligned rows");
-    const int64_t per = max_wg / np;
+    // Whole row groups per launch.
+    const int64_t per = (max_wg / np) / hg * hg;
+    if (per == 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention: %lld heads per row exceed one launch", (long long)hg);
+    const int ihg = (int)hg, irs = (int)rs;
     for (int64_t b0 = 0; b0 < batch; b0 += per) {
-        const int64_t nb = std::min(per, batch - b0);
-        const float *qb = q + b0 * sq, *kb = k + b0 * sk, *vb = v + b0 * sv;
-        float* ob = o + b0 * so;
+        const int64_t nb = std::min(per, batch - b0), g0 = b0 / hg;
+        const float *qb = q + g0 * sq, *kb = k + g0 * sk, *vb = v + g0 * sv;
+        float* ob = o + g0 * so;
         switch (dh) {
-            case 16: MLXHIP_TRY(launch<16>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, s)); break;
-            case 32: MLXHIP_TRY(launch<32>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, s)); break;
-            case 64: MLXHIP_TRY(launch<64>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, s)); break;
-            default: MLXHIP_TRY(launch<128>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, s)); break;
+            case 16: MLXHIP_TRY(launch<16>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, ihg, irs, s)); break;
+            case 32: MLXHIP_TRY(launch<32>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, ihg, irs, s)); break;
+            case 64: MLXHIP_TRY(launch<64>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, ihg, irs, s)); break;
+            default: MLXHIP_TRY(launch<128>(qb, kb, vb, ob, nb, tq, tk, sq, sk, sv, so, scale, causal, ihg, irs, s)); break;
         }
     }
     return MLXHIP_OK;

@@ -85,9 +85,15 @@ __device__ inline void lds_row32(const float* p, float* r) {
 // log-sum-exp), relative error about |x| 2^-24 plus one ulp.
 __device__ inline float exp2_small(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Lane l's 32 values of row `row` of a [T, DH] head: d = 32 h + s, s < 32.
-__device__ inline void load_row_half(const float* __restrict__ head, int row, int h, float* r) {
-    const f32x4* p = reinterpret_cast<const f32x4*>(head + (int64_t)row * DH + 32 * h);
+// Offset of head `head`'s first row: head % hg of row group head / hg, the
+// groups T rows of rs floats each (hg = 1, rs = DH: [heads][T][DH]).
+__device__ inline int64_t head_offset(int64_t head, int T, int hg, int rs) {
+    return (head / hg) * (int64_t)T * rs + (head % hg) * DH;
+}
+
+// Lane l's 32 values of row `row` of a head (rows rs floats apart): d = 32 h + s, s < 32.
+__device__ inline void load_row_half(const float* __restrict__ head, int row, int rs, int h, float* r) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(head + (int64_t)row * rs + 32 * h);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const f32x4 t = p[i];
@@ -97,11 +103,11 @@ __device__ inline void load_row_half(const float* __restrict__ head, int row, in
 
 // A 64 x DH block of rows row0 .. row0+63 of a head into registers (4 vectors
 // per thread), then into LDS rows of PITCH floats.
-__device__ inline void block_load(const float* __restrict__ head, int row0, int tid, f32x4 (&r)[4]) {
+__device__ inline void block_load(const float* __restrict__ head, int row0, int rs, int tid, f32x4 (&r)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int e = (i * THREADS + tid) * 4;  // element in the block
-        r[i] = *reinterpret_cast<const f32x4*>(head + (int64_t)(row0 + e / DH) * DH + e % DH);
+        r[i] = *reinterpret_cast<const f32x4*>(head + (int64_t)(row0 + e / DH) * rs + e % DH);
     }
 }
 __device__ inline void block_store(float* lds, int tid, const f32x4 (&r)[4]) {
@@ -143,7 +149,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
                                                                const float* __restrict__ V, const float* __restrict__ O,
                                                                const float* __restrict__ dO, float* __restrict__ dQ,
                                                                float* __restrict__ lse_out, float* __restrict__ d_out,
-                                                               int T, float scale, int causal) {
+                                                               int T, float scale, int causal, int hg, int rs) {
     // K and V blocks; at the end the kh = 1 partials of dQ ([qh][64 d][33]).
     __shared__ __align__(16) float smem[2 * BT * PITCH];
     __shared__ float xch[2][2][32][2];  // (m, l) per query half, key half, query
@@ -155,17 +161,17 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const int64_t head = head_i;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int qh = wave & 1, kh = wave >> 1, c = lane & 31, h = lane >> 5;
-    const int64_t hoff = head * (int64_t)T * DH;
+    const int64_t hoff = head_offset(head, T, hg, rs);
     const float *Qh = Q + hoff, *Kh = K + hoff, *Vh = V + hoff, *Oh = O + hoff, *dOh = dO + hoff;
     const int q = qb * BT + 32 * qh + c;
 
     float qr[32], dor[32];
-    load_row_half(Qh, q, h, qr);
-    load_row_half(dOh, q, h, dor);
+    load_row_half(Qh, q, rs, h, qr);
+    load_row_half(dOh, q, rs, h, dor);
     float Dq;
     {
         float orow[32];
-        load_row_half(Oh, q, h, orow);
+        load_row_half(Oh, q, rs, h, orow);
         float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) s += dor[i] * orow[i];
@@ -183,7 +189,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     // prefetch would leave room for only one).
     float m = -INFINITY, l = 0.0f;
     for (int kb = 0; kb < nkb; ++kb) {
-        block_load(Kh, kb * BT, tid, kc);
+        block_load(Kh, kb * BT, rs, tid, kc);
         __syncthreads();  // the previous block's readers are done
         block_store(Ks, tid, kc);
         __syncthreads();
@@ -242,8 +248,8 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     // Pass 2: dQ^T (rows d, columns queries) += K^T dS^T over the wave's keys.
     f32x16 dq0 = zero16(), dq1 = zero16();
     for (int kb = 0; kb < nkb; ++kb) {
-        block_load(Kh, kb * BT, tid, kc);
-        block_load(Vh, kb * BT, tid, vc);
+        block_load(Kh, kb * BT, rs, tid, kc);
+        block_load(Vh, kb * BT, rs, tid, vc);
         __syncthreads();
         block_store(Ks, tid, kc);
         block_store(Vs, tid, vc);
@@ -305,7 +311,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
     __syncthreads();
     if (kh == 0) {
-        float* out = dQ + hoff + (int64_t)q * DH;
+        float* out = dQ + hoff + (int64_t)q * rs;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             f32x4 a, b;
@@ -331,7 +337,7 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
                                                                  const float* __restrict__ V, const float* __restrict__ dO,
                                                                  const float* __restrict__ lse, const float* __restrict__ dd,
                                                                  float* __restrict__ dK, float* __restrict__ dV, int T,
-                                                                 float scale, int causal) {
+                                                                 float scale, int causal, int hg, int rs) {
     // Q and dO blocks; at the end the qh = 1 partials ([kh][dK 64 + dV 64][33]).
     constexpr int SMEM = 2 * BT * PITCH > 2 * 128 * 33 ? 2 * BT * PITCH : 2 * 128 * 33;
     __shared__ __align__(16) float smem[SMEM];
@@ -344,21 +350,21 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const int64_t head = head_i;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int qh = wave & 1, kh = wave >> 1, c = lane & 31, h = lane >> 5;
-    const int64_t hoff = head * (int64_t)T * DH;
+    const int64_t hoff = head_offset(head, T, hg, rs);
     const float *Qh = Q + hoff, *Kh = K + hoff, *Vh = V + hoff, *dOh = dO + hoff;
     const int j = kb * BT + 32 * kh + c;
 
     float kr[32], vr[32];
-    load_row_half(Kh, j, h, kr);
-    load_row_half(Vh, j, h, vr);
+    load_row_half(Kh, j, rs, h, kr);
+    load_row_half(Vh, j, rs, h, vr);
     f32x16 dk0 = zero16(), dk1 = zero16(), dv0 = zero16(), dv1 = zero16();
     // Blocks staged without prefetch (two workgroups per CU, as in the dQ kernel).
     f32x4 qc[4], oc[4];
     const int qb0 = causal ? kb : 0, nqb = T / BT;
     const int lrow = tid < BT ? tid : 0;
     for (int qb = qb0; qb < nqb; ++qb) {
-        block_load(Qh, qb * BT, tid, qc);
-        block_load(dOh, qb * BT, tid, oc);
+        block_load(Qh, qb * BT, rs, tid, qc);
+        block_load(dOh, qb * BT, rs, tid, oc);
         const float lv = lse[head * T + qb * BT + lrow], dv = dd[head * T + qb * BT + lrow];
         __syncthreads();
         block_store(Qs, tid, qc);
@@ -438,8 +444,8 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
     __syncthreads();
     if (qh == 0) {
-        float* ok = dK + hoff + (int64_t)j * DH;
-        float* ov = dV + hoff + (int64_t)j * DH;
+        float* ok = dK + hoff + (int64_t)j * rs;
+        float* ov = dV + hoff + (int64_t)j * rs;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d0 = 8 * g + 4 * h;
@@ -476,8 +482,13 @@ bool attention_vjp_supported(int64_t dh, int64_t tq, int64_t tk) {
 
 int attention_vjp(const float* q, const float* k, const float* v, const float* o, const float* dout, float* dq,
                   float* dk, float* dv, int64_t batch, int64_t t, int64_t dh, float scale, int causal,
-                  hipStream_t s) {
+                  hipStream_t s, int64_t hg, int64_t rs) {
     if (batch <= 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention vjp: batch %lld", (long long)batch);
+    if (rs == 0) rs = dh;
+    if (hg < 1 || batch % hg || rs < hg * dh || rs % 4 || rs > INT32_MAX || hg > INT32_MAX ||
+        (batch / hg) * t * rs >= ((int64_t)1 << 40))
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "attention vjp: %lld heads per row of %lld floats (dh %lld, batch %lld)",
+                    (long long)hg, (long long)rs, (long long)dh, (long long)batch);
     if (!attention_vjp_supported(dh, t, t))
         return fail(MLXHIP_ERR_INVALID_ARGUMENT,
                     "attention vjp: needs dh = %d and a sequence length that is a multiple of %d (dh=%lld t=%lld)", DH,
@@ -496,10 +507,10 @@ int attention_vjp(const float* q, const float* k, const float* v, const float* o
     float* lse = static_cast<float*>(ws);
     float* dd = lse + batch * t;
     hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3((unsigned)blocks), dim3(THREADS), 0, s, q, k, v, o, dout, dq, lse, dd,
-                       (int)t, scale, causal);
+                       (int)t, scale, causal, (int)hg, (int)rs);
     MLXHIP_TRY(launch_check("attn_bwd_dq_kernel"));
     hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3((unsigned)blocks), dim3(THREADS), 0, s, q, k, v, dout, lse, dd, dk,
-                       dv, (int)t, scale, causal);
+                       dv, (int)t, scale, causal, (int)hg, (int)rs);
     return launch_check("attn_bwd_dkdv_kernel");
 }
 

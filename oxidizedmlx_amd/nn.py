@@ -130,11 +130,13 @@ class CausalSelfAttention:
             raise abi.InvalidArgument(f"attention input {list(x.shape)} does not match "
                                       f"batch {self.b} x seq {self.s}, {self.h} heads")
         dh = d // self.h
-        q, k, v = self._heads(self.wq(x)), self._heads(self.wk(x)), self._heads(self.wv(x))
         if self.fused:
-            o = q.head_attention(k, v, 1.0 / math.sqrt(dh), True)        # [B*H, S, Dh]
-            o = o.reshape((self.b, self.h, self.s, dh)).transpose((0, 2, 1, 3)).reshape((bs, d))
-            return self.wo(o)
+            # Heads side by side in the projections' rows: [B*S, D] viewed as
+            # [B, S, D], no head split or merge.
+            q, k, v = (lin(x).reshape((self.b, self.s, d)) for lin in (self.wq, self.wk, self.wv))
+            o = q.head_attention(k, v, 1.0 / math.sqrt(dh), True, heads=self.h)   # [B, S, D]
+            return self.wo(o.reshape((bs, d)))
+        q, k, v = self._heads(self.wq(x)), self._heads(self.wk(x)), self._heads(self.wv(x))
         scores = q.matmul(k.transpose((0, 2, 1)))                      # [B*H, S, S]
         st = x.stream
         scale = _fixed_constant(("scale", dh), np.array([1.0 / math.sqrt(dh)], np.float32), (), st)

@@ -179,14 +179,15 @@ class OpKind:
         return Op("Attention", scale=scale, causal=causal)
 
     @staticmethod
-    def HeadAttention(scale: float, causal: bool) -> Op:
-        """Attention of every head of Q, K, V [heads, t, dh] (no reference
-        counterpart; differentiable on a HIP stream)."""
-        return Op("HeadAttention", scale=scale, causal=causal)
+    def HeadAttention(scale: float, causal: bool, heads: Optional[int] = None) -> Op:
+        """Attention of every head of Q, K, V (no reference counterpart;
+        differentiable on a HIP stream): [heads, t, dh], or with ``heads``
+        [groups, t, heads * dh] with the heads side by side in each row."""
+        return Op("HeadAttention", scale=scale, causal=causal, axis=heads)
 
     @staticmethod
-    def HeadAttentionVjp(scale: float, causal: bool) -> Op:
-        return Op("HeadAttentionVjp", scale=scale, causal=causal)
+    def HeadAttentionVjp(scale: float, causal: bool, heads: Optional[int] = None) -> Op:
+        return Op("HeadAttentionVjp", scale=scale, causal=causal, axis=heads)
 
     @staticmethod
     def LayerNormVjp(eps: float) -> Op:

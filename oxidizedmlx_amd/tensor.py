@@ -310,19 +310,25 @@ class Tensor:
         return self._lazy(OpKind.Attention(scale, causal), [self, k, v], self.shape)
 
     # ── row ops (tensor.rs:379-435) ──────────────────────────────────────
-    def head_attention(self, k: "Tensor", v: "Tensor", scale: float, causal: bool) -> "Tensor":
+    def head_attention(self, k: "Tensor", v: "Tensor", scale: float, causal: bool,
+                       heads: Optional[int] = None) -> "Tensor":
         """Attention of every head: Q [H, Tq, Dh], K/V [H, Tk, Dh] -> [H, Tq, Dh],
-        per head the arithmetic of ``attention``. No reference counterpart;
+        per head the arithmetic of ``attention``. With ``heads`` = H the heads
+        sit side by side in each row instead: Q [B, Tq, H*Dh], K/V [B, Tk, H*Dh]
+        -> [B, Tq, H*Dh] (a [B*T, d_model] projection viewed as [B, T, d_model],
+        so no head split or merge is needed). No reference counterpart;
         unlike ``attention`` it has a VJP (one fused backward op) on a HIP
         stream, so a block can train through the fused kernels."""
         if len(self.shape) != 3 or len(k.shape) != 3 or len(v.shape) != 3:
             raise abi.InvalidArgument("head_attention requires 3D tensors [heads, seq, head_dim]")
+        if heads is not None and (heads < 1 or self.shape[2] % heads):
+            raise abi.InvalidArgument(f"head_attention: {heads} heads do not divide rows of {self.shape[2]}")
         if k.shape[0] != self.shape[0] or k.shape[2] != self.shape[2]:
             raise abi.ShapeMismatch(f"expected {list(self.shape)}, got {list(k.shape)}",
                                     list(self.shape), list(k.shape))
         if v.shape != k.shape:
             raise abi.ShapeMismatch(f"expected {list(k.shape)}, got {list(v.shape)}", list(k.shape), list(v.shape))
-        return self._lazy(OpKind.HeadAttention(scale, causal), [self, k, v], self.shape)
+        return self._lazy(OpKind.HeadAttention(scale, causal, heads), [self, k, v], self.shape)
 
     def softmax(self, axis: int) -> "Tensor":
         nd = len(self.shape)

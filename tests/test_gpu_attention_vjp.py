@@ -140,3 +140,35 @@ def test_attention_vjp_rejects_unsupported_shapes():
     with pytest.raises(Exception, match="attention vjp"):
         hb.attention_vjp(buf, buf, buf, buf, buf, buf, buf, buf, 1, 64, 32, 1.0, True)   # dh 32
     hb.attention_vjp(buf, buf, buf, buf, buf, buf, buf, buf, 0, 64, 64, 1.0, True)       # no heads: nothing to do
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip")
+@pytest.mark.parametrize("b,t,heads,causal", [(2, 128, 4, True), (1, 192, 2, False), (4, 64, 16, True)])
+def test_heads_in_rows_layout_matches_head_major(b, t, heads, causal):
+    """HeadAttention with heads side by side in rows ([B, T, H*dh], the
+    projections' own layout) gives, forward and through its VJP, exactly the
+    values of the head-major form ([B*H, T, dh]) on the permuted inputs: per
+    head the same kernels' arithmetic, only the addressing differs."""
+    from oxidizedmlx_amd.backend import HipStream
+    dh = 64
+    d = heads * dh
+    print(f"heads in rows b={b} t={t} heads={heads} causal={causal}", flush=True)
+    q, k, v, g = (synth.normal(1300 + 7 * t + i + heads, (b, t, d)) for i in range(4))
+    scale = 1.0 / math.sqrt(dh)
+
+    def head_major(a):
+        return np.ascontiguousarray(a.reshape(b, t, heads, dh).transpose(0, 2, 1, 3).reshape(b * heads, t, dh))
+
+    def run(arrs, heads_arg):
+        st = HipStream()
+        tq, tk, tv, tg = (Tensor.from_f32_on_stream(a.reshape(-1), a.shape, st) for a in arrs)
+        o = tq.head_attention(tk, tv, scale, causal, heads=heads_arg)
+        loss = o.mul(tg).sum_all()
+        _, grads = value_and_grad(loss, [tq, tk, tv])
+        return [o.to_numpy().reshape(arrs[0].shape)] + [x.to_numpy().reshape(arrs[0].shape) for x in grads]
+
+    rows = run((q, k, v, g), heads)
+    hm = run(tuple(head_major(a) for a in (q, k, v, g)), None)
+    for name, a, e in zip(("O", "dQ", "dK", "dV"), rows, hm):
+        np.testing.assert_array_equal(head_major(a), e, err_msg=name)
