@@ -524,6 +524,31 @@ int eval_head_attention_vjp(const mlxhip_op_t& op, const mlxhip_input_t* in, siz
 
 }  // namespace
 
+int eval_matmul_group(int groups, const mlxhip_input_t* in, const int* hints, float* const* outs, hipStream_t s,
+                      Scratch& scratch) {
+    if (groups < 2 || groups > 4) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul group of %d", groups);
+    const mlxhip_input_t &a = in[0], &b = in[1];
+    if (a.ndim != 2 || b.ndim != 2) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul group: rank-2 operands only");
+    const bool ta = hints[0] != 0, tb = hints[1] != 0;
+    const int64_t m = ta ? a.shape[1] : a.shape[0], k = ta ? a.shape[0] : a.shape[1];
+    const int64_t k2 = tb ? b.shape[1] : b.shape[0], n = tb ? b.shape[0] : b.shape[1];
+    if (k != k2) return fail_shape({m, k}, {k2, n});
+    const float* pa[4];
+    const float* pb[4];
+    for (int i = 0; i < groups; ++i) {
+        const mlxhip_input_t &ai = in[2 * i], &bi = in[2 * i + 1];
+        if (ai.ndim != 2 || bi.ndim != 2 || ai.shape[0] != a.shape[0] || ai.shape[1] != a.shape[1] ||
+            bi.shape[0] != b.shape[0] || bi.shape[1] != b.shape[1] || hints[2 * i] != hints[0] ||
+            hints[2 * i + 1] != hints[1])
+            return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul group: products of different shapes");
+        if ((int64_t)ai.len != a.shape[0] * a.shape[1] || (int64_t)bi.len != b.shape[0] * b.shape[1])
+            return fail_shape({a.shape[0] * a.shape[1]}, {(int64_t)ai.len}, "matmul group operand length");
+        pa[i] = ai.data;
+        pb[i] = bi.data;
+    }
+    return gemm_f32_grouped(ta, tb, m, n, k, groups, pa, ta ? m : k, pb, tb ? k : n, outs, n, s, scratch.planes);
+}
+
 int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,
                      const mlxhip_meta_t& meta, float* out, hipStream_t s, Scratch& scratch,
                      const int* trans_hint) {

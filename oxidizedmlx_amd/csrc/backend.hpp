@@ -60,6 +60,13 @@ int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* inputs, size_t
                      const mlxhip_meta_t& out_meta, float* out, hipStream_t s, Scratch& scratch,
                      const int* trans_hint = nullptr);
 
+// `groups` (2..4) rank-2 MatMuls of one shape and operand layout, evaluated
+// together (sibling products of the Stream's graph): group i's operands are
+// inputs[2i], inputs[2i + 1] with the folded-Transpose hints hints[2i],
+// hints[2i + 1] (the same for every group), its result goes to outs[i].
+int eval_matmul_group(int groups, const mlxhip_input_t* inputs, const int* hints, float* const* outs,
+                      hipStream_t s, Scratch& scratch);
+
 // Per-thread HIP stream used by the synchronous host-vector entry points.
 hipStream_t thread_stream();
 

@@ -298,51 +298,60 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
 // Generation numbers of split-f32 products: each call's flag value.
 std::atomic<uint32_t> g_x6_gen{0};
 
-// f32 product through the bf16 planes (gemm16_x6.hip): one launch splits
-// the operands (those `cache` does not already hold), one runs the plane
-// products (and, when split over K, one sums the partials). Planes and
-// partials come from the stream's workspaces, or from the fixed scratch
-// (fs, no cache). Sets *ran = false, doing nothing, when the planes would
-// not fit the kernel's 32-bit buffer offsets.
+// f32 products through the bf16 planes (gemm16_x6.hip): `groups` products
+// of one shape and layout (groups > 1: batch 1, one launch, product i in
+// batch slot i). One launch (or one per five operands) splits the operands
+// that `cache` does not already hold, one runs the plane products (and, when
+// split over K, one sums the partials). Planes and partials come from the
+// stream's workspaces, or from the fixed scratch (fs, no cache). Sets *ran =
+// false, doing nothing, when the planes would not fit the kernel's 32-bit
+// buffer offsets.
 //
 // Planes hold the operand as stored ([rows][cols] per batch slice) with both
 // extents padded with zeros to multiples of 32, which serves it in either
 // role and either orientation: K, whichever extent it is, becomes whole K
 // tiles, and the padded M / N rows only feed C elements that are not stored.
-int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const float* a, int64_t lda,
-            int64_t stride_a, const float* b, int64_t ldb, int64_t stride_b, float* c, int64_t ldc,
-            int64_t stride_c, hipStream_t s, PlaneCache* cache, FixedScratch* fs, bool* ran) {
+int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int groups, const float* const* a,
+            int64_t lda, int64_t stride_a, const float* const* b, int64_t ldb, int64_t stride_b, float* const* c,
+            int64_t ldc, int64_t stride_c, hipStream_t s, PlaneCache* cache, FixedScratch* fs, bool* ran) {
     *ran = false;
+    if (groups < 1 || groups > gemm16::Args::MAX_GROUPS || (groups > 1 && batch != 1))
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: %d grouped products", groups);
     const int64_t kp = ceil_div(k, 32) * 32;  // segment length: whole K tiles
-    struct Operand {
-        X6SplitOp op;
-        bool fresh;  // to be split by this call
-    };
-    Operand opd[2];
-    const float* srcs[2] = {a, b};
+    // Operand 2i is product i's A, 2i + 1 its B.
+    const int nops = 2 * groups;
+    X6SplitOp op[2 * gemm16::Args::MAX_GROUPS];
+    bool fresh[2 * gemm16::Args::MAX_GROUPS];
+    int same_as[2 * gemm16::Args::MAX_GROUPS];  // an earlier operand with the same planes, or -1
     const int64_t lds[2] = {lda, ldb}, strides[2] = {stride_a, stride_b};
     const int64_t rows[2] = {ta ? k : m, tb ? n : k}, cols[2] = {ta ? m : k, tb ? k : n};
-    for (int i = 0; i < 2; ++i) {
-        X6SplitOp& o = opd[i].op;
+    for (int i = 0; i < nops; ++i) {
+        const int r = i & 1;
+        X6SplitOp& o = op[i];
         o = X6SplitOp{};
-        o.src = srcs[i];
-        o.ld = lds[i];
-        o.stride = batch > 1 ? strides[i] : 0;
-        o.rows = rows[i];
-        o.cols = cols[i];
-        o.rows_p = ceil_div(rows[i], 32) * 32;
-        o.cols_p = ceil_div(cols[i], 32) * 32;
+        o.src = r ? b[i / 2] : a[i / 2];
+        o.ld = lds[r];
+        o.stride = batch > 1 ? strides[r] : 0;
+        o.rows = rows[r];
+        o.cols = cols[r];
+        o.rows_p = ceil_div(rows[r], 32) * 32;
+        o.cols_p = ceil_div(cols[r], 32) * 32;
         o.plane = batch * o.rows_p * o.cols_p;
         o.chunks = o.plane / 8;
         // The descriptor of one slice spans two whole planes plus the slice.
         if (o.chunks >= ((int64_t)1 << 31) ||
             (2 * o.plane + o.rows_p * o.cols_p) * 2 >= (int64_t)gemm16::OOB - 4096)
             return MLXHIP_OK;
-        opd[i].fresh = true;
+        fresh[i] = true;
+        same_as[i] = -1;
+        for (int j = 0; j < i; ++j)
+            if (op[j].src == o.src && op[j].ld == o.ld && op[j].stride == o.stride && op[j].rows == o.rows &&
+                op[j].cols == o.cols) {
+                same_as[i] = j;
+                fresh[i] = false;
+                break;
+            }
     }
-    auto same = [](const X6SplitOp& x, const X6SplitOp& y) {
-        return x.src == y.src && x.ld == y.ld && x.stride == y.stride && x.rows == y.rows && x.cols == y.cols;
-    };
     auto new_gen = [] {
         uint32_t g = 0;
         while (g == 0) g = ++g_x6_gen;
@@ -350,26 +359,28 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
     };
     const size_t flag_room = 256;
     auto plane_bytes = [](const X6SplitOp& o) { return ((size_t)(3 * o.plane * 2) + 255) & ~size_t(255); };
+    auto copy_planes = [](X6SplitOp& to, const X6SplitOp& from) {
+        to.dst = from.dst;
+        to.flag = from.flag;
+        to.gen = from.gen;
+    };
     if (cache && cache->alloc && !fs) {
-        for (int i = 0; i < 2; ++i) {
-            X6SplitOp& o = opd[i].op;
+        for (int i = 0; i < nops; ++i) {
+            X6SplitOp& o = op[i];
+            if (same_as[i] >= 0) {
+                copy_planes(o, op[same_as[i]]);
+                continue;
+            }
             for (const PlaneCache::Entry& e : cache->entries)
                 if (e.src == o.src && e.ld == o.ld && e.stride == o.stride && e.rows == o.rows && e.cols == o.cols &&
                     e.batch == batch) {
                     o.dst = e.planes;
                     o.flag = e.flag;
                     o.gen = e.gen;
-                    opd[i].fresh = false;
+                    fresh[i] = false;
                     break;
                 }
-            if (!opd[i].fresh) continue;
-            if (i == 1 && same(o, opd[0].op)) {  // A and B are one matrix, split above
-                o.dst = opd[0].op.dst;
-                o.flag = opd[0].op.flag;
-                o.gen = opd[0].op.gen;
-                opd[i].fresh = false;
-                continue;
-            }
+            if (!fresh[i]) continue;
             const size_t pb = plane_bytes(o);
             char* blk = static_cast<char*>(cache->alloc(cache->ctx, pb + flag_room));
             if (!blk) return fail(MLXHIP_ERR_FFI_FAILED, "gemm: device allocation of %zu bytes failed", pb + flag_room);
@@ -380,31 +391,28 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
                                                        o.gen});
         }
     } else {
-        const bool one = same(opd[0].op, opd[1].op);
-        const size_t pa = plane_bytes(opd[0].op), pb = one ? 0 : plane_bytes(opd[1].op);
+        size_t total = 0;
+        for (int i = 0; i < nops; ++i)
+            if (fresh[i]) total += plane_bytes(op[i]) + flag_room;
         void* ws = nullptr;
-        MLXHIP_TRY(take_workspace(fs, s, WS_PACK, pa + pb + 2 * flag_room, &ws));
-        char* base = static_cast<char*>(ws);
-        opd[0].op.dst = reinterpret_cast<uint16_t*>(base);
-        opd[0].op.flag = reinterpret_cast<uint32_t*>(base + pa + pb);
-        opd[0].op.gen = new_gen();
-        if (one) {
-            opd[1].op.dst = opd[0].op.dst;
-            opd[1].op.flag = opd[0].op.flag;
-            opd[1].op.gen = opd[0].op.gen;
-            opd[1].fresh = false;
-        } else {
-            opd[1].op.dst = reinterpret_cast<uint16_t*>(base + pa);
-            opd[1].op.flag = reinterpret_cast<uint32_t*>(base + pa + pb + flag_room);
-            opd[1].op.gen = new_gen();
+        MLXHIP_TRY(take_workspace(fs, s, WS_PACK, total, &ws));
+        char* at = static_cast<char*>(ws);
+        for (int i = 0; i < nops; ++i) {
+            X6SplitOp& o = op[i];
+            if (!fresh[i]) {
+                copy_planes(o, op[same_as[i]]);
+                continue;
+            }
+            const size_t pb = plane_bytes(o);
+            o.dst = reinterpret_cast<uint16_t*>(at);
+            o.flag = reinterpret_cast<uint32_t*>(at + pb);
+            o.gen = new_gen();
+            at += pb + flag_room;
         }
     }
-    X6SplitPair sp{};
-    for (int i = 0; i < 2; ++i)
-        if (opd[i].fresh) sp.op[sp.n++] = opd[i].op;
-    const X6SplitOp &oa = opd[0].op, &ob = opd[1].op;
 
     gemm16::Args h{};
+    const X6SplitOp &oa = op[0], &ob = op[1];
     h.m = m;
     h.n = n;
     h.k = kp;
@@ -414,17 +422,17 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
     h.b = ob.dst;
     h.ldb = ob.cols_p;
     h.sb = ob.rows_p * ob.cols_p;
-    h.c = c;
+    h.c = c[0];
     h.ldc = ldc;
     h.sc = stride_c;
     h.a_bytes = (uint32_t)((2 * oa.plane + h.sa) * 2);
     h.b_bytes = (uint32_t)((2 * ob.plane + h.sb) * 2);
     h.plane_a = (uint32_t)(oa.plane * 2);
     h.plane_b = (uint32_t)(ob.plane * 2);
-    h.fa = a;
+    h.fa = a[0];
     h.flda = lda;
     h.fsa = stride_a;
-    h.fb = b;
+    h.fb = b[0];
     h.fldb = ldb;
     h.fsb = stride_b;
     h.fk = k;
@@ -432,6 +440,14 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
     h.gen_a = oa.gen;
     h.flag_b = ob.flag;
     h.gen_b = ob.gen;
+    if (groups > 1) {
+        h.groups = groups;
+        for (int i = 0; i < groups; ++i) {
+            const X6SplitOp &ga = op[2 * i], &gb = op[2 * i + 1];
+            h.grp[i] = gemm16::Args::Group{ga.dst, gb.dst, c[i], a[i], b[i], ga.flag, gb.flag, ga.gen, gb.gen};
+        }
+    }
+    const int64_t slots = groups > 1 ? groups : batch;  // gridDim.y before splits
 
     // Block tile and split (measured on the config-4 shapes, split and
     // partial sums included): the interleaved kernel, whose 144 KiB of LDS
@@ -440,12 +456,13 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
     // segment-by-segment kernel), else 128x128 blocks split over K to one
     // workgroup per CU (2048x1024x1024 split 2: 41 us against 54 us;
     // 1024x1024x2048 split 4: 42 us against 55 us; 4096x1024x2048 unsplit:
-    // 104 us against 124 us). MLXHIP_X6="cfg,splits" forces them (tuning;
-    // cfg 0-2 the segment-by-segment kernel with 256x256, 128x128 and
-    // 256x128 blocks, 3-4 the interleaved one with 256x128 and 128x128).
+    // 104 us against 124 us). Grouped products count every group's tiles and
+    // run unsplit. MLXHIP_X6="cfg,splits" forces them (tuning; cfg 0-2 the
+    // segment-by-segment kernel with 256x256, 128x128 and 256x128 blocks,
+    // 3-4 the interleaved one with 256x128 and 128x128).
     const int64_t kv = gemm16::X6_SEGS * kp;
-    const int64_t wide_tiles = ceil_div(m, 256) * ceil_div(n, 128) * batch;
-    const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * batch;
+    const int64_t wide_tiles = ceil_div(m, 256) * ceil_div(n, 128) * slots;
+    const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * slots;
     int cfg = 3, sp_k = 1;
     if (wide_tiles < 224) {
         cfg = 4;
@@ -458,10 +475,23 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
             sp_k = v;
         }
     }
-    if (batch * sp_k > 65535) sp_k = 1;
+    if (groups > 1) {
+        sp_k = 1;
+        if (cfg < 3) cfg = 3;
+    }
+    if (slots * sp_k > 65535) sp_k = 1;
+    X6SplitPair sp{};
+    for (int i = 0; i < nops; ++i) {
+        if (!fresh[i]) continue;
+        sp.op[sp.n++] = op[i];
+        if (sp.n == X6SplitPair::MAX) {
+            MLXHIP_TRY(x6_split(sp, s));
+            sp.n = 0;
+        }
+    }
     if (sp.n) MLXHIP_TRY(x6_split(sp, s));
     if (sp_k == 1) {
-        MLXHIP_TRY(gemm16_x6(ta, tb, h, batch, cfg, s));
+        MLXHIP_TRY(gemm16_x6(ta, tb, h, slots, cfg, s));
         *ran = true;
         return MLXHIP_OK;
     }
@@ -477,7 +507,7 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, cons
     h.ldc = ldw;
     h.sc = m * ldw;
     MLXHIP_TRY(gemm16_x6(ta, tb, h, batch, cfg, s));
-    MLXHIP_TRY(splitk_reduce(MLXHIP_DTYPE_F32, static_cast<const float*>(part), c, m, n, ldw, ldc, stride_c,
+    MLXHIP_TRY(splitk_reduce(MLXHIP_DTYPE_F32, static_cast<const float*>(part), c[0], m, n, ldw, ldc, stride_c,
                              h.splits, batch, s));
     *ran = true;
     return MLXHIP_OK;
@@ -491,6 +521,37 @@ bool use_x6(int path, int64_t m, int64_t n, int64_t k, int64_t batch) {
     return m >= 256 && n >= 256 && k >= 256 && (double)m * (double)n * (double)k * (double)batch >= 2147483648.0;
 }
 }  // namespace
+
+// MLXHIP_GEMM_GROUPS=0 turns grouping off (each product its own launch;
+// read on every call, for comparisons).
+bool gemm_f32_groupable(int64_t m, int64_t n, int64_t k) {
+    const char* e = getenv("MLXHIP_GEMM_GROUPS");
+    if (e && !strcmp(e, "0")) return false;
+    const int path = gemm_path();
+    return (path == 0 || path == 5) && use_x6(path, m, n, k, 1);
+}
+
+int gemm_f32_grouped(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, int groups, const float* const* a,
+                     int64_t lda, const float* const* b, int64_t ldb, float* const* c, int64_t ldc, hipStream_t s,
+                     PlaneCache* planes) {
+    if (groups < 1 || groups > gemm16::Args::MAX_GROUPS)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: %d grouped products", groups);
+    if (m < 0 || n < 0 || k < 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: negative size");
+    for (int i = 0; i < groups; ++i)
+        if (!a[i] || !b[i] || !c[i]) return fail(MLXHIP_ERR_NULL_PTR, "gemm: null operand in group %d", i);
+    if (ldc < n || lda < (trans_a ? m : k) || ldb < (trans_b ? k : n))
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: leading dimension too small");
+    if (groups > 1 && m > 0 && n > 0 && k > 0 && gemm_f32_groupable(m, n, k)) {
+        bool ran = false;
+        MLXHIP_TRY(gemm_x6(trans_a, trans_b, m, n, k, 1, groups, a, lda, 0, b, ldb, 0, c, ldc, 0, s, planes, nullptr,
+                           &ran));
+        if (ran) return MLXHIP_OK;
+    }
+    for (int i = 0; i < groups; ++i)
+        MLXHIP_TRY(gemm_impl(MLXHIP_DTYPE_F32, MLXHIP_DTYPE_F32, trans_a, trans_b, m, n, k, 1, a[i], lda, 0, b[i], ldb,
+                             0, c[i], ldc, 0, s, false, nullptr, planes));
+    return MLXHIP_OK;
+}
 
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
@@ -544,9 +605,11 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     if (ab_dtype == MLXHIP_DTYPE_F32 && c_dtype == MLXHIP_DTYPE_F32 && !padded &&
         use_x6(gemm_path(), m, n, k, batch)) {
         bool ran = false;
-        MLXHIP_TRY(gemm_x6(trans_a, trans_b, m, n, k, batch, static_cast<const float*>(a), lda, stride_a,
-                           static_cast<const float*>(b), ldb, stride_b, static_cast<float*>(c), ldc, stride_c, s,
-                           cache, fs, &ran));
+        const float* fa = static_cast<const float*>(a);
+        const float* fb = static_cast<const float*>(b);
+        float* fc = static_cast<float*>(c);
+        MLXHIP_TRY(gemm_x6(trans_a, trans_b, m, n, k, batch, 1, &fa, lda, stride_a, &fb, ldb, stride_b, &fc, ldc,
+                           stride_c, s, cache, fs, &ran));
         if (ran) return MLXHIP_OK;
     }
 

@@ -125,7 +125,35 @@ struct Args {
     const uint32_t* flag_a = nullptr;
     const uint32_t* flag_b = nullptr;
     uint32_t gen_a = 0, gen_b = 0;
+    // Grouped products (interleaved split-f32 kernel only, one split): with
+    // groups > 0, batch index b runs product grp[b] of the same shapes and
+    // layouts, its planes, C and f32 operands at the pointers given here
+    // instead of base + b * stride.
+    struct Group {
+        const void* a;
+        const void* b;
+        void* c;
+        const float* fa;
+        const float* fb;
+        const uint32_t* flag_a;
+        const uint32_t* flag_b;
+        uint32_t gen_a, gen_b;
+    };
+    static constexpr int MAX_GROUPS = 4;
+    int groups = 0;
+    Group grp[MAX_GROUPS] = {};
 };
+
+// Group b of a grouped launch, read with constant offsets (a run-time index
+// into the kernel arguments would copy them to scratch).
+__device__ inline Args::Group group_of(const Args& g, int b) {
+    switch (b) {
+        case 0: return g.grp[0];
+        case 1: return g.grp[1];
+        case 2: return g.grp[2];
+        default: return g.grp[3];
+    }
+}
 
 // Plane pairs of the 6 k segments, smallest products first so the f32
 // accumulators add the large hi*hi terms last: (mid, mid), (lo, hi),
@@ -374,7 +402,7 @@ __device__ inline TileId tile_of(const Args& g) {
 // Epilogue of the kernels below (C tile of one workgroup, after its last
 // MFMA), through the first bytes of the operand stages' LDS.
 template <int CT, class C, int PIPE_BYTES>
-__device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN], MLXHIP_LDS char* smem, int64_t slice,
+__device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN], MLXHIP_LDS char* smem, char* Cp,
                                int64_t m0, int64_t n0, int wave, int lane) {
     // Through LDS. acc[i][j][v] = C[m][n] with m = WR wm + 32 i +
     // lane % 32 and n = WC wn + 32 j + 8 (v / 4) + 4 (lane / 32) + v % 4
@@ -395,7 +423,6 @@ __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN],
     constexpr int ROWS_PER_READ = 64 / LANES_PER_ROW;
     static_assert(LANES_PER_ROW <= 64 && 64 % LANES_PER_ROW == 0, "epilogue read shape");
     MLXHIP_LDS char* region = smem + wave * PASS_ROWS * PITCH;
-    char* Cp = static_cast<char*>(g.c) + slice * g.sc * ES;
     const int64_t row0 = m0 + 32 * TM * wm, col0 = n0 + 32 * TN * wn;
     const bool vec_ok = (g.ldc * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(Cp) % 16) == 0;
 #pragma unroll
@@ -458,11 +485,8 @@ constexpr int epi_bytes() {
 // whole K, so infinities and NaNs combine as in an f32 product. Split 0 of a
 // split-K launch holds the product, the other splits zeros.
 template <int TA, int TB, class C>
-__device__ void x6_direct(const Args& g, int64_t batch, int64_t split, int64_t slice, int64_t m0, int64_t n0,
-                          int tid) {
-    const float* A = g.fa + batch * g.fsa;
-    const float* B = g.fb + batch * g.fsb;
-    float* Cp = static_cast<float*>(g.c) + slice * g.sc;
+__device__ void x6_direct(const Args& g, const float* A, const float* B, float* Cp, int64_t split, int64_t m0,
+                          int64_t n0, int tid) {
     for (int e = tid; e < C::BM * C::BN; e += C::THREADS) {
         const int64_t m = m0 + e / C::BN, n = n0 + e % C::BN;
         if (m >= g.m || n >= g.n) continue;
@@ -500,7 +524,8 @@ void gemm16_kernel(Args g) {
     if constexpr (X6) {
         if (__atomic_load_n(g.flag_a, __ATOMIC_RELAXED) == g.gen_a ||
             __atomic_load_n(g.flag_b, __ATOMIC_RELAXED) == g.gen_b) {
-            x6_direct<TA, TB, C>(g, batch, split, slice, m0, n0, tid);
+            x6_direct<TA, TB, C>(g, g.fa + batch * g.fsa, g.fb + batch * g.fsb, static_cast<float*>(g.c) + slice * g.sc,
+                                 split, m0, n0, tid);
             return;
         }
     }
@@ -634,7 +659,8 @@ void gemm16_kernel(Args g) {
         }
     }
 
-    store_c<CT, C, PIPE_BYTES>(g, acc, smem, slice, m0, n0, wave, lane);
+    store_c<CT, C, PIPE_BYTES>(g, acc, smem, static_cast<char*>(g.c) + slice * g.sc * (CT == MLXHIP_DTYPE_F32 ? 4 : 2),
+                               m0, n0, wave, lane);
 }
 
 // Host-side check of what the kernel assumes about its operands; returns
@@ -713,9 +739,10 @@ struct X6SplitOp {
     uint32_t* flag;          // receives gen if a value is not finite or its
     uint32_t gen;            // hi plane rounds out of range
 };
-// Up to two operands in one launch (gridDim.y = n).
+// Up to MAX operands in one launch (gridDim.y = n).
 struct X6SplitPair {
-    X6SplitOp op[2];
+    static constexpr int MAX = 5;
+    X6SplitOp op[MAX];
     int n;
 };
 int x6_split(const X6SplitPair& sp, hipStream_t s);

@@ -81,10 +81,10 @@ __device__ inline void split_store(const X6SplitOp& o, const SplitChunk& k, cons
     *reinterpret_cast<u16x8*>(dst + 2 * o.plane) = lo;
 }
 
-// Two chunks per thread per step, both loaded before either is split, so
-// each wave keeps four 16-byte loads per lane in flight.
-__global__ void __launch_bounds__(256) x6_split_kernel(X6SplitPair sp) {
-    const X6SplitOp& o = sp.op[blockIdx.y];
+// The split of one operand by this workgroup: two chunks per thread per
+// step, both loaded before either is split, so each wave keeps four 16-byte
+// loads per lane in flight.
+__device__ inline void split_op(const X6SplitOp& o) {
     const uint32_t cpr = (uint32_t)(o.cols_p / 8);  // 8-element chunks per plane row
     const uint32_t rows_p = (uint32_t)o.rows_p;
     const bool vec = o.ld % 4 == 0 && reinterpret_cast<uintptr_t>(o.src) % 16 == 0 && o.stride % 4 == 0;
@@ -102,10 +102,22 @@ __global__ void __launch_bounds__(256) x6_split_kernel(X6SplitPair sp) {
     if (bad) *o.flag = o.gen;
 }
 
+// gridDim.y = operands; each case names its operand with a constant index (a
+// run-time index into the kernel arguments would copy them to scratch).
+__global__ void __launch_bounds__(256) x6_split_kernel(X6SplitPair sp) {
+    switch (blockIdx.y) {
+        case 0: split_op(sp.op[0]); break;
+        case 1: split_op(sp.op[1]); break;
+        case 2: split_op(sp.op[2]); break;
+        case 3: split_op(sp.op[3]); break;
+        default: split_op(sp.op[4]); break;
+    }
+}
+
 }  // namespace
 
 int x6_split(const X6SplitPair& sp, hipStream_t s) {
-    if (sp.n < 0 || sp.n > 2) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: split-f32 operand count");
+    if (sp.n < 0 || sp.n > X6SplitPair::MAX) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: split-f32 operand count");
     int64_t most = 0;
     for (int i = 0; i < sp.n; ++i) {
         const X6SplitOp& o = sp.op[i];
@@ -162,9 +174,37 @@ void gemm_x6i_kernel(Args g) {
     const TileId tl = tile_of<C>(g);
     const int64_t slice = tl.slice, batch = tl.batch, split = tl.split, m0 = tl.m0, n0 = tl.n0;
 
-    if (__atomic_load_n(g.flag_a, __ATOMIC_RELAXED) == g.gen_a ||
-        __atomic_load_n(g.flag_b, __ATOMIC_RELAXED) == g.gen_b) {
-        x6_direct<TA, TB, C>(g, batch, split, slice, m0, n0, tid);
+    // This slice's planes, C and f32 operands (a group's, or base + stride).
+    const char *pa, *pb;
+    char* pc;
+    const float *fa32, *fb32;
+    const uint32_t *flag_a, *flag_b;
+    uint32_t gen_a, gen_b;
+    if (g.groups) {
+        const Args::Group gr = group_of(g, (int)batch);
+        pa = static_cast<const char*>(gr.a);
+        pb = static_cast<const char*>(gr.b);
+        pc = static_cast<char*>(gr.c);
+        fa32 = gr.fa;
+        fb32 = gr.fb;
+        flag_a = gr.flag_a;
+        flag_b = gr.flag_b;
+        gen_a = gr.gen_a;
+        gen_b = gr.gen_b;
+    } else {
+        pa = static_cast<const char*>(g.a) + batch * g.sa * 2;
+        pb = static_cast<const char*>(g.b) + batch * g.sb * 2;
+        pc = static_cast<char*>(g.c) + slice * g.sc * 4;
+        fa32 = g.fa + batch * g.fsa;
+        fb32 = g.fb + batch * g.fsb;
+        flag_a = g.flag_a;
+        flag_b = g.flag_b;
+        gen_a = g.gen_a;
+        gen_b = g.gen_b;
+    }
+
+    if (__atomic_load_n(flag_a, __ATOMIC_RELAXED) == gen_a || __atomic_load_n(flag_b, __ATOMIC_RELAXED) == gen_b) {
+        x6_direct<TA, TB, C>(g, fa32, fb32, reinterpret_cast<float*>(pc), split, m0, n0, tid);
         return;
     }
 
@@ -173,8 +213,8 @@ void gemm_x6i_kernel(Args g) {
     const int64_t kb = split * g.k_chunk;
     const int64_t klen = g.splits > 1 ? min(g.k - kb, g.k_chunk) : g.k;
     const int64_t a_koff = (KCA ? kb : kb * g.lda) * 2, b_koff = (KCB ? kb : kb * g.ldb) * 2;
-    const char* A = static_cast<const char*>(g.a) + batch * g.sa * 2 + a_koff;
-    const char* B = static_cast<const char*>(g.b) + batch * g.sb * 2 + b_koff;
+    const char* A = pa + a_koff;
+    const char* B = pb + b_koff;
     const __amdgpu_buffer_rsrc_t ra =
         __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)(g.a_bytes - (uint32_t)a_koff), BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t rb =
@@ -273,7 +313,7 @@ void gemm_x6i_kernel(Args g) {
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    store_c<MLXHIP_DTYPE_F32, C, PIPE_BYTES>(g, acc, smem, slice, m0, n0, wave, lane);
+    store_c<MLXHIP_DTYPE_F32, C, PIPE_BYTES>(g, acc, smem, pc, m0, n0, wave, lane);
 }
 
 template <int TA, int TB, class C>

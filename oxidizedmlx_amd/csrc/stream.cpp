@@ -262,7 +262,18 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     Scratch scratch;
     scratch.planes = &planes;
     int rc = MLXHIP_OK;
-    for (uint64_t id : order) {
+    // A MatMul operand's source node after folded Transposes, and how many
+    // Transposes (mod 2) lie between: the GEMM reads the source with the
+    // layout flipped that many times.
+    auto resolve = [&](uint64_t src, int* hint) {
+        while (folded_transpose.count(src)) {
+            *hint ^= 1;
+            src = nodes.at(src).inputs[0];
+        }
+        return src;
+    };
+    for (size_t oi = 0; oi < order.size(); ++oi) {
+        const uint64_t id = order[oi];
         if (buffers.count(id) || folded_transpose.count(id) || interior.count(id) || virtual_bcast.count(id) ||
             absorbed_matmul.count(id))
             continue;
@@ -369,6 +380,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         // Transpose runs its MatMul as B^T A^T.
         std::vector<mlxhip_input_t> ins;
         int hint[2] = {0, 0};
+        uint64_t msrc[2] = {0, 0};  // a MatMul's resolved operand sources
         bool missing = false;
         const bool swapped = swapped_matmul.count(id) != 0;
         const Node& en = swapped ? nodes.at(n.inputs[0]) : n;  // the node whose op runs
@@ -384,11 +396,84 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
                     src = nodes.at(src).inputs[0];
                 }
             }
+            if (j < 2) msrc[j] = src;
             auto b = buffers.find(src);
             if (b == buffers.end()) { missing = true; break; }
             ins.push_back(input_of(src, b->second.ptr));
         }
         if (missing) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "input node should be evaluated before dependents"); break; }
+        // Sibling products: later MatMuls of this evaluation that share one
+        // operand with this one (same source, same layout), whose other
+        // operand has the same shape and layout and is ready, run with it in
+        // one grouped launch (the Q/K/V projections of one input). They get
+        // their buffers now, and the loop skips them when it reaches them.
+        std::vector<uint64_t> sib;
+        std::vector<mlxhip_input_t> gin;  // 2 per product, this one first
+        if (fusion && !swapped && en.op.op.kind == MLXHIP_OP_MATMUL && ins.size() == 2 && ins[0].ndim == 2 &&
+            ins[1].ndim == 2 && n.meta.dtype == MLXHIP_DTYPE_F32) {
+            const int64_t m = hint[0] ? ins[0].shape[1] : ins[0].shape[0], k = hint[0] ? ins[0].shape[0] : ins[0].shape[1];
+            const int64_t nn = hint[1] ? ins[1].shape[0] : ins[1].shape[1];
+            int share = -1;  // 0: A in common, 1: B
+            for (size_t oj = oi + 1; oj < order.size() && sib.size() < 3 && gemm_f32_groupable(m, nn, k); ++oj) {
+                const uint64_t cid = order[oj];
+                if (buffers.count(cid) || folded_transpose.count(cid) || absorbed_matmul.count(cid) ||
+                    swapped_matmul.count(cid))
+                    continue;
+                const Node& cn = nodes.at(cid);
+                if (cn.op.op.kind != MLXHIP_OP_MATMUL || cn.inputs.size() != 2 || cn.meta.dtype != MLXHIP_DTYPE_F32 ||
+                    cn.meta.shape != n.meta.shape)
+                    continue;
+                int ch[2] = {0, 0};
+                const uint64_t cs[2] = {resolve(cn.inputs[0], &ch[0]), resolve(cn.inputs[1], &ch[1])};
+                if (ch[0] != hint[0] || ch[1] != hint[1] || !buffers.count(cs[0]) || !buffers.count(cs[1]) ||
+                    nodes.at(cs[0]).meta.shape != nodes.at(msrc[0]).meta.shape ||
+                    nodes.at(cs[1]).meta.shape != nodes.at(msrc[1]).meta.shape)
+                    continue;
+                const int sh = cs[0] == msrc[0] ? 0 : cs[1] == msrc[1] ? 1 : -1;
+                if (sh < 0 || (cs[0] == msrc[0] && cs[1] == msrc[1]) || (share >= 0 && sh != share)) continue;
+                share = sh;
+                sib.push_back(cid);
+                gin.push_back(input_of(cs[0], buffers.at(cs[0]).ptr));
+                gin.push_back(input_of(cs[1], buffers.at(cs[1]).ptr));
+            }
+        }
+        if (!sib.empty()) {
+            std::vector<float*> outs(1 + sib.size(), nullptr);
+            if ((rc = alloc_out(id, &outs[0])) != MLXHIP_OK) break;
+            for (size_t i = 0; i < sib.size() && rc == MLXHIP_OK; ++i) rc = alloc_out(sib[i], &outs[1 + i]);
+            std::vector<mlxhip_input_t> all{ins[0], ins[1]};
+            all.insert(all.end(), gin.begin(), gin.end());
+            std::vector<int> hints;
+            for (size_t i = 0; i < outs.size(); ++i) hints.insert(hints.end(), {hint[0], hint[1]});
+            if (rc == MLXHIP_OK)
+                rc = eval_matmul_group((int)outs.size(), all.data(), hints.data(), outs.data(), hs, scratch);
+            if (rc != MLXHIP_OK) {
+                for (uint64_t g : sib) {
+                    auto b = buffers.find(g);
+                    if (b != buffers.end()) {
+                        release_later(b->second.ptr);
+                        buffers.erase(b);
+                    }
+                }
+                auto b = buffers.find(id);
+                if (b != buffers.end()) {
+                    release_later(b->second.ptr);
+                    buffers.erase(b);
+                }
+                break;
+            }
+            for (uint64_t g : sib) {
+                covered += 1;
+                for (uint64_t src : nodes.at(g).inputs)
+                    while (folded_transpose.count(src)) {
+                        if (counted_folded.insert(src).second) covered += 1;
+                        src = nodes.at(src).inputs[0];
+                    }
+            }
+            eval_calls += covered;
+            launches += 1;
+            continue;
+        }
         float* out = nullptr;
         if ((rc = alloc_out(id, &out)) != MLXHIP_OK) break;
         const mlxhip_op_t op = en.op.c();

@@ -589,3 +589,44 @@ def test_split_f32_planes_reused_across_evaluations_and_dropped_at_clear():
         gemm_full_check(s.get_buffer(y).reshape(T, O), x0, w0.T, "f32", f"x W^T, round {rnd}")
         gemm_full_check(s.get_buffer(dx).reshape(T, I), g0, w0, "f32", f"g W, round {rnd}")
         s.clear()
+
+
+@pytest.mark.parametrize("shared", ["A", "B"])
+def test_sibling_products_run_as_one_grouped_launch(shared):
+    # Three products with one operand in common (x W_i^T, the Q/K/V
+    # projections of one input; or dY_i^T X, sharing X) at a size that takes
+    # the split-f32 path run as one grouped launch; every output against
+    # float64 with the f32 accumulation bound, and against the unfused graph
+    # (which runs them one by one) within the same bound.
+    from parity import gemm_full_check
+    T, I, O = 1024, 2048, 1024
+    x0 = synth.normal(561, (T, I))
+    ws0 = [synth.normal(562 + i, (O, I)) for i in range(3)]
+    res = {}
+    for fusion in (True, False):
+        s = HipStream(fusion=fusion)
+        if shared == "A":
+            x = s.add_constant(x0, meta((T, I)))
+            outs = []
+            for w0 in ws0:
+                w = s.add_constant(w0, meta((O, I)))
+                wt = s.add_op(OpKind.Transpose(None), [w], meta((I, O)))
+                outs.append(s.add_op(OpKind.MatMul, [x, wt], meta((T, O))))          # x W_i^T
+            refs = [(x0, w0.T) for w0 in ws0]
+        else:
+            x = s.add_constant(x0, meta((T, I)))
+            outs = []
+            for w0 in ws0:
+                dy = s.add_constant(np.ascontiguousarray(w0[:, :T].T), meta((T, O)))
+                dyt = s.add_op(OpKind.Transpose(None), [dy], meta((O, T)))
+                outs.append(s.add_op(OpKind.MatMul, [dyt, x], meta((O, I))))         # dY_i^T X
+            refs = [(np.ascontiguousarray(w0[:, :T]), x0) for w0 in ws0]
+        before = s.launch_count()
+        s.eval_many(outs)
+        res[fusion] = ([s.get_buffer(o).reshape(refs[0][0].shape[0], refs[0][1].shape[1]) for o in outs],
+                       s.launch_count() - before)
+    got, launches = res[True]
+    assert launches == 1, f"{launches} launches for three sibling products"
+    for i, ((a, b), g, u) in enumerate(zip(refs, got, res[False][0])):
+        gemm_full_check(g, a, b, "f32", f"grouped product {i} (shared {shared})")
+        gemm_full_check(u, a, b, "f32", f"separate product {i}")
