@@ -402,18 +402,17 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             ins.push_back(input_of(src, b->second.ptr));
         }
         if (missing) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "input node should be evaluated before dependents"); break; }
-        // Sibling products: later MatMuls of this evaluation that share one
-        // operand with this one (same source, same layout), whose other
-        // operand has the same shape and layout and is ready, run with it in
-        // one grouped launch (the Q/K/V projections of one input). They get
-        // their buffers now, and the loop skips them when it reaches them.
+        // Sibling products: later MatMuls of this evaluation with operands of
+        // the same shapes and layouts, both ready, run with this one in one
+        // grouped launch (the Q/K/V projections of one input; the three
+        // products of their input gradient). They get their buffers now, and
+        // the loop skips them when it reaches them.
         std::vector<uint64_t> sib;
         std::vector<mlxhip_input_t> gin;  // 2 per product, this one first
         if (fusion && !swapped && en.op.op.kind == MLXHIP_OP_MATMUL && ins.size() == 2 && ins[0].ndim == 2 &&
             ins[1].ndim == 2 && n.meta.dtype == MLXHIP_DTYPE_F32) {
             const int64_t m = hint[0] ? ins[0].shape[1] : ins[0].shape[0], k = hint[0] ? ins[0].shape[0] : ins[0].shape[1];
             const int64_t nn = hint[1] ? ins[1].shape[0] : ins[1].shape[1];
-            int share = -1;  // 0: A in common, 1: B
             for (size_t oj = oi + 1; oj < order.size() && sib.size() < 3 && gemm_f32_groupable(m, nn, k); ++oj) {
                 const uint64_t cid = order[oj];
                 if (buffers.count(cid) || folded_transpose.count(cid) || absorbed_matmul.count(cid) ||
@@ -429,9 +428,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
                     nodes.at(cs[0]).meta.shape != nodes.at(msrc[0]).meta.shape ||
                     nodes.at(cs[1]).meta.shape != nodes.at(msrc[1]).meta.shape)
                     continue;
-                const int sh = cs[0] == msrc[0] ? 0 : cs[1] == msrc[1] ? 1 : -1;
-                if (sh < 0 || (cs[0] == msrc[0] && cs[1] == msrc[1]) || (share >= 0 && sh != share)) continue;
-                share = sh;
+                if (cs[0] == msrc[0] && cs[1] == msrc[1]) continue;  // the same product
                 sib.push_back(cid);
                 gin.push_back(input_of(cs[0], buffers.at(cs[0]).ptr));
                 gin.push_back(input_of(cs[1], buffers.at(cs[1]).ptr));

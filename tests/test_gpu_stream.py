@@ -591,10 +591,11 @@ def test_split_f32_planes_reused_across_evaluations_and_dropped_at_clear():
         s.clear()
 
 
-@pytest.mark.parametrize("shared", ["A", "B"])
+@pytest.mark.parametrize("shared", ["A", "B", "none"])
 def test_sibling_products_run_as_one_grouped_launch(shared):
     # Three products with one operand in common (x W_i^T, the Q/K/V
-    # projections of one input; or dY_i^T X, sharing X) at a size that takes
+    # projections of one input; or dY_i^T X, sharing X) or none (dY_i W_i,
+    # the products of the input's gradient) at a size that takes
     # the split-f32 path run as one grouped launch; every output against
     # float64 with the f32 accumulation bound, and against the unfused graph
     # (which runs them one by one) within the same bound.
@@ -613,6 +614,14 @@ def test_sibling_products_run_as_one_grouped_launch(shared):
                 wt = s.add_op(OpKind.Transpose(None), [w], meta((I, O)))
                 outs.append(s.add_op(OpKind.MatMul, [x, wt], meta((T, O))))          # x W_i^T
             refs = [(x0, w0.T) for w0 in ws0]
+        elif shared == "none":
+            # dY_i W_i: no operand in common (the input gradient's products).
+            outs = []
+            for i, w0 in enumerate(ws0):
+                dy = s.add_constant(synth.normal(571 + i, (T, O)), meta((T, O)))
+                w = s.add_constant(w0, meta((O, I)))
+                outs.append(s.add_op(OpKind.MatMul, [dy, w], meta((T, I))))
+            refs = [(synth.normal(571 + i, (T, O)), w0) for i, w0 in enumerate(ws0)]
         else:
             x = s.add_constant(x0, meta((T, I)))
             outs = []
