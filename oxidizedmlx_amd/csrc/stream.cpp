@@ -407,23 +407,28 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         // grouped launch (the Q/K/V projections of one input; the three
         // products of their input gradient). They get their buffers now, and
         // the loop skips them when it reaches them.
+        // A swapped product (a Transpose computed as B^T A^T, every weight
+        // gradient) groups with other swapped products, its operands taken
+        // in the swapped order.
         std::vector<uint64_t> sib;
         std::vector<mlxhip_input_t> gin;  // 2 per product, this one first
-        if (fusion && !swapped && en.op.op.kind == MLXHIP_OP_MATMUL && ins.size() == 2 && ins[0].ndim == 2 &&
+        if (fusion && en.op.op.kind == MLXHIP_OP_MATMUL && ins.size() == 2 && ins[0].ndim == 2 &&
             ins[1].ndim == 2 && n.meta.dtype == MLXHIP_DTYPE_F32) {
             const int64_t m = hint[0] ? ins[0].shape[1] : ins[0].shape[0], k = hint[0] ? ins[0].shape[0] : ins[0].shape[1];
             const int64_t nn = hint[1] ? ins[1].shape[0] : ins[1].shape[1];
             for (size_t oj = oi + 1; oj < order.size() && sib.size() < 3 && gemm_f32_groupable(m, nn, k); ++oj) {
                 const uint64_t cid = order[oj];
                 if (buffers.count(cid) || folded_transpose.count(cid) || absorbed_matmul.count(cid) ||
-                    swapped_matmul.count(cid))
+                    (swapped_matmul.count(cid) != 0) != swapped)
                     continue;
                 const Node& cn = nodes.at(cid);
-                if (cn.op.op.kind != MLXHIP_OP_MATMUL || cn.inputs.size() != 2 || cn.meta.dtype != MLXHIP_DTYPE_F32 ||
+                const Node& ce = swapped ? nodes.at(cn.inputs[0]) : cn;  // the node whose op runs
+                if (ce.op.op.kind != MLXHIP_OP_MATMUL || ce.inputs.size() != 2 || cn.meta.dtype != MLXHIP_DTYPE_F32 ||
                     cn.meta.shape != n.meta.shape)
                     continue;
-                int ch[2] = {0, 0};
-                const uint64_t cs[2] = {resolve(cn.inputs[0], &ch[0]), resolve(cn.inputs[1], &ch[1])};
+                int ch[2] = {swapped ? 1 : 0, swapped ? 1 : 0};
+                const uint64_t cs[2] = {resolve(ce.inputs[swapped ? 1 : 0], &ch[0]),
+                                        resolve(ce.inputs[swapped ? 0 : 1], &ch[1])};
                 if (ch[0] != hint[0] || ch[1] != hint[1] || !buffers.count(cs[0]) || !buffers.count(cs[1]) ||
                     nodes.at(cs[0]).meta.shape != nodes.at(msrc[0]).meta.shape ||
                     nodes.at(cs[1]).meta.shape != nodes.at(msrc[1]).meta.shape)
@@ -460,8 +465,8 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
                 break;
             }
             for (uint64_t g : sib) {
-                covered += 1;
-                for (uint64_t src : nodes.at(g).inputs)
+                covered += swapped ? 2 : 1;
+                for (uint64_t src : nodes.at(swapped ? nodes.at(g).inputs[0] : g).inputs)
                     while (folded_transpose.count(src)) {
                         if (counted_folded.insert(src).second) covered += 1;
                         src = nodes.at(src).inputs[0];

@@ -600,7 +600,9 @@ def test_sibling_products_run_as_one_grouped_launch(shared):
     # float64 with the f32 accumulation bound, and against the unfused graph
     # (which runs them one by one) within the same bound.
     from parity import gemm_full_check
-    T, I, O = 1024, 2048, 1024
+    # Shapes whose three products together fill the chip unsplit (384 tiles
+    # of 128x128), so the grouped launch runs.
+    T, I, O = 1024, 2048, (2048 if shared == "A" else 1024)
     x0 = synth.normal(561, (T, I))
     ws0 = [synth.normal(562 + i, (O, I)) for i in range(3)]
     res = {}
@@ -639,3 +641,26 @@ def test_sibling_products_run_as_one_grouped_launch(shared):
     for i, ((a, b), g, u) in enumerate(zip(refs, got, res[False][0])):
         gemm_full_check(g, a, b, "f32", f"grouped product {i} (shared {shared})")
         gemm_full_check(u, a, b, "f32", f"separate product {i}")
+
+
+def test_swapped_sibling_products_run_as_one_grouped_launch():
+    # Four weight-gradient-shaped products (dY_i^T X)^T, each a Transpose of
+    # a MatMul nothing else reads, run as swapped products X^T dY_i, and as
+    # one grouped launch; every output against float64 with the f32 bound.
+    from parity import gemm_full_check
+    T, I, O = 2048, 1024, 1024
+    x0 = synth.normal(581, (T, I))
+    dys = [synth.normal(582 + i, (T, O)) for i in range(4)]
+    s = HipStream()
+    x = s.add_constant(x0, meta((T, I)))
+    outs = []
+    for dy0 in dys:
+        dy = s.add_constant(dy0, meta((T, O)))
+        dyt = s.add_op(OpKind.Transpose(None), [dy], meta((O, T)))
+        prod = s.add_op(OpKind.MatMul, [dyt, x], meta((O, I)))                       # dY^T X
+        outs.append(s.add_op(OpKind.Transpose((1, 0)), [prod], meta((I, O))))       # (dY^T X)^T
+    before = s.launch_count()
+    s.eval_many(outs)
+    assert s.launch_count() - before == 1
+    for i, (o, dy0) in enumerate(zip(outs, dys)):
+        gemm_full_check(s.get_buffer(o).reshape(I, O), np.ascontiguousarray(x0.T), dy0, "f32", f"swapped product {i}")
