@@ -20,6 +20,7 @@
 // evaluation report the same count.
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -482,10 +483,12 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         const mlxhip_meta_t meta = n.meta.c();
         eval_calls += covered;
         launches += 1;
-        // A leaf axis reduction over a long axis runs on the side queue.
+        // A leaf axis reduction over a long axis runs on the side queue
+        // (MLXHIP_SIDE_QUEUE=0: on the stream's own queue, for comparisons).
         hipStream_t q = hs;
         const int kind = en.op.op.kind;
-        if ((kind == MLXHIP_OP_SUM || kind == MLXHIP_OP_MEAN || kind == MLXHIP_OP_MAX) && en.op.op.has_axis &&
+        static const bool side_ok = !(getenv("MLXHIP_SIDE_QUEUE") && !strcmp(getenv("MLXHIP_SIDE_QUEUE"), "0"));
+        if (side_ok && (kind == MLXHIP_OP_SUM || kind == MLXHIP_OP_MEAN || kind == MLXHIP_OP_MAX) && en.op.op.has_axis &&
             !swapped && consumers[id] == 0 && ins.size() == 1 && ins[0].ndim >= 1) {
             int64_t ax = en.op.op.axis;
             if (ax < 0) ax += (int64_t)ins[0].ndim;
