@@ -110,8 +110,10 @@ def test_x6_block_and_split_settings(monkeypatch, setting):
 ])
 def test_x6_chosen_for_config4_shapes(m, n, k, ta, tb):
     """The shapes the block's f32 products take through the automatic choice
-    (the split-f32 kernel), sampled rows against the oracle."""
-    check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), seed=m + n + k + 1, rows=sample_rows(m, 8))
+    (the split-f32 kernel), sampled rows against the oracle; the two
+    1024-wide ones also every element against float64."""
+    check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), seed=m + n + k + 1, rows=sample_rows(m, 8),
+               full=(n == 1024 and k <= 2048))
 
 
 def run_f32(a, b, ta=False, tb=False):

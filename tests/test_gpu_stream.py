@@ -664,3 +664,34 @@ def test_swapped_sibling_products_run_as_one_grouped_launch():
     assert s.launch_count() - before == 1
     for i, (o, dy0) in enumerate(zip(outs, dys)):
         gemm_full_check(s.get_buffer(o).reshape(I, O), np.ascontiguousarray(x0.T), dy0, "f32", f"swapped product {i}")
+
+
+def test_grouped_products_with_non_finite_operand():
+    # A grouped launch where one product's weight holds inf and NaN: that
+    # product takes the exact f32 path (its flag), giving what an f32 product
+    # gives; the others keep the split-f32 result (float64 bound).
+    from parity import gemm_full_check
+    T, I, O = 2048, 1024, 1024
+    x0 = synth.normal(591, (T, I))
+    ws0 = [synth.normal(592 + i, (O, I)) for i in range(3)]
+    ws0[1][5, 7] = np.inf
+    ws0[1][9, 3] = np.nan
+    s = HipStream()
+    x = s.add_constant(x0, meta((T, I)))
+    outs = []
+    for w0 in ws0:
+        w = s.add_constant(w0, meta((O, I)))
+        wt = s.add_op(OpKind.Transpose(None), [w], meta((I, O)))
+        outs.append(s.add_op(OpKind.MatMul, [x, wt], meta((T, O))))
+    s.eval_many(outs)
+    got = [s.get_buffer(o).reshape(T, O) for o in outs]
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref1 = (x0.astype(np.float64) @ ws0[1].T.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(np.isnan(got[1]), np.isnan(ref1))
+    assert np.array_equal(np.isposinf(got[1]), np.isposinf(ref1))
+    assert np.array_equal(np.isneginf(got[1]), np.isneginf(ref1))
+    fin = np.isfinite(ref1)
+    mag = np.abs(x0).astype(np.float64) @ np.abs(np.nan_to_num(ws0[1], nan=0, posinf=0, neginf=0)).T
+    assert np.all(np.abs(got[1][fin] - ref1[fin]) <= 1e-6 * np.sqrt(I) * mag[fin] + 1e-30)
+    for i in (0, 2):
+        gemm_full_check(got[i], x0, ws0[i].T, "f32", f"finite product {i} of the group")
