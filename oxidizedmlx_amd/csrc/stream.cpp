@@ -22,6 +22,7 @@
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -263,6 +264,50 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     Scratch scratch;
     scratch.planes = &planes;
     int rc = MLXHIP_OK;
+    // Reshape keeps the data as it is (row-major, contiguous): the node
+    // aliases its input's buffer, which lives as long as the stream. Narrow
+    // along an axis with only size-1 axes before it takes a contiguous range
+    // of its input: the node aliases that range (node buffers live until the
+    // stream is cleared, like Reshape's). Sets node id's buffer and returns
+    // true when id is such a node and its input has a buffer.
+    auto alias = [&](uint64_t id) -> bool {
+        const Node& n = nodes.at(id);
+        if (n.inputs.size() != 1) return false;
+        auto src = buffers.find(n.inputs[0]);
+        if (src == buffers.end()) return false;
+        if (n.op.op.kind == MLXHIP_OP_RESHAPE) {
+            if ((int64_t)src->second.len != n.meta.numel()) return false;
+            buffers[id] = DevBuf{src->second.ptr, src->second.len, false};
+            return true;
+        }
+        if (n.op.op.kind != MLXHIP_OP_NARROW) return false;
+        const std::vector<int64_t>& ish = nodes.at(n.inputs[0]).meta.shape;
+        int64_t ax = n.op.op.axis;
+        if (ax < 0) ax += (int64_t)ish.size();
+        if (ax < 0 || ax >= (int64_t)ish.size()) return false;
+        int64_t outer = 1, inner = 1;
+        for (int64_t d = 0; d < ax; ++d) outer *= ish[d];
+        for (int64_t d = ax + 1; d < (int64_t)ish.size(); ++d) inner *= ish[d];
+        const int64_t st = n.op.op.start, ln = n.op.op.length;
+        if (outer != 1 || st < 0 || ln < 0 || st + ln > ish[ax] || (int64_t)src->second.len != ish[ax] * inner ||
+            ln * inner != n.meta.numel())
+            return false;
+        buffers[id] = DevBuf{src->second.ptr + st * inner, (size_t)(ln * inner), false};
+        return true;
+    };
+    // Whether node id has a buffer, giving it one first if it is a chain of
+    // aliases (above) over a node that has one (the sibling search's
+    // operands: dQ/dK/dV are Narrow views of one gradient node).
+    std::function<bool(uint64_t, int)> ready_alias = [&](uint64_t id, int depth) -> bool {
+        if (buffers.count(id)) return true;
+        if (depth > 8 || !in_order.count(id)) return false;
+        const Node& n = nodes.at(id);
+        if ((n.op.op.kind != MLXHIP_OP_RESHAPE && n.op.op.kind != MLXHIP_OP_NARROW) || n.inputs.size() != 1)
+            return false;
+        if (!ready_alias(n.inputs[0], depth + 1) || !alias(id)) return false;
+        eval_calls += 1;
+        return true;
+    };
     // A MatMul operand's source node after folded Transposes, and how many
     // Transposes (mod 2) lie between: the GEMM reads the source with the
     // layout flipped that many times.
@@ -344,36 +389,9 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             }
             continue;
         }
-        // Reshape keeps the data as it is (row-major, contiguous): the node
-        // aliases its input's buffer, which lives as long as the stream.
-        if (n.op.op.kind == MLXHIP_OP_RESHAPE && n.inputs.size() == 1) {
-            auto src = buffers.find(n.inputs[0]);
-            if (src != buffers.end() && (int64_t)src->second.len == n.meta.numel()) {
-                buffers[id] = DevBuf{src->second.ptr, src->second.len, false};
-                eval_calls += 1;
-                continue;
-            }
-        }
-        // Narrow along an axis with only size-1 axes before it takes a
-        // contiguous range of its input: the node aliases that range (node
-        // buffers live until the stream is cleared, like Reshape's).
-        if (n.op.op.kind == MLXHIP_OP_NARROW && n.inputs.size() == 1) {
-            auto src = buffers.find(n.inputs[0]);
-            const std::vector<int64_t>& ish = nodes.at(n.inputs[0]).meta.shape;
-            int64_t ax = n.op.op.axis;
-            if (ax < 0) ax += (int64_t)ish.size();
-            if (src != buffers.end() && ax >= 0 && ax < (int64_t)ish.size()) {
-                int64_t outer = 1, inner = 1;
-                for (int64_t d = 0; d < ax; ++d) outer *= ish[d];
-                for (int64_t d = ax + 1; d < (int64_t)ish.size(); ++d) inner *= ish[d];
-                const int64_t st = n.op.op.start, ln = n.op.op.length;
-                if (outer == 1 && st >= 0 && ln >= 0 && st + ln <= ish[ax] &&
-                    (int64_t)src->second.len == ish[ax] * inner && ln * inner == n.meta.numel()) {
-                    buffers[id] = DevBuf{src->second.ptr + st * inner, (size_t)(ln * inner), false};
-                    eval_calls += 1;
-                    continue;
-                }
-            }
+        if (alias(id)) {
+            eval_calls += 1;
+            continue;
         }
         // Single node through HipBackend::eval_node. A MatMul operand that is
         // a folded Transpose (or a chain of them) is read from the source
@@ -430,7 +448,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
                 int ch[2] = {swapped ? 1 : 0, swapped ? 1 : 0};
                 const uint64_t cs[2] = {resolve(ce.inputs[swapped ? 1 : 0], &ch[0]),
                                         resolve(ce.inputs[swapped ? 0 : 1], &ch[1])};
-                if (ch[0] != hint[0] || ch[1] != hint[1] || !buffers.count(cs[0]) || !buffers.count(cs[1]) ||
+                if (ch[0] != hint[0] || ch[1] != hint[1] || !ready_alias(cs[0], 0) || !ready_alias(cs[1], 0) ||
                     nodes.at(cs[0]).meta.shape != nodes.at(msrc[0]).meta.shape ||
                     nodes.at(cs[1]).meta.shape != nodes.at(msrc[1]).meta.shape)
                     continue;
