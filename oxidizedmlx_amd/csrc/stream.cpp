@@ -318,6 +318,38 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         }
         return src;
     };
+    // Products waiting for their siblings (sibling grouping, below): their
+    // operands, ready when they were reached, and their share of eval_count.
+    struct Pending {
+        uint64_t id;
+        mlxhip_input_t in[2];
+        int hint[2];
+        bool swapped;
+        uint64_t covered;
+        size_t deadline;  // the first position that reads its result
+    };
+    std::vector<Pending> pending;
+    std::unordered_map<uint64_t, size_t> pos;
+    std::unordered_map<uint64_t, std::vector<uint64_t>> readers;
+    for (size_t i = 0; i < order.size(); ++i) {
+        pos[order[i]] = i;
+        for (uint64_t in : nodes.at(order[i]).inputs) readers[in].push_back(order[i]);
+    }
+    // The first position of this evaluation at which a node reads id's buffer:
+    // its readers, and through folded Transposes and Reshape / Narrow views
+    // (which alias it), theirs.
+    std::function<size_t(uint64_t, int)> first_read = [&](uint64_t id, int depth) -> size_t {
+        size_t best = SIZE_MAX;
+        auto it = readers.find(id);
+        if (it == readers.end()) return best;
+        for (uint64_t u : it->second) {
+            best = std::min(best, pos.at(u));
+            const int uk = nodes.at(u).op.op.kind;
+            if (depth < 16 && (folded_transpose.count(u) || uk == MLXHIP_OP_RESHAPE || uk == MLXHIP_OP_NARROW))
+                best = std::min(best, first_read(u, depth + 1));
+        }
+        return best;
+    };
     for (size_t oi = 0; oi < order.size(); ++oi) {
         const uint64_t id = order[oi];
         if (buffers.count(id) || folded_transpose.count(id) || interior.count(id) || virtual_bcast.count(id) ||
@@ -428,14 +460,33 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         // the loop skips them when it reaches them.
         // A swapped product (a Transpose computed as B^T A^T, every weight
         // gradient) groups with other swapped products, its operands taken
-        // in the swapped order.
+        // in the swapped order. A product whose siblings' operands are not
+        // ready yet waits for them (pending) when nothing reads its result
+        // before the last of them: the weight gradients of Q, K and V, whose
+        // dQ/dK/dV come out of separate kernels.
         std::vector<uint64_t> sib;
-        std::vector<mlxhip_input_t> gin;  // 2 per product, this one first
+        std::vector<mlxhip_input_t> gin;  // 2 per product after this one
+        std::vector<size_t> pend;         // pending products that join this launch
         if (fusion && en.op.op.kind == MLXHIP_OP_MATMUL && ins.size() == 2 && ins[0].ndim == 2 &&
             ins[1].ndim == 2 && n.meta.dtype == MLXHIP_DTYPE_F32) {
             const int64_t m = hint[0] ? ins[0].shape[1] : ins[0].shape[0], k = hint[0] ? ins[0].shape[0] : ins[0].shape[1];
             const int64_t nn = hint[1] ? ins[1].shape[0] : ins[1].shape[1];
-            for (size_t oj = oi + 1; oj < order.size() && sib.size() < 3 && gemm_f32_groupable(m, nn, k); ++oj) {
+            const bool groupable = gemm_f32_groupable(m, nn, k);
+            auto same_operands = [&](const mlxhip_input_t* o) {
+                for (int j = 0; j < 2; ++j)
+                    if (o[j].ndim != 2 || o[j].shape[0] != ins[j].shape[0] || o[j].shape[1] != ins[j].shape[1])
+                        return false;
+                return true;
+            };
+            for (size_t i = 0; groupable && i < pending.size() && pend.size() < 3; ++i) {
+                const Pending& pm = pending[i];
+                if (pm.swapped == swapped && pm.hint[0] == hint[0] && pm.hint[1] == hint[1] &&
+                    nodes.at(pm.id).meta.shape == n.meta.shape && same_operands(pm.in))
+                    pend.push_back(i);
+            }
+            bool waiting = false;  // a later sibling whose operands are not ready
+            size_t last = oi;      // the position of the last later sibling
+            for (size_t oj = oi + 1; groupable && oj < order.size(); ++oj) {
                 const uint64_t cid = order[oj];
                 if (buffers.count(cid) || folded_transpose.count(cid) || absorbed_matmul.count(cid) ||
                     (swapped_matmul.count(cid) != 0) != swapped)
@@ -448,38 +499,59 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
                 int ch[2] = {swapped ? 1 : 0, swapped ? 1 : 0};
                 const uint64_t cs[2] = {resolve(ce.inputs[swapped ? 1 : 0], &ch[0]),
                                         resolve(ce.inputs[swapped ? 0 : 1], &ch[1])};
-                if (ch[0] != hint[0] || ch[1] != hint[1] || !ready_alias(cs[0], 0) || !ready_alias(cs[1], 0) ||
-                    nodes.at(cs[0]).meta.shape != nodes.at(msrc[0]).meta.shape ||
+                if (ch[0] != hint[0] || ch[1] != hint[1] || nodes.at(cs[0]).meta.shape != nodes.at(msrc[0]).meta.shape ||
                     nodes.at(cs[1]).meta.shape != nodes.at(msrc[1]).meta.shape)
                     continue;
                 if (cs[0] == msrc[0] && cs[1] == msrc[1]) continue;  // the same product
-                sib.push_back(cid);
-                gin.push_back(input_of(cs[0], buffers.at(cs[0]).ptr));
-                gin.push_back(input_of(cs[1], buffers.at(cs[1]).ptr));
+                last = oj;
+                if (!ready_alias(cs[0], 0) || !ready_alias(cs[1], 0)) {
+                    waiting = true;
+                    continue;
+                }
+                if (pend.size() + sib.size() < 3) {
+                    sib.push_back(cid);
+                    gin.push_back(input_of(cs[0], buffers.at(cs[0]).ptr));
+                    gin.push_back(input_of(cs[1], buffers.at(cs[1]).ptr));
+                }
+            }
+            // Waiting holds back the pending products it would join too.
+            bool can_wait = waiting && pend.size() + sib.size() < 3;
+            for (size_t i : pend) can_wait = can_wait && pending[i].deadline > last;
+            const size_t deadline = can_wait ? first_read(id, 0) : 0;
+            if (can_wait && deadline > last) {
+                pending.push_back(Pending{id, {ins[0], ins[1]}, {hint[0], hint[1]}, swapped, covered, deadline});
+                continue;
             }
         }
-        if (!sib.empty()) {
-            std::vector<float*> outs(1 + sib.size(), nullptr);
-            if ((rc = alloc_out(id, &outs[0])) != MLXHIP_OK) break;
-            for (size_t i = 0; i < sib.size() && rc == MLXHIP_OK; ++i) rc = alloc_out(sib[i], &outs[1 + i]);
-            std::vector<mlxhip_input_t> all{ins[0], ins[1]};
+        if (!sib.empty() || !pend.empty()) {
+            // Products: the pending ones, this one, the later ready ones.
+            std::vector<uint64_t> ids;
+            std::vector<mlxhip_input_t> all;
+            for (size_t i : pend) {
+                ids.push_back(pending[i].id);
+                all.push_back(pending[i].in[0]);
+                all.push_back(pending[i].in[1]);
+                covered += pending[i].covered;
+            }
+            ids.push_back(id);
+            all.push_back(ins[0]);
+            all.push_back(ins[1]);
+            ids.insert(ids.end(), sib.begin(), sib.end());
             all.insert(all.end(), gin.begin(), gin.end());
+            for (size_t j = pend.size(); j-- > 0;) pending.erase(pending.begin() + (std::ptrdiff_t)pend[j]);
+            std::vector<float*> outs(ids.size(), nullptr);
+            for (size_t i = 0; i < ids.size() && rc == MLXHIP_OK; ++i) rc = alloc_out(ids[i], &outs[i]);
             std::vector<int> hints;
             for (size_t i = 0; i < outs.size(); ++i) hints.insert(hints.end(), {hint[0], hint[1]});
             if (rc == MLXHIP_OK)
                 rc = eval_matmul_group((int)outs.size(), all.data(), hints.data(), outs.data(), hs, scratch);
             if (rc != MLXHIP_OK) {
-                for (uint64_t g : sib) {
+                for (uint64_t g : ids) {
                     auto b = buffers.find(g);
                     if (b != buffers.end()) {
                         release_later(b->second.ptr);
                         buffers.erase(b);
                     }
-                }
-                auto b = buffers.find(id);
-                if (b != buffers.end()) {
-                    release_later(b->second.ptr);
-                    buffers.erase(b);
                 }
                 break;
             }
@@ -518,6 +590,23 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             release_later(out);
             buffers.erase(id);
             break;
+        }
+    }
+    // A product still pending (its siblings failed to come) runs alone.
+    for (size_t i = 0; rc == MLXHIP_OK && i < pending.size(); ++i) {
+        const Pending& pm = pending[i];
+        const Node& pn = nodes.at(pm.id);
+        const Node& pe = pm.swapped ? nodes.at(pn.inputs[0]) : pn;
+        float* out = nullptr;
+        if ((rc = alloc_out(pm.id, &out)) != MLXHIP_OK) break;
+        const mlxhip_op_t op = pe.op.c();
+        const mlxhip_meta_t meta = pn.meta.c();
+        rc = eval_node_device(op, pm.in, 2, meta, out, hs, scratch, pm.hint);
+        eval_calls += pm.covered;
+        launches += 1;
+        if (rc != MLXHIP_OK) {
+            release_later(out);
+            buffers.erase(pm.id);
         }
     }
     {

@@ -666,6 +666,38 @@ def test_swapped_sibling_products_run_as_one_grouped_launch():
         gemm_full_check(s.get_buffer(o).reshape(I, O), np.ascontiguousarray(x0.T), dy0, "f32", f"swapped product {i}")
 
 
+@pytest.mark.parametrize("early_read", [False, True])
+def test_products_wait_for_siblings_whose_operands_come_later(early_read):
+    # Four weight-gradient-shaped products (-dY_i^T X)^T whose dY_i come out
+    # of separate kernels between them (dQ/dK/dV of a backward pass): the
+    # first three wait for the last one's operand and the four run as one
+    # grouped launch. When a node reads the first product before the last
+    # sibling's operand exists, that product runs alone and the other three
+    # group. Every output against float64 with the f32 bound.
+    from parity import gemm_full_check
+    T, I, O = 2048, 1024, 1024
+    x0 = synth.normal(601, (T, I))
+    dys = [synth.normal(602 + i, (T, O)) for i in range(4)]
+    s = HipStream()
+    x = s.add_constant(x0, meta((T, I)))
+    outs = []
+    for dy0 in dys:
+        dy = s.add_op(OpKind.Neg, [s.add_constant(dy0, meta((T, O)))], meta((T, O)))
+        dyt = s.add_op(OpKind.Transpose(None), [dy], meta((O, T)))
+        prod = s.add_op(OpKind.MatMul, [dyt, x], meta((O, I)))                       # -dY^T X
+        outs.append(s.add_op(OpKind.Transpose((1, 0)), [prod], meta((I, O))))
+    targets = list(outs)
+    if early_read:
+        targets[0] = s.add_op(OpKind.Neg, [outs[0]], meta((I, O)))
+    before = s.launch_count()
+    s.eval_many(targets)
+    assert s.launch_count() - before == (4 + 1 + 1 + 1 if early_read else 4 + 1)
+    for i, (o, dy0) in enumerate(zip(outs, dys)):
+        gemm_full_check(s.get_buffer(o).reshape(I, O), np.ascontiguousarray(x0.T), -dy0, "f32", f"product {i}")
+    if early_read:
+        assert np.array_equal(s.get_buffer(targets[0]), -s.get_buffer(outs[0]))
+
+
 def test_grouped_products_with_non_finite_operand():
     # A grouped launch where one product's weight holds inf and NaN: that
     # product takes the exact f32 path (its flag), giving what an f32 product
