@@ -410,7 +410,9 @@ __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN],
     // sub-tile into padded LDS rows (PITCH = row bytes + 16: consecutive rows
     // fall in distinct bank groups for the 8/16-byte writes) and reads it
     // back row by row, so every global store instruction writes whole row
-    // segments instead of 16-byte pieces of 32 rows.
+    // segments instead of 16-byte pieces of 32 rows. The row segments are
+    // stored non-temporally: C is written once, so it streams out rather
+    // than leaving the L2s full of dirty lines at the end of the kernel.
     constexpr int TM = C::TM, TN = C::TN;
     constexpr int ES = CT == MLXHIP_DTYPE_F32 ? 4 : 2;
     constexpr int PASS_ROWS = pass_rows<C, ES>(PIPE_BYTES);
@@ -458,7 +460,7 @@ __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN],
             if (m >= g.m || n >= g.n) continue;
             char* dst = Cp + (m * g.ldc + n) * ES;
             if (vec_ok && n + 16 / ES <= g.n) {
-                *reinterpret_cast<u32x4*>(dst) = v;
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
             } else {
                 // Row end or unaligned C: element stores.
 #pragma unroll
