@@ -393,7 +393,7 @@ int ew2(int ew_op, const float* acc, const float* other, float* out, int64_t n, 
     } while (0)
 
 int eval_matmul(const mlxhip_input_t* in, size_t n_inputs, const mlxhip_meta_t& meta, float* out,
-                hipStream_t s, Scratch& scratch, const int* trans_hint) {
+                hipStream_t s, Scratch& scratch, const int* trans_hint, const float* bias = nullptr) {
     // Rank 2: matmul (cpu_kernels.rs:197-230). Rank 3: [B,M,K] @ [B,K,N] ->
     // [B,M,N], one product per batch slice, the batched form the reference
     // specifies for matmul (evals/tasks/003_matmul_batch_3d.json); ranks must
@@ -421,7 +421,7 @@ int eval_matmul(const mlxhip_input_t* in, size_t n_inputs, const mlxhip_meta_t& 
     // here too. The 16-bit MFMA path (operands held as bf16/f16) is the
     // explicit mlxhip_gemm with ab_dtype BF16/F16.
     return gemm(MLXHIP_DTYPE_F32, MLXHIP_DTYPE_F32, ta, tb, m, n, k, batch, a.data, lda, m * k, b.data, ldb,
-                k * n, out, n, m * n, s, scratch.planes);
+                k * n, out, n, m * n, s, scratch.planes, bias);
 }
 
 int eval_attention(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,
@@ -525,7 +525,7 @@ int eval_head_attention_vjp(const mlxhip_op_t& op, const mlxhip_input_t* in, siz
 }  // namespace
 
 int eval_matmul_group(int groups, const mlxhip_input_t* in, const int* hints, float* const* outs, hipStream_t s,
-                      Scratch& scratch) {
+                      Scratch& scratch, const float* const* biases) {
     if (groups < 2 || groups > 4) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul group of %d", groups);
     const mlxhip_input_t &a = in[0], &b = in[1];
     if (a.ndim != 2 || b.ndim != 2) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul group: rank-2 operands only");
@@ -546,7 +546,15 @@ int eval_matmul_group(int groups, const mlxhip_input_t* in, const int* hints, fl
         pa[i] = ai.data;
         pb[i] = bi.data;
     }
-    return gemm_f32_grouped(ta, tb, m, n, k, groups, pa, ta ? m : k, pb, tb ? k : n, outs, n, s, scratch.planes);
+    return gemm_f32_grouped(ta, tb, m, n, k, groups, pa, ta ? m : k, pb, tb ? k : n, outs, n, s, scratch.planes,
+                            biases);
+}
+
+int eval_matmul_bias(const mlxhip_input_t* in, const mlxhip_meta_t& meta, float* out, hipStream_t s,
+                     Scratch& scratch, const int* trans_hint, const float* bias) {
+    if (in[0].ndim != 2 || in[1].ndim != 2)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "matmul with a bias term: rank-2 operands only");
+    return eval_matmul(in, 2, meta, out, s, scratch, trans_hint, bias);
 }
 
 int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* in, size_t n_inputs,

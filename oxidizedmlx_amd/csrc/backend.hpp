@@ -65,7 +65,15 @@ int eval_node_device(const mlxhip_op_t& op, const mlxhip_input_t* inputs, size_t
 // inputs[2i], inputs[2i + 1] with the folded-Transpose hints hints[2i],
 // hints[2i + 1] (the same for every group), its result goes to outs[i].
 int eval_matmul_group(int groups, const mlxhip_input_t* inputs, const int* hints, float* const* outs,
-                      hipStream_t s, Scratch& scratch);
+                      hipStream_t s, Scratch& scratch, const float* const* biases = nullptr);
+
+// A rank-2 f32 MatMul followed by the Add of a bias row broadcast over its
+// rows (out = A B + bias, bias[j] added to column j; the Stream's linear
+// layers): the bias is added as C is stored, the same f32 addition a
+// separate Add performs. eval_matmul_group's `biases` (one per group, or
+// nullptr) do the same for grouped products.
+int eval_matmul_bias(const mlxhip_input_t* inputs, const mlxhip_meta_t& out_meta, float* out, hipStream_t s,
+                     Scratch& scratch, const int* trans_hint, const float* bias);
 
 // Per-thread HIP stream used by the synchronous host-vector entry points.
 hipStream_t thread_stream();

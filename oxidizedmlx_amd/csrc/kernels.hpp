@@ -164,7 +164,8 @@ struct PlaneCache {
 };
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
-         int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, PlaneCache* planes = nullptr);
+         int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, PlaneCache* planes = nullptr,
+         const float* bias = nullptr);
 // Up to 4 f32 products of one shape and layout (C_i = op(A_i) op(B_i),
 // rank 2), in one split-f32 launch when gemm_f32_groupable(m, n, k) (the
 // products siblings of one graph, such as the Q/K/V projections of one
@@ -173,7 +174,7 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
 bool gemm_f32_groupable(int64_t m, int64_t n, int64_t k);
 int gemm_f32_grouped(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, int groups, const float* const* a,
                      int64_t lda, const float* const* b, int64_t ldb, float* const* c, int64_t ldc, hipStream_t s,
-                     PlaneCache* planes = nullptr);
+                     PlaneCache* planes = nullptr, const float* const* bias = nullptr);
 // gemm_small.hip: f32 products small enough for one or two rounds of 32 x 32
 // tiles with K <= 512, one launch, no workspace, any alignment.
 bool gemm_small_f32_fits(int64_t m, int64_t n, int64_t k, int64_t batch);

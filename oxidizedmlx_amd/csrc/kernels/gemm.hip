@@ -48,7 +48,7 @@ constexpr int SPLIT_MAX = 8;  // every split plan uses at most 8 splits
 template <int CT, bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, void* c, int64_t m,
                                                             int64_t n, int64_t ldw, int64_t ldc, int64_t sc,
-                                                            int splits) {
+                                                            int splits, const float* __restrict__ bias) {
     const int64_t b = blockIdx.y;
     const int64_t groups = (n + 3) / 4;
     const int gx = threadIdx.x % RED_COLS, gy = threadIdx.x / RED_COLS;
@@ -59,6 +59,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     const int64_t rblocks = gridDim.x / col_blocks;
     const int64_t g = (blockIdx.x % col_blocks) * RED_COLS + gx;
     if (g >= groups) return;
+    // A bias term (f32 C only): the thread's four columns, loaded once.
+    float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (bias)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = bias[std::min<int64_t>(4 * g + e, n - 1)];
     for (int64_t row = (int64_t)(blockIdx.x / col_blocks) * RED_ROWS + gy; row < m; row += rblocks * RED_ROWS) {
         const float* pr = ws + b * splits * slice + row * ldw;
         {
@@ -85,6 +90,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[e] += v[s][e];
             }
+            // The bias term: one f32 addition to the sum.
+            if (bias)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] += bv[e];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (col + e < n) gemm_detail::store_c<CT>(c, b * sc + row * ldc + col + e, acc[e]);
@@ -93,7 +102,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 }
 
 int splitk_reduce(int c_dtype, const float* ws, void* c, int64_t m, int64_t n, int64_t ldw, int64_t ldc,
-                  int64_t sc, int splits, int64_t batch, hipStream_t s) {
+                  int64_t sc, int splits, int64_t batch, hipStream_t s, const float* bias = nullptr) {
+    if (bias && c_dtype != MLXHIP_DTYPE_F32) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "splitk_reduce: bias needs f32 C");
     // VEC: every float4 read stays inside a row of the partials (ldw a
     // multiple of 4; reads past n up to ldw stay in the row padding).
     const bool vec = ldw % 4 == 0 && reinterpret_cast<uintptr_t>(ws) % 16 == 0 && ceil_div(n, 4) * 4 <= ldw;
@@ -106,9 +116,9 @@ int splitk_reduce(int c_dtype, const float* ws, void* c, int64_t m, int64_t n, i
 #define MLXHIP_RED(CT)                                                                                       \
     do {                                                                                                    \
         if (vec) hipLaunchKernelGGL((splitk_reduce_kernel<CT, true>), grid, dim3(256), 0, s, ws, c, m, n, ldw, \
-                                    ldc, sc, splits);                                                        \
+                                    ldc, sc, splits, bias);                                                  \
         else hipLaunchKernelGGL((splitk_reduce_kernel<CT, false>), grid, dim3(256), 0, s, ws, c, m, n, ldw,    \
-                                ldc, sc, splits);                                                            \
+                                ldc, sc, splits, bias);                                                      \
     } while (0)
     switch (c_dtype) {
         case MLXHIP_DTYPE_F32: MLXHIP_RED(MLXHIP_DTYPE_F32); break;
@@ -117,6 +127,24 @@ int splitk_reduce(int c_dtype, const float* ws, void* c, int64_t m, int64_t n, i
     }
 #undef MLXHIP_RED
     return launch_check("splitk_reduce_kernel");
+}
+
+// C[i][j] += bias[j] over an f32 [m, n] C with row pitch ldc: the bias term
+// of a product whose kernel has no bias in its store.
+__global__ __launch_bounds__(256) void add_bias_kernel(float* __restrict__ c, int64_t m, int64_t n, int64_t ldc,
+                                                       const float* __restrict__ bias) {
+    const int64_t total = m * n;
+    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / n, j = i - r * n;
+        c[r * ldc + j] += bias[j];
+    }
+}
+
+int add_bias(float* c, int64_t m, int64_t n, int64_t ldc, const float* bias, hipStream_t s) {
+    if (m == 0 || n == 0) return MLXHIP_OK;
+    const int64_t blocks = std::min<int64_t>(ceil_div(m * n, 256), 4096);
+    hipLaunchKernelGGL(add_bias_kernel, dim3((unsigned)blocks), dim3(256), 0, s, c, m, n, ldc, bias);
+    return launch_check("add_bias_kernel");
 }
 
 // One operand to copy into a zero-padded rows_p x cols_p buffer per batch
@@ -313,8 +341,10 @@ std::atomic<uint32_t> g_x6_gen{0};
 // tiles, and the padded M / N rows only feed C elements that are not stored.
 int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int groups, const float* const* a,
             int64_t lda, int64_t stride_a, const float* const* b, int64_t ldb, int64_t stride_b, float* const* c,
-            int64_t ldc, int64_t stride_c, hipStream_t s, PlaneCache* cache, FixedScratch* fs, bool* ran) {
+            int64_t ldc, int64_t stride_c, hipStream_t s, PlaneCache* cache, FixedScratch* fs, bool* ran,
+            const float* const* bias = nullptr) {
     *ran = false;
+    if (bias && batch != 1) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: a bias term needs batch 1");
     if (groups < 1 || groups > gemm16::Args::MAX_GROUPS || (groups > 1 && batch != 1))
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: %d grouped products", groups);
     const int64_t kp = ceil_div(k, 32) * 32;  // segment length: whole K tiles
@@ -444,7 +474,8 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int 
         h.groups = groups;
         for (int i = 0; i < groups; ++i) {
             const X6SplitOp &ga = op[2 * i], &gb = op[2 * i + 1];
-            h.grp[i] = gemm16::Args::Group{ga.dst, gb.dst, c[i], a[i], b[i], ga.flag, gb.flag, ga.gen, gb.gen};
+            h.grp[i] = gemm16::Args::Group{ga.dst, gb.dst, c[i], a[i], b[i], ga.flag, gb.flag, ga.gen, gb.gen,
+                                           bias ? bias[i] : nullptr};
         }
     }
     const int64_t slots = groups > 1 ? groups : batch;  // gridDim.y before splits
@@ -491,7 +522,12 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int 
     }
     if (sp.n) MLXHIP_TRY(x6_split(sp, s));
     if (sp_k == 1) {
+        // The interleaved kernel adds the bias as it stores C; the other one
+        // (a forced setting) leaves it to one more launch per product.
+        if (bias && cfg >= 3) h.bias = bias[0];
         MLXHIP_TRY(gemm16_x6(ta, tb, h, slots, cfg, s));
+        if (bias && cfg < 3)
+            for (int i = 0; i < groups; ++i) MLXHIP_TRY(add_bias(c[i], m, n, ldc, bias[i], s));
         *ran = true;
         return MLXHIP_OK;
     }
@@ -508,7 +544,7 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int 
     h.sc = m * ldw;
     MLXHIP_TRY(gemm16_x6(ta, tb, h, batch, cfg, s));
     MLXHIP_TRY(splitk_reduce(MLXHIP_DTYPE_F32, static_cast<const float*>(part), c[0], m, n, ldw, ldc, stride_c,
-                             h.splits, batch, s));
+                             h.splits, batch, s, bias ? bias[0] : nullptr));
     *ran = true;
     return MLXHIP_OK;
 }
@@ -533,7 +569,7 @@ bool gemm_f32_groupable(int64_t m, int64_t n, int64_t k) {
 
 int gemm_f32_grouped(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, int groups, const float* const* a,
                      int64_t lda, const float* const* b, int64_t ldb, float* const* c, int64_t ldc, hipStream_t s,
-                     PlaneCache* planes) {
+                     PlaneCache* planes, const float* const* bias) {
     if (groups < 1 || groups > gemm16::Args::MAX_GROUPS)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: %d grouped products", groups);
     if (m < 0 || n < 0 || k < 0) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: negative size");
@@ -550,20 +586,39 @@ int gemm_f32_grouped(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, 
     if (groups > 1 && fills && m > 0 && n > 0 && k > 0 && gemm_f32_groupable(m, n, k)) {
         bool ran = false;
         MLXHIP_TRY(gemm_x6(trans_a, trans_b, m, n, k, 1, groups, a, lda, 0, b, ldb, 0, c, ldc, 0, s, planes, nullptr,
-                           &ran));
+                           &ran, bias));
         if (ran) return MLXHIP_OK;
     }
     for (int i = 0; i < groups; ++i)
-        MLXHIP_TRY(gemm_impl(MLXHIP_DTYPE_F32, MLXHIP_DTYPE_F32, trans_a, trans_b, m, n, k, 1, a[i], lda, 0, b[i], ldb,
-                             0, c[i], ldc, 0, s, false, nullptr, planes));
+        MLXHIP_TRY(gemm(MLXHIP_DTYPE_F32, MLXHIP_DTYPE_F32, trans_a, trans_b, m, n, k, 1, a[i], lda, 0, b[i], ldb, 0,
+                        c[i], ldc, 0, s, planes, bias ? bias[i] : nullptr));
     return MLXHIP_OK;
 }
 
 int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
          int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
-         int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, PlaneCache* planes) {
-    return gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
-                     ldc, stride_c, s, false, nullptr, planes);
+         int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s, PlaneCache* planes,
+         const float* bias) {
+    if (!bias)
+        return gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
+                         ldc, stride_c, s, false, nullptr, planes);
+    // C = op(A) op(B) + bias (row broadcast): the split-f32 kernel adds it as
+    // it stores C (or its split-K sum does); any other path, one more launch.
+    if (ab_dtype != MLXHIP_DTYPE_F32 || c_dtype != MLXHIP_DTYPE_F32 || batch != 1)
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm: a bias term needs f32 operands and C, batch 1");
+    if (m > 0 && n > 0 && k > 0 && a && b && c && ldc >= n && lda >= (trans_a ? m : k) &&
+        ldb >= (trans_b ? k : n) && use_x6(gemm_path(), m, n, k, 1)) {
+        bool ran = false;
+        const float* fa = static_cast<const float*>(a);
+        const float* fb = static_cast<const float*>(b);
+        float* fc = static_cast<float*>(c);
+        MLXHIP_TRY(gemm_x6(trans_a, trans_b, m, n, k, 1, 1, &fa, lda, stride_a, &fb, ldb, stride_b, &fc, ldc, stride_c,
+                           s, planes, nullptr, &ran, &bias));
+        if (ran) return MLXHIP_OK;
+    }
+    MLXHIP_TRY(gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
+                         ldc, stride_c, s, false, nullptr, planes));
+    return add_bias(static_cast<float*>(c), m, n, ldc, bias, s);
 }
 
 int gemm_noalloc(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,

@@ -125,6 +125,10 @@ struct Args {
     const uint32_t* flag_a = nullptr;
     const uint32_t* flag_b = nullptr;
     uint32_t gen_a = 0, gen_b = 0;
+    // Split-f32 mode, interleaved kernel, one split: bias[n] is added to
+    // every element of C's column n as it is stored (the row-broadcast bias
+    // of a linear layer; nullptr: none).
+    const float* bias = nullptr;
     // Grouped products (interleaved split-f32 kernel only, one split): with
     // groups > 0, batch index b runs product grp[b] of the same shapes and
     // layouts, its planes, C and f32 operands at the pointers given here
@@ -138,6 +142,7 @@ struct Args {
         const uint32_t* flag_a;
         const uint32_t* flag_b;
         uint32_t gen_a, gen_b;
+        const float* bias;
     };
     static constexpr int MAX_GROUPS = 4;
     int groups = 0;
@@ -403,7 +408,7 @@ __device__ inline TileId tile_of(const Args& g) {
 // MFMA), through the first bytes of the operand stages' LDS.
 template <int CT, class C, int PIPE_BYTES>
 __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN], MLXHIP_LDS char* smem, char* Cp,
-                               int64_t m0, int64_t n0, int wave, int lane) {
+                               int64_t m0, int64_t n0, int wave, int lane, const float* bias = nullptr) {
     // Through LDS. acc[i][j][v] = C[m][n] with m = WR wm + 32 i +
     // lane % 32 and n = WC wn + 32 j + 8 (v / 4) + 4 (lane / 32) + v % 4
     // inside the tile (WR x WC: the wave's sub-tile). Each wave converts its
@@ -427,6 +432,17 @@ __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN],
     MLXHIP_LDS char* region = smem + wave * PASS_ROWS * PITCH;
     const int64_t row0 = m0 + 32 * TM * wm, col0 = n0 + 32 * TN * wn;
     const bool vec_ok = (g.ldc * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(Cp) % 16) == 0;
+    // A lane stores the same 16-byte column range of every row it stores:
+    // its four bias values are loaded once, before the first store.
+    float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (ES == 4) {
+        if (bias) {
+            const int64_t nb = col0 + ((lane % LANES_PER_ROW) * 16) / ES;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (nb + e < g.n) bv[e] = bias[nb + e];
+        }
+    }
 #pragma unroll
     for (int pass = 0; pass < 32 * TM / PASS_ROWS; ++pass) {
 #pragma unroll
@@ -454,10 +470,18 @@ __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN],
         for (int rr = 0; rr < PASS_ROWS; rr += ROWS_PER_READ) {
             const int r = rr + lane / LANES_PER_ROW;
             const int cb = (lane % LANES_PER_ROW) * 16;  // byte offset inside the row
-            const u32x4 v = *(const MLXHIP_LDS u32x4*)(region + r * PITCH + cb);
+            u32x4 v = *(const MLXHIP_LDS u32x4*)(region + r * PITCH + cb);
             const int64_t m = row0 + pass * PASS_ROWS + r;
             const int64_t n = col0 + cb / ES;
             if (m >= g.m || n >= g.n) continue;
+            if constexpr (ES == 4) {
+                // The bias term: the f32 value of C, then one f32 addition,
+                // as a separate elementwise Add would give.
+                if (bias) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = __float_as_uint(__uint_as_float(v[e]) + bv[e]);
+                }
+            }
             char* dst = Cp + (m * g.ldc + n) * ES;
             if (vec_ok && n + 16 / ES <= g.n) {
                 __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
@@ -488,7 +512,7 @@ constexpr int epi_bytes() {
 // split-K launch holds the product, the other splits zeros.
 template <int TA, int TB, class C>
 __device__ void x6_direct(const Args& g, const float* A, const float* B, float* Cp, int64_t split, int64_t m0,
-                          int64_t n0, int tid) {
+                          int64_t n0, int tid, const float* bias = nullptr) {
     for (int e = tid; e < C::BM * C::BN; e += C::THREADS) {
         const int64_t m = m0 + e / C::BN, n = n0 + e % C::BN;
         if (m >= g.m || n >= g.n) continue;
@@ -497,7 +521,7 @@ __device__ void x6_direct(const Args& g, const float* A, const float* B, float* 
             for (int64_t k = 0; k < g.fk; ++k)
                 acc = fmaf(TA ? A[k * g.flda + m] : A[m * g.flda + k], TB ? B[n * g.fldb + k] : B[k * g.fldb + n],
                            acc);
-        Cp[m * g.ldc + n] = acc;
+        Cp[m * g.ldc + n] = bias ? acc + bias[n] : acc;
     }
 }
 

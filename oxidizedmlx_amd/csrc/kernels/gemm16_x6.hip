@@ -180,6 +180,7 @@ void gemm_x6i_kernel(Args g) {
     const float *fa32, *fb32;
     const uint32_t *flag_a, *flag_b;
     uint32_t gen_a, gen_b;
+    const float* bias;
     if (g.groups) {
         const Args::Group gr = group_of(g, (int)batch);
         pa = static_cast<const char*>(gr.a);
@@ -191,6 +192,7 @@ void gemm_x6i_kernel(Args g) {
         flag_b = gr.flag_b;
         gen_a = gr.gen_a;
         gen_b = gr.gen_b;
+        bias = gr.bias;
     } else {
         pa = static_cast<const char*>(g.a) + batch * g.sa * 2;
         pb = static_cast<const char*>(g.b) + batch * g.sb * 2;
@@ -201,10 +203,11 @@ void gemm_x6i_kernel(Args g) {
         flag_b = g.flag_b;
         gen_a = g.gen_a;
         gen_b = g.gen_b;
+        bias = g.bias;
     }
 
     if (__atomic_load_n(flag_a, __ATOMIC_RELAXED) == gen_a || __atomic_load_n(flag_b, __ATOMIC_RELAXED) == gen_b) {
-        x6_direct<TA, TB, C>(g, fa32, fb32, reinterpret_cast<float*>(pc), split, m0, n0, tid);
+        x6_direct<TA, TB, C>(g, fa32, fb32, reinterpret_cast<float*>(pc), split, m0, n0, tid, bias);
         return;
     }
 
@@ -313,7 +316,7 @@ void gemm_x6i_kernel(Args g) {
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    store_c<MLXHIP_DTYPE_F32, C, PIPE_BYTES>(g, acc, smem, pc, m0, n0, wave, lane);
+    store_c<MLXHIP_DTYPE_F32, C, PIPE_BYTES>(g, acc, smem, pc, m0, n0, wave, lane, bias);
 }
 
 template <int TA, int TB, class C>

@@ -125,7 +125,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         if (!buffers.count(o)) todo.push_back(o);
     }
     if (todo.empty()) return MLXHIP_OK;
-    const std::vector<uint64_t> order = topo_sort(todo);
+    const std::vector<uint64_t> order = topo_sort(todo, true);
     std::unordered_set<uint64_t> in_order(order.begin(), order.end());
     // Requested outputs are always materialised: never a chain interior or a
     // folded Transpose.
@@ -144,6 +144,16 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     // evaluated needs nothing more; one evaluated later finds no buffer and
     // plans the broadcast again.)
     std::unordered_map<uint64_t, int64_t> virtual_bcast;            // node -> period (elements)
+    // A rank-2 f32 MatMul whose one consumer is the Add of a bias row
+    // broadcast over its rows (a linear layer): the product adds the bias as
+    // it stores C, into the Add's buffer; neither the MatMul nor the Add is
+    // evaluated on its own.
+    struct BiasTerm {
+        uint64_t add;   // the Add node, whose buffer the product writes
+        uint64_t bcast; // the (virtual) Broadcast of the bias
+        uint64_t src;   // the bias, [N] values
+    };
+    std::unordered_map<uint64_t, BiasTerm> bias_of;  // MatMul -> its bias Add
     if (fusion) {
         std::unordered_map<uint64_t, std::vector<uint64_t>> users;
         for (uint64_t id : order)
@@ -259,6 +269,33 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         }
     }
 
+    // A chain that is a single Add of a MatMul and a virtual row broadcast
+    // whose source already has its buffer becomes the MatMul's bias term.
+    for (auto it = chain_of.begin(); fusion && it != chain_of.end();) {
+        const uint64_t aid = it->first;
+        const Node& an = nodes.at(aid);
+        bool taken = false;
+        if (it->second.size() == 1 && an.op.op.kind == MLXHIP_OP_ADD && an.inputs.size() == 2 &&
+            an.inputs[0] != an.inputs[1] && an.meta.dtype == MLXHIP_DTYPE_F32 && an.meta.shape.size() == 2) {
+            for (int c = 0; c < 2 && !taken; ++c) {
+                const uint64_t mid = an.inputs[c], vid = an.inputs[1 - c];
+                const Node& mn = nodes.at(mid);
+                auto v = virtual_bcast.find(vid);
+                if (mn.op.op.kind != MLXHIP_OP_MATMUL || mn.inputs.size() != 2 || mn.meta.dtype != MLXHIP_DTYPE_F32 ||
+                    mn.meta.shape != an.meta.shape || !in_order.count(mid) || buffers.count(mid) ||
+                    requested.count(mid) || consumers[mid] != 1 || absorbed_matmul.count(mid) || bias_of.count(mid) ||
+                    v == virtual_bcast.end() || v->second != an.meta.shape[1])
+                    continue;
+                const uint64_t src = nodes.at(vid).inputs[0];
+                if (!buffers.count(src) || nodes.at(src).meta.numel() != an.meta.shape[1]) continue;
+                bias_of[mid] = BiasTerm{aid, vid, src};
+                taken = true;
+            }
+        }
+        if (taken) it = chain_of.erase(it);
+        else ++it;
+    }
+
     // ── evaluation ────────────────────────────────────────────────────────
     std::unordered_set<uint64_t> counted_virtual, counted_folded;  // eval_count covers each once
     Scratch scratch;
@@ -318,6 +355,17 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         }
         return src;
     };
+    // The node whose buffer a MatMul's result goes to: its bias Add, if any.
+    auto out_of = [&](uint64_t id) {
+        auto b = bias_of.find(id);
+        return b == bias_of.end() ? id : b->second.add;
+    };
+    // A bias term's share of eval_count: the Add, and its broadcast once.
+    auto bias_covered = [&](uint64_t id) -> uint64_t {
+        auto b = bias_of.find(id);
+        if (b == bias_of.end()) return 0;
+        return 1 + (counted_virtual.insert(b->second.bcast).second ? 1 : 0);
+    };
     // Products waiting for their siblings (sibling grouping, below): their
     // operands, ready when they were reached, and their share of eval_count.
     struct Pending {
@@ -353,7 +401,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     for (size_t oi = 0; oi < order.size(); ++oi) {
         const uint64_t id = order[oi];
         if (buffers.count(id) || folded_transpose.count(id) || interior.count(id) || virtual_bcast.count(id) ||
-            absorbed_matmul.count(id))
+            absorbed_matmul.count(id) || buffers.count(out_of(id)))  // a product already run with its bias term
             continue;
         const Node& n = nodes.at(id);
         auto ch = chain_of.find(id);
@@ -481,7 +529,8 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             for (size_t i = 0; groupable && i < pending.size() && pend.size() < 3; ++i) {
                 const Pending& pm = pending[i];
                 if (pm.swapped == swapped && pm.hint[0] == hint[0] && pm.hint[1] == hint[1] &&
-                    nodes.at(pm.id).meta.shape == n.meta.shape && same_operands(pm.in))
+                    nodes.at(pm.id).meta.shape == n.meta.shape && same_operands(pm.in) &&
+                    bias_of.count(pm.id) == bias_of.count(id))
                     pend.push_back(i);
             }
             bool waiting = false;  // a later sibling whose operands are not ready
@@ -489,7 +538,8 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             for (size_t oj = oi + 1; groupable && oj < order.size(); ++oj) {
                 const uint64_t cid = order[oj];
                 if (buffers.count(cid) || folded_transpose.count(cid) || absorbed_matmul.count(cid) ||
-                    (swapped_matmul.count(cid) != 0) != swapped)
+                    (swapped_matmul.count(cid) != 0) != swapped || bias_of.count(cid) != bias_of.count(id) ||
+                    buffers.count(out_of(cid)))
                     continue;
                 const Node& cn = nodes.at(cid);
                 const Node& ce = swapped ? nodes.at(cn.inputs[0]) : cn;  // the node whose op runs
@@ -540,14 +590,21 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             all.insert(all.end(), gin.begin(), gin.end());
             for (size_t j = pend.size(); j-- > 0;) pending.erase(pending.begin() + (std::ptrdiff_t)pend[j]);
             std::vector<float*> outs(ids.size(), nullptr);
-            for (size_t i = 0; i < ids.size() && rc == MLXHIP_OK; ++i) rc = alloc_out(ids[i], &outs[i]);
+            for (size_t i = 0; i < ids.size() && rc == MLXHIP_OK; ++i) rc = alloc_out(out_of(ids[i]), &outs[i]);
             std::vector<int> hints;
             for (size_t i = 0; i < outs.size(); ++i) hints.insert(hints.end(), {hint[0], hint[1]});
+            std::vector<const float*> biases;
+            if (bias_of.count(id))
+                for (uint64_t g : ids) {
+                    biases.push_back(buffers.at(bias_of.at(g).src).ptr);
+                    covered += bias_covered(g);
+                }
             if (rc == MLXHIP_OK)
-                rc = eval_matmul_group((int)outs.size(), all.data(), hints.data(), outs.data(), hs, scratch);
+                rc = eval_matmul_group((int)outs.size(), all.data(), hints.data(), outs.data(), hs, scratch,
+                                       biases.empty() ? nullptr : biases.data());
             if (rc != MLXHIP_OK) {
                 for (uint64_t g : ids) {
-                    auto b = buffers.find(g);
+                    auto b = buffers.find(out_of(g));
                     if (b != buffers.end()) {
                         release_later(b->second.ptr);
                         buffers.erase(b);
@@ -565,6 +622,21 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             }
             eval_calls += covered;
             launches += 1;
+            continue;
+        }
+        if (bias_of.count(id)) {
+            // The product and its bias term, into the Add's buffer.
+            const BiasTerm& bt = bias_of.at(id);
+            float* out = nullptr;
+            if ((rc = alloc_out(bt.add, &out)) != MLXHIP_OK) break;
+            eval_calls += covered + bias_covered(id);
+            launches += 1;
+            rc = eval_matmul_bias(ins.data(), n.meta.c(), out, hs, scratch, hint, buffers.at(bt.src).ptr);
+            if (rc != MLXHIP_OK) {
+                release_later(out);
+                buffers.erase(bt.add);
+                break;
+            }
             continue;
         }
         float* out = nullptr;
@@ -598,15 +670,18 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         const Node& pn = nodes.at(pm.id);
         const Node& pe = pm.swapped ? nodes.at(pn.inputs[0]) : pn;
         float* out = nullptr;
-        if ((rc = alloc_out(pm.id, &out)) != MLXHIP_OK) break;
+        if ((rc = alloc_out(out_of(pm.id), &out)) != MLXHIP_OK) break;
         const mlxhip_op_t op = pe.op.c();
         const mlxhip_meta_t meta = pn.meta.c();
-        rc = eval_node_device(op, pm.in, 2, meta, out, hs, scratch, pm.hint);
-        eval_calls += pm.covered;
+        if (bias_of.count(pm.id))
+            rc = eval_matmul_bias(pm.in, meta, out, hs, scratch, pm.hint, buffers.at(bias_of.at(pm.id).src).ptr);
+        else
+            rc = eval_node_device(op, pm.in, 2, meta, out, hs, scratch, pm.hint);
+        eval_calls += pm.covered + bias_covered(pm.id);
         launches += 1;
         if (rc != MLXHIP_OK) {
             release_later(out);
-            buffers.erase(pm.id);
+            buffers.erase(out_of(pm.id));
         }
     }
     {

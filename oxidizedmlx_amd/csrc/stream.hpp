@@ -260,7 +260,10 @@ struct mlxhip_stream_t {
     // Depth-first post-order of the subgraph rooted at `outs` (graph.rs:268-294:
     // one shared visited set, outputs in order, inputs in order), iterative so
     // deep graphs cannot overflow the native stack.
-    std::vector<uint64_t> topo_sort(const std::vector<uint64_t>& outs) {
+    // stop_at_buffers: a node that holds its buffer needs none of its inputs,
+    // so the walk does not go past it (evaluation); else the whole graph
+    // behind `outs` (autograd).
+    std::vector<uint64_t> topo_sort(const std::vector<uint64_t>& outs, bool stop_at_buffers = false) {
         std::vector<uint64_t> order;
         std::unordered_set<uint64_t> visited;
         std::vector<std::pair<uint64_t, size_t>> st;
@@ -270,7 +273,12 @@ struct mlxhip_stream_t {
             while (!st.empty()) {
                 auto& top = st.back();
                 auto it = nodes.find(top.first);
-                if (it != nodes.end() && top.second < it->second.inputs.size()) {
+                // Past a node with a buffer, an evaluation would meet nodes
+                // that were never materialised (a MatMul whose result went
+                // into its bias Add's buffer, a fused chain's interior) and
+                // evaluate them again.
+                if (it != nodes.end() && !(stop_at_buffers && buffers.count(top.first)) &&
+                    top.second < it->second.inputs.size()) {
                     const uint64_t nxt = it->second.inputs[top.second++];
                     if (visited.insert(nxt).second) st.emplace_back(nxt, 0);
                 } else {

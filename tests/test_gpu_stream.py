@@ -698,6 +698,60 @@ def test_products_wait_for_siblings_whose_operands_come_later(early_read):
         assert np.array_equal(s.get_buffer(targets[0]), -s.get_buffer(outs[0]))
 
 
+def _linear(s, x, t, i, o, w0, b0):
+    """x W^T + b with b broadcast over the rows (crates/mlx-nn/src/linear.rs:34-43)."""
+    w = s.add_constant(w0, meta((o, i)))
+    wt = s.add_op(OpKind.Transpose(None), [w], meta((i, o)))
+    y = s.add_op(OpKind.MatMul, [x, wt], meta((t, o)))
+    bb = s.add_op(OpKind.Broadcast((t, o)), [s.add_constant(b0, meta((o,)))], meta((t, o)))
+    return s.add_op(OpKind.Add, [y, bb], meta((t, o)))
+
+
+@pytest.mark.parametrize("t,i,o", [(2048, 1024, 1024), (2048, 1024, 4096), (67, 45, 93)])
+def test_linear_bias_added_in_the_product_store(t, i, o):
+    # A linear layer's MatMul + Add of the broadcast bias runs as one product
+    # whose store adds the bias (the split-f32 kernel, or its split-K sum),
+    # or, below the split-f32 sizes, the product and one bias launch. The
+    # same f32 addition as the unfused graph's Add: identical results, the
+    # same eval_count.
+    x0 = synth.normal(611, (t, i))
+    w0 = synth.normal(612, (o, i))
+    b0 = synth.normal(613, (o,))
+    res = {}
+    for fusion in (True, False):
+        s = HipStream(fusion=fusion)
+        y = _linear(s, s.add_constant(x0, meta((t, i))), t, i, o, w0, b0)
+        before, calls = s.launch_count(), s.eval_count()
+        s.eval_many([y])
+        res[fusion] = (s.get_buffer(y).reshape(t, o), s.launch_count() - before, s.eval_count() - calls)
+    assert res[True][1] == 1
+    assert res[True][2] == res[False][2]
+    assert np.array_equal(res[True][0], res[False][0])
+    # x W^T + b as one product over K + 1: [x | 1] [W^T ; b].
+    from parity import gemm_full_check
+    gemm_full_check(res[True][0], np.hstack([x0, np.ones((t, 1), np.float32)]), np.vstack([w0.T, b0[None, :]]),
+                    "f32", "linear with bias")
+
+
+def test_grouped_linears_add_their_biases():
+    # The Q/K/V projections of one input with their biases: one grouped
+    # launch whose store adds each product's own bias; each against float64.
+    from parity import gemm_full_check
+    t, i, o = 2048, 1024, 1024
+    x0 = synth.normal(621, (t, i))
+    ws0 = [synth.normal(622 + j, (o, i)) for j in range(3)]
+    bs0 = [synth.normal(632 + j, (o,)) for j in range(3)]
+    s = HipStream()
+    x = s.add_constant(x0, meta((t, i)))
+    outs = [_linear(s, x, t, i, o, w0, b0) for w0, b0 in zip(ws0, bs0)]
+    before = s.launch_count()
+    s.eval_many(outs)
+    assert s.launch_count() - before == 1
+    xa = np.hstack([x0, np.ones((t, 1), np.float32)])
+    for j, (y, w0, b0) in enumerate(zip(outs, ws0, bs0)):
+        gemm_full_check(s.get_buffer(y).reshape(t, o), xa, np.vstack([w0.T, b0[None, :]]), "f32", f"projection {j}")
+
+
 def test_grouped_products_with_non_finite_operand():
     # A grouped launch where one product's weight holds inf and NaN: that
     # product takes the exact f32 path (its flag), giving what an f32 product
