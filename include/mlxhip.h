@@ -283,7 +283,9 @@ int mlxhip_stream_synchronize(mlxhip_stream_t* s);
  * reused; using an old one is MLXHIP_ERR_INVALID_ARGUMENT). Their HBM
  * returns to the library: with asynchronous evaluation the stream's later
  * work may reuse it at once, in queue order, without waiting for the
- * kernels already queued. No reference counterpart (a reference Stream keeps
+ * kernels already queued; caller memory that view constants read
+ * (mlxhip_stream_add_constant_view) may still be read by those kernels until
+ * the stream is next synchronized. No reference counterpart (a reference Stream keeps
  * every node until it is dropped, backend.rs:37-185); for a loop that builds
  * a new graph every step on one stream. */
 int mlxhip_stream_clear(mlxhip_stream_t* s);
@@ -301,11 +303,15 @@ int mlxhip_stream_eval_many(mlxhip_stream_t* s, const uint64_t* nodes, size_t n)
 uint64_t mlxhip_stream_add_constant_dev(mlxhip_stream_t* s, const float* data, size_t len,
                                         const mlxhip_meta_t* meta);
 /* As mlxhip_stream_add_constant_dev without the copy: the node reads `data`
- * (256-byte-aligned device memory of the caller) in place, so `data` must
- * stay valid and unchanged for as long as the node exists (until the stream
- * is cleared or freed); the stream never writes or frees it. No reference
- * counterpart; for inputs that already live in HBM, such as a model's
- * weights read by every step. */
+ * (256-byte-aligned device memory of the caller) in place; the stream never
+ * writes or frees it. `data` must stay valid and unchanged for as long as a
+ * queued kernel may read it: while the node exists and, with asynchronous
+ * evaluation, until the stream is next synchronized (mlxhip_stream_synchronize,
+ * mlxhip_stream_get_buffer, turning asynchronous evaluation off, or freeing
+ * the stream), even after mlxhip_stream_clear, which does not wait for
+ * queued kernels. With synchronous evaluation, clearing or freeing the
+ * stream ends it. No reference counterpart; for inputs that already live in
+ * HBM, such as a model's weights read by every step. */
 uint64_t mlxhip_stream_add_constant_view(mlxhip_stream_t* s, const float* data, size_t len,
                                          const mlxhip_meta_t* meta);
 /* value_and_grad / backward (crates/mlx-autograd/src/lib.rs:30-107) with the
@@ -348,13 +354,18 @@ int mlxhip_gemm(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t tran
 /* mlxhip_gemm for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc). No
  * counterpart in the reference. Same arguments, kernels, split-K plan and
- * results (bit for bit) as mlxhip_gemm, but its workspace (split-K partials,
+ * results (bit for bit) as mlxhip_gemm, except as noted below, but its workspace (split-K partials,
  * zero-padded copies of unaligned operands, the bf16 planes of large f32
  * products) comes from one fixed device array
  * of mlxhip_gemm_noalloc_scratch_bytes() bytes (64 MiB) per device, held
  * until the process ends; it calls no hipMalloc/hipFree and no allocating
- * library routine. A product whose workspace exceeds that array returns
- * MLXHIP_ERR_INVALID_ARGUMENT (C is then unchanged). Every call on one device
+ * library routine. A large f32 product whose bf16 planes (1.5x the f32 bytes
+ * of both operands, padded to multiples of 32) and split-K partials do not
+ * fit that array runs on the direct f32 MFMA kernel instead, which needs
+ * none (e.g. 4096^3 f32: 192 MiB of planes); its result is then within the
+ * f32 bound but not bit-identical to mlxhip_gemm's. Any other product whose
+ * workspace exceeds the array returns MLXHIP_ERR_INVALID_ARGUMENT (C is then
+ * unchanged). Every call on one device
  * shares that device's array: calls that overlap on one device (several
  * streams or threads at once) race, so the caller serialises them. */
 int mlxhip_gemm_noalloc(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t trans_b,

@@ -135,8 +135,12 @@ class HipStream:
 
     def add_constant_view(self, ptr: int, m: TensorMeta) -> int:
         """Constant that reads numel(m) floats at device address ``ptr``
-        (256-byte aligned) in place; the memory must stay valid and unchanged
-        while the node exists (until clear / close)."""
+        (256-byte aligned) in place. The memory must stay valid and unchanged
+        while a queued kernel may read it: while the node exists and, with
+        asynchronous evaluation, until the stream is next synchronized
+        (``synchronize``, ``get_buffer``, ``close``), even after ``clear``,
+        which does not wait for queued kernels. With synchronous evaluation,
+        ``clear`` / ``close`` end it."""
         cm, keep = m.to_c()
         nid = self._L.mlxhip_stream_add_constant_view(self._s, ptr, m.numel(), C.byref(cm))
         if nid == 0:

@@ -287,6 +287,19 @@ int vjp(Builder& b, uint64_t id, const Node& n, uint64_t g, const std::vector<bo
             if (!arity(3)) return MLXHIP_ERR_INVALID_ARGUMENT;
             if (!b.same_shape(g, id, "HeadAttention")) return recorded_status();
             const std::vector<int64_t> sh = b.shape(id);
+            {
+                // The gradient kernels' shape limits, checked here so that an
+                // unsupported shape fails when the gradient is built, not
+                // when it is first evaluated.
+                const int64_t hg = n.op.op.has_axis ? n.op.op.axis : 1;
+                const int64_t t = sh.size() == 3 ? sh[1] : 0, w = sh.size() == 3 ? sh[2] : 0;
+                if (sh.size() != 3 || hg < 1 || w % hg || !mlxhip::attention_vjp_supported(w / hg, t, t))
+                    return fail(MLXHIP_ERR_INVALID_ARGUMENT,
+                                "HeadAttention gradient: the fused gradient needs [heads, t, dh] operands with "
+                                "dh = 64 and t a multiple of 64 (got t=%lld, %lld heads per row of %lld values); "
+                                "compose the attention from MatMul and Softmax to differentiate other shapes",
+                                (long long)t, (long long)hg, (long long)w);
+            }
             std::vector<int64_t> vsh{3};
             vsh.insert(vsh.end(), sh.begin(), sh.end());
             mlxhip_op_t vo = Builder::op(MLXHIP_OP_HEAD_ATTENTION_VJP);

@@ -394,6 +394,56 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int 
         to.flag = from.flag;
         to.gen = from.gen;
     };
+    const int64_t slots = groups > 1 ? groups : batch;  // gridDim.y before splits
+
+    // Block tile and split (measured on the config-4 shapes, split and
+    // partial sums included): the interleaved kernel, whose 144 KiB of LDS
+    // stages allow one workgroup per CU; 256x128 blocks when they alone come
+    // to about one per CU (2048x4096x1024: 94 us, against 123 us for the
+    // segment-by-segment kernel), else 128x128 blocks split over K to one
+    // workgroup per CU (2048x1024x1024 split 2: 41 us against 54 us;
+    // 1024x1024x2048 split 4: 42 us against 55 us; 4096x1024x2048 unsplit:
+    // 104 us against 124 us). Grouped products count every group's tiles and
+    // run unsplit. MLXHIP_X6="cfg,splits" forces them (tuning; cfg 0-2 the
+    // segment-by-segment kernel with 256x256, 128x128 and 256x128 blocks,
+    // 3-4 the interleaved one with 256x128 and 128x128).
+    const int64_t wide_tiles = ceil_div(m, 256) * ceil_div(n, 128) * slots;
+    const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * slots;
+    int cfg = 3, sp_k = 1;
+    if (wide_tiles < 224) {
+        cfg = 4;
+        while (sp_k < 8 && mid_tiles * sp_k < 256 && kp / (2 * sp_k) >= 128) sp_k *= 2;
+    }
+    if (const char* e = getenv("MLXHIP_X6")) {
+        int cf = 0, v = 0;
+        if (sscanf(e, "%d,%d", &cf, &v) == 2 && cf >= 0 && cf <= 4 && v >= 1 && v <= 8) {
+            cfg = cf;
+            sp_k = v;
+        }
+    }
+    if (groups > 1) {
+        sp_k = 1;
+        if (cfg < 3) cfg = 3;
+    }
+    if (slots * sp_k > 65535) sp_k = 1;
+    // The f32 partials of a product split over K (sp_k > 1).
+    const int64_t kspan = cfg >= 3 ? kp : gemm16::X6_SEGS * kp;
+    const int64_t k_chunk = sp_k > 1 ? ceil_div(ceil_div(kspan, sp_k), 32) * 32 : 0;
+    const int splits = sp_k > 1 ? (int)ceil_div(kspan, k_chunk) : 1;
+    const int64_t ldw = ceil_div(n, 4) * 4;
+    const size_t part_bytes = sp_k > 1 ? (size_t)(batch * splits * m * ldw) * sizeof(float) : 0;
+    if (fs) {
+        // Fixed scratch (gemm_noalloc): when the planes and partials do not
+        // fit, the product runs on the direct f32 MFMA kernel instead, which
+        // needs no planes (within the f32 bound, not bit-identical to the
+        // split-f32 result).
+        size_t need = 0;
+        for (int i = 0; i < nops; ++i)
+            if (fresh[i]) need += plane_bytes(op[i]) + flag_room;
+        need = ((need + 255) & ~size_t(255)) + part_bytes + 256;
+        const size_t used = (fs->used + 255) & ~size_t(255);
+        if (used > fs->cap || need > fs->cap - used) return MLXHIP_OK;
+    }
     if (cache && cache->alloc && !fs) {
         for (int i = 0; i < nops; ++i) {
             X6SplitOp& o = op[i];
@@ -478,39 +528,7 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int 
                                            bias ? bias[i] : nullptr};
         }
     }
-    const int64_t slots = groups > 1 ? groups : batch;  // gridDim.y before splits
 
-    // Block tile and split (measured on the config-4 shapes, split and
-    // partial sums included): the interleaved kernel, whose 144 KiB of LDS
-    // stages allow one workgroup per CU; 256x128 blocks when they alone come
-    // to about one per CU (2048x4096x1024: 94 us, against 123 us for the
-    // segment-by-segment kernel), else 128x128 blocks split over K to one
-    // workgroup per CU (2048x1024x1024 split 2: 41 us against 54 us;
-    // 1024x1024x2048 split 4: 42 us against 55 us; 4096x1024x2048 unsplit:
-    // 104 us against 124 us). Grouped products count every group's tiles and
-    // run unsplit. MLXHIP_X6="cfg,splits" forces them (tuning; cfg 0-2 the
-    // segment-by-segment kernel with 256x256, 128x128 and 256x128 blocks,
-    // 3-4 the interleaved one with 256x128 and 128x128).
-    const int64_t kv = gemm16::X6_SEGS * kp;
-    const int64_t wide_tiles = ceil_div(m, 256) * ceil_div(n, 128) * slots;
-    const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * slots;
-    int cfg = 3, sp_k = 1;
-    if (wide_tiles < 224) {
-        cfg = 4;
-        while (sp_k < 8 && mid_tiles * sp_k < 256 && kp / (2 * sp_k) >= 128) sp_k *= 2;
-    }
-    if (const char* e = getenv("MLXHIP_X6")) {
-        int cf = 0, v = 0;
-        if (sscanf(e, "%d,%d", &cf, &v) == 2 && cf >= 0 && cf <= 4 && v >= 1 && v <= 8) {
-            cfg = cf;
-            sp_k = v;
-        }
-    }
-    if (groups > 1) {
-        sp_k = 1;
-        if (cfg < 3) cfg = 3;
-    }
-    if (slots * sp_k > 65535) sp_k = 1;
     X6SplitPair sp{};
     for (int i = 0; i < nops; ++i) {
         if (!fresh[i]) continue;
@@ -533,12 +551,10 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int 
     }
     // The interleaved kernel (cfg 3 / 4) runs all six products per K tile:
     // its splits divide the planes' K, the other kernel's the 6 segments.
-    const int64_t kspan = cfg >= 3 ? kp : kv;
-    h.k_chunk = ceil_div(ceil_div(kspan, sp_k), 32) * 32;
-    h.splits = (int)ceil_div(kspan, h.k_chunk);
-    const int64_t ldw = ceil_div(n, 4) * 4;
+    h.k_chunk = k_chunk;
+    h.splits = splits;
     void* part = nullptr;
-    MLXHIP_TRY(take_workspace(fs, s, WS_SPLITK, (size_t)(batch * h.splits * m * ldw) * sizeof(float), &part));
+    MLXHIP_TRY(take_workspace(fs, s, WS_SPLITK, part_bytes, &part));
     h.c = part;
     h.ldc = ldw;
     h.sc = m * ldw;

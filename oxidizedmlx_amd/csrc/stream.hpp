@@ -119,8 +119,18 @@ struct mlxhip_stream_t {
     mlxhip_stream_t& operator=(const mlxhip_stream_t&) = delete;
 
     ~mlxhip_stream_t() {
-        if (side) (void)hipStreamSynchronize(side);
-        if (hs) (void)hipStreamSynchronize(hs);
+        // The queues' cached workspaces (split-K partials, padded operand
+        // copies, reduction partials, attention-gradient row statistics) are
+        // keyed by (device, queue): return them to the pool with this
+        // stream's device current, once the queues are idle, before the
+        // handles die (a later queue may reuse the handle value).
+        int cur = 0;
+        const bool have_cur = hipGetDevice(&cur) == hipSuccess;
+        if (have_cur && cur != device) (void)hipSetDevice(device);
+        if (side && hipStreamSynchronize(side) == hipSuccess) mlxhip::release_stream_workspaces(side);
+        if (hs && hipStreamSynchronize(hs) == hipSuccess) mlxhip::release_stream_workspaces(hs);
+        if (have_cur && cur != device) (void)hipSetDevice(cur);
+        (void)hipGetLastError();
         for (auto& b : pending) mlxhip::pool_release(b.second);
         for (auto& kv : buffers)
             if (kv.second.owned) mlxhip::pool_release(kv.second.ptr);

@@ -172,3 +172,24 @@ def test_heads_in_rows_layout_matches_head_major(b, t, heads, causal):
     hm = run(tuple(head_major(a) for a in (q, k, v, g)), None)
     for name, a, e in zip(("O", "dQ", "dK", "dV"), rows, hm):
         np.testing.assert_array_equal(head_major(a), e, err_msg=name)
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip")
+@pytest.mark.parametrize("shape,heads", [((4, 64, 32), None), ((2, 96, 64), None), ((2, 64, 96), 3)],
+                         ids=["dh32", "t96", "rows_dh32"])
+def test_unsupported_gradient_shapes_fail_when_the_gradient_is_built(shape, heads):
+    """The fused gradient covers dh = 64 with t a multiple of 64. Other
+    shapes still run forward, but asking for their gradient fails at once in
+    value_and_grad (InvalidArgument), not later when the gradient is
+    evaluated."""
+    from oxidizedmlx_amd import abi
+    from oxidizedmlx_amd.backend import HipStream
+    st = HipStream()
+    q, k, v = (synth.normal(1500 + i, shape) for i in range(3))
+    tq, tk, tv = (Tensor.from_f32_on_stream(a.reshape(-1), a.shape, st) for a in (q, k, v))
+    o = tq.head_attention(tk, tv, 0.25, True, heads=heads)
+    assert np.isfinite(o.to_numpy()).all()
+    with pytest.raises(abi.InvalidArgument, match="HeadAttention gradient"):
+        value_and_grad(o.sum_all(), [tq])
+    st.close()

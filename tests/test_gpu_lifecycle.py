@@ -103,3 +103,47 @@ def test_buffer_lifecycle_10k_and_null_frees():
     after = free_device_bytes()
     print(f"free device memory {before} -> {after} bytes over 10k alloc/free", flush=True)
     assert before - after < (64 << 20)
+
+
+def test_freed_streams_return_their_workspaces():
+    """A stream's cached workspaces (split-K partials of a 1024 x 1024 x 2048
+    f32 product, the partial sums of a reduction over a 4096-long axis) go
+    back to the pool when the stream is freed: free device memory stays
+    bounded over many create / evaluate / free cycles. Two streams are
+    alive at a time, so queue handles are not simply reused in turn."""
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((1024, 2048), dtype=np.float32)
+    b = rng.standard_normal((2048, 1024), dtype=np.float32)
+    x = rng.standard_normal((4096, 256), dtype=np.float32)
+    want_sum = x.astype(np.float64).sum(axis=0)
+
+    def cycle(s):
+        ia = s.add_constant(a, meta([1024, 2048]))
+        ib = s.add_constant(b, meta([2048, 1024]))
+        ix = s.add_constant(x, meta([4096, 256]))
+        c = s.add_op(OpKind.MatMul, [ia, ib], meta([1024, 1024]))
+        r = s.add_op(OpKind.Sum(0), [ix], meta([256]))
+        s.eval(c)
+        s.eval(r)
+        got = s.get_buffer(r)
+        assert np.max(np.abs(got - want_sum)) < 1e-2, np.max(np.abs(got - want_sum))
+        assert np.isfinite(s.get_buffer(c)).all()
+
+    keep = hb.HipStream()
+    cycle(keep)
+    for _ in range(3):
+        s = hb.HipStream()
+        cycle(s)
+        s.close()
+    hb.synchronize()
+    before = free_device_bytes()
+    for i in range(24):
+        s = hb.HipStream()
+        cycle(s)
+        old, keep = keep, s
+        old.close()
+    keep.close()
+    hb.synchronize()
+    after = free_device_bytes()
+    print(f"free device memory {before} -> {after} bytes over 24 stream cycles", flush=True)
+    assert before - after < (64 << 20)

@@ -781,3 +781,32 @@ def test_grouped_products_with_non_finite_operand():
     assert np.all(np.abs(got[1][fin] - ref1[fin]) <= 1e-6 * np.sqrt(I) * mag[fin] + 1e-30)
     for i in (0, 2):
         gemm_full_check(got[i], x0, ws0[i].T, "f32", f"finite product {i} of the group")
+
+
+def test_async_view_constant_rewritten_after_synchronize():
+    """The view-constant contract under asynchronous evaluation: kernels
+    queued before clear() may still read the caller's memory, so the caller
+    rewrites it only after synchronizing. Two steps on one stream: step 1
+    reads the view, is cleared without waiting, the stream is synchronized,
+    the memory is rewritten, and step 2 sees the new values while step 1's
+    result (taken before the clear) keeps the old ones."""
+    from oxidizedmlx_amd import backend as _hb
+    x = np.arange(4096, dtype=np.float32).reshape(64, 64) / 7.0
+    buf = _hb.DeviceBuffer.from_array(x)
+    s = HipStream(async_eval=True)
+    v = s.add_constant_view(buf.ptr, meta([64, 64]))
+    two = s.add_constant(np.full((64, 64), 2.0, np.float32), meta([64, 64]))
+    y = s.add_op(OpKind.Mul, [v, two], meta([64, 64]))
+    s.eval(y)
+    first = s.get_buffer(y).reshape(64, 64)
+    s.clear()
+    s.synchronize()
+    buf.upload(-x)
+    v = s.add_constant_view(buf.ptr, meta([64, 64]))
+    two = s.add_constant(np.full((64, 64), 2.0, np.float32), meta([64, 64]))
+    y = s.add_op(OpKind.Mul, [v, two], meta([64, 64]))
+    s.eval(y)
+    second = s.get_buffer(y).reshape(64, 64)
+    s.close()
+    np.testing.assert_array_equal(first, x * np.float32(2.0))
+    np.testing.assert_array_equal(second, -x * np.float32(2.0))

@@ -75,3 +75,23 @@ def test_noalloc_rejects_products_beyond_its_scratch():
         hb.gemm_noalloc(F32, F32, False, False, m, n, k, da, lda, db, ldb, dc, n)
     hb.synchronize()
     assert np.array_equal(dc.download(np.float32, 16), sentinel)
+
+
+def test_noalloc_f32_planes_beyond_scratch_take_the_direct_kernel():
+    """An aligned f32 product whose bf16 planes (72 MiB here) exceed the
+    64 MiB fixed scratch runs on the direct f32 MFMA kernel instead of
+    failing: checked against float64 with the f32 accumulation bound (the
+    result need not match mlxhip_gemm's split-f32 bits)."""
+    m, n, k = 2048, 2048, 3072
+    A = synth.normal(31, (m, k))
+    B = synth.normal(32, (k, n))
+    da, db = _dev(A, F32), _dev(B, F32)
+    dc = hb.DeviceBuffer(m * n * 4)
+    print(f"noalloc f32 direct fallback: {m}x{n}x{k}", flush=True)
+    hb.gemm_noalloc(F32, F32, False, False, m, n, k, da, k, db, n, dc, n)
+    hb.synchronize()
+    got = dc.download(np.float32, m * n).reshape(m, n).astype(np.float64)
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    bound = (k * np.finfo(np.float32).eps) * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64))
+    err = np.abs(got - ref)
+    assert np.all(err <= bound + 1e-30), float((err / np.maximum(bound, 1e-30)).max())
