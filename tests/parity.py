@@ -245,3 +245,92 @@ def tree_sum_f32(x, blocks: int = 1024, threads: int = 256) -> np.float32:
     for j in range(0, blocks, threads):
         fin = fin + part[j:j + threads]
     return np.float32(halve(fin))
+
+
+# ── Elementwise chains: float64 value and f32 error bound ────────────────────
+
+F32_MAX = float(np.finfo(np.float32).max)
+TINY = 2.0 ** -126  # smallest normal f32: a subnormal result may also come out flushed to zero
+
+
+def chain_bound(ins, prog, unary, binary):
+    """Float64 value v of the chain on the f32 inputs, with a bound E on how
+    far an f32 evaluation whose every operation errs by at most a few units
+    of roundoff (one for + - * / and sqrt, 8 for exp, log, SiLU and GELU) can
+    land from v, and a mask of `uncertain` elements where no bound holds:
+    the interval a Log, Sqrt or Div reads reaches zero or below, a value may
+    overflow f32, or the bound is not finite. Each step also allows an
+    absolute error of the smallest normal f32 (TINY): a result in the
+    subnormal range may come out flushed or off by a subnormal unit. prog
+    steps are (code, j, left): code < len(unary) applies unary[code];
+    otherwise binary[code - len(unary)] with input j as the right
+    (left=True) or left operand. Mistakes this pins: a wrong op or operand
+    order, a dropped step, a step applied twice (each moves the value far
+    beyond E), or an f32 error above the stated few ulp."""
+    v = ins[0].astype(np.float64)
+    e = np.zeros_like(v)
+    unc = np.zeros(v.shape, bool)
+    with np.errstate(all="ignore"):
+        for code, j, left in prog:
+            if code < len(unary):
+                op = unary[code].name
+                if op == "Neg":
+                    v = -v
+                elif op == "Exp":
+                    nv = np.exp(v)
+                    e = nv * np.expm1(e) + 8 * U32 * np.exp(v + e) + TINY
+                    v = nv
+                elif op == "Log":
+                    unc |= v - e <= 0
+                    nv = np.log(v)
+                    e = -np.log1p(-e / v) + 8 * U32 * np.abs(nv) + TINY
+                    v = nv
+                elif op == "Sqrt":
+                    unc |= v - e < 0
+                    nv = np.sqrt(v)
+                    e = e / (np.sqrt(np.maximum(v - e, 0.0)) + nv) + U32 * nv + TINY
+                    v = nv
+                elif op == "Silu":
+                    nv = v / (1.0 + np.exp(-v))
+                    e = 1.1 * e + 8 * U32 * np.abs(nv) + TINY
+                    v = nv
+                else:  # Gelu, tanh form
+                    nv = 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v ** 3)))
+                    e = 1.13 * e + 16 * U32 * (np.abs(v) + np.abs(nv)) + TINY
+                    v = nv
+            else:
+                o = ins[j].astype(np.float64)
+                a, ea, b, eb = (v, e, o, 0.0) if left else (o, 0.0, v, e)
+                op = binary[code - len(unary)].name
+                if op == "Add":
+                    v, e = a + b, ea + eb
+                elif op == "Sub":
+                    v, e = a - b, ea + eb
+                elif op == "Mul":
+                    v, e = a * b, np.abs(a) * eb + np.abs(b) * ea + ea * eb
+                else:  # Div
+                    unc |= np.abs(b) <= eb
+                    v = a / b
+                    e = (ea + np.abs(v) * eb) / (np.abs(b) - eb)
+                e = e + U32 * np.abs(v) + TINY
+            unc |= ~np.isfinite(e) | (np.abs(v) + e >= F32_MAX) | np.isinf(v)
+    return v, e, unc
+
+
+def assert_chain_within_bound(hip, cpu, v, e, unc):
+    """Both f32 results lie within E of v, so they differ by at most 2E;
+    where v is NaN (a certain domain error) both must be NaN."""
+    h = hip.astype(np.float64)
+    c = cpu.astype(np.float64)
+    nan = np.isnan(v) & ~unc
+    assert np.all(np.isnan(h[nan]) & np.isnan(c[nan])), "a certain NaN is not NaN on both sides"
+    ok = ~unc & ~np.isnan(v)
+    assert np.all(np.isfinite(h[ok]) & np.isfinite(c[ok])), "a finite value came out non-finite"
+    d = np.abs(h[ok] - c[ok])
+    lim = 2 * e[ok]
+    bad = ~(d <= lim)
+    if bad.any():
+        i = int(np.flatnonzero(ok)[np.argmax(bad)])
+        raise AssertionError(f"chain mismatch at [{i}]: hip={hip[i]} cpu={cpu[i]} exact={v[i]} bound={2 * e[i]}")
+    print(f"  chain checked {int(ok.sum())} of {v.size} (certain NaN {int(nan.sum())}, "
+          f"max diff / bound {float((d / np.maximum(lim, 1e-300)).max()) if d.size else 0.0:.3f})", flush=True)

@@ -3,8 +3,9 @@ pass) and on copies with one planted mistake (must raise). The mistakes are
 planted in CPU-side results only; no GPU is involved.
 
 Checkers covered: the full-output float64 GEMM bound (gemm_full_check), the
-tree-sum bound of the whole-tensor Sum/Mean (tree_sum_bound, tree_sum_f32)
-and the closed-form RoPE pin (rope_closed_form_check).
+tree-sum bound of the whole-tensor Sum/Mean (tree_sum_bound, tree_sum_f32),
+the closed-form RoPE pin (rope_closed_form_check) and the error bound of
+random elementwise chains (chain_bound, assert_chain_within_bound).
 """
 import math
 
@@ -14,7 +15,8 @@ import pytest
 from oracle.cpu_ref import CpuRefBackend, gen_data
 from oxidizedmlx_amd import synth
 from oxidizedmlx_amd.opkind import NodeInput, OpKind, meta
-from parity import gemm_full_check, rope_closed_form_check, tree_sum_bound, tree_sum_f32
+from parity import (assert_chain_within_bound, chain_bound, cpu_stream, gemm_full_check, rope_closed_form_check,
+                    tree_sum_bound, tree_sum_f32)
 
 pytestmark = pytest.mark.usefixtures("oracle_lib")
 
@@ -159,3 +161,71 @@ def test_rope_closed_form_pins_oracle_and_rejects_mistakes(traditional):
         with pytest.raises(AssertionError):
             rope_closed_form_check(_py_rope(base, off, traditional, **wrong), hd, rows, off, base,
                                    traditional, f"planted {wrong}")
+
+
+# ── Elementwise chains: the f32 error bound of a random program ─────────────
+
+CHAIN_UNARY = [OpKind.Neg, OpKind.Silu, OpKind.Gelu, OpKind.Exp, OpKind.Log, OpKind.Sqrt]
+CHAIN_BINARY = [OpKind.Add, OpKind.Sub, OpKind.Mul, OpKind.Div]
+
+
+def _oracle_chain(ins, prog, unary=CHAIN_UNARY, binary=CHAIN_BINARY):
+    s = cpu_stream()
+    n = ins[0].size
+    leaves = [s.add_constant(a, meta([n])) for a in ins]
+    acc = leaves[0]
+    for code, j, left in prog:
+        if code < len(unary):
+            acc = s.add_op(unary[code], [acc], meta([n]))
+        else:
+            other = leaves[j]
+            acc = s.add_op(binary[code - len(unary)], [acc, other] if left else [other, acc], meta([n]))
+    s.eval(acc)
+    return s.get_buffer(acc)
+
+
+def _programs():
+    rng = np.random.default_rng(2024)
+    for _ in range(60):
+        L = int(rng.integers(1, 9))
+        yield [(int(rng.integers(0, 10)), int(rng.integers(0, 3)), bool(rng.integers(0, 2))) for _ in range(L)]
+
+
+def test_chain_bound_holds_for_the_oracle():
+    """The oracle's own f32 chain lies within E (half the cross-check's 2E)
+    of the float64 value on 60 random programs over every op."""
+    n = 2000
+    ins = [synth.normal(n * 3 + j, (n,), 0.0, 1.0) for j in range(3)]
+    checked = 0
+    for prog in _programs():
+        out = _oracle_chain(ins, prog)
+        v, e, unc = chain_bound(ins, prog, CHAIN_UNARY, CHAIN_BINARY)
+        ok = ~unc & np.isfinite(v)
+        assert np.all(np.abs(out[ok].astype(np.float64) - v[ok]) <= e[ok]), prog
+        assert np.all(np.isnan(out[np.isnan(v) & ~unc])), prog
+        checked += int(ok.sum())
+    assert checked > 60 * n // 4
+
+
+@pytest.mark.parametrize("swap", ["exp_for_neg", "div_for_mul", "operand_side", "dropped_step"])
+def test_chain_bound_catches_planted_mistakes(swap):
+    """One wrong step in the evaluated chain (a different op, swapped
+    operands of a Sub, a missing step) moves results far beyond the bound."""
+    n = 2000
+    ins = [synth.normal(n * 3 + j, (n,), 0.0, 1.0) for j in range(3)]
+    prog = [(0, 0, True), (6, 1, True), (8, 2, True), (1, 0, True), (7, 1, False)]  # Neg, Add, Mul, Silu, Sub
+    bad = list(prog)
+    if swap == "exp_for_neg":
+        bad[0] = (3, 0, True)
+    elif swap == "div_for_mul":
+        bad[2] = (9, 2, True)
+    elif swap == "operand_side":
+        bad[4] = (7, 1, True)
+    else:
+        bad = bad[:3] + bad[4:]
+    good = _oracle_chain(ins, prog)
+    wrong = _oracle_chain(ins, bad)
+    bound = chain_bound(ins, prog, CHAIN_UNARY, CHAIN_BINARY)
+    assert_chain_within_bound(good, good, *bound)
+    with pytest.raises(AssertionError):
+        assert_chain_within_bound(wrong, good, *bound)

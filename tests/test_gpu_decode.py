@@ -154,7 +154,10 @@ def test_config5_matches_stream_forward():
     batch 8, prompt 16, 128 new tokens): the decoder's logits at all 143
     positions against the causal forward of the same mlx-nn model on the
     HipStream (f32 GEMMs over the bf16-valued weights) on the tokens the
-    decoder consumed."""
+    decoder consumed, and one whole sequence (all 143 positions of sequence
+    3, teacher-forced) against the oracle's mlx-nn decoder: every logit and
+    every clear-margin argmax decision of the generate the bench times
+    (crates/mlx-conformance/tests/ttft_behavior.rs:101-216 loops 128 steps)."""
     cfg = nn.DecoderConfig()
     P = nn.decoder_params(cfg, 2024)
     dec = HipDecoder(cfg)
@@ -168,6 +171,10 @@ def test_config5_matches_stream_forward():
     clear, total = check_logits_and_argmax(lg, am, ref, "config 5")
     print(f"  config 5: {clear} of {total} argmax decisions with a clear margin", flush=True)
     assert clear >= total * 0.9
+    print("config 5, oracle on the whole of sequence 3 (143 positions)", flush=True)
+    ref3 = oracle_logits(cfg, P, seq[3:4])
+    clear3, total3 = check_logits_and_argmax(lg[3:4], am[3:4], ref3, "config 5 sequence 3 vs oracle")
+    assert total3 == 143 and clear3 >= total3 * 0.9
 
 
 def test_config5_full_size_matches_oracle():

@@ -33,6 +33,10 @@ def test_gate_unary():
     run_parity(lambda s: unary_op(s, OpKind.Exp, e, meta([1024])), 1e-6, 1e-6, "Exp")
     p = gen_positive_data(1024, 5)
     run_parity(lambda s: unary_op(s, OpKind.Log, p, meta([1024])), 1e-6, 1e-6, "Log")
+    # Sqrt (cpu_kernels.rs:85-88, f32::sqrt): correctly rounded on both sides,
+    # held to the elementwise tolerance of crates/mlx-parity/tests/elementwise.rs:8-9.
+    r = gen_positive_data(1024, 6)
+    run_parity(lambda s: unary_op(s, OpKind.Sqrt, r, meta([1024])), 1e-6, 1e-6, "Sqrt")
 
 
 def test_gate_activations_and_softmax():
@@ -146,6 +150,19 @@ def test_parity_elementwise():
     run_parity(lambda s: unary_op(s, OpKind.Exp, a, meta([1024])), 1e-6, 1e-6, "Exp")
     a = gen_positive_data(1024, 54)
     run_parity(lambda s: unary_op(s, OpKind.Log, a, meta([1024])), 1e-6, 1e-6, "Log")
+    a = gen_positive_data(4096, 55)
+    h, c = run_parity(lambda s: unary_op(s, OpKind.Sqrt, a, meta([4096])), 1e-6, 1e-6, "Sqrt")
+    np.testing.assert_array_equal(h, c)  # IEEE square root: correctly rounded, so bit for bit
+    # Special values: sqrt(+0) = +0, sqrt(-0) = -0, sqrt(+inf) = +inf, negatives and NaN give NaN.
+    sp = np.array([0.0, -0.0, np.inf, -1.0, np.nan, 1e-40, 4.0, 2.0], np.float32)
+    got = []
+    for st in (hip_stream(), cpu_stream()):
+        out = unary_op(st, OpKind.Sqrt, sp, meta([8]))
+        st.eval(out)
+        got.append(st.get_buffer(out))
+    h, c = got
+    np.testing.assert_array_equal(np.signbit(h[:3]), np.signbit(c[:3]))
+    np.testing.assert_array_equal(h, c)
 
 
 @pytest.mark.parametrize("rows,cols,seed", [(4, 8, 130), (64, 128, 131), (1000, 777, 132)])

@@ -123,6 +123,26 @@ def test_batched_cfg3(ab, tb):
                full=True)
 
 
+@pytest.mark.parametrize("ab", [BF16, F16])
+@pytest.mark.parametrize("tb", [False, True])
+def test_batched_cfg3_c_in_operand_dtype(ab, tb):
+    # The config-3 products as bench.py times them: C in the operands' dtype,
+    # as the reference's matmul gives its result the left operand's dtype
+    # (crates/mlx-core/src/tensor.rs:294), rounded once from the f32
+    # accumulator. Three rows per slice against the oracle; every element of
+    # all 32 slices against float64 with the accumulation bound plus one
+    # rounding to the 16-bit type.
+    check_gemm(1024, 1024, 1024, ab, ab, tb=tb, batch=32, seed=22, rows=np.array([0, 511, 1023]),
+               full=True)
+
+
+@pytest.mark.parametrize("ab", [BF16, F16])
+def test_odd_cfg3_c_in_operand_dtype(ab):
+    # The odd shape as bench.py times it (16-bit C; split over K, so the
+    # rounding happens in the partial-sum kernel).
+    check_gemm(1000, 777, 1531, ab, ab, seed=32, rows=sample_rows(1000, 24), full=True)
+
+
 @pytest.mark.parametrize("ab", [BF16, F16, F32])
 def test_odd_cfg3(ab):
     # Config 3 odd shape M=1000, N=777, K=1531 (edge tiles; unaligned rows).

@@ -19,7 +19,7 @@ from hypothesis import strategies as st
 from oxidizedmlx_amd import backend as hb
 from oxidizedmlx_amd import synth
 from oxidizedmlx_amd.opkind import OpKind, meta
-from parity import assert_allclose, cpu_stream, hip_stream
+from parity import assert_allclose, assert_chain_within_bound, chain_bound, cpu_stream, hip_stream
 from test_gpu_gemm import BF16, F16, F32, check_gemm
 from test_gpu_rows import oracle, run_rows
 
@@ -168,17 +168,18 @@ def oracle_reduce(op, x, out_shape):
     return CpuRefBackend().eval_node(op, [NodeInput(x.reshape(-1), x.shape)], meta(out_shape)).reshape(-1)
 
 
-UNARY = [OpKind.Neg, OpKind.Silu, OpKind.Gelu]
-BINARY = [OpKind.Add, OpKind.Sub, OpKind.Mul]
-
-
+UNARY = [OpKind.Neg, OpKind.Silu, OpKind.Gelu, OpKind.Exp, OpKind.Log, OpKind.Sqrt]
+BINARY = [OpKind.Add, OpKind.Sub, OpKind.Mul, OpKind.Div]
 @CASES
-@given(n=st.integers(1, 3000), prog=st.lists(st.tuples(st.integers(0, 5), st.integers(0, 2), st.booleans()),
+@given(n=st.integers(1, 3000), prog=st.lists(st.tuples(st.integers(0, len(UNARY) + len(BINARY) - 1),
+                                                       st.integers(0, 2), st.booleans()),
                                               min_size=1, max_size=8), fusion=st.booleans())
 def test_elementwise_chain_any_program(n, prog, fusion):
-    """A random chain over three inputs: step i applies a unary op, or a
-    binary op with input j on either side; the fusing stream must match the
-    oracle's node-by-node evaluation."""
+    """A random chain over three inputs: step i applies a unary op (Neg,
+    SiLU, GELU, Exp, Log, Sqrt), or a binary op (Add, Sub, Mul, Div) with
+    input j on either side; the fusing stream and the oracle's node-by-node
+    evaluation must both lie within the chain's f32 error bound of the
+    float64 value, and agree on certain NaNs."""
     print(f"chain n={n} prog={prog} fusion={fusion}", flush=True)
     ins = [synth.normal(n * 3 + j, (n,), 0.0, 1.0) for j in range(3)]
 
@@ -186,11 +187,11 @@ def test_elementwise_chain_any_program(n, prog, fusion):
         leaves = [s.add_constant(a, meta([n])) for a in ins]
         acc = leaves[0]
         for code, j, left in prog:
-            if code < 3:
+            if code < len(UNARY):
                 acc = s.add_op(UNARY[code], [acc], meta([n]))
             else:
                 other = leaves[j]
-                acc = s.add_op(BINARY[code - 3], [acc, other] if left else [other, acc], meta([n]))
+                acc = s.add_op(BINARY[code - len(UNARY)], [acc, other] if left else [other, acc], meta([n]))
         return acc
 
     cpu, hip = cpu_stream(), hip_stream()
@@ -198,4 +199,4 @@ def test_elementwise_chain_any_program(n, prog, fusion):
     c_out, h_out = build(cpu), build(hip)
     cpu.eval(c_out)
     hip.eval(h_out)
-    assert_allclose(hip.get_buffer(h_out), cpu.get_buffer(c_out), 1e-6, 1e-5, "chain")
+    assert_chain_within_bound(hip.get_buffer(h_out), cpu.get_buffer(c_out), *chain_bound(ins, prog, UNARY, BINARY))
