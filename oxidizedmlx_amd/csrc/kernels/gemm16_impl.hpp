@@ -102,6 +102,9 @@ struct Args {
     int64_t ldc, sc;
     uint32_t a_bytes, b_bytes;  // byte extent of one batch slice (descriptor range)
     int tiles_m, tiles_n;
+    // C row segments are stored non-temporally (c_nt != 0) or as plain
+    // write-back stores; set by launch() from the grid (see there).
+    int c_nt = 1;
     // Split-K (splits > 1): gridDim.y = batch * splits; split s of batch b
     // covers k in [s * k_chunk, min(k, (s + 1) * k_chunk)) and writes its
     // f32 partial to c + (b * splits + s) * sc (the kernel is instantiated
@@ -415,9 +418,10 @@ __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN],
     // sub-tile into padded LDS rows (PITCH = row bytes + 16: consecutive rows
     // fall in distinct bank groups for the 8/16-byte writes) and reads it
     // back row by row, so every global store instruction writes whole row
-    // segments instead of 16-byte pieces of 32 rows. The row segments are
-    // stored non-temporally: C is written once, so it streams out rather
-    // than leaving the L2s full of dirty lines at the end of the kernel.
+    // segments instead of 16-byte pieces of 32 rows. With g.c_nt the row
+    // segments are stored non-temporally (C is written once, so it streams
+    // out instead of filling the L2s that later tiles' operands need);
+    // otherwise as plain write-back stores.
     constexpr int TM = C::TM, TN = C::TN;
     constexpr int ES = CT == MLXHIP_DTYPE_F32 ? 4 : 2;
     constexpr int PASS_ROWS = pass_rows<C, ES>(PIPE_BYTES);
@@ -484,7 +488,8 @@ __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN],
             }
             char* dst = Cp + (m * g.ldc + n) * ES;
             if (vec_ok && n + 16 / ES <= g.n) {
-                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
+                if (g.c_nt) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
+                else *reinterpret_cast<u32x4*>(dst) = v;
             } else {
                 // Row end or unaligned C: element stores.
 #pragma unroll
@@ -722,6 +727,14 @@ int launch(const Args& a0, int64_t batch, hipStream_t s) {
     a.tiles_m = (int)ceil_div(a.m, C::BM);
     a.tiles_n = (int)ceil_div(a.n, C::BN);
     dim3 grid((unsigned)(a.tiles_m * a.tiles_n), (unsigned)(batch * a.splits));
+    // A grid that runs in one round of workgroups (one per CU for the
+    // 256 x 256 blocks) stores C with plain stores: nothing runs after the
+    // tiles' epilogues, and write-back stores drain faster at the kernel's
+    // end (4096^3 bf16: 120.0-120.3 us against 121.9-122.1 us steady state,
+    // alternating on one MI355X). Later rounds' operands need the L2s, so a
+    // larger grid stores non-temporally (config 3, 512 tiles: 3-4 us faster
+    // per call that way).
+    a.c_nt = (int64_t)grid.x * grid.y > 256 ? 1 : 0;
     hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, C, true, X6>), grid, dim3(C::THREADS), 0, s, a);
     return launch_check("gemm16_kernel");
 }
