@@ -58,6 +58,7 @@ SOURCES = [
     "kernels/gemm16_bf16.hip",
     "kernels/gemm16_f16.hip",
     "kernels/gemm16_x6.hip",
+    "kernels/gemm16_small.hip",
     "kernels/decode.hip",
     "kernels/attention.hip",
     "kernels/attention_bwd.hip",

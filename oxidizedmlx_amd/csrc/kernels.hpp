@@ -175,6 +175,14 @@ bool gemm_f32_groupable(int64_t m, int64_t n, int64_t k);
 int gemm_f32_grouped(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, int groups, const float* const* a,
                      int64_t lda, const float* const* b, int64_t ldb, float* const* c, int64_t ldc, hipStream_t s,
                      PlaneCache* planes = nullptr, const float* const* bias = nullptr);
+// gemm16_small.hip: bf16 / f16 products in one launch of 64 x 64 tiles with
+// register-staged, realigned operand loads (any 2-byte-aligned operand, no
+// workspace); c_dtype F32 / BF16 / F16.
+bool gemm16_small_fits(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t lda, int64_t ldb, int ta, int tb);
+int gemm16_small(int ab_dtype, int c_dtype, int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch,
+                 const void* a, int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, void* c,
+                 int64_t ldc, int64_t sc, hipStream_t s);
+
 // gemm_small.hip: f32 products small enough for one or two rounds of 32 x 32
 // tiles with K <= 512, one launch, no workspace, any alignment.
 bool gemm_small_f32_fits(int64_t m, int64_t n, int64_t k, int64_t batch);

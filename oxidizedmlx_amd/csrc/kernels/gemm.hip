@@ -229,7 +229,8 @@ int pack2(int dt, const PackPair& pp, int64_t batch, hipStream_t s) {
 // MLXHIP_GEMM_PATH: unset/"auto" = choose by shape, "general" = always the
 // general kernel, "lds16" = the direct-to-LDS 16-bit kernel whenever the
 // operands allow it ("lds16_256" / "lds16_128": with that block size),
-// "x6" = every f32 product through the split-f32 kernel. Read on every call
+// "x6" = every f32 product through the split-f32 kernel, "small16" = every
+// 16-bit product through the one-launch 64 x 64 kernel. Read on every call
 // so one process (the tests) can cover every kernel.
 int gemm_path() {
     const char* e = getenv("MLXHIP_GEMM_PATH");
@@ -239,6 +240,7 @@ int gemm_path() {
     if (!strcmp(e, "lds16_256")) return 3;
     if (!strcmp(e, "lds16_128")) return 4;
     if (!strcmp(e, "x6")) return 5;
+    if (!strcmp(e, "small16")) return 6;
     return 0;
 }
 
@@ -704,6 +706,19 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
                          reinterpret_cast<uintptr_t>(b) % 16 == 0 && lda % ch == 0 &&
                          ldb % ch == 0 && (batch == 1 || (stride_a % ch == 0 && stride_b % ch == 0));
     const int path = gemm_path();
+    // 16-bit products the direct-to-LDS kernel cannot read as they are
+    // (rows that are not whole 16-byte chunks) or that have too few 128 x 128
+    // tiles to fill the chip: one launch of 64 x 64 tiles, no packed copies,
+    // no K split. The odd 1000 x 777 x 1531 bf16 product: pack + split GEMM +
+    // partial sums took ~25 us per call (three launches).
+    if (ab_dtype != MLXHIP_DTYPE_F32 && (path == 6 || path == 0) && !padded &&
+        gemm16_small_fits(m, n, k, batch, lda, ldb, trans_a, trans_b)) {
+        const int64_t big_tiles = ceil_div(m, 256) * ceil_div(n, 256) * batch;
+        const int64_t mid_tiles = ceil_div(m, 128) * ceil_div(n, 128) * batch;
+        if (path == 6 || (big_tiles < 128 && (!aligned || mid_tiles < 16)))
+            return gemm16_small(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb,
+                                stride_b, c, ldc, stride_c, s);
+    }
     if (!aligned && path != 1) {
         // Unaligned operands (odd leading dimension, offset pointer): copy both
         // into zero-padded buffers whose rows are whole 16-byte chunks (K and

@@ -102,9 +102,6 @@ struct Args {
     int64_t ldc, sc;
     uint32_t a_bytes, b_bytes;  // byte extent of one batch slice (descriptor range)
     int tiles_m, tiles_n;
-    // C row segments are stored non-temporally (c_nt != 0) or as plain
-    // write-back stores; set by launch() from the grid (see there).
-    int c_nt = 1;
     // Split-K (splits > 1): gridDim.y = batch * splits; split s of batch b
     // covers k in [s * k_chunk, min(k, (s + 1) * k_chunk)) and writes its
     // f32 partial to c + (b * splits + s) * sc (the kernel is instantiated
@@ -409,7 +406,7 @@ __device__ inline TileId tile_of(const Args& g) {
 
 // Epilogue of the kernels below (C tile of one workgroup, after its last
 // MFMA), through the first bytes of the operand stages' LDS.
-template <int CT, class C, int PIPE_BYTES>
+template <int CT, class C, int PIPE_BYTES, bool NT = true>
 __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN], MLXHIP_LDS char* smem, char* Cp,
                                int64_t m0, int64_t n0, int wave, int lane, const float* bias = nullptr) {
     // Through LDS. acc[i][j][v] = C[m][n] with m = WR wm + 32 i +
@@ -418,7 +415,7 @@ __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN],
     // sub-tile into padded LDS rows (PITCH = row bytes + 16: consecutive rows
     // fall in distinct bank groups for the 8/16-byte writes) and reads it
     // back row by row, so every global store instruction writes whole row
-    // segments instead of 16-byte pieces of 32 rows. With g.c_nt the row
+    // segments instead of 16-byte pieces of 32 rows. With NT the row
     // segments are stored non-temporally (C is written once, so it streams
     // out instead of filling the L2s that later tiles' operands need);
     // otherwise as plain write-back stores.
@@ -488,7 +485,7 @@ __device__ inline void store_c(const Args& g, const f32x16 (&acc)[C::TM][C::TN],
             }
             char* dst = Cp + (m * g.ldc + n) * ES;
             if (vec_ok && n + 16 / ES <= g.n) {
-                if (g.c_nt) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
+                if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
                 else *reinterpret_cast<u32x4*>(dst) = v;
             } else {
                 // Row end or unaligned C: element stores.
@@ -530,7 +527,7 @@ __device__ void x6_direct(const Args& g, const float* A, const float* B, float* 
     }
 }
 
-template <int DT, int CT, int TA, int TB, class C, bool SPREAD, bool X6 = false>
+template <int DT, int CT, int TA, int TB, class C, bool SPREAD, bool X6 = false, bool NTC = true>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::THREADS, C::THREADS),
                           amdgpu_waves_per_eu(C::WPE, C::WPE)))
 void gemm16_kernel(Args g) {
@@ -690,7 +687,7 @@ void gemm16_kernel(Args g) {
         }
     }
 
-    store_c<CT, C, PIPE_BYTES>(g, acc, smem, static_cast<char*>(g.c) + slice * g.sc * (CT == MLXHIP_DTYPE_F32 ? 4 : 2),
+    store_c<CT, C, PIPE_BYTES, NTC>(g, acc, smem, static_cast<char*>(g.c) + slice * g.sc * (CT == MLXHIP_DTYPE_F32 ? 4 : 2),
                                m0, n0, wave, lane);
 }
 
@@ -734,8 +731,16 @@ int launch(const Args& a0, int64_t batch, hipStream_t s) {
     // alternating on one MI355X). Later rounds' operands need the L2s, so a
     // larger grid stores non-temporally (config 3, 512 tiles: 3-4 us faster
     // per call that way).
-    a.c_nt = (int64_t)grid.x * grid.y > 256 ? 1 : 0;
-    hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, C, true, X6>), grid, dim3(C::THREADS), 0, s, a);
+    // (The choice is a template parameter: a run-time flag in the store
+    // loop cost config 3 3-9 us per call.) Split-f32 products keep
+    // non-temporal stores.
+    if constexpr (!X6) {
+        if ((int64_t)grid.x * grid.y <= 256) {
+            hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, C, true, X6, false>), grid, dim3(C::THREADS), 0, s, a);
+            return launch_check("gemm16_kernel");
+        }
+    }
+    hipLaunchKernelGGL((gemm16_kernel<DT, CT, TA, TB, C, true, X6, true>), grid, dim3(C::THREADS), 0, s, a);
     return launch_check("gemm16_kernel");
 }
 

@@ -1,0 +1,380 @@
+// gemm16_small.hip — bf16 / f16 GEMM in one launch for products whose
+// operands the direct-to-LDS kernel cannot read as they are (rows that are
+// not whole 16-byte chunks: odd K or N, offset pointers) or that have too
+// few 128 x 128 tiles to occupy the chip; replaces the pack / split-K /
+// partial-sum sequence there.
+//
+// C_b[M,N] = op(A_b) * op(B_b), f32 accumulation, C in f32 / bf16 / f16
+// (round to nearest even); replaces matmul (crates/mlx-core/src/
+// cpu_kernels.rs:197-230) at these shapes (config 3's 1000 x 777 x 1531).
+//
+// Work decomposition
+//   * One workgroup per 64 x 64 tile of C, gridDim.y = batch: KS groups of 4
+//     waves (2 x 2 waves of 32 x 32, one v_mfma_f32_32x32x16 accumulator
+//     each), group i over the i-th part of K; the groups' partial tiles meet
+//     in LDS and are added in group order. The odd config-3 product makes 208
+//     workgroups of 16 waves (4 per SIMD), so no second kernel.
+//   * K tiles of 64. Each thread moves two 8-element chunks of each operand
+//     per K tile: chunk = 8 consecutive elements along the operand's
+//     contiguous axis. A chunk is read as one 16-byte and one 4-byte buffer
+//     load from the dword boundary at or below its first element and shifted
+//     down by one element when that element sits at an odd position (any
+//     2-byte-aligned operand), then elements past the matrix edge are
+//     zeroed. Dwords past the descriptor's range (the slice) read as zeros.
+//   * Loads run DEPTH K tiles ahead in registers (20 VGPRs per tile), so the
+//     L2 / HBM latency overlaps DEPTH tiles of work per group; LDS is
+//     double-buffered per group with one barrier per K tile.
+//   * LDS holds both operands K-contiguous, [64 rows][64 k], 16-byte chunks
+//     XOR-swizzled per row (lds_at): a K-contiguous chunk is one
+//     ds_write_b128, an MN-contiguous chunk is written transposed as 8
+//     ds_write_b16. Fragments are ds_read_b128 (lane = row l % 32, k-group
+//     l / 32).
+//   * MFMA roles are swapped (src_a = B fragment) as in the 16-bit kernel of
+//     gemm16_impl.hpp: lane l then holds C[m][n .. n+3] for m = l % 32.
+#include "../common.hpp"
+#include "../kernels.hpp"
+
+namespace mlxhip {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+#define SMALL16_LDS __attribute__((address_space(3)))
+
+constexpr int TILE = 64, BK = 64;
+constexpr uint32_t OOB_OFF = 0xFFFFFF00u;      // beyond every descriptor range
+constexpr int BUF_FLAGS = 0x00020000;          // gfx9 buffer descriptor word 3 (32-bit data format)
+
+struct Small16Args {
+    int64_t m, n, k;
+    const void* a;
+    int64_t lda, sa;
+    const void* b;
+    int64_t ldb, sb;
+    void* c;
+    int64_t ldc, sc;
+    int tiles_n;
+};
+
+// One operand of one batch slice: a buffer descriptor from the dword
+// boundary at or below the slice's first element to its last byte, and the
+// element index (from that boundary) of the slice's element 0.
+struct Operand {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int64_t e0;
+    uint32_t nrec;  // descriptor range: the slice's bytes rounded up to whole dwords
+};
+
+__device__ inline Operand make_operand(const void* p, int64_t slice_off, int64_t rows, int64_t cols, int64_t ld) {
+    const uintptr_t addr = reinterpret_cast<uintptr_t>(p) + (uintptr_t)(slice_off * 2);
+    const uintptr_t base = addr & ~uintptr_t(3);
+    const int64_t e0 = (int64_t)((addr - base) >> 1);
+    const int64_t bytes = rows > 0 && cols > 0 ? (e0 + (rows - 1) * ld + cols) * 2 : 0;
+    Operand o;
+    o.nrec = (uint32_t)((bytes + 3) & ~int64_t(3));
+    o.rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)o.nrec, BUF_FLAGS);
+    o.e0 = e0;
+    return o;
+}
+
+// The raw dwords of one chunk: 5 dwords from the dword boundary at or below
+// element e (or zeros for an out-of-range chunk).
+struct Raw {
+    u32x4 lo;
+    uint32_t hi;
+};
+
+// One 16-byte and one 4-byte load (dword-aligned). The descriptor's range
+// check is per dword, so a chunk that ends its slice keeps its in-range
+// dwords and reads zeros past them (established on MI355X by an in-bounds
+// probe); every dword read lies inside the slice's last dword.
+__device__ inline void issue_chunk(const Operand& o, int64_t e, bool in_range, Raw& r) {
+    const uint32_t off = in_range ? (uint32_t)(((o.e0 + e) >> 1) << 2) : OOB_OFF;
+    r.lo = __builtin_amdgcn_raw_buffer_load_b128(o.rsrc, off, 0, 0);
+    r.hi = __builtin_amdgcn_raw_buffer_load_b32(o.rsrc, off + 16, 0, 0);
+}
+
+// The chunk's 8 elements (4 dwords, element 2j in the low half of dword j):
+// shifted down one element when element e is at an odd position, elements
+// valid .. 7 zeroed.
+__device__ inline u32x4 finish_chunk(const Raw& r, int64_t e_abs, int valid) {
+    // Branch-free (a funnel shift by 0 or 16 bits, then masks), so the
+    // loads of later K tiles stay in flight across it.
+    const uint32_t sh = (uint32_t)(e_abs & 1) * 16;
+    const uint32_t w0 = __builtin_amdgcn_alignbit(r.lo.y, r.lo.x, sh);
+    const uint32_t w1 = __builtin_amdgcn_alignbit(r.lo.z, r.lo.y, sh);
+    const uint32_t w2 = __builtin_amdgcn_alignbit(r.lo.w, r.lo.z, sh);
+    const uint32_t w3 = __builtin_amdgcn_alignbit(r.hi, r.lo.w, sh);
+    auto keep = [valid](int j) {
+        return (2 * j + 1 < valid ? 0xFFFF0000u : 0u) | (2 * j < valid ? 0x0000FFFFu : 0u);
+    };
+    return u32x4{w0 & keep(0), w1 & keep(1), w2 & keep(2), w3 & keep(3)};
+}
+
+// LDS position (in elements) of the 8-element chunk c (k = 8c .. 8c+7) of
+// tile row `row`: rows of 64 elements (128 bytes), chunks XOR-swizzled by
+// the row's low three bits (8 consecutive rows, as a fragment read takes
+// them, land in 8 distinct 16-byte bank groups) and by the row's group of 8
+// (8 rows 8 apart, as a transposed chunk writes them, do too).
+__device__ inline int lds_at(int row, int c) { return row * TILE + 8 * (c ^ (row & 7) ^ ((row >> 3) & 7)); }
+
+// Where chunk i (0, 1) of this thread sits in the K tile at k0, for an
+// operand with R rows / columns starting at r0 and K extent K. KC: stored
+// [R][K] (chunk along K); else [K][R] (chunk along the rows / columns).
+template <bool KC>
+struct ChunkPos {
+    int row[2], kk[2];  // tile-local row / column and k of the chunk's first element
+    __device__ inline void init(int tid) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = tid + 256 * i;
+            if constexpr (KC) {
+                row[i] = q >> 3;
+                kk[i] = 8 * (q & 7);
+            } else {
+                kk[i] = q >> 3;
+                row[i] = 8 * (q & 7);
+            }
+        }
+    }
+};
+
+template <bool KC>
+__device__ inline void issue_tile(const Operand& o, const ChunkPos<KC>& cp, int64_t r0, int64_t R, int64_t ld,
+                                  int64_t K, int64_t k0, Raw* raw) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int64_t r = r0 + cp.row[i], k = k0 + cp.kk[i];
+        if constexpr (KC) issue_chunk(o, r * ld + k, r < R && k < K, raw[i]);
+        else issue_chunk(o, k * ld + r, k < K && r < R, raw[i]);
+    }
+}
+
+template <bool KC>
+__device__ inline void store_tile(const Operand& o, const ChunkPos<KC>& cp, int64_t r0, int64_t R, int64_t ld,
+                                  int64_t K, int64_t k0, const Raw* raw, SMALL16_LDS uint16_t* s) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int64_t r = r0 + cp.row[i], k = k0 + cp.kk[i];
+        if constexpr (KC) {
+            const int valid = (int)max<int64_t>(0, min<int64_t>(8, K - k));
+            const u32x4 v = finish_chunk(raw[i], o.e0 + r * ld + k, valid);
+            *(SMALL16_LDS u32x4*)(s + lds_at(cp.row[i], cp.kk[i] >> 3)) = v;
+        } else {
+            const int valid = (int)max<int64_t>(0, min<int64_t>(8, R - r));
+            const u32x4 v = finish_chunk(raw[i], o.e0 + k * ld + r, valid);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                s[lds_at(cp.row[i] + j, cp.kk[i] >> 3) + (cp.kk[i] & 7)] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+        }
+    }
+}
+
+template <int DT>
+__device__ inline void mfma16(const u32x4& a, const u32x4& b, f32x16& acc) {
+    if constexpr (DT == MLXHIP_DTYPE_BF16)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                      acc, 0, 0, 0);
+    else
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
+                                                     acc, 0, 0, 0);
+}
+
+template <int CT>
+__device__ inline void store_elem(void* c, int64_t idx, float v) {
+    if constexpr (CT == MLXHIP_DTYPE_F32) {
+        static_cast<float*>(c)[idx] = v;
+    } else if constexpr (CT == MLXHIP_DTYPE_BF16) {
+        static_cast<__bf16*>(c)[idx] = (__bf16)v;  // round to nearest even
+    } else {
+        static_cast<_Float16*>(c)[idx] = (_Float16)v;
+    }
+}
+
+template <int DT, int CT, bool KCA, bool KCB, int KS, int DEPTH>
+__global__ __attribute__((amdgpu_flat_work_group_size(256 * KS, 256 * KS), amdgpu_waves_per_eu(KS, KS)))
+void gemm16_small_kernel(Small16Args g) {
+    // KS groups of 4 waves, group i over its own contiguous range of K tiles
+    // with its own double-buffered LDS stages; the groups' partial tiles are
+    // added in group order at the end (deterministic).
+    __shared__ __attribute__((aligned(16))) uint16_t smem[KS][2][2][TILE * TILE];  // [group][stage][A, B]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2, lw = wave & 3, ltid = tid & 255;
+    const int wm = lw >> 1, wn = lw & 1;
+    // XCD-aware tile order: the hardware hands consecutive workgroup ids
+    // to the 8 XCDs in turn; give each XCD a contiguous range of (slice,
+    // tile) ids, i.e. whole rows of tiles, so its L2 holds the few A panels
+    // and the B panels its tiles share (the odd config-3 product: 2 tile
+    // rows per XCD, 2.8 MB, instead of all of A and B in every XCD's 4 MB L2).
+    const int64_t nt = (int64_t)gridDim.x * gridDim.y;
+    int64_t lin = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    if ((nt & 7) == 0) lin = (lin & 7) * (nt >> 3) + (lin >> 3);
+    const int64_t batch = lin / gridDim.x;
+    const int64_t tile = lin - batch * gridDim.x;
+    const int64_t m0 = (tile / g.tiles_n) * TILE, n0 = (tile % g.tiles_n) * TILE;
+
+    // A: op(A) is [M][K]; stored [M][K] (KCA) or [K][M]. B: op(B) is [K][N];
+    // stored [N][K] (KCB) or [K][N].
+    const Operand oa = make_operand(g.a, batch * g.sa, KCA ? g.m : g.k, KCA ? g.k : g.m, g.lda);
+    const Operand ob = make_operand(g.b, batch * g.sb, KCB ? g.n : g.k, KCB ? g.k : g.n, g.ldb);
+    ChunkPos<KCA> pa;
+    ChunkPos<KCB> pb;
+    pa.init(ltid);
+    pb.init(ltid);
+
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+
+    // Every group runs the same number of K tiles, a whole number of DEPTH
+    // groups, so the loop body has no conditional steps (tiles past K load
+    // and multiply zeros), the barriers line up across groups, and the
+    // compiler's load-wait counts stay those of the steady state.
+    const int nkt = (int)((g.k + BK - 1) / BK);
+    const int ntg = (((nkt + KS - 1) / KS) + DEPTH - 1) / DEPTH * DEPTH;
+    const int64_t kg = (int64_t)grp * ntg * BK;  // first k of this group
+    Raw ra[DEPTH][2], rb[DEPTH][2];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+        issue_tile<KCA>(oa, pa, m0, g.m, g.lda, g.k, kg + (int64_t)d * BK, ra[d]);
+        issue_tile<KCB>(ob, pb, n0, g.n, g.ldb, g.k, kg + (int64_t)d * BK, rb[d]);
+    }
+    const int fr = lane & 31, fc = lane >> 5;
+    for (int t0 = 0; t0 < ntg; t0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int t = t0 + d;
+            SMALL16_LDS uint16_t* sa = (SMALL16_LDS uint16_t*)smem[grp][t & 1][0];
+            SMALL16_LDS uint16_t* sb = (SMALL16_LDS uint16_t*)smem[grp][t & 1][1];
+            const int64_t k0 = kg + (int64_t)t * BK;
+            store_tile<KCA>(oa, pa, m0, g.m, g.lda, g.k, k0, ra[d], sa);
+            store_tile<KCB>(ob, pb, n0, g.n, g.ldb, g.k, k0, rb[d], sb);
+            __syncthreads();
+            // Tile t + DEPTH into the registers just consumed (zeros past K).
+            issue_tile<KCA>(oa, pa, m0, g.m, g.lda, g.k, k0 + DEPTH * BK, ra[d]);
+            issue_tile<KCB>(ob, pb, n0, g.n, g.ldb, g.k, k0 + DEPTH * BK, rb[d]);
+#pragma unroll
+            for (int s = 0; s < BK / 16; ++s) {
+                const u32x4 af = *(const SMALL16_LDS u32x4*)(sa + lds_at(32 * wm + fr, 2 * s + fc));
+                const u32x4 bf = *(const SMALL16_LDS u32x4*)(sb + lds_at(32 * wn + fr, 2 * s + fc));
+                mfma16<DT>(bf, af, acc);
+            }
+        }
+    }
+
+    if constexpr (KS > 1) {
+        // Groups 1 .. KS-1 hand their partial tiles to group 0 through LDS
+        // (reusing the stages once every group is done with them).
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(&smem[0][0][0][0]);
+        if (grp > 0) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) red[(((grp - 1) * 4 + lw) * 16 + v) * 64 + lane] = acc[v];
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int j = 0; j < KS - 1; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[v] += red[((j * 4 + lw) * 16 + v) * 64 + lane];
+    }
+
+    // lane l: C[m][n + 8q + 4(l/32) + r] = acc[4q + r], m = 32 wm + l % 32.
+    const int64_t m = m0 + 32 * wm + (lane & 31);
+    if (m >= g.m) return;
+    char* cbase = static_cast<char*>(g.c);
+    const int64_t row = batch * g.sc + m * g.ldc;
+    constexpr int ES = CT == MLXHIP_DTYPE_F32 ? 4 : 2;
+    const bool vec = (reinterpret_cast<uintptr_t>(cbase) % (4 * ES)) == 0 && g.ldc % 4 == 0 && g.sc % 4 == 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t n = n0 + 32 * wn + 8 * q + 4 * (lane >> 5);
+        if (vec && n + 3 < g.n) {
+            if constexpr (CT == MLXHIP_DTYPE_F32) {
+                *reinterpret_cast<float4*>(cbase + (row + n) * 4) =
+                    float4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) store_elem<CT>(cbase, row + n + r, acc[4 * q + r]);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (n + r < g.n) store_elem<CT>(cbase, row + n + r, acc[4 * q + r]);
+        }
+    }
+}
+
+// K split over 4 groups of waves when K holds 8 or more K tiles, over 2 from
+// 4 (MLXHIP_SMALL16_KSPLIT = 1, 2 or 4 forces it; tuning).
+int small16_ksplit(int64_t k) {
+    if (const char* e = getenv("MLXHIP_SMALL16_KSPLIT")) {
+        const int v = atoi(e);
+        if (v == 1 || v == 2 || v == 4) return v;
+    }
+    const int64_t nkt = (k + BK - 1) / BK;
+    return nkt >= 8 ? 4 : nkt >= 4 ? 2 : 1;
+}
+
+template <int DT, int CT, bool KCA, bool KCB>
+void launch_ks(const Small16Args& a, dim3 grid, hipStream_t s) {
+    switch (small16_ksplit(a.k)) {
+        case 4: hipLaunchKernelGGL((gemm16_small_kernel<DT, CT, KCA, KCB, 4, 2>), grid, dim3(1024), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((gemm16_small_kernel<DT, CT, KCA, KCB, 2, 3>), grid, dim3(512), 0, s, a); break;
+        default: hipLaunchKernelGGL((gemm16_small_kernel<DT, CT, KCA, KCB, 1, 3>), grid, dim3(256), 0, s, a);
+    }
+}
+
+template <int DT, int CT>
+int launch_small16(int ta, int tb, const Small16Args& a, int64_t batch, hipStream_t s) {
+    const dim3 grid((unsigned)(ceil_div(a.m, TILE) * a.tiles_n), (unsigned)batch);
+    // KCA: A stored [M][K] (not transposed); KCB: B stored [N][K] (transposed).
+    if (!ta && !tb) launch_ks<DT, CT, true, false>(a, grid, s);
+    else if (!ta && tb) launch_ks<DT, CT, true, true>(a, grid, s);
+    else if (ta && !tb) launch_ks<DT, CT, false, false>(a, grid, s);
+    else launch_ks<DT, CT, false, true>(a, grid, s);
+    return launch_check("gemm16_small_kernel");
+}
+
+template <int DT>
+int dispatch_ct(int c_dtype, int ta, int tb, const Small16Args& a, int64_t batch, hipStream_t s) {
+    switch (c_dtype) {
+        case MLXHIP_DTYPE_F32: return launch_small16<DT, MLXHIP_DTYPE_F32>(ta, tb, a, batch, s);
+        case MLXHIP_DTYPE_BF16: return launch_small16<DT, MLXHIP_DTYPE_BF16>(ta, tb, a, batch, s);
+        default: return launch_small16<DT, MLXHIP_DTYPE_F16>(ta, tb, a, batch, s);
+    }
+}
+
+}  // namespace
+
+bool gemm16_small_fits(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t lda, int64_t ldb, int ta,
+                       int tb) {
+    if (m <= 0 || n <= 0 || k <= 0 || batch <= 0 || batch > 65535) return false;
+    if (ceil_div(m, TILE) * ceil_div(n, TILE) > INT32_MAX / 2) return false;
+    // 32-bit buffer offsets: every slice (plus alignment slack and the 20
+    // bytes a chunk reads) well below the out-of-range offset.
+    const int64_t a_ext = ((ta ? k : m) - 1) * lda + (ta ? m : k) + 2;
+    const int64_t b_ext = ((tb ? n : k) - 1) * ldb + (tb ? k : n) + 2;
+    return a_ext * 2 + 64 < (int64_t)OOB_OFF && b_ext * 2 + 64 < (int64_t)OOB_OFF;
+}
+
+int gemm16_small(int ab_dtype, int c_dtype, int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch,
+                 const void* a, int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, void* c,
+                 int64_t ldc, int64_t sc, hipStream_t s) {
+    if (!gemm16_small_fits(m, n, k, batch, lda, ldb, ta, tb))
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm16_small: %lld x %lld x %lld (batch %lld) out of range",
+                    (long long)m, (long long)n, (long long)k, (long long)batch);
+    if (reinterpret_cast<uintptr_t>(a) % 2 || reinterpret_cast<uintptr_t>(b) % 2 ||
+        reinterpret_cast<uintptr_t>(c) % (c_dtype == MLXHIP_DTYPE_F32 ? 4 : 2))
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm16_small: operands must be element-aligned");
+    Small16Args g{m, n, k, a, lda, batch > 1 ? sa : 0, b, ldb, batch > 1 ? sb : 0, c, ldc, batch > 1 ? sc : 0,
+                  (int)ceil_div(n, TILE)};
+    return ab_dtype == MLXHIP_DTYPE_BF16 ? dispatch_ct<MLXHIP_DTYPE_BF16>(c_dtype, ta, tb, g, batch, s)
+                                         : dispatch_ct<MLXHIP_DTYPE_F16>(c_dtype, ta, tb, g, batch, s);
+}
+
+}  // namespace mlxhip

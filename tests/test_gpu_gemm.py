@@ -216,3 +216,41 @@ def test_f32_block_and_split_choices(monkeypatch, m, n, k, ta, tb):
 def test_f32_narrow_products(m, n, k, ta, tb, batch):
     check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), batch=batch, seed=m + n + k + batch,
                rows=sample_rows(m, 6))
+
+
+@pytest.mark.parametrize("ab,cd", [(BF16, BF16), (F16, F16), (BF16, F32)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_small16_kernel_any_alignment(monkeypatch, ab, cd, ta, tb):
+    """The one-launch 64 x 64 kernel (forced for every shape here) on
+    operands that start one element past a 4-byte boundary, with odd leading
+    dimensions and odd batch strides (so rows and slices alternate between
+    even and odd element positions), K not a multiple of its 64-wide K tile
+    and edge tiles in M and N; every element of every slice against float64
+    with the accumulation bound. The last chunk of each slice ends exactly
+    at the descriptor's range."""
+    monkeypatch.setenv("MLXHIP_GEMM_PATH", "small16")
+    m, n, k, batch = 130, 97, 203, 3
+    seed = 60 + 4 * ta + 2 * tb + ab
+    A = synth.normal(seed, (batch, k, m) if ta else (batch, m, k))
+    B = synth.normal(seed + 1, (batch, n, k) if tb else (batch, k, n))
+    Ar, Br = rounded(A, ab), rounded(B, ab)
+    lda, ldb = A.shape[2] + 1, B.shape[2] + 1         # odd leading dimensions
+    sa, sb = A.shape[1] * lda + 1, B.shape[1] * ldb   # odd slice strides
+
+    def packed(x, ld, stride):
+        flat = np.zeros(1 + batch * stride, np.float32)   # element 0: offset by one element
+        for bi in range(batch):
+            for r in range(x.shape[1]):
+                o = 1 + bi * stride + r * ld
+                flat[o:o + x.shape[2]] = x[bi, r]
+        return flat
+
+    da, db = to_dev(packed(A, lda, sa), ab), to_dev(packed(B, ldb, sb), ab)
+    dc = hb.DeviceBuffer(batch * m * n * (4 if cd == F32 else 2))
+    hb.gemm(ab, cd, ta, tb, m, n, k, da.ptr + 2, lda, db.ptr + 2, ldb, dc, n, batch=batch,
+            stride_a=sa, stride_b=sb, stride_c=m * n)
+    C = from_dev(dc, cd, batch * m * n).reshape(batch, m, n)
+    for bi in range(batch):
+        opA = Ar[bi].T if ta else Ar[bi]
+        opB = Br[bi].T if tb else Br[bi]
+        gemm_full_check(C[bi], opA, opB, OUT_NAME[cd], f"small16 ab={ab} c={cd} ta={ta} tb={tb} batch {bi}")
