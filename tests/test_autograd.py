@@ -277,6 +277,34 @@ def test_hip_block_config4_prefix_matches_oracle():
     assert not bad, "; ".join(bad)
 
 
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip", "oracle_lib")
+def test_hip_block_config4_last_sequence_prefix_matches_oracle():
+    """The same check on another part of config 4: the loss weights gy are
+    non-zero only on the first P = 256 positions of the last sequence of the
+    batch (rows 3*512 .. 3*512+255), so the GPU's full-size block must give
+    the gradients the oracle computes on that sequence's prefix alone, and an
+    x gradient that is exactly zero on every other row (sequences 0-2 and the
+    rest of sequence 3). This covers the batch indexing of every kernel
+    (attention rows of another sequence, bias gradients summed over rows that
+    mostly carry zero cotangents)."""
+    cfg = nn.BlockConfig()
+    P, b = 256, cfg.batch - 1
+    arrs, x, gy = block_arrays(cfg, seed=47)
+    r0 = b * cfg.seq
+    gy_masked = np.zeros_like(gy)
+    gy_masked[r0:r0 + P] = gy[r0:r0 + P]
+    print(f"config 4 on the GPU, loss on the first {P} positions of sequence {b}", flush=True)
+    loss_h, gh = block_grads(hip_stream(), cfg, arrs, x, gy_masked)
+    cfg_p = nn.BlockConfig(d_model=cfg.d_model, n_heads=cfg.n_heads, seq=P, batch=1, eps=cfg.eps)
+    print(f"oracle on the {P}-position prefix of sequence {b}", flush=True)
+    loss_o, go = block_grads(OracleStream(), cfg_p, arrs, x[r0:r0 + P], gy[r0:r0 + P])
+    outside = np.ones(x.shape[0], bool)
+    outside[r0:r0 + P] = False
+    assert not gh["x"][outside].any(), "x gradient outside the prefix is not zero"
+    compare_block_grads(dict(gh, x=gh["x"][r0:r0 + P]), go, loss_h, loss_o)
+
+
 def compare_block_grads(gh, go, loss_h, loss_o):
     assert abs(loss_h - loss_o) <= 1e-4 * max(1.0, abs(loss_o)), (loss_h, loss_o)
     top = max(float(np.abs(g).max()) for g in go.values())
