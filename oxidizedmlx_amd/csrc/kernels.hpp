@@ -184,8 +184,9 @@ int gemm16_small(int ab_dtype, int c_dtype, int ta, int tb, int64_t m, int64_t n
                  int64_t ldc, int64_t sc, hipStream_t s);
 
 // gemm_small.hip: f32 products small enough for one or two rounds of 32 x 32
-// tiles with K <= 512, one launch, no workspace, any alignment.
-bool gemm_small_f32_fits(int64_t m, int64_t n, int64_t k, int64_t batch);
+// tiles with K <= 512, one launch, no workspace, any alignment; operand
+// slices under 2 GiB.
+bool gemm_small_f32_fits(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t lda, int64_t ldb, int ta, int tb);
 int gemm_small_f32(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const float* a, int64_t lda,
                    int64_t sa, const float* b, int64_t ldb, int64_t sb, float* c, int64_t ldc, int64_t sc,
                    hipStream_t s);

@@ -697,7 +697,8 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     // a reduction (measured 13.7 us per call for 512^3 that way, kernels
     // and launches included).
     if (ab_dtype == MLXHIP_DTYPE_F32 && c_dtype == MLXHIP_DTYPE_F32 && gemm_path() == 0 &&
-        ceil_div(m, 64) * ceil_div(n, 64) * batch < 256 && gemm_small_f32_fits(m, n, k, batch))
+        ceil_div(m, 64) * ceil_div(n, 64) * batch < 256 &&
+        gemm_small_f32_fits(m, n, k, batch, lda, ldb, trans_a, trans_b))
         return gemm_small_f32(trans_a, trans_b, m, n, k, batch, static_cast<const float*>(a), lda, stride_a,
                               static_cast<const float*>(b), ldb, stride_b, static_cast<float*>(c), ldc, stride_c, s);
 

@@ -101,7 +101,58 @@ def check_gemm(m, n, k, ab, cd, ta=False, tb=False, batch=1, seed=1, rows=None, 
 
 def test_f32_512_cfg1():
     # Config 1: f32 C = A.B, M = N = K = 512, N(0,1); all rows checked.
-    check_gemm(512, 512, 512, F32, F32, rows=np.arange(512), seed=0x5EED0001)
+    check_gemm(512, 512, 512, F32, F32, rows=np.arange(512), seed=0x5EED0001, full=True)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("m,n,k,batch", [
+    (64, 64, 64, 1),      # whole tiles, 8 k per half-wave
+    (96, 64, 128, 2),     # 16
+    (128, 160, 256, 1),   # 32
+    (512, 512, 512, 1),   # 64 (config 1)
+    (33, 47, 1, 1),       # ragged: edge tiles, K below one run
+    (100, 77, 300, 3),    # ragged K inside the last run, batch
+    (31, 65, 129, 1),     # one k past a whole run
+])
+def test_small_f32_kernel_shapes(ta, tb, m, n, k, batch):
+    """The one-launch f32 kernel for small products (32 x 32 tiles, K over 8
+    half-wave runs): whole-tile products take its variant without range
+    selects, the others read zeros past the matrix edge through the buffer
+    descriptor. Every element of every slice against float64 with the
+    accumulation bound, and sampled rows against the oracle."""
+    check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), batch=batch, seed=m + 3 * n + 7 * k + ta + 2 * tb,
+               rows=sample_rows(m, 6), full=True)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_small_f32_kernel_any_alignment(ta, tb):
+    """The small f32 kernel on operands one element past a 16-byte boundary,
+    with odd leading dimensions and odd batch strides (no K-contiguous run is
+    16-byte aligned, so whole tiles take the 4-byte-load variant); each
+    slice's last element ends exactly at its descriptor's range."""
+    m, n, k, batch = 64, 96, 128, 3
+    A = synth.normal(70 + ta, (batch, k, m) if ta else (batch, m, k))
+    B = synth.normal(72 + tb, (batch, n, k) if tb else (batch, k, n))
+    lda, ldb = A.shape[2] + 1, B.shape[2] + 3
+    sa, sb = A.shape[1] * lda + 1, B.shape[1] * ldb + 5
+
+    def packed(x, ld, stride):
+        flat = np.zeros(1 + batch * stride, np.float32)
+        for bi in range(batch):
+            for r in range(x.shape[1]):
+                o = 1 + bi * stride + r * ld
+                flat[o:o + x.shape[2]] = x[bi, r]
+        return flat
+
+    da, db = to_dev(packed(A, lda, sa), F32), to_dev(packed(B, ldb, sb), F32)
+    dc = hb.DeviceBuffer(batch * m * n * 4)
+    hb.gemm(F32, F32, ta, tb, m, n, k, da.ptr + 4, lda, db.ptr + 4, ldb, dc, n, batch=batch,
+            stride_a=sa, stride_b=sb, stride_c=m * n)
+    C = from_dev(dc, F32, batch * m * n).reshape(batch, m, n)
+    for bi in range(batch):
+        opA = A[bi].T if ta else A[bi]
+        opB = B[bi].T if tb else B[bi]
+        gemm_full_check(C[bi], opA, opB, "f32", f"small f32 ta={ta} tb={tb} batch {bi}")
 
 
 @pytest.mark.parametrize("cd", [BF16, F32])
