@@ -86,31 +86,13 @@ struct Raw {
     uint32_t hi;
 };
 
-// One 16-byte and one 4-byte load (dword-aligned). The descriptor's range
-// check is per dword, so a chunk that ends its slice keeps its in-range
-// dwords and reads zeros past them (established on MI355X by an in-bounds
-// probe); every dword read lies inside the slice's last dword.
-__device__ inline void issue_chunk(const Operand& o, int64_t e, bool in_range, Raw& r) {
-    const uint32_t off = in_range ? (uint32_t)(((o.e0 + e) >> 1) << 2) : OOB_OFF;
-    r.lo = __builtin_amdgcn_raw_buffer_load_b128(o.rsrc, off, 0, 0);
-    r.hi = __builtin_amdgcn_raw_buffer_load_b32(o.rsrc, off + 16, 0, 0);
-}
-
-// The chunk's 8 elements (4 dwords, element 2j in the low half of dword j):
-// shifted down one element when element e is at an odd position, elements
-// valid .. 7 zeroed.
-__device__ inline u32x4 finish_chunk(const Raw& r, int64_t e_abs, int valid) {
-    // Branch-free (a funnel shift by 0 or 16 bits, then masks), so the
-    // loads of later K tiles stay in flight across it.
-    const uint32_t sh = (uint32_t)(e_abs & 1) * 16;
-    const uint32_t w0 = __builtin_amdgcn_alignbit(r.lo.y, r.lo.x, sh);
-    const uint32_t w1 = __builtin_amdgcn_alignbit(r.lo.z, r.lo.y, sh);
-    const uint32_t w2 = __builtin_amdgcn_alignbit(r.lo.w, r.lo.z, sh);
-    const uint32_t w3 = __builtin_amdgcn_alignbit(r.hi, r.lo.w, sh);
+// Keep-masks of a chunk's 4 dwords (element 2j in the low half of dword
+// j) when only its first `valid` elements (0 .. 8) are inside the matrix.
+__device__ inline u32x4 chunk_keep(int valid) {
     auto keep = [valid](int j) {
         return (2 * j + 1 < valid ? 0xFFFF0000u : 0u) | (2 * j < valid ? 0x0000FFFFu : 0u);
     };
-    return u32x4{w0 & keep(0), w1 & keep(1), w2 & keep(2), w3 & keep(3)};
+    return u32x4{keep(0), keep(1), keep(2), keep(3)};
 }
 
 // LDS position (in elements) of the 8-element chunk c (k = 8c .. 8c+7) of
@@ -120,58 +102,84 @@ __device__ inline u32x4 finish_chunk(const Raw& r, int64_t e_abs, int valid) {
 // (8 rows 8 apart, as a transposed chunk writes them, do too).
 __device__ inline int lds_at(int row, int c) { return row * TILE + 8 * (c ^ (row & 7) ^ ((row >> 3) & 7)); }
 
-// Where chunk i (0, 1) of this thread sits in the K tile at k0, for an
-// operand with R rows / columns starting at r0 and K extent K. KC: stored
-// [R][K] (chunk along K); else [K][R] (chunk along the rows / columns).
+// One of a thread's two chunks of one operand, for the whole K loop. Chunk i
+// of thread q covers, in every K tile: KC (operand stored [R][K]) row q / 8
+// and k = 8 (q % 8) .. +7 of the tile; otherwise (stored [K][R]) k = q / 8
+// and rows 8 (q % 8) .. +7. Everything that does not change from one K tile
+// to the next is worked out once, in 32-bit arithmetic: the byte offset of
+// the chunk's first dword in tile 0 (the next tile's is a fixed step
+// further: 64 elements along K), the funnel-shift amount (the element's
+// parity, the same in every tile since a tile step is an even number of
+// elements), and whether its rows / columns are inside the matrix.
 template <bool KC>
-struct ChunkPos {
-    int row[2], kk[2];  // tile-local row / column and k of the chunk's first element
-    __device__ inline void init(int tid) {
+struct Chunk {
+    uint32_t off0;  // byte offset of the dword at or below the first element, tile 0
+    uint32_t sh;    // 16 when that element is the upper half of its dword, else 0
+    int k0;         // k of the chunk's first element in tile 0 (group-relative tile index 0)
+    int lrow, lc;   // tile-local row (KC) / first row (MN), and 8-element chunk index along K
+    bool ok;        // KC: its row is inside the matrix; MN: its first row is
+    u32x4 keep;     // MN: masks of the rows past the matrix edge (fixed)
+
+    __device__ inline void init(const Operand& o, int q, int64_t r0, int64_t R, int64_t ld, int64_t kg) {
+        int64_t e;
+        if constexpr (KC) {
+            lrow = q >> 3;
+            lc = q & 7;
+            k0 = (int)(kg + 8 * lc);
+            const int64_t r = r0 + lrow;
+            ok = r < R;
+            e = o.e0 + (ok ? r : 0) * ld + k0;
+            keep = u32x4{~0u, ~0u, ~0u, ~0u};
+        } else {
+            lrow = 8 * (q & 7);
+            lc = (q >> 3) >> 3;
+            k0 = (int)(kg + (q >> 3));
+            const int64_t r = r0 + lrow;
+            ok = r < R;
+            e = o.e0 + (int64_t)k0 * ld + (ok ? r : 0);
+            keep = chunk_keep((int)max<int64_t>(0, min<int64_t>(8, R - r)));
+        }
+        off0 = (uint32_t)((e >> 1) << 2);
+        sh = (uint32_t)(e & 1) * 16;
+    }
+
+    // One 16-byte and one 4-byte load (dword-aligned) of the chunk in K tile
+    // t (group-relative); `step` is the byte distance between two K tiles.
+    // Out-of-range chunks read through an offset past the descriptor's
+    // range: zeros. The descriptor's range check is per dword, so a chunk
+    // that ends its slice keeps its in-range dwords and reads zeros past
+    // them (established on MI355X by an in-bounds probe); every dword read
+    // lies inside the slice's last dword.
+    __device__ inline void issue(const Operand& o, int t, uint32_t step, int K, Raw& r) const {
+        const bool in = ok && k0 + t * BK < K;
+        const uint32_t off = in ? off0 + (uint32_t)t * step : OOB_OFF;
+        r.lo = __builtin_amdgcn_raw_buffer_load_b128(o.rsrc, off, 0, 0);
+        r.hi = __builtin_amdgcn_raw_buffer_load_b32(o.rsrc, off + 16, 0, 0);
+    }
+
+    // The chunk's 8 elements of K tile t, shifted down one element when the
+    // first one is at an odd position and masked past the matrix edge, into
+    // the group's LDS stage. `tail`: K tile t holds the end of K (uniform
+    // across the workgroup), where a K-contiguous chunk can straddle it.
+    __device__ inline void store(const Raw& r, int t, int K, bool tail, SMALL16_LDS uint16_t* s) const {
+        // Branch-free funnel shift by 0 or 16 bits, so the loads of later K
+        // tiles stay in flight across it.
+        u32x4 v{__builtin_amdgcn_alignbit(r.lo.y, r.lo.x, sh), __builtin_amdgcn_alignbit(r.lo.z, r.lo.y, sh),
+                __builtin_amdgcn_alignbit(r.lo.w, r.lo.z, sh), __builtin_amdgcn_alignbit(r.hi, r.lo.w, sh)};
+        if constexpr (KC) {
+            // Elements past K belong to the next row: zero them (only in the
+            // tile holding the end of K; chunks wholly past K read zeros).
+            if (tail) v &= chunk_keep(max(0, min(8, K - (k0 + t * BK))));
+            *(SMALL16_LDS u32x4*)(s + lds_at(lrow, lc)) = v;
+        } else {
+            v &= keep;
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            const int kk = (k0 & 63) & 7;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int q = tid + 256 * i;
-            if constexpr (KC) {
-                row[i] = q >> 3;
-                kk[i] = 8 * (q & 7);
-            } else {
-                kk[i] = q >> 3;
-                row[i] = 8 * (q & 7);
-            }
+            for (int j = 0; j < 8; ++j) s[lds_at(lrow + j, lc) + kk] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
         }
     }
 };
-
-template <bool KC>
-__device__ inline void issue_tile(const Operand& o, const ChunkPos<KC>& cp, int64_t r0, int64_t R, int64_t ld,
-                                  int64_t K, int64_t k0, Raw* raw) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int64_t r = r0 + cp.row[i], k = k0 + cp.kk[i];
-        if constexpr (KC) issue_chunk(o, r * ld + k, r < R && k < K, raw[i]);
-        else issue_chunk(o, k * ld + r, k < K && r < R, raw[i]);
-    }
-}
-
-template <bool KC>
-__device__ inline void store_tile(const Operand& o, const ChunkPos<KC>& cp, int64_t r0, int64_t R, int64_t ld,
-                                  int64_t K, int64_t k0, const Raw* raw, SMALL16_LDS uint16_t* s) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int64_t r = r0 + cp.row[i], k = k0 + cp.kk[i];
-        if constexpr (KC) {
-            const int valid = (int)max<int64_t>(0, min<int64_t>(8, K - k));
-            const u32x4 v = finish_chunk(raw[i], o.e0 + r * ld + k, valid);
-            *(SMALL16_LDS u32x4*)(s + lds_at(cp.row[i], cp.kk[i] >> 3)) = v;
-        } else {
-            const int valid = (int)max<int64_t>(0, min<int64_t>(8, R - r));
-            const u32x4 v = finish_chunk(raw[i], o.e0 + k * ld + r, valid);
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                s[lds_at(cp.row[i] + j, cp.kk[i] >> 3) + (cp.kk[i] & 7)] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
-        }
-    }
-}
 
 template <int DT>
 __device__ inline void mfma16(const u32x4& a, const u32x4& b, f32x16& acc) {
@@ -221,11 +229,6 @@ void gemm16_small_kernel(Small16Args g) {
     // stored [N][K] (KCB) or [K][N].
     const Operand oa = make_operand(g.a, batch * g.sa, KCA ? g.m : g.k, KCA ? g.k : g.m, g.lda);
     const Operand ob = make_operand(g.b, batch * g.sb, KCB ? g.n : g.k, KCB ? g.k : g.n, g.ldb);
-    ChunkPos<KCA> pa;
-    ChunkPos<KCB> pb;
-    pa.init(ltid);
-    pb.init(ltid);
-
     f32x16 acc;
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
@@ -234,15 +237,29 @@ void gemm16_small_kernel(Small16Args g) {
     // groups, so the loop body has no conditional steps (tiles past K load
     // and multiply zeros), the barriers line up across groups, and the
     // compiler's load-wait counts stay those of the steady state.
-    const int nkt = (int)((g.k + BK - 1) / BK);
+    const int K = (int)g.k;
+    const int nkt = (K + BK - 1) / BK;
     const int ntg = (((nkt + KS - 1) / KS) + DEPTH - 1) / DEPTH * DEPTH;
-    const int64_t kg = (int64_t)grp * ntg * BK;  // first k of this group
+    const int kg = grp * ntg * BK;  // first k of this group
+    // Byte distance between consecutive K tiles of a chunk: 64 elements
+    // along K (K-contiguous) or 64 rows of the leading dimension.
+    const uint32_t step_a = KCA ? 2u * BK : (uint32_t)(2 * BK * g.lda);
+    const uint32_t step_b = KCB ? 2u * BK : (uint32_t)(2 * BK * g.ldb);
+    Chunk<KCA> ca[2];
+    Chunk<KCB> cb[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        ca[i].init(oa, ltid + 256 * i, m0, g.m, g.lda, kg);
+        cb[i].init(ob, ltid + 256 * i, n0, g.n, g.ldb, kg);
+    }
     Raw ra[DEPTH][2], rb[DEPTH][2];
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-        issue_tile<KCA>(oa, pa, m0, g.m, g.lda, g.k, kg + (int64_t)d * BK, ra[d]);
-        issue_tile<KCB>(ob, pb, n0, g.n, g.ldb, g.k, kg + (int64_t)d * BK, rb[d]);
-    }
+    for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            ca[i].issue(oa, d, step_a, K, ra[d][i]);
+            cb[i].issue(ob, d, step_b, K, rb[d][i]);
+        }
     const int fr = lane & 31, fc = lane >> 5;
     for (int t0 = 0; t0 < ntg; t0 += DEPTH) {
 #pragma unroll
@@ -250,13 +267,19 @@ void gemm16_small_kernel(Small16Args g) {
             const int t = t0 + d;
             SMALL16_LDS uint16_t* sa = (SMALL16_LDS uint16_t*)smem[grp][t & 1][0];
             SMALL16_LDS uint16_t* sb = (SMALL16_LDS uint16_t*)smem[grp][t & 1][1];
-            const int64_t k0 = kg + (int64_t)t * BK;
-            store_tile<KCA>(oa, pa, m0, g.m, g.lda, g.k, k0, ra[d], sa);
-            store_tile<KCB>(ob, pb, n0, g.n, g.ldb, g.k, k0, rb[d], sb);
+            const bool tail = kg + (t + 1) * BK > K;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                ca[i].store(ra[d][i], t, K, tail, sa);
+                cb[i].store(rb[d][i], t, K, tail, sb);
+            }
             __syncthreads();
             // Tile t + DEPTH into the registers just consumed (zeros past K).
-            issue_tile<KCA>(oa, pa, m0, g.m, g.lda, g.k, k0 + DEPTH * BK, ra[d]);
-            issue_tile<KCB>(ob, pb, n0, g.n, g.ldb, g.k, k0 + DEPTH * BK, rb[d]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                ca[i].issue(oa, t + DEPTH, step_a, K, ra[d][i]);
+                cb[i].issue(ob, t + DEPTH, step_b, K, rb[d][i]);
+            }
 #pragma unroll
             for (int s = 0; s < BK / 16; ++s) {
                 const u32x4 af = *(const SMALL16_LDS u32x4*)(sa + lds_at(32 * wm + fr, 2 * s + fc));
@@ -353,7 +376,7 @@ int dispatch_ct(int c_dtype, int ta, int tb, const Small16Args& a, int64_t batch
 
 bool gemm16_small_fits(int64_t m, int64_t n, int64_t k, int64_t batch, int64_t lda, int64_t ldb, int ta,
                        int tb) {
-    if (m <= 0 || n <= 0 || k <= 0 || batch <= 0 || batch > 65535) return false;
+    if (m <= 0 || n <= 0 || k <= 0 || k > INT32_MAX / 4 || batch <= 0 || batch > 65535) return false;
     if (ceil_div(m, TILE) * ceil_div(n, TILE) > INT32_MAX / 2) return false;
     // 32-bit buffer offsets: every slice (plus alignment slack and the 20
     // bytes a chunk reads) well below the out-of-range offset.
