@@ -112,11 +112,26 @@ __device__ inline void merge_moments(float& n, float& mean, float& m2, float n2,
     n = nn;
 }
 
-template <int WPR>
+// merge_moments for two groups of the same count n: n2 / (n + n2) is then
+// exactly 0.5, so this gives the same values without the division.
+__device__ inline void merge_moments_equal(float& n, float& mean, float& m2, float mean2, float m22) {
+    const float delta = mean2 - mean;
+    mean = mean + delta * 0.5f;
+    m2 = m2 + m22 + delta * delta * (n * 0.5f);
+    n = n + n;
+}
+
+// EQUAL: every lane of the row holds the same number of values (whole rows),
+// so each butterfly step merges equal counts.
+template <int WPR, bool EQUAL = false>
 __device__ inline void row_reduce_moments(float& n, float& mean, float& m2, float* slot, int wave_in_row, int lane) {
 #pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1)
-        merge_moments(n, mean, m2, __shfl_xor(n, o, WAVE), __shfl_xor(mean, o, WAVE), __shfl_xor(m2, o, WAVE));
+    for (int o = WAVE / 2; o > 0; o >>= 1) {
+        if constexpr (EQUAL)
+            merge_moments_equal(n, mean, m2, __shfl_xor(mean, o, WAVE), __shfl_xor(m2, o, WAVE));
+        else
+            merge_moments(n, mean, m2, __shfl_xor(n, o, WAVE), __shfl_xor(mean, o, WAVE), __shfl_xor(m2, o, WAVE));
+    }
     if constexpr (WPR > 1) {
         if (lane == 0) {
             slot[3 * wave_in_row] = n;
@@ -272,7 +287,8 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) ls += v[j * VEC + e];
             }
-        float mean = cnt > 0.0f ? ls / cnt : 0.0f;
+        // Whole rows: cnt is N, a power of two, and ls * (1 / N) is ls / N exactly.
+        float mean = (EVEN && (N & (N - 1)) == 0) ? ls * (1.0f / (float)N) : (cnt > 0.0f ? ls / cnt : 0.0f);
         float q = 0.0f;
 #pragma unroll
         for (int j = 0; j < NV; ++j)
@@ -282,7 +298,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
                     float dv = v[j * VEC + e] - mean;
                     q += dv * dv;
                 }
-        row_reduce_moments<WPR>(cnt, mean, q, slot0, wave_in_row, lane);
+        row_reduce_moments<WPR, EVEN>(cnt, mean, q, slot0, wave_in_row, lane);
         const float var = q / d;
         float sd = sqrtf(var + p), r;
         row_divisor(sd, r);
