@@ -367,7 +367,11 @@ int mlxhip_gemm(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t tran
  * workspace exceeds the array returns MLXHIP_ERR_INVALID_ARGUMENT (C is then
  * unchanged). Every call on one device
  * shares that device's array: calls that overlap on one device (several
- * streams or threads at once) race, so the caller serialises them. */
+ * streams or threads at once) race, so the caller serialises them. A call on
+ * a different stream than the previous call on that device, made while the
+ * previous call's kernels have not finished, returns
+ * MLXHIP_ERR_INVALID_ARGUMENT instead of racing (C unchanged); this check
+ * is skipped for calls made under stream capture. */
 int mlxhip_gemm_noalloc(int32_t ab_dtype, int32_t c_dtype, int32_t trans_a, int32_t trans_b,
                         int64_t m, int64_t n, int64_t k, int64_t batch,
                         const void* a, int64_t lda, int64_t stride_a,

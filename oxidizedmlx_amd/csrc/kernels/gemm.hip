@@ -300,23 +300,36 @@ int take_workspace(FixedScratch* fs, hipStream_t s, int slot, size_t bytes, void
     return MLXHIP_OK;
 }
 
+// Per device: the device address of `scratch` (null until resolved), and
+// the stream of the last call outside graph capture with an event recorded
+// after that call's kernels, so that a call on another stream can tell
+// whether the scratch is still in use. g_scratch_mu is held for a whole
+// call, from that check to the recording of its own event.
+struct ScratchState {
+    void* dev_ptr = nullptr;
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool used = false;
+};
 std::mutex g_scratch_mu;
-void* g_scratch_dev[64];  // device address of `scratch` per device (null until resolved)
+ScratchState g_scratch[64];
 
-// Device address of the current device's fixed scratch, resolved on the
-// first call on that device (with that device current).
-int fixed_scratch(void** out) {
+// The current device's scratch state, resolved on the first call on that
+// device (with that device current): the symbol's device address and the
+// event (no device memory is allocated). Caller holds g_scratch_mu.
+int fixed_scratch_locked(ScratchState** out) {
     int dev = 0;
     MLXHIP_HIP(hipGetDevice(&dev));
     if (dev < 0 || dev >= 64) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm_noalloc: device %d", dev);
-    std::lock_guard<std::mutex> g(g_scratch_mu);
-    if (!g_scratch_dev[dev]) {
+    ScratchState& st = g_scratch[dev];
+    if (!st.dev_ptr) {
         void* p = nullptr;
         MLXHIP_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         if (!p) return fail(MLXHIP_ERR_FFI_FAILED, "gemm_noalloc: scratch has no device address");
-        g_scratch_dev[dev] = p;
+        MLXHIP_HIP(hipEventCreateWithFlags(&st.done, hipEventDisableTiming));
+        st.dev_ptr = p;
     }
-    *out = g_scratch_dev[dev];
+    *out = &st;
     return MLXHIP_OK;
 }
 
@@ -642,11 +655,36 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
 int gemm_noalloc(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
                  int64_t batch, const void* a, int64_t lda, int64_t stride_a, const void* b, int64_t ldb,
                  int64_t stride_b, void* c, int64_t ldc, int64_t stride_c, hipStream_t s) {
-    void* base = nullptr;
-    MLXHIP_TRY(fixed_scratch(&base));
-    FixedScratch fs{static_cast<char*>(base), GEMM_NOALLOC_SCRATCH_BYTES, 0};
-    return gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
-                     ldc, stride_c, s, false, &fs);
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    ScratchState* st = nullptr;
+    MLXHIP_TRY(fixed_scratch_locked(&st));
+    // Overlapping calls share the scratch. A call on another stream than
+    // the last one while the last one's kernels may still run is refused
+    // (work on one stream runs in order, so same-stream calls never
+    // overlap). Under graph capture the order of the replays is not known
+    // here, so nothing is checked or recorded.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    MLXHIP_HIP(hipStreamIsCapturing(s, &cap));
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    if (!capturing && st->used && st->last != s) {
+        const hipError_t q = hipEventQuery(st->done);
+        if (q == hipErrorNotReady)
+            return fail(MLXHIP_ERR_INVALID_ARGUMENT,
+                        "gemm_noalloc: the fixed scratch is still in use by a call on another stream; calls that "
+                        "may overlap on one device must be serialised (C is unchanged)");
+        if (q != hipSuccess) return hip_fail(q, "hipEventQuery");
+    }
+    FixedScratch fs{static_cast<char*>(st->dev_ptr), GEMM_NOALLOC_SCRATCH_BYTES, 0};
+    const int rc = gemm_impl(ab_dtype, c_dtype, trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb,
+                             stride_b, c, ldc, stride_c, s, false, &fs);
+    if (!capturing) {
+        // Recorded whatever rc says: kernels enqueued before a failure
+        // still use the scratch.
+        MLXHIP_HIP(hipEventRecord(st->done, s));
+        st->last = s;
+        st->used = true;
+    }
+    return rc;
 }
 
 namespace {

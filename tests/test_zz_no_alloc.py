@@ -95,3 +95,45 @@ def test_noalloc_f32_planes_beyond_scratch_take_the_direct_kernel():
     bound = (k * np.finfo(np.float32).eps) * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64))
     err = np.abs(got - ref)
     assert np.all(err <= bound + 1e-30), float((err / np.maximum(bound, 1e-30)).max())
+
+
+def test_noalloc_refuses_another_stream_while_the_scratch_is_busy():
+    """A noalloc call on a second stream while the first stream's noalloc
+    kernels are still queued is refused (InvalidArgument, C untouched)
+    instead of sharing the scratch; once the first stream has drained, the
+    same call runs and matches mlxhip_gemm. Every buffer is made before the
+    work is queued: a blocking copy on the null stream would wait for
+    stream 1 to drain."""
+    s1, s2 = hb.create_stream(), hb.create_stream()
+    try:
+        n = 4096
+        busy = [hb.DeviceBuffer.from_array(synth.bf16_bits(synth.normal(93 + i, (n, n)))) for i in range(2)]
+        busy_c = hb.DeviceBuffer(n * n * 2)
+        m, k, nn = 512, 1024, 512
+        da, db = _dev(synth.normal(91, (m, k)), F32), _dev(synth.normal(92, (k, nn)), F32)
+        c1 = hb.DeviceBuffer(m * nn * 4)
+        sentinel = np.full(m * nn, 7.0, np.float32)
+        c2 = hb.DeviceBuffer.from_array(sentinel)
+        ref = hb.DeviceBuffer(m * nn * 4)
+        hb.synchronize()
+        # ~3 ms of 4096^3 bf16 products ahead of stream 1's noalloc call.
+        for _ in range(24):
+            hb.gemm(BF16, BF16, False, False, n, n, n, busy[0], n, busy[1], n, busy_c, n, stream=s1)
+        hb.gemm_noalloc(F32, F32, False, False, m, nn, k, da, k, db, nn, c1, nn, stream=s1)
+        print("noalloc: second stream while the first is busy", flush=True)
+        with pytest.raises(abi.InvalidArgument, match="still in use"):
+            hb.gemm_noalloc(F32, F32, False, False, m, nn, k, da, k, db, nn, c2, nn, stream=s2)
+        hb.synchronize(s1)
+        np.testing.assert_array_equal(c2.download(np.float32, m * nn), sentinel)
+        hb.gemm_noalloc(F32, F32, False, False, m, nn, k, da, k, db, nn, c2, nn, stream=s2)
+        hb.synchronize(s2)
+        hb.gemm(F32, F32, False, False, m, nn, k, da, k, db, nn, ref, nn)
+        hb.synchronize()
+        got = c2.download(np.uint32, m * nn)
+        assert np.array_equal(got, ref.download(np.uint32, m * nn))
+        assert np.array_equal(got, c1.download(np.uint32, m * nn))
+    finally:
+        hb.synchronize(s1)
+        hb.synchronize(s2)
+        hb.destroy_stream(s1)
+        hb.destroy_stream(s2)
