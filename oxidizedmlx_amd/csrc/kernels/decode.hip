@@ -63,10 +63,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int WAVE = 64;
 constexpr int KSTEP = 32;                 // k per MFMA
 constexpr int NSTEP = 6;                  // MFMA steps per pass (W and X fragments of a pass held in registers)
-constexpr int KPASS = NSTEP * KSTEP;      // k per wave per pass
 constexpr int TILE_N = 16;                // output features per wave tile
 constexpr int MAX_WAVES = 16;
 constexpr int XN = 4;                     // X units (8 k of 3 planes) per thread per round
+// The LM head's shape: one k-slice per wave over the whole K in one pass (up
+// to WIDE_NSTEP steps), up to WIDE_WAVES row tiles per workgroup, fewer X
+// units per thread (more threads per unit of X).
+constexpr int WIDE_NSTEP = 24;
+constexpr int WIDE_XN = 2;
+constexpr int WIDE_WAVES = 8;
 constexpr int XPAD = 8;                   // bf16 padding of each LDS plane row (spreads rows over the banks)
 constexpr int XROWS = 3 * DEC_MAX_BATCH;  // hi, mid, lo rows of the batch
 constexpr int WSS_FLOATS = 2 * DEC_MAX_BATCH;  // rms, 1/rms
@@ -102,6 +107,18 @@ __device__ inline void store_embedding_unit(const uint4 e, float* x, uint16_t* x
     *reinterpret_cast<uint4*>(xs + (int64_t)b * ld + k) = e;
     *reinterpret_cast<uint4*>(xs + (int64_t)(DEC_MAX_BATCH + b) * ld + k) = make_uint4(0u, 0u, 0u, 0u);
     *reinterpret_cast<uint4*>(xs + (int64_t)(2 * DEC_MAX_BATCH + b) * ld + k) = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Maximum over the lanes of a wave that share lane % 8 (one sequence each).
+__device__ inline uint64_t wave_max_u64_by8(uint64_t v) {
+#pragma unroll
+    for (int o = 8; o < WAVE; o <<= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)v, o, WAVE);
+        const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, WAVE);
+        const uint64_t w = ((uint64_t)hi << 32) | lo;
+        v = w > v ? w : v;
+    }
+    return v;
 }
 
 __device__ inline uint64_t wave_max_u64(uint64_t v) {
@@ -148,8 +165,13 @@ __device__ inline uint32_t order_key(float f) {
 //
 // ARGMAX (the LM head) publishes each workgroup's per-sequence maximum key
 // for decode_finish.
-template <int EPI, bool NORM>
-__global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks, int r_tiles, int kw) {
+//
+// NS, XNT: MFMA steps per pass and X units per thread per round (the LM
+// head's wide shape holds a whole K of 768 in registers: 8 waves at most).
+template <int EPI, bool NORM, int NS = NSTEP, int XNT = XN>
+__global__ __launch_bounds__((NS > NSTEP ? WIDE_WAVES : MAX_WAVES) * WAVE) void gemv_kernel(DecGemv p, int ks,
+                                                                                            int r_tiles, int kw) {
+    constexpr int KP = NS * KSTEP;  // k per wave per pass
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int K = p.k, N = p.n, B = p.batch;
     constexpr int TB = TILE_N * DEC_MAX_BATCH;  // outputs of one row tile
@@ -157,7 +179,7 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                                    // [24][pitch]
     float* red = reinterpret_cast<float*>(smem + (size_t)XROWS * pitch * 2);            // [r_tiles * ks][TB]
     float* wss = red + r_tiles * ks * TB;                                                // [2][8]: rms, 1/rms
-    uint64_t* keys = reinterpret_cast<uint64_t*>(wss + WSS_FLOATS);                     // ARGMAX: [r_tiles * TB]
+    uint64_t* keys = reinterpret_cast<uint64_t*>(wss + WSS_FLOATS);                     // ARGMAX: [nwaves][8] of [r_tiles * TB]
     float* psum = reinterpret_cast<float*>(keys + (EPI == DEC_EPI_ARGMAX ? r_tiles * TB : 0));  // NORM: [8][K/8]
 
     const int tid = threadIdx.x, nthr = blockDim.x;
@@ -174,10 +196,10 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     // ── loads issued up front ───────────────────────────────────────────────
     // X unit u (u < B*K/8): sequence u / (K/8), k = 8 * (u % (K/8)), three planes.
     const int k8 = K / 8, nunits = B * k8;
-    u32x4 xu[XN][3];
+    u32x4 xu[XNT][3];
     auto load_units = [&](int u0) {
 #pragma unroll
-        for (int i = 0; i < XN; ++i) {
+        for (int i = 0; i < XNT; ++i) {
             const int u = u0 + tid + i * nthr;
             if (u < nunits) {
                 const int b = u / k8, k = 8 * (u - b * k8);
@@ -193,11 +215,11 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     // fragments of one 32-k step are 1 KB of consecutive memory.
     const int col = lane & 15, kg = lane >> 4;
     const uint16_t* wp = p.w + ((int64_t)(n0 / TILE_N) * (K / KSTEP) * WAVE + lane) * 8;
-    u32x4 a[NSTEP];
+    u32x4 a[NS];
     auto load_pass = [&](int k0) {
-        const int steps = active ? min(NSTEP, (ke - k0) / KSTEP) : 0;
+        const int steps = active ? min(NS, (ke - k0) / KSTEP) : 0;
 #pragma unroll
-        for (int s = 0; s < NSTEP; ++s)
+        for (int s = 0; s < NS; ++s)
             if (s < steps) a[s] = *reinterpret_cast<const u32x4*>(wp + (int64_t)(k0 / KSTEP + s) * WAVE * 8);
     };
     load_pass(kb);
@@ -220,7 +242,7 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     // ── X planes into LDS (and the squares of X) ───────────────────────────
     auto store_units = [&](int u0) {
 #pragma unroll
-        for (int i = 0; i < XN; ++i) {
+        for (int i = 0; i < XNT; ++i) {
             const int u = u0 + tid + i * nthr;
             if (u < nunits) {
                 const int b = u / k8, c = u - b * k8;
@@ -244,8 +266,8 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
         }
     };
     store_units(0);
-    // Rows wider than XN * nthr units (not met at decode sizes) take more rounds.
-    for (int u0 = XN * nthr; u0 < nunits; u0 += XN * nthr) {
+    // Rows wider than XNT * nthr units (not met at decode sizes) take more rounds.
+    for (int u0 = XNT * nthr; u0 < nunits; u0 += XNT * nthr) {
         load_units(u0);
         store_units(u0);
     }
@@ -273,11 +295,11 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     const bool zero1 = col >= 8;
     f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
-    for (int k0 = kb; k0 < ke; k0 += KPASS) {
+    for (int k0 = kb; k0 < ke; k0 += KP) {
         if (k0 != kb) load_pass(k0);
-        const int steps = active ? min(NSTEP, (ke - k0) / KSTEP) : 0;
+        const int steps = active ? min(NS, (ke - k0) / KSTEP) : 0;
 #pragma unroll
-        for (int s = 0; s < NSTEP; ++s) {
+        for (int s = 0; s < NS; ++s) {
             if (s < steps) {
                 const int ko = k0 + s * KSTEP;
                 const u32x4 b0 = *reinterpret_cast<const u32x4*>(x0 + ko);
@@ -304,6 +326,9 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
     __syncthreads();
 
     // ── epilogue: sum the k-slices in order, 1/rms, bias, then the op ──────
+    // ARGMAX: the thread's items all belong to sequence tid % 8 (item i is
+    // sequence i % 8, and nthr is a multiple of 8); kmax is their largest key.
+    uint64_t kmax = 0;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int i = tid + e * nthr;
@@ -344,14 +369,20 @@ __global__ __launch_bounds__(MAX_WAVES* WAVE) void gemv_kernel(DecGemv p, int ks
             }
         } else {  // DEC_EPI_ARGMAX
             if (valid && p.out) p.out[(int64_t)b * p.ldo + (int64_t)t * N + n] = v;
-            keys[i] = valid ? ((uint64_t)order_key(v) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)n) : 0ull;
+            const uint64_t key = valid ? ((uint64_t)order_key(v) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)n) : 0ull;
+            kmax = key > kmax ? key : kmax;
         }
     }
     if constexpr (EPI == DEC_EPI_ARGMAX) {
+        // Per sequence: across the wave's lanes of that sequence, then across
+        // the waves (keys[w * 8 + b]); the maximum of the keys does not
+        // depend on the order it is taken in.
+        kmax = wave_max_u64_by8(kmax);
+        if (lane < DEC_MAX_BATCH) keys[wave * DEC_MAX_BATCH + lane] = kmax;
         __syncthreads();
         if (tid < DEC_MAX_BATCH) {
             uint64_t m = 0;
-            for (int i = tid; i < nitems; i += DEC_MAX_BATCH) m = keys[i] > m ? keys[i] : m;
+            for (int w = 0; w < nwaves; ++w) m = keys[w * DEC_MAX_BATCH + tid] > m ? keys[w * DEC_MAX_BATCH + tid] : m;
             p.part[(int64_t)blockIdx.x * DEC_MAX_BATCH + tid] = m;
         }
     }
@@ -588,11 +619,14 @@ __global__ void decode_set_kernel(int* __restrict__ p, int v) { *p = v; }
 
 // Launch shape: a problem with fewer than 512 row tiles gives each
 // workgroup one row tile and splits K into slices of ~64 (up to 16 waves),
-// so its W and X loads spread over many waves; a wide problem (the LM head)
-// uses slices of up to KPASS and up to 16/KS row tiles per workgroup while
-// that still leaves >= 256 workgroups (the row tiles of a workgroup share
-// their X fragments in the L1 cache). MLXHIP_DEC_WIDE="ks,r" overrides the
-// wide shape (tuning).
+// so its W and X loads spread over many waves. The LM head (ARGMAX with 512
+// or more row tiles) gives each wave a whole row tile over all of K in one
+// pass and each workgroup up to 8 row tiles, keeping at least 256
+// workgroups when that leaves a whole one-round grid: with the 1024-thread
+// shape it had before (4 k-slices x 4 row tiles, 500 workgroups for a
+// 32000-word vocabulary) its registers allowed one workgroup per CU, so the
+// launch ran in two rounds. MLXHIP_DEC_WIDE="ks,r" overrides the wide shape
+// (tuning; ks > 1 or r * ks > 8 takes the 1024-thread kernel).
 //
 // K is not split across workgroups: adding partial sums of several
 // workgroups takes a device-scope fence per workgroup (an L2 write-back and
@@ -600,20 +634,22 @@ __global__ void decode_set_kernel(int* __restrict__ p, int v) { *p = v; }
 // workgroups of a decode step, where a whole GEMV takes 5-12 us.
 struct GemvShape {
     int ks, r, kw, grid;
+    bool wide;  // the WIDE_NSTEP kernel
 };
 
-GemvShape gemv_shape(int n, int k) {
-    GemvShape g{1, 1, 0, 0};
+GemvShape gemv_shape(int n, int k, bool argmax) {
+    GemvShape g{1, 1, 0, 0, false};
     const int ntiles = (int)ceil_div(n, TILE_N);
-    if (ntiles >= 512) {
-        g.ks = std::min(MAX_WAVES, (int)ceil_div(k, KPASS));
-        while ((g.r * 2) * g.ks <= MAX_WAVES && ceil_div(ntiles, g.r * 2) >= 256) g.r *= 2;
+    if (argmax && ntiles >= 512) {
+        g.ks = 1;
+        g.r = WIDE_WAVES;
         static const char* env = std::getenv("MLXHIP_DEC_WIDE");
         int eks = 0, er = 0;
         if (env && std::sscanf(env, "%d,%d", &eks, &er) == 2 && eks >= 1 && er >= 1 && eks * er <= MAX_WAVES) {
             g.ks = eks;
             g.r = er;
         }
+        g.wide = g.ks == 1 && g.r <= WIDE_WAVES;
     } else {
         g.ks = std::max(1, std::min(MAX_WAVES, (int)ceil_div(k, 64)));
     }
@@ -624,7 +660,7 @@ GemvShape gemv_shape(int n, int k) {
 
 template <int EPI, bool NORM>
 int launch_gemv(const DecGemv& p, hipStream_t s) {
-    const GemvShape g = gemv_shape(p.n, p.k);
+    const GemvShape g = gemv_shape(p.n, p.k, EPI == DEC_EPI_ARGMAX);
     const size_t lds = dec_gemv_lds_bytes(p.k, g.ks, g.r, EPI == DEC_EPI_ARGMAX, NORM);
     if (lds > DEC_LDS_LIMIT)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: K = %d needs %zu bytes of LDS (limit %d)", p.k,
@@ -632,13 +668,20 @@ int launch_gemv(const DecGemv& p, hipStream_t s) {
     if (EPI == DEC_EPI_ARGMAX && g.grid > p.part_capacity)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: %d workgroups exceed the partial-max buffer (%d)",
                     g.grid, p.part_capacity);
+    if constexpr (EPI == DEC_EPI_ARGMAX) {
+        if (g.wide) {
+            hipLaunchKernelGGL((gemv_kernel<EPI, NORM, WIDE_NSTEP, WIDE_XN>), dim3(g.grid), dim3(g.r * WAVE), lds, s,
+                               p, g.ks, g.r, g.kw);
+            return launch_check("decode gemv_kernel (wide)");
+        }
+    }
     hipLaunchKernelGGL((gemv_kernel<EPI, NORM>), dim3(g.grid), dim3(g.r * g.ks * WAVE), lds, s, p, g.ks, g.r, g.kw);
     return launch_check("decode gemv_kernel");
 }
 
-template <int EPI, bool NORM>
+template <int EPI, bool NORM, int NS = NSTEP, int XNT = XN>
 int set_lds_attr() {
-    MLXHIP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<EPI, NORM>),
+    MLXHIP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<EPI, NORM, NS, XNT>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, DEC_LDS_LIMIT));
     return MLXHIP_OK;
 }
@@ -654,7 +697,7 @@ size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax, bool norm) {
     return b;
 }
 
-int dec_gemv_groups(int n, int k) { return gemv_shape(n, k).grid; }
+int dec_gemv_groups(int n, int k) { return gemv_shape(n, k, true).grid; }
 
 size_t dec_tiled_index(int64_t n, int64_t k, int64_t K) {
     const int64_t tile = n / TILE_N, step = k / KSTEP;
@@ -667,6 +710,7 @@ int dec_prepare() {
     MLXHIP_TRY((set_lds_attr<DEC_EPI_RESID, false>()));
     MLXHIP_TRY((set_lds_attr<DEC_EPI_SILU, true>()));
     MLXHIP_TRY((set_lds_attr<DEC_EPI_ARGMAX, true>()));
+    MLXHIP_TRY((set_lds_attr<DEC_EPI_ARGMAX, true, WIDE_NSTEP, WIDE_XN>()));
     return MLXHIP_OK;
 }
 
