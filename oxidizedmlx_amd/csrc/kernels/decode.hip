@@ -166,11 +166,21 @@ __device__ inline uint32_t order_key(float f) {
 // ARGMAX (the LM head) publishes each workgroup's per-sequence maximum key
 // for decode_finish.
 //
+// groups > 1 splits the batch: the workgroups of one row-tile set each take
+// ceil(B/groups) consecutive sequences, staging only their planes (the other
+// LDS rows hold whatever was there; an MFMA output column depends only on its
+// own B column, and those columns are never stored). A launch with few row
+// tiles (N = 768: 48 workgroups) then spreads its X traffic, which at
+// K = 3072 is larger than its W, over 4x the CUs. When the row-tile sets are a
+// multiple of 8, the groups of one set share an XCD (workgroup i runs on XCD
+// i % 8), so its W comes from HBM once per set and from that L2 after.
+//
 // NS, XNT: MFMA steps per pass and X units per thread per round (the LM
 // head's wide shape holds a whole K of 768 in registers: 8 waves at most).
 template <int EPI, bool NORM, int NS = NSTEP, int XNT = XN>
 __global__ __launch_bounds__((NS > NSTEP ? WIDE_WAVES : MAX_WAVES) * WAVE) void gemv_kernel(DecGemv p, int ks,
-                                                                                            int r_tiles, int kw) {
+                                                                                            int r_tiles, int kw,
+                                                                                            int groups) {
     constexpr int KP = NS * KSTEP;  // k per wave per pass
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int K = p.k, N = p.n, B = p.batch;
@@ -186,7 +196,21 @@ __global__ __launch_bounds__((NS > NSTEP ? WIDE_WAVES : MAX_WAVES) * WAVE) void 
     const int wave = tid / WAVE, lane = tid % WAVE;
     const int nwaves = nthr / WAVE;
     const int ksl = wave % ks, rl = wave / ks;
-    const int tile0 = blockIdx.x * r_tiles;
+    int tset = blockIdx.x, grp = 0;
+    if (groups > 1) {
+        const int nsets = gridDim.x / groups;
+        if (nsets % 8 == 0) {
+            const int j = blockIdx.x / 8;
+            tset = (j / groups) * 8 + blockIdx.x % 8;
+            grp = j % groups;
+        } else {
+            tset = blockIdx.x / groups;
+            grp = blockIdx.x % groups;
+        }
+    }
+    const int bg = (B + groups - 1) / groups;
+    const int b0 = min(B, grp * bg), b1 = min(B, b0 + bg), nb = b1 - b0;  // this workgroup's sequences
+    const int tile0 = tset * r_tiles;
     const int n0 = (tile0 + rl) * TILE_N;
     const int kb = ksl * kw;
     const int ke = min(K, kb + kw);
@@ -194,18 +218,19 @@ __global__ __launch_bounds__((NS > NSTEP ? WIDE_WAVES : MAX_WAVES) * WAVE) void 
     const int nitems = r_tiles * TB;
 
     // ── loads issued up front ───────────────────────────────────────────────
-    // X unit u (u < B*K/8): sequence u / (K/8), k = 8 * (u % (K/8)), three planes.
-    const int k8 = K / 8, nunits = B * k8;
+    // X unit u (u < nb*K/8): sequence b0 + u / (K/8), k = 8 * (u % (K/8)), three planes.
+    const int k8 = K / 8, nunits = nb * k8;
     u32x4 xu[XNT][3];
     auto load_units = [&](int u0) {
 #pragma unroll
         for (int i = 0; i < XNT; ++i) {
             const int u = u0 + tid + i * nthr;
             if (u < nunits) {
-                const int b = u / k8, k = 8 * (u - b * k8);
+                const int bl = u / k8, k = 8 * (u - bl * k8);
 #pragma unroll
                 for (int q = 0; q < 3; ++q)
-                    xu[i][q] = *reinterpret_cast<const u32x4*>(p.xs + (int64_t)(q * DEC_MAX_BATCH + b) * p.ldxs + k);
+                    xu[i][q] =
+                        *reinterpret_cast<const u32x4*>(p.xs + (int64_t)(q * DEC_MAX_BATCH + b0 + bl) * p.ldxs + k);
             }
         }
     };
@@ -232,7 +257,7 @@ __global__ __launch_bounds__((NS > NSTEP ? WIDE_WAVES : MAX_WAVES) * WAVE) void 
         if (i < nitems) {
             const int rr = i / TB, row = (i % TB) / DEC_MAX_BATCH, b = i % DEC_MAX_BATCH;
             const int n = (tile0 + rr) * TILE_N + row;
-            if (n < N && b < B) {
+            if (n < N && b >= b0 && b < b1) {
                 if (p.bias) pre_bias[e] = bf16_f32(p.bias[n]);
                 if constexpr (EPI == DEC_EPI_RESID) pre_res[e] = p.out[(int64_t)b * p.ldo + n];
             }
@@ -245,10 +270,10 @@ __global__ __launch_bounds__((NS > NSTEP ? WIDE_WAVES : MAX_WAVES) * WAVE) void 
         for (int i = 0; i < XNT; ++i) {
             const int u = u0 + tid + i * nthr;
             if (u < nunits) {
-                const int b = u / k8, c = u - b * k8;
+                const int bl = u / k8, c = u - bl * k8;
 #pragma unroll
                 for (int q = 0; q < 3; ++q)
-                    *reinterpret_cast<u32x4*>(xl + (q * DEC_MAX_BATCH + b) * pitch + 8 * c) = xu[i][q];
+                    *reinterpret_cast<u32x4*>(xl + (q * DEC_MAX_BATCH + b0 + bl) * pitch + 8 * c) = xu[i][q];
                 if constexpr (NORM) {
                     // rms_norm, cpu_kernels.rs:647-669: sqrt(sum(x*x)/d + eps), y = x / rms.
                     float ss = 0.0f;
@@ -273,15 +298,15 @@ __global__ __launch_bounds__((NS > NSTEP ? WIDE_WAVES : MAX_WAVES) * WAVE) void 
     }
     __syncthreads();
     if constexpr (NORM) {
-        for (int b = wave; b < B; b += nwaves) {
+        for (int bl = wave; bl < nb; bl += nwaves) {
             float ss = 0.0f;
-            for (int c = lane; c < k8; c += WAVE) ss += psum[b * k8 + c];
+            for (int c = lane; c < k8; c += WAVE) ss += psum[bl * k8 + c];
             ss = wave_sum(ss);
             if (lane == 0) {
                 float rms = sqrtf(ss / (float)K + p.eps), r;
                 shared_divisor(rms, r);
-                wss[b] = rms;
-                wss[DEC_MAX_BATCH + b] = r;
+                wss[b0 + bl] = rms;
+                wss[DEC_MAX_BATCH + b0 + bl] = r;
             }
         }
     }
@@ -338,9 +363,9 @@ __global__ __launch_bounds__((NS > NSTEP ? WIDE_WAVES : MAX_WAVES) * WAVE) void 
         const int n = (tile0 + rr) * TILE_N + row;
         float v = red[(rr * ks) * TB + ei];
         for (int s = 1; s < ks; ++s) v += red[(rr * ks + s) * TB + ei];
-        const bool valid = n < N && b < B;
+        const bool valid = n < N && b >= b0 && b < b1;
         if constexpr (NORM) {
-            if (b < B) v = div_by(v, wss[b], wss[DEC_MAX_BATCH + b]);
+            if (valid) v = div_by(v, wss[b], wss[DEC_MAX_BATCH + b]);
         }
         if (p.bias) v = v + pre_bias[e];
         if constexpr (EPI == DEC_EPI_SILU) {
@@ -634,11 +659,16 @@ __global__ void decode_set_kernel(int* __restrict__ p, int v) { *p = v; }
 // workgroups of a decode step, where a whole GEMV takes 5-12 us.
 struct GemvShape {
     int ks, r, kw, grid;
-    bool wide;  // the WIDE_NSTEP kernel
+    bool wide;   // the WIDE_NSTEP kernel
+    int groups;  // batch groups (workgroups per row-tile set)
 };
 
-GemvShape gemv_shape(int n, int k, bool argmax) {
-    GemvShape g{1, 1, 0, 0, false};
+// MI355X's CU count: the batch is split while the launch still fits one
+// workgroup per CU (a shape choice only; results do not depend on it).
+constexpr int DEC_CUS = 256;
+
+GemvShape gemv_shape(int n, int k, bool argmax, int batch) {
+    GemvShape g{1, 1, 0, 0, false, 1};
     const int ntiles = (int)ceil_div(n, TILE_N);
     if (argmax && ntiles >= 512) {
         g.ks = 1;
@@ -654,13 +684,26 @@ GemvShape gemv_shape(int n, int k, bool argmax) {
         g.ks = std::max(1, std::min(MAX_WAVES, (int)ceil_div(k, 64)));
     }
     g.kw = (int)ceil_div(ceil_div(k, g.ks), KSTEP) * KSTEP;
-    g.grid = (int)ceil_div(ntiles, g.r);
+    const int sets = (int)ceil_div(ntiles, g.r);
+    if (!argmax) {
+        static const char* genv = std::getenv("MLXHIP_DEC_GROUPS");
+        const int want = genv ? std::atoi(genv) : 0;
+        if (want >= 1) {
+            g.groups = want;
+        } else {
+            while (g.groups * 2 <= DEC_MAX_BATCH && sets * g.groups * 2 <= DEC_CUS) g.groups *= 2;
+        }
+        // No empty group: groups = ceil(batch / ceil(batch / groups)).
+        g.groups = std::max(1, std::min(g.groups, batch));
+        g.groups = (int)ceil_div(batch, ceil_div(batch, g.groups));
+    }
+    g.grid = sets * g.groups;
     return g;
 }
 
 template <int EPI, bool NORM>
 int launch_gemv(const DecGemv& p, hipStream_t s) {
-    const GemvShape g = gemv_shape(p.n, p.k, EPI == DEC_EPI_ARGMAX);
+    const GemvShape g = gemv_shape(p.n, p.k, EPI == DEC_EPI_ARGMAX, p.batch);
     const size_t lds = dec_gemv_lds_bytes(p.k, g.ks, g.r, EPI == DEC_EPI_ARGMAX, NORM);
     if (lds > DEC_LDS_LIMIT)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "decode gemv: K = %d needs %zu bytes of LDS (limit %d)", p.k,
@@ -671,11 +714,12 @@ int launch_gemv(const DecGemv& p, hipStream_t s) {
     if constexpr (EPI == DEC_EPI_ARGMAX) {
         if (g.wide) {
             hipLaunchKernelGGL((gemv_kernel<EPI, NORM, WIDE_NSTEP, WIDE_XN>), dim3(g.grid), dim3(g.r * WAVE), lds, s,
-                               p, g.ks, g.r, g.kw);
+                               p, g.ks, g.r, g.kw, g.groups);
             return launch_check("decode gemv_kernel (wide)");
         }
     }
-    hipLaunchKernelGGL((gemv_kernel<EPI, NORM>), dim3(g.grid), dim3(g.r * g.ks * WAVE), lds, s, p, g.ks, g.r, g.kw);
+    hipLaunchKernelGGL((gemv_kernel<EPI, NORM>), dim3(g.grid), dim3(g.r * g.ks * WAVE), lds, s, p, g.ks, g.r, g.kw,
+                       g.groups);
     return launch_check("decode gemv_kernel");
 }
 
@@ -697,7 +741,7 @@ size_t dec_gemv_lds_bytes(int k, int ks, int r, bool argmax, bool norm) {
     return b;
 }
 
-int dec_gemv_groups(int n, int k) { return gemv_shape(n, k, true).grid; }
+int dec_gemv_groups(int n, int k) { return gemv_shape(n, k, true, DEC_MAX_BATCH).grid; }
 
 size_t dec_tiled_index(int64_t n, int64_t k, int64_t K) {
     const int64_t tile = n / TILE_N, step = k / KSTEP;
