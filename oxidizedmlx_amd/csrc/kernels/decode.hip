@@ -510,6 +510,13 @@ __global__ __launch_bounds__(FIN_BLOCK) void decode_finish_kernel(
 constexpr int ATT_BLOCK = 256;
 constexpr int ATT_WAVES = ATT_BLOCK / WAVE;
 
+// v[w] of (v0, v1, v2, v3) by value selects on the bits of w (0 <= w < 4).
+__device__ inline float pick4(int w, float v0, float v1, float v2, float v3) {
+    const float lo = (w & 1) ? v1 : v0;
+    const float hi = (w & 1) ? v3 : v2;
+    return (w & 2) ? hi : lo;
+}
+
 template <int HD>
 __global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __restrict__ q,
                                                                 const float* __restrict__ kc,
@@ -579,23 +586,28 @@ __global__ __launch_bounds__(ATT_BLOCK) void decode_attn_kernel(const float* __r
     float m = slot[0];
 #pragma unroll
     for (int w = 1; w < ATT_WAVES; ++w) m = fmaxf(m, slot[2 * w]);
-    float f[ATT_WAVES], l = 0.0f;
-#pragma unroll
-    for (int w = 0; w < ATT_WAVES; ++w) {
-        f[w] = slot[2 * w] == -INFINITY ? 0.0f : expf(slot[2 * w] - m);
-        l += slot[2 * w + 1] * f[w];
-    }
-    static_assert(ATT_WAVES == 4, "factor select below");
-    auto prob = [&](int j) {
-        const int w = (j >> 6) & 3;
-        const float fw = w == 0 ? f[0] : (w == 1 ? f[1] : (w == 2 ? f[2] : f[3]));
-        return j < T ? s[j] * fw : 0.0f;
+    static_assert(ATT_WAVES == 4, "four wave factors");
+    auto wave_factor = [&](int w) { return slot[2 * w] == -INFINITY ? 0.0f : expf(slot[2 * w] - m); };
+    const float f0 = wave_factor(0), f1 = wave_factor(1), f2 = wave_factor(2), f3 = wave_factor(3);
+    const float l = ((slot[1] * f0 + slot[3] * f1) + slot[5] * f2) + slot[7] * f3;
+    // The factor of position j is wave ((j >> 6) & 3)'s, selected from four
+    // values (a select over an array, or over references to the four, is
+    // compiled to an indexed load from scratch memory).
+    auto factor = [f0, f1, f2, f3](int w) { return pick4(w, f0, f1, f2, f3); };
+    auto prob = [&](int j) { return j < T ? s[j] * factor((j >> 6) & 3) : 0.0f; };
+    // In the first VCH rows, j = g + u*G with g < G: for G <= 64 (a power of
+    // two, so g + (u*G mod 64) < 64) the wave of j is that of u*G, known at
+    // compile time.
+    auto prob_first = [&](int u) {
+        const int j = g + u * G;
+        const int w = G <= 64 ? ((u * G) >> 6) & 3 : (j >> 6) & 3;
+        return j < T ? s[j] * factor(w) : 0.0f;
     };
 
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int u = 0; u < VCH; ++u) {
-        const float pj = prob(g + u * G);
+        const float pj = prob_first(u);
         acc.x += pj * vr[u].x;
         acc.y += pj * vr[u].y;
         acc.z += pj * vr[u].z;

@@ -147,10 +147,35 @@ __device__ inline void row_reduce_moments(float& n, float& mean, float& m2, floa
     }
 }
 
+// Rows whose vectors are not all present (EVEN false) read and write
+// through a buffer descriptor over the row: a vector outside the row gets
+// an offset past the descriptor's range, so it reads as zeros and its store
+// is dropped, with no branch around the access (branches there made the
+// compiler keep the whole row live across them and spill) and no memory
+// traffic for it.
+constexpr uint32_t ROW_OOB = 0xFFFFFF00u;   // past every row's range (rows are < 64 KiB here)
+constexpr int ROW_BUF_FLAGS = 0x00020000;   // gfx9 buffer descriptor word 3 (32-bit data format)
+constexpr int ROW_NT = 2;                   // cache policy: non-temporal
+
+__device__ inline __amdgpu_buffer_rsrc_t row_rsrc(const float* row, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, bytes, ROW_BUF_FLAGS);
+}
+
 template <int VEC>
 struct Vec;
 template <>
 struct Vec<4> {
+    static __device__ inline void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off, float* d) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const f32x4 t = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, ROW_NT));
+        d[0] = t[0]; d[1] = t[1]; d[2] = t[2]; d[3] = t[3];
+    }
+    static __device__ inline void store_buf(__amdgpu_buffer_rsrc_t r, uint32_t off, const float* d) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{d[0], d[1], d[2], d[3]}), r, off, 0,
+                                               ROW_NT);
+    }
     using T = float4;
     // Non-temporal loads: every input element is read exactly once (0.2-0.8
     // us less per [4096, 4096] row op from cold HBM than plain loads).
@@ -169,6 +194,12 @@ struct Vec<4> {
 };
 template <>
 struct Vec<1> {
+    static __device__ inline void load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off, float* d) {
+        d[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, ROW_NT));
+    }
+    static __device__ inline void store_buf(__amdgpu_buffer_rsrc_t r, uint32_t off, const float* d) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, d[0]), r, off, 0, ROW_NT);
+    }
     static __device__ inline void load(const float* p, float* d) { d[0] = __builtin_nontemporal_load(p); }
     static __device__ inline void store(float* p, const float* d) { __builtin_nontemporal_store(d[0], p); }
 };
@@ -213,19 +244,21 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
     float v[N];
     float w[TWO ? N : 1];
     bool ok[NV];
+    // Without EVEN, vectors outside the row read as zeros (row_rsrc).
+    const int row_bytes = live ? cols * 4 : 0;
+    const __amdgpu_buffer_rsrc_t ra = row_rsrc(ar, row_bytes);
+    const __amdgpu_buffer_rsrc_t rb = row_rsrc(TWO ? br : ar, row_bytes);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = (j * TPR + t) * VEC;
         ok[j] = EVEN || (live && c < cols);
-        if (ok[j]) {
+        if constexpr (EVEN) {
             Vec<VEC>::load(ar + c, &v[j * VEC]);
             if constexpr (TWO) Vec<VEC>::load(br + c, &w[j * VEC]);
         } else {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                v[j * VEC + e] = 0.0f;
-                if constexpr (TWO) w[j * VEC + e] = 0.0f;
-            }
+            const uint32_t off = ok[j] ? 4u * (uint32_t)c : ROW_OOB;
+            Vec<VEC>::load_buf(ra, off, &v[j * VEC]);
+            if constexpr (TWO) Vec<VEC>::load_buf(rb, off, &w[j * VEC]);
         }
     }
     const float d = (float)cols;
@@ -375,10 +408,14 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(
     }
 
     float* yr = y + (live ? row : 0) * (int64_t)cols;
+    const __amdgpu_buffer_rsrc_t ry = row_rsrc(yr, row_bytes);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = (j * TPR + t) * VEC;
-        if (ok[j]) Vec<VEC>::store(yr + c, &v[j * VEC]);
+        if constexpr (EVEN)
+            Vec<VEC>::store(yr + c, &v[j * VEC]);
+        else
+            Vec<VEC>::store_buf(ry, ok[j] ? 4u * (uint32_t)c : ROW_OOB, &v[j * VEC]);
     }
 }
 

@@ -65,7 +65,8 @@ def test_rmsnorm_cfg2(cfg2_x):
 
 
 RAGGED = [(3, 1), (5, 3), (7, 5), (9, 63), (4, 64), (4, 65), (3, 255), (3, 257), (5, 1000),
-          (6, 4095), (3, 4097), (2, 8192), (2, 12000), (2, 16384), (2, 16385), (1, 40000)]
+          (5, 2000), (5, 2048), (6, 4095), (3, 4097), (2, 8192), (2, 12000), (2, 16384), (2, 16385),
+          (1, 40000)]
 
 
 @pytest.mark.parametrize("rows,cols", RAGGED)
