@@ -341,7 +341,11 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     // Q and dO blocks; at the end the qh = 1 partials ([kh][dK 64 + dV 64][33]).
     constexpr int SMEM = 2 * BT * PITCH > 2 * 128 * 33 ? 2 * BT * PITCH : 2 * 128 * 33;
     __shared__ __align__(16) float smem[SMEM];
-    __shared__ float Ls[BT], Ds[BT];
+    // L and D of the block's queries; slot BT takes the (unused) values of
+    // the threads past the block, so every thread stores without a branch
+    // (loads that only feed a store under a branch were sunk into it and
+    // issued one at a time behind spilled addresses).
+    __shared__ float Ls[BT + 1], Ds[BT + 1];
     float* Qs = smem;
     float* dOs = smem + BT * PITCH;
     const int nkb = T / BT;
@@ -361,18 +365,20 @@ __global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
     // Blocks staged without prefetch (two workgroups per CU, as in the dQ kernel).
     f32x4 qc[4], oc[4];
     const int qb0 = causal ? kb : 0, nqb = T / BT;
-    const int lrow = tid < BT ? tid : 0;
+    const int lrow = tid < BT ? tid : 0, lslot = tid < BT ? tid : BT;
+    const float* lse_h = lse + head * T;  // the head's L and D (uniform bases)
+    const float* dd_h = dd + head * T;
     for (int qb = qb0; qb < nqb; ++qb) {
+        // L and D first: gfx9 waits for loads in issue order, so the Q / dO
+        // loads behind them do not hold up their stores.
+        const float lv = lse_h[qb * BT + lrow], dv = dd_h[qb * BT + lrow];
         block_load(Qh, qb * BT, rs, tid, qc);
         block_load(dOh, qb * BT, rs, tid, oc);
-        const float lv = lse[head * T + qb * BT + lrow], dv = dd[head * T + qb * BT + lrow];
         __syncthreads();
         block_store(Qs, tid, qc);
         block_store(dOs, tid, oc);
-        if (tid < BT) {
-            Ls[tid] = lv;
-            Ds[tid] = dv;
-        }
+        Ls[lslot] = lv;
+        Ds[lslot] = dv;
         __syncthreads();
         f32x16 s2[2] = {zero16(), zero16()}, p2[2] = {zero16(), zero16()};
         // Two halves of 16 steps, each half's LDS reads issued before its MFMAs.
