@@ -149,6 +149,20 @@ def test_vocab_tail_and_wide_mlp():
     check_logits_and_argmax(lg, am, oracle_logits(cfg, P, seq), "vocab 777")
 
 
+def test_wide_lm_head_with_a_partial_last_workgroup():
+    """vocab 8200: 513 row tiles, so the LM head takes its wide shape (8 row
+    tiles per workgroup) and the last workgroup holds one tile in range; its
+    RMS still sums the squares of every step of the activation."""
+    cfg = nn.DecoderConfig(n_layers=1, d_model=128, n_heads=4, vocab=8200, mlp_ratio=2, max_batch=8, max_seq=8)
+    P = nn.decoder_params(cfg, 515)
+    dec = HipDecoder(cfg)
+    dec.load(P)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab, size=(5, 2))
+    toks, am, lg = dec.generate(prompt, 4, argmax=True, logits=True)
+    seq = np.concatenate([prompt, toks[:, :-1]], axis=1)
+    check_logits_and_argmax(lg, am, oracle_logits(cfg, P, seq), "vocab 8200")
+
+
 def test_config5_matches_stream_forward():
     """Config 5 at full size (12 layers, d_model 768, 12 heads, vocab 32000,
     batch 8, prompt 16, 128 new tokens): the decoder's logits at all 143
