@@ -81,7 +81,8 @@ def test_rows_ragged_and_misaligned(rows, cols, offset):
     assert_allclose(y, oracle(OpKind.RmsNorm(1e-5), x), 1e-6, 1e-5, f"rmsnorm {rows}x{cols}")
 
 
-@pytest.mark.parametrize("rows,cols", [(2048, 1024), (64, 512), (3, 77), (2, 20000)])
+@pytest.mark.parametrize("rows,cols", [(2048, 1024), (64, 512), (3, 77), (5, 1000), (3, 2048), (2, 6000),
+                                       (2, 20000)])
 def test_vjp_rows(rows, cols):
     x = synth.normal(7 + cols, (rows, cols), 0.0, 1.0)
     dy = synth.normal(8 + cols, (rows, cols), 0.0, 1.0)
@@ -94,7 +95,7 @@ def test_vjp_rows(rows, cols):
     assert_allclose(g, oracle(OpKind.SoftmaxVjp(-1), dy, s), 1e-6, 1e-4, "softmax_vjp")
 
 
-@pytest.mark.parametrize("n,causal", [(512, True), (512, False), (77, True)])
+@pytest.mark.parametrize("n,causal", [(512, True), (512, False), (77, True), (1000, True)])
 def test_scaled_masked_softmax(n, causal):
     x = synth.normal(99 + n, (n, n), 0.0, 1.0)
     scale = 1.0 / np.sqrt(64.0)
