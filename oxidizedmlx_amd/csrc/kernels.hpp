@@ -37,6 +37,15 @@ int ew_chain(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inp
 // full-size input). periods may be null.
 int ew_chain_periodic(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs,
                       const int64_t* periods, int n_inputs, float* out, int64_t numel, hipStream_t s);
+// ew_chain_periodic that also writes the output's three bf16 planes for the
+// split-f32 GEMM (the split pass's arithmetic, x6_split), in storage order:
+// plane p at planes + p * numel (16-byte aligned), *flag = gen when a value
+// cannot be split. *written says whether it did: only the vector kernel
+// writes planes (every pointer 16-byte aligned, numel % 4 == 0); otherwise
+// the chain runs alone.
+int ew_chain_planes(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs, const int64_t* periods,
+                    int n_inputs, float* out, int64_t numel, uint16_t* planes, uint32_t* flag, uint32_t gen,
+                    bool* written, hipStream_t s);
 // General N-D permutation (rank <= 8): y[new] = x[old], out shape = shape[perm].
 int permute(const float* x, float* y, const int64_t* shape, const int64_t* perm, int ndim,
             hipStream_t s);
@@ -172,6 +181,18 @@ int gemm(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, int64_t
 // input), else one gemm call each. Results within f32 accuracy of separate
 // calls (the launch may tile and split them differently).
 bool gemm_f32_groupable(int64_t m, int64_t n, int64_t k);
+// Whether an f32 product of this shape runs on the split-f32 planes.
+bool gemm_f32_reads_planes(int64_t m, int64_t n, int64_t k, int64_t batch);
+// A plane block for an f32 operand that a producer splits itself: `src`
+// stored contiguously as batch x [rows][cols] (rows and cols multiples of
+// 32, so the planes need no padding and hold the operand in storage order),
+// entered in `cache` under the key the split-f32 GEMM looks up, so products
+// reading src skip its split. *planes stays null (nothing entered) when the
+// shape needs padding or the cache cannot allocate. The producer must write
+// all three planes (plane p at *planes + p * batch*rows*cols) and store
+// *gen into *flag if a value cannot be split, before any product reads it.
+int x6_plane_block(PlaneCache* cache, const void* src, int64_t rows, int64_t cols, int64_t batch, uint16_t** planes,
+                   uint32_t** flag, uint32_t* gen);
 int gemm_f32_grouped(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, int groups, const float* const* a,
                      int64_t lda, const float* const* b, int64_t ldb, float* const* c, int64_t ldc, hipStream_t s,
                      PlaneCache* planes = nullptr, const float* const* bias = nullptr);

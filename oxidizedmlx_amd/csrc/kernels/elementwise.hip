@@ -93,7 +93,28 @@ struct EwProg {
     int operand[MLXHIP_EW_MAX_INSTR];
     int n_instr;
     int scalar_mask;  // bit i: input i is one value for every element (vector kernel)
+    // Optional (vector kernel): the output's three bf16 planes for the
+    // split-f32 GEMM, in storage order (plane p at planes + p * plane), and
+    // the flag word that receives gen when a value cannot be split.
+    uint16_t* planes;
+    int64_t plane;
+    uint32_t* flag;
+    uint32_t gen;
 };
+
+// The split-f32 GEMM's split of one f32 value (x6_split_kernel's
+// arithmetic): hi = RN(x), mid = RN(x - hi), lo = RN(x - hi - mid), bf16
+// round to nearest even; both differences are exact in f32. bad: hi is not
+// finite (x is not, or rounds past the bf16 range).
+__device__ inline void split3(float x, uint32_t& h, uint32_t& m, uint32_t& l, bool& bad) {
+    const uint16_t hb = __builtin_bit_cast(uint16_t, (__bf16)x);
+    const float r1 = x - __uint_as_float((uint32_t)hb << 16);
+    const uint16_t mb = __builtin_bit_cast(uint16_t, (__bf16)r1);
+    const float r2 = r1 - __uint_as_float((uint32_t)mb << 16);
+    const uint16_t lb = __builtin_bit_cast(uint16_t, (__bf16)r2);
+    bad |= !__builtin_isfinite(__uint_as_float((uint32_t)hb << 16));
+    h = hb, m = mb, l = lb;
+}
 
 __device__ inline float4 apply4(int op, float4 a, float4 b) {
     return make_float4(apply(op, a.x, b.x), apply(op, a.y, b.y), apply(op, a.z, b.z), apply(op, a.w, b.w));
@@ -110,6 +131,7 @@ template <int NI, int U, bool NT, bool PERIODIC>
 __global__ __launch_bounds__(BLOCK) void ew_chain_vec_kernel(EwProg prog, float* __restrict__ out,
                                                              int64_t n_vec) {
     const int64_t stride = (int64_t)gridDim.x * BLOCK * U;
+    bool bad = false;  // a value the planes cannot hold (prog.planes)
     for (int64_t base = (int64_t)blockIdx.x * BLOCK * U + threadIdx.x; base < n_vec;
          base += stride) {
         float4 in[NI][U];
@@ -158,9 +180,22 @@ __global__ __launch_bounds__(BLOCK) void ew_chain_vec_kernel(EwProg prog, float*
                 const f32x4 v = {acc[u].x, acc[u].y, acc[u].z, acc[u].w};
                 if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out) + idx);
                 else reinterpret_cast<f32x4*>(out)[idx] = v;
+                if (prog.planes) {
+                    uint32_t h[4], m[4], l[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) split3(v[e], h[e], m[e], l[e], bad);
+                    uint2* hp = reinterpret_cast<uint2*>(prog.planes) + idx;
+                    hp[0] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+                    reinterpret_cast<uint2*>(prog.planes + prog.plane)[idx] =
+                        make_uint2(m[0] | (m[1] << 16), m[2] | (m[3] << 16));
+                    reinterpret_cast<uint2*>(prog.planes + 2 * prog.plane)[idx] =
+                        make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+                }
             }
         }
     }
+    // Every writer stores the same word, so the stores need no order.
+    if (bad) *prog.flag = prog.gen;
 }
 
 // One float4 per input per thread: with more per thread, each instruction's
@@ -625,6 +660,13 @@ int ew_chain(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inp
 
 int ew_chain_periodic(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs,
                       const int64_t* periods, int n_inputs, float* out, int64_t numel, hipStream_t s) {
+    return ew_chain_planes(prog, n_instr, inputs, periods, n_inputs, out, numel, nullptr, nullptr, 0, nullptr, s);
+}
+
+int ew_chain_planes(const mlxhip_ew_instr_t* prog, int n_instr, const float* const* inputs, const int64_t* periods,
+                    int n_inputs, float* out, int64_t numel, uint16_t* planes, uint32_t* flag, uint32_t gen,
+                    bool* written, hipStream_t s) {
+    if (written) *written = false;
     if (n_instr < 0 || n_instr > MLXHIP_EW_MAX_INSTR)
         return fail(MLXHIP_ERR_INVALID_ARGUMENT, "ew_chain: %d instructions (max %d)", n_instr,
                     MLXHIP_EW_MAX_INSTR);
@@ -663,6 +705,15 @@ int ew_chain_periodic(const mlxhip_ew_instr_t* prog, int n_instr, const float* c
     }
     p.n_instr = n_instr;
     if (numel == 0) return MLXHIP_OK;
+    // Planes only from the vector kernel covering every element.
+    const bool with_planes = planes && flag && aligned && numel % 4 == 0 &&
+                             reinterpret_cast<uintptr_t>(planes) % 16 == 0;
+    if (with_planes) {
+        p.planes = planes;
+        p.plane = numel;
+        p.flag = flag;
+        p.gen = gen;
+    }
     int64_t done = 0;
     if (aligned) {
         const int64_t n_vec = numel / 4;
@@ -694,6 +745,7 @@ int ew_chain_periodic(const mlxhip_ew_instr_t* prog, int n_instr, const float* c
                            p, out, done, numel);
         MLXHIP_TRY(launch_check("ew_chain_scalar_kernel"));
     }
+    if (written) *written = with_planes;
     return MLXHIP_OK;
 }
 

@@ -341,6 +341,17 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
 // Generation numbers of split-f32 products: each call's flag value.
 std::atomic<uint32_t> g_x6_gen{0};
 
+uint32_t next_x6_gen() {
+    uint32_t g = 0;
+    while (g == 0) g = ++g_x6_gen;
+    return g;
+}
+
+// A plane block: three planes of `plane` elements, rounded up to 256 bytes,
+// then the flag word (256 bytes of room).
+constexpr size_t X6_FLAG_ROOM = 256;
+size_t x6_planes_bytes(int64_t plane) { return ((size_t)(3 * plane * 2) + 255) & ~size_t(255); }
+
 // f32 products through the bf16 planes (gemm16_x6.hip): `groups` products
 // of one shape and layout (groups > 1: batch 1, one launch, product i in
 // batch slot i). One launch (or one per five operands) splits the operands
@@ -397,13 +408,9 @@ int gemm_x6(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int 
                 break;
             }
     }
-    auto new_gen = [] {
-        uint32_t g = 0;
-        while (g == 0) g = ++g_x6_gen;
-        return g;
-    };
-    const size_t flag_room = 256;
-    auto plane_bytes = [](const X6SplitOp& o) { return ((size_t)(3 * o.plane * 2) + 255) & ~size_t(255); };
+    auto new_gen = [] { return next_x6_gen(); };
+    const size_t flag_room = X6_FLAG_ROOM;
+    auto plane_bytes = [](const X6SplitOp& o) { return x6_planes_bytes(o.plane); };
     auto copy_planes = [](X6SplitOp& to, const X6SplitOp& from) {
         to.dst = from.dst;
         to.flag = from.flag;
@@ -588,6 +595,27 @@ bool use_x6(int path, int64_t m, int64_t n, int64_t k, int64_t batch) {
     return m >= 256 && n >= 256 && k >= 256 && (double)m * (double)n * (double)k * (double)batch >= 2147483648.0;
 }
 }  // namespace
+
+bool gemm_f32_reads_planes(int64_t m, int64_t n, int64_t k, int64_t batch) {
+    const int path = gemm_path();
+    return (path == 0 || path == 5) && use_x6(path, m, n, k, batch);
+}
+
+int x6_plane_block(PlaneCache* cache, const void* src, int64_t rows, int64_t cols, int64_t batch, uint16_t** planes,
+                   uint32_t** flag, uint32_t* gen) {
+    *planes = nullptr;
+    if (!cache || !cache->alloc || rows % 32 || cols % 32 || rows <= 0 || cols <= 0 || batch <= 0) return MLXHIP_OK;
+    const int64_t plane = batch * rows * cols;
+    const size_t pb = x6_planes_bytes(plane);
+    char* blk = static_cast<char*>(cache->alloc(cache->ctx, pb + X6_FLAG_ROOM));
+    if (!blk) return fail(MLXHIP_ERR_FFI_FAILED, "gemm: device allocation of %zu bytes failed", pb + X6_FLAG_ROOM);
+    *planes = reinterpret_cast<uint16_t*>(blk);
+    *flag = reinterpret_cast<uint32_t*>(blk + pb);
+    *gen = next_x6_gen();
+    cache->entries.push_back(PlaneCache::Entry{src, cols, batch > 1 ? rows * cols : 0, rows, cols, batch, *planes,
+                                               *flag, *gen});
+    return MLXHIP_OK;
+}
 
 // MLXHIP_GEMM_GROUPS=0 turns grouping off (each product its own launch;
 // read on every call, for comparisons).

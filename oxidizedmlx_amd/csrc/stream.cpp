@@ -386,6 +386,56 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
     // The first position of this evaluation at which a node reads id's buffer:
     // its readers, and through folded Transposes and Reshape / Narrow views
     // (which alias it), theirs.
+    // Chains whose result an f32 product of this evaluation reads through
+    // the split-f32 planes write those planes themselves (ew_chain_planes),
+    // so that product skips the split of that operand: the stored operand
+    // (the chain's result, or a Reshape of it) with rows and cols multiples
+    // of 32. Value: the operand's stored rows, cols and batch.
+    struct PlaneView {
+        int64_t rows, cols, batch;
+    };
+    std::unordered_map<uint64_t, PlaneView> plane_out;
+    if (fusion) {
+        for (const auto& ce : chain_of) {
+            const uint64_t cid = ce.first;
+            const Node& cn = nodes.at(cid);
+            if (cn.meta.dtype != MLXHIP_DTYPE_F32) continue;
+            // Readers of cid, directly or through Reshape views and folded Transposes.
+            std::vector<std::pair<uint64_t, uint64_t>> frontier{{cid, cid}};  // (reader, operand node as stored)
+            bool found = false;
+            for (size_t fi = 0; fi < frontier.size() && fi < 64 && !found; ++fi) {
+                const uint64_t at = frontier[fi].first, stored = frontier[fi].second;
+                auto rd = readers.find(at);
+                if (rd == readers.end()) continue;
+                for (uint64_t u : rd->second) {
+                    const Node& un = nodes.at(u);
+                    const int uk = un.op.op.kind;
+                    if (folded_transpose.count(u)) {
+                        frontier.push_back({u, stored});
+                        continue;
+                    }
+                    if (uk == MLXHIP_OP_RESHAPE && un.meta.numel() == cn.meta.numel() && at == stored) {
+                        frontier.push_back({u, u});
+                        continue;
+                    }
+                    if (uk != MLXHIP_OP_MATMUL || un.inputs.size() != 2 || un.meta.dtype != MLXHIP_DTYPE_F32 ||
+                        un.meta.shape.size() < 2 || buffers.count(u))
+                        continue;
+                    const std::vector<int64_t>& os = un.meta.shape;
+                    const std::vector<int64_t>& as = nodes.at(un.inputs[0]).meta.shape;
+                    const std::vector<int64_t>& ss = nodes.at(stored).meta.shape;
+                    if (as.size() != os.size() || ss.size() != os.size() || (os.size() != 2 && os.size() != 3)) continue;
+                    const int64_t batch = os.size() == 3 ? os[0] : 1;
+                    const int64_t m = os[os.size() - 2], n = os[os.size() - 1], k = as[as.size() - 1];
+                    const int64_t rows = ss[ss.size() - 2], cols = ss[ss.size() - 1];
+                    if (!gemm_f32_reads_planes(m, n, k, batch) || rows % 32 || cols % 32) continue;
+                    plane_out[cid] = PlaneView{rows, cols, batch};
+                    found = true;
+                    break;
+                }
+            }
+        }
+    }
     std::function<size_t(uint64_t, int)> first_read = [&](uint64_t id, int depth) -> size_t {
         size_t best = SIZE_MAX;
         auto it = readers.find(id);
@@ -411,7 +461,8 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
                     if (virtual_bcast.count(in)) return true;
             return false;
         };
-        if (ch != chain_of.end() && (ch->second.size() > 1 || reads_virtual(ch->second))) {
+        auto pv = plane_out.find(id);
+        if (ch != chain_of.end() && (ch->second.size() > 1 || reads_virtual(ch->second) || pv != plane_out.end())) {
             // One fused kernel for the whole chain.
             const std::vector<uint64_t>& nodes_in_chain = ch->second;
             std::vector<const float*> ins;
@@ -458,8 +509,17 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             if (rc != MLXHIP_OK) break;
             float* out = nullptr;
             if ((rc = alloc_out(id, &out)) != MLXHIP_OK) break;
-            rc = ew_chain_periodic(prog.data(), (int)prog.size(), ins.data(), periods.data(), (int)ins.size(), out,
-                                   n.meta.numel(), hs);
+            uint16_t* pl = nullptr;
+            uint32_t* fl = nullptr;
+            uint32_t gen = 0;
+            if (pv != plane_out.end() &&
+                (rc = x6_plane_block(&planes, out, pv->second.rows, pv->second.cols, pv->second.batch, &pl, &fl,
+                                     &gen)) != MLXHIP_OK)
+                break;
+            bool written = false;
+            rc = ew_chain_planes(prog.data(), (int)prog.size(), ins.data(), periods.data(), (int)ins.size(), out,
+                                 n.meta.numel(), pl, fl, gen, &written, hs);
+            if (pl && !written) planes.entries.pop_back();  // the product splits it after all
             eval_calls += nodes_in_chain.size();
             launches += 1;
             if (rc != MLXHIP_OK) {

@@ -810,3 +810,44 @@ def test_async_view_constant_rewritten_after_synchronize():
     s.close()
     np.testing.assert_array_equal(first, x * np.float32(2.0))
     np.testing.assert_array_equal(second, -x * np.float32(2.0))
+
+
+@pytest.mark.parametrize("overflow", [False, True])
+def test_chain_writes_the_planes_its_product_reads(overflow):
+    # A chain whose result a split-f32 product reads writes that operand's
+    # bf16 planes itself (the split pass's arithmetic), so the product skips
+    # its split: GELU(x) . W at 1024 x 2048 x 1024 gives the unfused graph's
+    # result bit for bit. With a value the planes cannot hold (exp overflow)
+    # the chain raises the product's flag and the product forms C from the
+    # f32 operands, as after a split. A second product reads the chain's
+    # result transposed (g^T . v, the weight-gradient form) from the same
+    # planes; it is held to the float64 bound.
+    from parity import gemm_full_check
+    t, i, o = 1024, 1024, 2048
+    x0 = synth.normal(641, (t, i))
+    if overflow:
+        x0[5, 7] = 100.0  # exp(100) is +inf in f32
+    w0 = synth.normal(642, (i, o), 0.0, 0.05)
+    v0 = synth.normal(643, (t, o), 0.0, 0.05)
+    op = OpKind.Exp if overflow else OpKind.Gelu
+    res = {}
+    for fusion in (True, False):
+        s = HipStream(fusion=fusion)
+        x = s.add_constant(x0, meta((t, i)))
+        w = s.add_constant(w0, meta((i, o)))
+        v = s.add_constant(v0, meta((t, o)))
+        g = s.add_op(op, [x], meta((t, i)))
+        y = s.add_op(OpKind.MatMul, [g, w], meta((t, o)))
+        gt = s.add_op(OpKind.Transpose(None), [g], meta((i, t)))
+        z = s.add_op(OpKind.MatMul, [gt, v], meta((i, o)))
+        s.eval_many([y, z])
+        res[fusion] = (s.get_buffer(y).reshape(t, o), s.get_buffer(z).reshape(i, o), s.get_buffer(g).reshape(t, i))
+    np.testing.assert_array_equal(res[True][2], res[False][2])
+    np.testing.assert_array_equal(res[True][0], res[False][0])
+    if overflow:
+        assert not np.isfinite(res[True][0][5]).all()
+        assert np.isfinite(np.delete(res[True][0], 5, axis=0)).all()
+    else:
+        gv = res[True][2]
+        gemm_full_check(res[True][0], gv, w0, "f32", "GELU(x) . W from the chain's planes")
+        gemm_full_check(res[True][1], np.ascontiguousarray(gv.T), v0, "f32", "GELU(x)^T . v from the chain's planes")
