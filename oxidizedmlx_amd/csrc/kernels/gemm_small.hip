@@ -22,12 +22,14 @@
 // accumulator chains (summed in chain order at the end), so the matrix pipe
 // is not held up by the latency of one chain of dependent MFMAs.
 //
-// Whole-tile products (M, N multiples of 32, K = 8 * KH, K-contiguous
-// operands 16-byte aligned) run a variant without the range selects.
-// Measured on MI355X for 512^3 (NN): 6.0 us per launch back to back, of
-// which 2.5 us is the cost of launching an empty grid of the same shape;
-// the previous form (8 waves of 32 k, 64-bit clamped addresses per load)
-// took 8.5 us.
+// Whole-tile products (M, N multiples of 32, K = 8 * KH, every operand run
+// 16-byte aligned) run an 8-wave kernel instead (gemm_small_staged_kernel)
+// that brings MN-contiguous operands in through LDS with 16-byte loads.
+// Measured on MI355X for 512^3 (NN): the 4-wave kernel without range
+// selects took 6.0 us per launch back to back on warm operands (2.5 us of it
+// the cost of launching an empty grid of the same shape) and 7.10-7.45 us on
+// eight operand sets in rotation; the staged kernel takes 6.46-6.61 us on
+// the rotating sets.
 #include "../common.hpp"
 #include "../kernels.hpp"
 
@@ -153,13 +155,127 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256))) void gemm_smal
     }
 }
 
+// Whole-tile products (EVEN), 8 waves: K is cut into 16 runs of KH (one per
+// half-wave, KH = 4 .. 32), and an MN-contiguous operand (A stored [K][M],
+// B stored [K][N]) is staged through LDS: its 32-wide panel over all of K
+// comes in with 16-byte loads along M / N (8 per k row) instead of one 4-byte
+// load per lane and k, and each lane then reads its own row's or column's KH
+// values from LDS. A K-contiguous operand is read straight into registers
+// with 16-byte loads along K, as in the kernel above. The eight waves'
+// partial tiles are summed in wave order through LDS (reusing the staging
+// area). 512^3 NN on MI355X, HIP events, eight operand sets in rotation:
+// 6.46-6.61 us per launch against 7.10-7.45 us for the 4-wave kernel.
+template <int TA, int TB, int KH>
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512))) void gemm_small_staged_kernel(SmallArgs g) {
+    constexpr int W = 8, NT = 64 * W, K = 2 * W * KH;
+    constexpr bool SA = TA == 1, SB = TB == 0;  // operands staged through LDS
+    constexpr int PITCH = 33;                   // floats per staged k row (32 + 1)
+    constexpr int A_OFF = 0, B_OFF = SA ? K * PITCH : 0;
+    constexpr int STAGE = (SA ? K * PITCH : 0) + (SB ? K * PITCH : 0);
+    constexpr int PART = W * 32 * 33;
+    __shared__ __attribute__((aligned(16))) float lds[STAGE > PART ? STAGE : PART];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Tile order as in gemm_small_kernel.
+    const int per_batch = g.tiles_m * g.tiles_n;
+    const int total = per_batch * (int)gridDim.y;
+    int lin = (int)blockIdx.x + (int)blockIdx.y * (int)gridDim.x;
+    if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+    const int bt = lin / per_batch;
+    const int id = lin - bt * per_batch;
+    constexpr int GROUP_M = 4;
+    const int in_group = GROUP_M * g.tiles_n;
+    const int first_m = (id / in_group) * GROUP_M;
+    const int gsz = min(g.tiles_m - first_m, GROUP_M);
+    const int64_t m0 = (int64_t)(first_m + (id % in_group) % gsz) * 32;
+    const int64_t n0 = (int64_t)((id % in_group) / gsz) * 32;
+    const int r = lane & 31, h = lane >> 5;
+    const int kb = (2 * wave + h) * KH;  // this half-wave's first k
+
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(g.a + bt * g.sa), (short)0, (int)g.nrec_a, BUF_FLAGS);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(g.b + bt * g.sb), (short)0, (int)g.nrec_b, BUF_FLAGS);
+    // Staged panels: thread t loads 16-byte chunk t % 8 of k rows t / 8 + 64 j.
+    constexpr int PJ = K * 8 / NT;
+    const int prow = tid / 8, pq = tid % 8;
+    f32x4v pa[SA ? PJ : 1], pb[SB ? PJ : 1];
+    if constexpr (SA) {
+#pragma unroll
+        for (int j = 0; j < PJ; ++j)
+            pa[j] = __builtin_bit_cast(f32x4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   ra, (uint32_t)(prow + (NT / 8) * j) * g.lda4 + (uint32_t)(m0 + 4 * pq) * 4u, 0, 0));
+    }
+    if constexpr (SB) {
+#pragma unroll
+        for (int j = 0; j < PJ; ++j)
+            pb[j] = __builtin_bit_cast(f32x4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rb, (uint32_t)(prow + (NT / 8) * j) * g.ldb4 + (uint32_t)(n0 + 4 * pq) * 4u, 0, 0));
+    }
+    // K-contiguous operands: the lane's KH values straight into registers.
+    float av[KH], bv[KH];
+    if constexpr (!SA) {
+        const uint32_t oa = first_offset<true>(m0 + r, kb, g.lda4);
+#pragma unroll
+        for (int i = 0; i < KH; i += 4) load4<true, true>(ra, oa, g.lda4, i, true, kb, g.k, av + i);
+    }
+    if constexpr (!SB) {
+        const uint32_t ob = first_offset<true>(n0 + r, kb, g.ldb4);
+#pragma unroll
+        for (int i = 0; i < KH; i += 4) load4<true, true>(rb, ob, g.ldb4, i, true, kb, g.k, bv + i);
+    }
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+        float* ra_row = lds + A_OFF + (prow + (NT / 8) * j) * PITCH + 4 * pq;
+        float* rb_row = lds + B_OFF + (prow + (NT / 8) * j) * PITCH + 4 * pq;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if constexpr (SA) ra_row[e] = pa[j][e];
+            if constexpr (SB) rb_row[e] = pb[j][e];
+        }
+    }
+    __syncthreads();
+    if constexpr (SA) {
+#pragma unroll
+        for (int i = 0; i < KH; ++i) av[i] = lds[A_OFF + (kb + i) * PITCH + r];
+    }
+    if constexpr (SB) {
+#pragma unroll
+        for (int i = 0; i < KH; ++i) bv[i] = lds[B_OFF + (kb + i) * PITCH + r];
+    }
+    f32x16 acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[q][v] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KH; ++i)
+        acc[i % 4] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[i], acc[i % 4], 0, 0, 0);
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[0][v] += acc[q][v];
+    __syncthreads();  // every wave is done with the staged panels
+    float* part = lds;  // [W][32][33]
+#pragma unroll
+    for (int v = 0; v < 16; ++v) part[(wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3)) * 33 + r] = acc[0][v];
+    __syncthreads();
+    float* cb = g.c + bt * g.sc;
+    for (int e = tid; e < 32 * 32; e += NT) {
+        const int i = e >> 5, j = e & 31;
+        float s = part[i * 33 + j];
+#pragma unroll
+        for (int w = 1; w < W; ++w) s += part[(w * 32 + i) * 33 + j];
+        cb[(m0 + i) * g.ldc + n0 + j] = s;
+    }
+}
+
 // Bytes of one operand slice: `rows` runs of `cols` elements, `ld` apart.
 int64_t slice_bytes(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 1) * ld + cols) * 4; }
 
 template <int TA, int TB, int KH>
 int launch_kh(const SmallArgs& g, bool even, int64_t batch, hipStream_t s) {
     const dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)batch);
-    if (even) hipLaunchKernelGGL((gemm_small_kernel<TA, TB, KH, true>), grid, dim3(256), 0, s, g);
+    if (even) hipLaunchKernelGGL((gemm_small_staged_kernel<TA, TB, KH / 2>), grid, dim3(512), 0, s, g);
     else hipLaunchKernelGGL((gemm_small_kernel<TA, TB, KH, false>), grid, dim3(256), 0, s, g);
     return launch_check("gemm_small_kernel");
 }
@@ -174,8 +290,9 @@ int launch_small(SmallArgs& g, const float* a, int64_t lda, int64_t sa, const fl
     auto kc_aligned = [&](const float* p, int64_t ld, int64_t st) {
         return reinterpret_cast<uintptr_t>(p) % 16 == 0 && ld % 4 == 0 && (batch == 1 || st % 4 == 0);
     };
-    const bool even = m % 32 == 0 && n % 32 == 0 && k == 8 * kh && (TA == 1 || kc_aligned(a, lda, sa)) &&
-                      (TB == 0 || kc_aligned(b, ldb, sb));
+    // Whole tiles: 16-byte loads along K (K-contiguous operands) or along
+    // M / N (the staged, MN-contiguous ones) need every run 16-byte aligned.
+    const bool even = m % 32 == 0 && n % 32 == 0 && k == 8 * kh && kc_aligned(a, lda, sa) && kc_aligned(b, ldb, sb);
     switch (kh) {
         case 8: return launch_kh<TA, TB, 8>(g, even, batch, s);
         case 16: return launch_kh<TA, TB, 16>(g, even, batch, s);

@@ -115,9 +115,10 @@ def test_f32_512_cfg1():
     (31, 65, 129, 1),     # one k past a whole run
 ])
 def test_small_f32_kernel_shapes(ta, tb, m, n, k, batch):
-    """The one-launch f32 kernel for small products (32 x 32 tiles, K over 8
-    half-wave runs): whole-tile products take its variant without range
-    selects, the others read zeros past the matrix edge through the buffer
+    """The one-launch f32 kernels for small products (32 x 32 tiles): whole
+    tiles take the 8-wave kernel that stages MN-contiguous operands through
+    LDS (K over 16 half-wave runs), the others the 4-wave kernel (K over 8
+    runs) that reads zeros past the matrix edge through the buffer
     descriptor. Every element of every slice against float64 with the
     accumulation bound, and sampled rows against the oracle."""
     check_gemm(m, n, k, F32, F32, ta=bool(ta), tb=bool(tb), batch=batch, seed=m + 3 * n + 7 * k + ta + 2 * tb,
