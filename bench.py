@@ -35,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+IDLE_S = 0.2                   # idle device time before each workload's warmup
 BF16_PEAK_TFLOPS = 2516.6      # dense bf16 MFMA
 SEEDS = {"A": 0x5EED0006, "B": 0x5EED0007, "x": 0x5EED0003, "w": 0x5EED0004, "b": 0x5EED0005}
 
@@ -416,12 +417,17 @@ def main() -> int:
     # Each workload's warmup steps run right before its timed steps, so no
     # workload is timed on a chip that another one's warmup has just heated
     # (the headline GEMM measured 1045 TFLOP/s after the f32 4096^3 warmups
-    # against 1170 TFLOP/s after its own).
+    # against 1170 TFLOP/s after its own). Before its warmup the device sits
+    # idle for IDLE_S, so a short workload is not timed while the power
+    # management still holds the clock down after the previous one (config 1
+    # measured 8.8-11.3 us per call right after the headline's launches,
+    # 7.1 us alone).
     log(f"bench: {args.warmup} warmup + {args.steps} timed steps per workload")
     t0 = time.perf_counter()
     wall_ms = {}
     graphs = []
     for k in names:
+        time.sleep(IDLE_S)
         for i in range(args.warmup):
             launch(k, i)
         hb.synchronize(None)
