@@ -52,6 +52,7 @@ SOURCES = [
     "kernels/elementwise.hip",
     "kernels/gemm.hip",
     "kernels/gemm_small.hip",
+    "kernels/gemm_thin.hip",
     "kernels/gemm_bf16.hip",
     "kernels/gemm_f16.hip",
     "kernels/gemm_f32.hip",

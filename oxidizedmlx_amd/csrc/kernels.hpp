@@ -204,6 +204,15 @@ int gemm16_small(int ab_dtype, int c_dtype, int ta, int tb, int64_t m, int64_t n
                  const void* a, int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, void* c,
                  int64_t ldc, int64_t sc, hipStream_t s);
 
+// Batched f32 products C = A B^T with K <= 64 (kernels/gemm_thin.hip): one
+// wave per 32 x 64 tile of C, for many tiles (attention scores over heads).
+bool gemm_thin_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
+                        int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, const void* c,
+                        int64_t ldc, int64_t sc);
+int gemm_thin_f32(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const float* a, int64_t lda,
+                  int64_t sa, const float* b, int64_t ldb, int64_t sb, float* c, int64_t ldc, int64_t sc,
+                  hipStream_t s);
+
 // gemm_small.hip: f32 products small enough for one or two rounds of 32 x 32
 // tiles with K <= 512, one launch, no workspace, any alignment; operand
 // slices under 2 GiB.

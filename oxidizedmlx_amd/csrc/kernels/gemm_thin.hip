@@ -1,0 +1,289 @@
+// gemm_thin.hip — batched f32 products with a short reduction axis, both
+// operands K-contiguous: C_b[M,N] = A_b[M,K] B_b[N,K]^T with K <= 64. These
+// are the score products of attention over many heads (S = Q K^T and
+// dP = dO V^T with head dimension 64, config 4's composed block); they
+// replace matmul (crates/mlx-core/src/cpu_kernels.rs:197-230) at these
+// shapes.
+//
+// Such a product writes far more than it reads (C is M x N, the operands
+// M x K and N x K), so it runs at the rate C can be written, as long as the
+// stores of some tiles overlap the loads and MFMAs of others. A block-tiled
+// GEMM with one large tile per CU does the opposite: every CU loads, then
+// computes, then stores its whole tile at the same moment as every other
+// CU.
+//
+// Here a workgroup of 4 waves owns a 64 x 128 block of C, and three
+// workgroups share a CU, each in its own phase. The block's rows of A and B
+// (K padded with zeros to KP = 2 KH, KH = 8, 16 or 32) come in with
+// coalesced 16-byte loads (KP / 4 lanes per row) and go to LDS rows of
+// KP + 4 floats; after one barrier each wave computes a 32 x 64 tile from
+// LDS. The K axis is cut into two runs of KH, one per half-wave: at step i
+// of v_mfma_f32_32x32x2_f32 lane (r, h) supplies A[m + r][KH h + i] and
+// B[n + 32 t + r][KH h + i] for the tile's column half t, read from LDS
+// with 16-byte reads. (Reading those runs straight from memory, a lane per
+// row, touches 64 cache lines per load instruction and ran at two thirds of
+// the block-tiled kernel's speed.) Products are exact f32 MFMA products
+// with f32 sums, as in the general kernel, one accumulator chain per column
+// half (the two chains alternate, so neither waits on its own previous
+// MFMA). Accumulator element v of lane (r, h) is C[8 (v / 4) + 4 h +
+// v % 4][r], so each store instruction writes two 128-byte row segments.
+//
+// Workgroups are ordered so that each XCD takes a contiguous range of
+// batch slices: a slice's operands are fetched into one L2.
+#include <algorithm>
+#include <atomic>
+#include <type_traits>
+
+#include "../common.hpp"
+#include "../kernels.hpp"
+
+namespace mlxhip {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t OOB_OFF = 0xFFFFFF00u;  // beyond every descriptor range (slices are < 2 GiB)
+constexpr int BUF_FLAGS = 0x00020000;      // gfx9 buffer descriptor word 3 (32-bit data format)
+constexpr int64_t SLICE_MAX_BYTES = (int64_t(1) << 31) - 256;
+constexpr int BM = 64, BN = 128;            // workgroup block
+constexpr int THREADS = 256;
+constexpr int C_POLICY = 2;                 // C stores: non-temporal (written once, read by a later kernel)
+
+struct ThinArgs {
+    const float* a;
+    const float* b;
+    float* c;
+    int64_t sa, sb, sc, ldc;
+    uint32_t lda4, ldb4, ldc4;        // leading dimensions in bytes
+    uint32_t nrec_a, nrec_b, nrec_c;  // descriptor ranges: one slice's bytes
+    int k;
+    int blocks_m, blocks_n;   // workgroup blocks per slice
+    int blocks;               // in all
+};
+
+template <int KH>
+__global__ __launch_bounds__(THREADS) void gemm_thin_nt_kernel(ThinArgs g) {
+    constexpr int KP = 2 * KH, PITCH = KP + 4, CPR = KP / 4;  // 16-byte chunks per row
+    __shared__ __attribute__((aligned(16))) float lds[(BM + BN) * PITCH];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int per_slice = g.blocks_m * g.blocks_n;
+    // Block j of this workgroup (g.blocks past the last one): XCD x
+    // (workgroup i runs on XCD i % 8) walks its own contiguous eighth of the
+    // blocks when they divide evenly.
+    const int nwg = (int)gridDim.x, w = (int)blockIdx.x;
+    const bool remap = (g.blocks & 7) == 0 && (nwg & 7) == 0;
+    auto block_of = [&](int j) {
+        if (!remap) return w + j * nwg;
+        const int l = (w >> 3) + j * (nwg >> 3);
+        return l < (g.blocks >> 3) ? (w & 7) * (g.blocks >> 3) + l : g.blocks;
+    };
+    // Chunk c of a block: row c / CPR, k = 4 (c % CPR). K is a multiple of
+    // 4, so a chunk is wholly inside K or wholly past it (zeros).
+    constexpr int CA = BM * CPR / THREADS, CB = BN * CPR / THREADS;
+    static_assert(CA * THREADS == BM * CPR && CB * THREADS == BN * CPR, "whole chunks per thread");
+    f32x4v xa[CA], xb[CB];
+    auto issue = [&](int blk) {
+        const int bt = blk / per_slice, id = blk - bt * per_slice;
+        const int64_t m0 = (int64_t)(id / g.blocks_n) * BM, n0 = (int64_t)(id % g.blocks_n) * BN;
+        const __amdgpu_buffer_rsrc_t ra =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(g.a + bt * g.sa), (short)0, (int)g.nrec_a, BUF_FLAGS);
+        const __amdgpu_buffer_rsrc_t rb =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(g.b + bt * g.sb), (short)0, (int)g.nrec_b, BUF_FLAGS);
+#pragma unroll
+        for (int j = 0; j < CA; ++j) {
+            const int c = tid + THREADS * j, row = c / CPR, k = 4 * (c % CPR);
+            const uint32_t off = k < g.k ? (uint32_t)(m0 + row) * g.lda4 + 4u * k : OOB_OFF;
+            xa[j] = __builtin_bit_cast(f32x4v, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
+        }
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+            const int c = tid + THREADS * j, row = c / CPR, k = 4 * (c % CPR);
+            const uint32_t off = k < g.k ? (uint32_t)(n0 + row) * g.ldb4 + 4u * k : OOB_OFF;
+            xb[j] = __builtin_bit_cast(f32x4v, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int j = 0; j < CA; ++j) {
+            const int c = tid + THREADS * j;
+            *reinterpret_cast<f32x4v*>(&lds[(c / CPR) * PITCH + 4 * (c % CPR)]) = xa[j];
+        }
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+            const int c = tid + THREADS * j;
+            *reinterpret_cast<f32x4v*>(&lds[(BM + c / CPR) * PITCH + 4 * (c % CPR)]) = xb[j];
+        }
+    };
+    const int r = lane & 31, h = lane >> 5, wm = wave >> 1, wn = wave & 1;
+    const float* pa = &lds[(32 * wm + r) * PITCH + KH * h];
+    const float* pb = &lds[(BM + 64 * wn + r) * PITCH + KH * h];
+    // Block blk's C through a buffer descriptor over its slice: the lane's
+    // byte offset (row 4 h, column r of the wave's 32 x 64 tile) in a VGPR,
+    // the per-element part (row 8 (v / 4) + v % 4, column 32 t) uniform.
+    struct COut {
+        __amdgpu_buffer_rsrc_t rs;
+        uint32_t off;
+    };
+    auto c_out = [&](int blk) {
+        const int bt = blk / per_slice, id = blk - bt * per_slice;
+        const int64_t m0 = (int64_t)(id / g.blocks_n) * BM, n0 = (int64_t)(id % g.blocks_n) * BN;
+        COut o;
+        o.rs = __builtin_amdgcn_make_buffer_rsrc((void*)(g.c + bt * g.sc), (short)0, (int)g.nrec_c, BUF_FLAGS);
+        o.off = (uint32_t)(((m0 + 32 * wm + 4 * h) * g.ldc + n0 + 64 * wn + r) * 4);
+        return o;
+    };
+    auto store_one = [&](const f32x16 (&acc)[2], const COut& o, int e) {
+        const int t = e >> 4, v = e & 15;
+        const uint32_t so = (uint32_t)(8 * (v >> 2) + (v & 3)) * g.ldc4 + 128u * t;
+        // The element as a scalar first: a bit cast of the vector element
+        // itself read element 0 of the vector.
+        const float x = acc[t][v];
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), o.rs, o.off, so, C_POLICY);
+    };
+    // The MFMAs of the block whose operands are in LDS into `cur`; with
+    // WITH_PREV, the 32 stores of the previous block's `prev` go out between
+    // them (32 / KH per step), so a wave whose store has to wait for the
+    // memory system holds up at most one step's MFMAs instead of a whole
+    // block's.
+    auto compute = [&](f32x16 (&cur)[2], const f32x16 (&prev)[2], const COut& po, auto with_prev) {
+        float av[KH], bv[2][KH];
+#pragma unroll
+        for (int i = 0; i < KH; i += 4) {
+            const f32x4v x = *reinterpret_cast<const f32x4v*>(pa + i);
+            const f32x4v y0 = *reinterpret_cast<const f32x4v*>(pb + i);
+            const f32x4v y1 = *reinterpret_cast<const f32x4v*>(pb + 32 * PITCH + i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) av[i + e] = x[e], bv[0][i + e] = y0[e], bv[1][i + e] = y1[e];
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) cur[t][v] = 0.0f;
+        constexpr int SPS = 32 / KH;  // stores per step
+#pragma unroll
+        for (int i = 0; i < KH; ++i) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                cur[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[t][i], cur[t], 0, 0, 0);
+            if constexpr (decltype(with_prev)::value) {
+#pragma unroll
+                for (int q = 0; q < SPS; ++q) store_one(prev, po, i * SPS + q);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto store_all = [&](const f32x16 (&acc)[2], const COut& o) {
+#pragma unroll
+        for (int e = 0; e < 32; ++e) store_one(acc, o, e);
+    };
+    // Requests block nxt's operands (before any store of the current step:
+    // memory operations complete in order, so the wait for them in stage()
+    // leaves the stores in flight).
+    auto next = [&](int j, int& nxt) {
+        nxt = block_of(j);
+        const bool more = nxt < g.blocks;
+        if (more) issue(nxt);
+        return more;
+    };
+    auto advance = [&]() {
+        __syncthreads();  // every wave has read this block's operands from LDS
+        stage();
+        __syncthreads();
+    };
+
+    f32x16 acc0[2], acc1[2];
+    int blk = block_of(0), nxt = 0;
+    issue(blk);
+    stage();
+    __syncthreads();
+    bool more = next(1, nxt);
+    COut po = c_out(blk);
+    compute(acc0, acc1, po, std::false_type{});
+    if (!more) {
+        store_all(acc0, po);
+        return;
+    }
+    advance();
+    blk = nxt;
+    for (int j = 2;; j += 2) {
+        more = next(j, nxt);
+        compute(acc1, acc0, po, std::true_type{});
+        po = c_out(blk);
+        if (!more) {
+            store_all(acc1, po);
+            return;
+        }
+        advance();
+        blk = nxt;
+        more = next(j + 1, nxt);
+        compute(acc0, acc1, po, std::true_type{});
+        po = c_out(blk);
+        if (!more) {
+            store_all(acc0, po);
+            return;
+        }
+        advance();
+        blk = nxt;
+    }
+}
+
+int64_t slice_bytes(int64_t rows, int64_t cols, int64_t ld) { return ((rows - 1) * ld + cols) * 4; }
+
+// Compute units of the current device (256 on MI355X), read once per device.
+int cu_count() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+}  // namespace
+
+bool gemm_thin_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
+                        int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, const void* c,
+                        int64_t ldc, int64_t sc) {
+    // A [M][K] and B [N][K] (C = A B^T), whole blocks, 16-byte runs along K,
+    // 32-bit offsets inside each slice, and enough blocks for several per CU
+    // (fewer go to the block-tiled kernels).
+    if (ta != 0 || tb != 1 || k < 1 || k > 64 || k % 4 || m % BM || n % BN || batch < 1) return false;
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (!al(a) || !al(b) || !c || lda % 4 || ldb % 4 || (batch > 1 && (sa % 4 || sb % 4))) return false;
+    if (ldc < n || slice_bytes(m, k, lda) >= SLICE_MAX_BYTES || slice_bytes(n, k, ldb) >= SLICE_MAX_BYTES ||
+        slice_bytes(m, n, ldc) >= SLICE_MAX_BYTES)
+        return false;
+    (void)sc;
+    const int64_t blocks = (m / BM) * (n / BN) * batch;
+    return blocks >= 1024 && blocks <= INT32_MAX;
+}
+
+int gemm_thin_f32(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const float* a, int64_t lda,
+                  int64_t sa, const float* b, int64_t ldb, int64_t sb, float* c, int64_t ldc, int64_t sc,
+                  hipStream_t s) {
+    if (!gemm_thin_f32_fits(ta, tb, m, n, k, batch, a, lda, sa, b, ldb, sb, c, ldc, sc))
+        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm_thin_f32: shape or layout outside the thin kernel's range");
+    ThinArgs g;
+    g.a = a, g.b = b, g.c = c;
+    g.sa = sa, g.sb = sb, g.sc = sc, g.ldc = ldc;
+    g.lda4 = (uint32_t)(lda * 4), g.ldb4 = (uint32_t)(ldb * 4), g.ldc4 = (uint32_t)(ldc * 4);
+    g.nrec_a = (uint32_t)slice_bytes(m, k, lda);
+    g.nrec_b = (uint32_t)slice_bytes(n, k, ldb);
+    g.nrec_c = (uint32_t)slice_bytes(m, n, ldc);
+    g.k = (int)k;
+    g.blocks_m = (int)(m / BM), g.blocks_n = (int)(n / BN);
+    g.blocks = (int)(g.blocks_m * g.blocks_n * batch);
+    // Persistent workgroups, two per CU (each block of every workgroup
+    // overlaps its C stores with the next block's loads and MFMAs).
+    const int per_cu = 2;
+    const dim3 grid((unsigned)std::min(g.blocks, per_cu * cu_count())), block(THREADS);
+    if (k <= 16) hipLaunchKernelGGL(gemm_thin_nt_kernel<8>, grid, block, 0, s, g);
+    else if (k <= 32) hipLaunchKernelGGL(gemm_thin_nt_kernel<16>, grid, block, 0, s, g);
+    else hipLaunchKernelGGL(gemm_thin_nt_kernel<32>, grid, block, 0, s, g);
+    return launch_check("gemm_thin_nt_kernel");
+}
+
+}  // namespace mlxhip

@@ -125,6 +125,24 @@ def test_small_f32_kernel_shapes(ta, tb, m, n, k, batch):
                rows=sample_rows(m, 6), full=True)
 
 
+@pytest.mark.parametrize("m,n,k,batch,ld_pad", [
+    (512, 512, 64, 64, 0),   # config 4's composed attention scores: 64 heads of Q K^T, head dim 64
+    (256, 512, 60, 64, 4),   # K not a multiple of 8, padded rows
+    (512, 256, 36, 64, 0),   # K = 36: the second half-wave's run is mostly past K
+    (256, 256, 32, 128, 0),  # K = 32: 16 per half-wave
+    (512, 256, 16, 64, 8),   # K = 16: 8 per half-wave
+    (256, 256, 4, 128, 0),   # K = 4: the second half-wave reads only zeros
+])
+def test_thin_f32_kernel(m, n, k, batch, ld_pad):
+    """The thin kernel for many f32 products C = A B^T with K <= 64 (64 x 128
+    blocks staged through LDS, K in two half-wave runs, zeros past K): every
+    element of every slice against float64 with the accumulation bound, and
+    sampled rows against the oracle."""
+    assert (m // 64) * (n // 128) * batch >= 1024  # the thin kernel's range
+    check_gemm(m, n, k, F32, F32, tb=True, batch=batch, seed=m + n + k + batch, rows=sample_rows(m, 3),
+               ld_pad=ld_pad, full=True)
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_small_f32_kernel_any_alignment(ta, tb):
     """The small f32 kernel on operands one element past a 16-byte boundary,
