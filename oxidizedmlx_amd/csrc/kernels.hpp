@@ -204,8 +204,12 @@ int gemm16_small(int ab_dtype, int c_dtype, int ta, int tb, int64_t m, int64_t n
                  const void* a, int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, void* c,
                  int64_t ldc, int64_t sc, hipStream_t s);
 
-// Batched f32 products C = A B^T with K <= 64 (kernels/gemm_thin.hip): one
-// wave per 32 x 64 tile of C, for many tiles (attention scores over heads).
+// Batched f32 products of attention over many heads (kernels/gemm_thin.hip):
+// C = A B^T with K <= 64 (scores), or C [M][64] = op(A) B with B [K][64]
+// (head-dimension outputs). gemm_thin_f32 runs whichever fits.
+bool gemm_thin_n64_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
+                            int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, const void* c,
+                            int64_t ldc, int64_t sc);
 bool gemm_thin_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
                         int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, const void* c,
                         int64_t ldc, int64_t sc);

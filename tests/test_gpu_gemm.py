@@ -143,6 +143,22 @@ def test_thin_f32_kernel(m, n, k, batch, ld_pad):
                ld_pad=ld_pad, full=True)
 
 
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("m,k,batch,ld_pad", [
+    (512, 512, 64, 0),   # config 4's composed attention: 64 heads of P V / P^T dO, head dimension 64
+    (192, 320, 171, 4),  # five chunks of K, an odd batch, padded rows
+    (128, 64, 256, 0),   # one chunk
+])
+def test_thin_n64_f32_kernel(ta, m, k, batch, ld_pad):
+    """The thin kernel for many f32 products with N = 64, C = op(A) B with B
+    [K][64] (K through two LDS stages of 64 k, A K-contiguous or
+    M-contiguous): every element of every slice against float64 with the
+    accumulation bound, and sampled rows against the oracle."""
+    assert (m // 64) * batch >= 512  # the kernel's range
+    check_gemm(m, 64, k, F32, F32, ta=bool(ta), batch=batch, seed=m + k + batch + ta, rows=sample_rows(m, 3),
+               ld_pad=ld_pad, full=True)
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_small_f32_kernel_any_alignment(ta, tb):
     """The small f32 kernel on operands one element past a 16-byte boundary,
