@@ -86,7 +86,7 @@ __device__ inline void load4(__amdgpu_buffer_rsrc_t rs, uint32_t off0, uint32_t 
     }
 }
 
-template <int TA, int TB, int KH, bool EVEN>
+template <int TA, int TB, int KH>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256))) void gemm_small_kernel(SmallArgs g) {
     __shared__ float part[4][32][33];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -121,8 +121,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256))) void gemm_smal
     float av[KH], bv[KH];
 #pragma unroll
     for (int i = 0; i < KH; i += 4) {
-        load4<TA == 0, EVEN>(ra, oa, g.lda4, i, a_ok, kb, g.k, av + i);
-        load4<TB == 1, EVEN>(rb, ob, g.ldb4, i, b_ok, kb, g.k, bv + i);
+        load4<TA == 0, false>(ra, oa, g.lda4, i, a_ok, kb, g.k, av + i);
+        load4<TB == 1, false>(rb, ob, g.ldb4, i, b_ok, kb, g.k, bv + i);
     }
     // Keep every load ahead of the MFMAs (one memory latency per wave);
     // left alone, the scheduler moves each load next to its MFMA to save
@@ -151,7 +151,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256))) void gemm_smal
         const int i = e >> 5, j = e & 31;
         const float s = ((part[0][i][j] + part[1][i][j]) + part[2][i][j]) + part[3][i][j];
         const int64_t row = m0 + i, col = n0 + j;
-        if (EVEN || (row < g.m && col < g.n)) cb[row * g.ldc + col] = s;
+        if (row < g.m && col < g.n) cb[row * g.ldc + col] = s;
     }
 }
 
@@ -276,7 +276,7 @@ template <int TA, int TB, int KH>
 int launch_kh(const SmallArgs& g, bool even, int64_t batch, hipStream_t s) {
     const dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)batch);
     if (even) hipLaunchKernelGGL((gemm_small_staged_kernel<TA, TB, KH / 2>), grid, dim3(512), 0, s, g);
-    else hipLaunchKernelGGL((gemm_small_kernel<TA, TB, KH, false>), grid, dim3(256), 0, s, g);
+    else hipLaunchKernelGGL((gemm_small_kernel<TA, TB, KH>), grid, dim3(256), 0, s, g);
     return launch_check("gemm_small_kernel");
 }
 
