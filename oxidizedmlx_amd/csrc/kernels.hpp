@@ -206,10 +206,18 @@ int gemm16_small(int ab_dtype, int c_dtype, int ta, int tb, int64_t m, int64_t n
 
 // Batched f32 products of attention over many heads (kernels/gemm_thin.hip):
 // C = A B^T with K <= 64 (scores), or C [M][64] = op(A) B with B [K][64]
-// (head-dimension outputs). gemm_thin_f32 runs whichever fits.
-bool gemm_thin_n64_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
-                            int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, const void* c,
-                            int64_t ldc, int64_t sc);
+// (head-dimension outputs). gemm_thin_f32 runs whichever fits, on plain
+// batch strides; gemm_thin_view on two-level ones: slice bt of an operand
+// starts (bt / inner) * s + (bt % inner) * s2 elements past p, its rows ld
+// apart (the heads of a [batch, seq, heads * dh] tensor without a permute).
+struct ThinView {
+    const float* p;
+    int64_t ld, s, s2;
+};
+bool gemm_thin_view_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int inner,
+                         const ThinView& a, const ThinView& b, const ThinView& c);
+int gemm_thin_view(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int inner, const ThinView& a,
+                   const ThinView& b, const ThinView& c, hipStream_t s);
 bool gemm_thin_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
                         int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, const void* c,
                         int64_t ldc, int64_t sc);

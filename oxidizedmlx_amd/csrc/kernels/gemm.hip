@@ -772,9 +772,7 @@ int gemm_impl(int ab_dtype, int c_dtype, int trans_a, int trans_b, int64_t m, in
     // bound by writing C) and head-dimension outputs (N = 64, bound by
     // reading A).
     if (ab_dtype == MLXHIP_DTYPE_F32 && c_dtype == MLXHIP_DTYPE_F32 && gemm_path() == 0 &&
-        (gemm_thin_f32_fits(trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c) ||
-         gemm_thin_n64_f32_fits(trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c, ldc,
-                                stride_c)))
+        gemm_thin_f32_fits(trans_a, trans_b, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c))
         return gemm_thin_f32(trans_a, trans_b, m, n, k, batch, static_cast<const float*>(a), lda, stride_a,
                              static_cast<const float*>(b), ldb, stride_b, static_cast<float*>(c), ldc, stride_c, s);
 

@@ -61,7 +61,18 @@ struct ThinArgs {
     int k;
     int blocks_m, blocks_n;   // workgroup blocks per slice
     int blocks;               // in all
+    // Slice bt starts (bt / inner) * s + (bt % inner) * s2 elements into its
+    // operand (s = sa, sb or sc; s2 = sa2, sb2 or sc2): heads of a
+    // [batch, seq, heads * dh] row-major tensor are slices with inner =
+    // heads, s = seq * heads * dh and s2 = dh. inner = 1: plain strides.
+    int inner;
+    int64_t sa2, sb2, sc2;
 };
+
+__device__ inline int64_t slice_at(int bt, int inner, int64_t s, int64_t s2) {
+    const int o = bt / inner;
+    return o * s + (int64_t)(bt - o * inner) * s2;
+}
 
 template <int KH>
 __global__ __launch_bounds__(THREADS) void gemm_thin_nt_kernel(ThinArgs g) {
@@ -88,9 +99,9 @@ __global__ __launch_bounds__(THREADS) void gemm_thin_nt_kernel(ThinArgs g) {
         const int bt = blk / per_slice, id = blk - bt * per_slice;
         const int64_t m0 = (int64_t)(id / g.blocks_n) * BM, n0 = (int64_t)(id % g.blocks_n) * BN;
         const __amdgpu_buffer_rsrc_t ra =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(g.a + bt * g.sa), (short)0, (int)g.nrec_a, BUF_FLAGS);
+            __builtin_amdgcn_make_buffer_rsrc((void*)(g.a + slice_at(bt, g.inner, g.sa, g.sa2)), (short)0, (int)g.nrec_a, BUF_FLAGS);
         const __amdgpu_buffer_rsrc_t rb =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(g.b + bt * g.sb), (short)0, (int)g.nrec_b, BUF_FLAGS);
+            __builtin_amdgcn_make_buffer_rsrc((void*)(g.b + slice_at(bt, g.inner, g.sb, g.sb2)), (short)0, (int)g.nrec_b, BUF_FLAGS);
 #pragma unroll
         for (int j = 0; j < CA; ++j) {
             const int c = tid + THREADS * j, row = c / CPR, k = 4 * (c % CPR);
@@ -130,7 +141,7 @@ __global__ __launch_bounds__(THREADS) void gemm_thin_nt_kernel(ThinArgs g) {
         const int bt = blk / per_slice, id = blk - bt * per_slice;
         const int64_t m0 = (int64_t)(id / g.blocks_n) * BM, n0 = (int64_t)(id % g.blocks_n) * BN;
         COut o;
-        o.rs = __builtin_amdgcn_make_buffer_rsrc((void*)(g.c + bt * g.sc), (short)0, (int)g.nrec_c, BUF_FLAGS);
+        o.rs = __builtin_amdgcn_make_buffer_rsrc((void*)(g.c + slice_at(bt, g.inner, g.sc, g.sc2)), (short)0, (int)g.nrec_c, BUF_FLAGS);
         o.off = (uint32_t)(((m0 + 32 * wm + 4 * h) * g.ldc + n0 + 64 * wn + r) * 4);
         return o;
     };
@@ -262,9 +273,9 @@ __global__ __launch_bounds__(THREADS * KS) void gemm_thin_n64_kernel(ThinArgs g)
     const int bt = w / g.blocks_m;
     const int64_t m0 = (int64_t)(w - bt * g.blocks_m) * 64;
     const __amdgpu_buffer_rsrc_t ra =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(g.a + bt * g.sa), (short)0, (int)g.nrec_a, BUF_FLAGS);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(g.a + slice_at(bt, g.inner, g.sa, g.sa2)), (short)0, (int)g.nrec_a, BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t rb =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(g.b + bt * g.sb), (short)0, (int)g.nrec_b, BUF_FLAGS);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(g.b + slice_at(bt, g.inner, g.sb, g.sb2)), (short)0, (int)g.nrec_b, BUF_FLAGS);
     // Chunk loads: 64 rows of 64 floats for each operand, 16 lanes per row.
     // A's rows are m (TA = 0, k along the row) or k (TA = 1, m along the
     // row); B's rows are k.
@@ -350,7 +361,7 @@ __global__ __launch_bounds__(THREADS * KS) void gemm_thin_n64_kernel(ThinArgs g)
         for (int v = 0; v < 16; ++v) sum[v] += part[(wq * 16 + v) * 64 + lane];
     }
     const __amdgpu_buffer_rsrc_t rc =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(g.c + bt * g.sc), (short)0, (int)g.nrec_c, BUF_FLAGS);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(g.c + slice_at(bt, g.inner, g.sc, g.sc2)), (short)0, (int)g.nrec_c, BUF_FLAGS);
     const uint32_t off = (uint32_t)(((m0 + 32 * wm + 4 * h) * g.ldc + 32 * wn + r) * 4);
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -374,7 +385,6 @@ int cu_count() {
     return n;
 }
 
-}  // namespace
 
 bool gemm_thin_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
                         int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, const void* c,
@@ -393,36 +403,60 @@ bool gemm_thin_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t
     return blocks >= 1024 && blocks <= INT32_MAX;
 }
 
-bool gemm_thin_n64_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
-                            int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, const void* c,
-                            int64_t ldc, int64_t sc) {
-    // op(A) [M][K] times B [K][64] (B not transposed), whole 64-row blocks,
-    // whole chunks of 64 k, 16-byte runs, 32-bit offsets inside each slice,
-    // and at least two blocks per CU.
-    if (tb != 0 || n != 64 || k < 64 || k % 64 || m % 64 || batch < 1) return false;
-    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-    if (!al(a) || !al(b) || !c || lda % 4 || ldb % 4 || (batch > 1 && (sa % 4 || sb % 4))) return false;
-    const int64_t a_bytes = ta ? slice_bytes(k, m, lda) : slice_bytes(m, k, lda);
-    if (ldc < n || a_bytes >= SLICE_MAX_BYTES || slice_bytes(k, n, ldb) >= SLICE_MAX_BYTES ||
-        slice_bytes(m, n, ldc) >= SLICE_MAX_BYTES)
-        return false;
-    (void)sc;
-    const int64_t blocks = (m / 64) * batch;
-    return blocks >= 512 && blocks <= INT32_MAX;
+// Both thin kernels' shared checks on one operand or C: a 16-byte-aligned
+// base, leading dimension and slice strides (so every slice starts on a
+// 16-byte boundary), and a slice (rows runs of cols, ld apart) addressable
+// with 32-bit offsets.
+bool view_ok(const ThinView& v, int64_t rows, int64_t cols, int64_t batch, int inner) {
+    if (!v.p || reinterpret_cast<uintptr_t>(v.p) % 16 || v.ld < cols || v.ld % 4) return false;
+    if (batch > inner && v.s % 4) return false;
+    if (inner > 1 && v.s2 % 4) return false;
+    return slice_bytes(rows, cols, v.ld) < SLICE_MAX_BYTES;
 }
 
-int gemm_thin_f32(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const float* a, int64_t lda,
-                  int64_t sa, const float* b, int64_t ldb, int64_t sb, float* c, int64_t ldc, int64_t sc,
-                  hipStream_t s) {
-    if (gemm_thin_n64_f32_fits(ta, tb, m, n, k, batch, a, lda, sa, b, ldb, sb, c, ldc, sc)) {
-        ThinArgs g{};
-        g.a = a, g.b = b, g.c = c;
-        g.sa = sa, g.sb = sb, g.sc = sc, g.ldc = ldc;
-        g.lda4 = (uint32_t)(lda * 4), g.ldb4 = (uint32_t)(ldb * 4), g.ldc4 = (uint32_t)(ldc * 4);
-        g.nrec_a = (uint32_t)(ta ? slice_bytes(k, m, lda) : slice_bytes(m, k, lda));
-        g.nrec_b = (uint32_t)slice_bytes(k, n, ldb);
-        g.nrec_c = (uint32_t)slice_bytes(m, n, ldc);
-        g.k = (int)k;
+int thin_kind(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int inner, const ThinView& a,
+              const ThinView& b, const ThinView& c) {
+    if (m < 1 || n < 1 || k < 1 || batch < 1 || inner < 1 || batch % inner) return 0;
+    if (!view_ok(c, m, n, batch, inner)) return 0;
+    // Scores: C = A B^T, A [M][K], B [N][K], K <= 64; whole 64 x 128 blocks
+    // and enough of them for several per CU (fewer go to the block-tiled
+    // kernels).
+    if (ta == 0 && tb == 1 && k <= 64 && k % 4 == 0 && m % BM == 0 && n % BN == 0 && view_ok(a, m, k, batch, inner) &&
+        view_ok(b, n, k, batch, inner)) {
+        const int64_t blocks = (m / BM) * (n / BN) * batch;
+        if (blocks >= 1024 && blocks <= INT32_MAX) return 1;
+    }
+    // Head-dimension outputs: op(A) [M][K] times B [K][64], whole 64-row
+    // blocks, whole chunks of 64 k, at least two blocks per CU.
+    if (tb == 0 && n == 64 && k % 64 == 0 && m % 64 == 0 && (ta ? view_ok(a, k, m, batch, inner) : view_ok(a, m, k, batch, inner)) &&
+        view_ok(b, k, n, batch, inner)) {
+        const int64_t blocks = (m / 64) * batch;
+        if (blocks >= 512 && blocks <= INT32_MAX) return 2;
+    }
+    return 0;
+}
+
+}  // namespace
+
+bool gemm_thin_view_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int inner,
+                         const ThinView& a, const ThinView& b, const ThinView& c) {
+    return thin_kind(ta, tb, m, n, k, batch, inner, a, b, c) != 0;
+}
+
+int gemm_thin_view(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, int inner, const ThinView& a,
+                   const ThinView& b, const ThinView& c, hipStream_t s) {
+    const int kind = thin_kind(ta, tb, m, n, k, batch, inner, a, b, c);
+    if (!kind) return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm_thin: shape or layout outside the thin kernels' range");
+    ThinArgs g{};
+    g.a = a.p, g.b = b.p, g.c = const_cast<float*>(c.p);
+    g.sa = a.s, g.sb = b.s, g.sc = c.s, g.sa2 = a.s2, g.sb2 = b.s2, g.sc2 = c.s2, g.inner = inner;
+    g.ldc = c.ld;
+    g.lda4 = (uint32_t)(a.ld * 4), g.ldb4 = (uint32_t)(b.ld * 4), g.ldc4 = (uint32_t)(c.ld * 4);
+    g.nrec_c = (uint32_t)slice_bytes(m, n, c.ld);
+    g.k = (int)k;
+    if (kind == 2) {
+        g.nrec_a = (uint32_t)(ta ? slice_bytes(k, m, a.ld) : slice_bytes(m, k, a.ld));
+        g.nrec_b = (uint32_t)slice_bytes(k, n, b.ld);
         g.blocks_m = (int)(m / 64), g.blocks_n = 1;
         g.blocks = (int)(g.blocks_m * batch);
         const dim3 grid((unsigned)g.blocks);
@@ -431,16 +465,8 @@ int gemm_thin_f32(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch
         else hipLaunchKernelGGL((gemm_thin_n64_kernel<0, KS, APOL>), grid, dim3(THREADS * KS), 0, s, g);
         return launch_check("gemm_thin_n64_kernel");
     }
-    if (!gemm_thin_f32_fits(ta, tb, m, n, k, batch, a, lda, sa, b, ldb, sb, c, ldc, sc))
-        return fail(MLXHIP_ERR_INVALID_ARGUMENT, "gemm_thin_f32: shape or layout outside the thin kernels' range");
-    ThinArgs g{};
-    g.a = a, g.b = b, g.c = c;
-    g.sa = sa, g.sb = sb, g.sc = sc, g.ldc = ldc;
-    g.lda4 = (uint32_t)(lda * 4), g.ldb4 = (uint32_t)(ldb * 4), g.ldc4 = (uint32_t)(ldc * 4);
-    g.nrec_a = (uint32_t)slice_bytes(m, k, lda);
-    g.nrec_b = (uint32_t)slice_bytes(n, k, ldb);
-    g.nrec_c = (uint32_t)slice_bytes(m, n, ldc);
-    g.k = (int)k;
+    g.nrec_a = (uint32_t)slice_bytes(m, k, a.ld);
+    g.nrec_b = (uint32_t)slice_bytes(n, k, b.ld);
     g.blocks_m = (int)(m / BM), g.blocks_n = (int)(n / BN);
     g.blocks = (int)(g.blocks_m * g.blocks_n * batch);
     // Persistent workgroups, two per CU (each block of every workgroup
@@ -451,6 +477,21 @@ int gemm_thin_f32(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch
     else if (k <= 32) hipLaunchKernelGGL(gemm_thin_nt_kernel<16>, grid, block, 0, s, g);
     else hipLaunchKernelGGL(gemm_thin_nt_kernel<32>, grid, block, 0, s, g);
     return launch_check("gemm_thin_nt_kernel");
+}
+
+bool gemm_thin_f32_fits(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const void* a,
+                        int64_t lda, int64_t sa, const void* b, int64_t ldb, int64_t sb, const void* c,
+                        int64_t ldc, int64_t sc) {
+    return gemm_thin_view_fits(ta, tb, m, n, k, batch, 1, ThinView{static_cast<const float*>(a), lda, sa, 0},
+                               ThinView{static_cast<const float*>(b), ldb, sb, 0},
+                               ThinView{static_cast<const float*>(c), ldc, sc, 0});
+}
+
+int gemm_thin_f32(int ta, int tb, int64_t m, int64_t n, int64_t k, int64_t batch, const float* a, int64_t lda,
+                  int64_t sa, const float* b, int64_t ldb, int64_t sb, float* c, int64_t ldc, int64_t sc,
+                  hipStream_t s) {
+    return gemm_thin_view(ta, tb, m, n, k, batch, 1, ThinView{a, lda, sa, 0}, ThinView{b, ldb, sb, 0},
+                          ThinView{c, ldc, sc, 0}, s);
 }
 
 }  // namespace mlxhip

@@ -94,6 +94,14 @@ bool is_matrix_swap(const Node& t) {
     return nd == 3 && t.op.has_axes && a.size() == 3 && a[0] == 0 && a[1] == 2 && a[2] == 1;
 }
 
+// A Transpose [B, S, H, dh] <-> [B, H, S, dh] (axes 0, 2, 1, 3): the split or
+// merge of attention heads.
+bool is_head_swap(const Node& t) {
+    const std::vector<int64_t>& a = t.op.axes;
+    return t.op.op.kind == MLXHIP_OP_TRANSPOSE && t.meta.shape.size() == 4 && t.op.has_axes && a.size() == 4 &&
+           a[0] == 0 && a[1] == 2 && a[2] == 1 && a[3] == 3;
+}
+
 // Period P when broadcasting `src` to `dst` only repeats src: after padding
 // src with leading 1s, src = [1,...,1, dst[j:]] for some j, so
 // out[i] = src[i % P] with P = numel(dst[j:]). 0 when it is no such tiling.
@@ -154,6 +162,25 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         uint64_t src;   // the bias, [N] values
     };
     std::unordered_map<uint64_t, BiasTerm> bias_of;  // MatMul -> its bias Add
+    // Heads of attention without the permutes. A [B*H, S, dh] operand that is
+    // Reshape(Transpose{0,2,1,3}(Reshape [B, S, H, dh] (src))) and is read
+    // only by batched MatMuls is read from src in place (head h of batch b at
+    // src + (b S H + h) dh, rows H dh apart) by the thin kernels; a batched
+    // product whose only reader is the reverse chain, Reshape [B, H, S, dh],
+    // Transpose{0,2,1,3}, Reshape (the head merge), writes the merged layout
+    // directly. The Transposes (and the views) are not materialised. When
+    // the product does not fit the thin kernels after all, the permutes run
+    // as before (head_materialise below).
+    struct HeadView {
+        uint64_t src;         // split: the [B*S, H*dh] source; merge: the merged node
+        int64_t B, S, H, dh;
+        uint64_t t, r;        // the Transpose and the inner Reshape
+    };
+    std::unordered_map<uint64_t, HeadView> head_in;   // split view node -> where its data lives
+    std::unordered_map<uint64_t, HeadView> head_out;  // product -> the merge it writes
+    std::unordered_set<uint64_t> head_skip;           // Transposes and inner Reshapes of both
+    // MLXHIP_HEAD_VIEWS=0: the permutes always run (for comparisons).
+    const bool head_views_on = !(getenv("MLXHIP_HEAD_VIEWS") && !strcmp(getenv("MLXHIP_HEAD_VIEWS"), "0"));
     if (fusion) {
         std::unordered_map<uint64_t, std::vector<uint64_t>> users;
         for (uint64_t id : order)
@@ -214,6 +241,68 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
                 continue;
             swapped_matmul.insert(id);
             absorbed_matmul.insert(m);
+        }
+        if (head_views_on) {
+            auto fresh = [&](uint64_t id) { return in_order.count(id) && !buffers.count(id) && !requested.count(id); };
+            // Split views: every reader a rank-3 f32 MatMul (directly or
+            // through folded matrix-swap Transposes).
+            for (uint64_t id : order) {
+                const Node& x = nodes.at(id);
+                if (!fresh(id) || x.op.op.kind != MLXHIP_OP_RESHAPE || x.inputs.size() != 1 || x.meta.shape.size() != 3 ||
+                    x.meta.dtype != MLXHIP_DTYPE_F32)
+                    continue;
+                const uint64_t t = x.inputs[0];
+                const Node& tn = nodes.at(t);
+                if (!fresh(t) || !is_head_swap(tn) || tn.inputs.size() != 1 || consumers[t] != 1) continue;
+                const uint64_t r = tn.inputs[0];
+                const Node& rn = nodes.at(r);
+                if (rn.op.op.kind != MLXHIP_OP_RESHAPE || rn.inputs.size() != 1 || rn.meta.shape.size() != 4) continue;
+                const std::vector<int64_t>& rs = rn.meta.shape;  // [B, S, H, dh]
+                const std::vector<int64_t>& xs = x.meta.shape;   // [B*H, S, dh]
+                if (xs[0] != rs[0] * rs[2] || xs[1] != rs[1] || xs[2] != rs[3] ||
+                    nodes.at(rn.inputs[0]).meta.numel() != rn.meta.numel())
+                    continue;
+                const std::vector<uint64_t>& u = users[id];
+                bool ok = !u.empty();
+                for (uint64_t c : u) {
+                    if (folded_transpose.count(c)) continue;
+                    const Node& cn = nodes.at(c);
+                    ok = ok && cn.op.op.kind == MLXHIP_OP_MATMUL && cn.inputs.size() == 2 && cn.inputs[0] != cn.inputs[1] &&
+                         cn.meta.shape.size() == 3 && cn.meta.dtype == MLXHIP_DTYPE_F32;
+                }
+                if (!ok) continue;
+                head_in[id] = HeadView{rn.inputs[0], rs[0], rs[1], rs[2], rs[3], t, r};
+                head_skip.insert(t);
+                if (consumers[r] == 1 && fresh(r)) head_skip.insert(r);
+            }
+            // Merges: a rank-3 f32 product (or a Transpose computed as one)
+            // whose only reader is Reshape [B, H, S, dh], whose only reader is
+            // the head swap, whose only reader is a Reshape.
+            for (uint64_t id : order) {
+                const Node& p = nodes.at(id);
+                const bool prod = (p.op.op.kind == MLXHIP_OP_MATMUL && !absorbed_matmul.count(id)) || swapped_matmul.count(id);
+                if (!prod || !fresh(id) || folded_transpose.count(id) || bias_of.count(id) || p.meta.shape.size() != 3 ||
+                    p.meta.dtype != MLXHIP_DTYPE_F32 || consumers[id] != 1 || users[id].size() != 1)
+                    continue;
+                const uint64_t r1 = users[id][0];
+                const Node& r1n = nodes.at(r1);
+                if (!fresh(r1) || r1n.op.op.kind != MLXHIP_OP_RESHAPE || r1n.meta.shape.size() != 4 || consumers[r1] != 1 ||
+                    users[r1].size() != 1)
+                    continue;
+                const std::vector<int64_t>& ps = p.meta.shape, &q = r1n.meta.shape;  // [B*H, S, dh], [B, H, S, dh]
+                if (ps[0] != q[0] * q[1] || ps[1] != q[2] || ps[2] != q[3]) continue;
+                const uint64_t t = users[r1][0];
+                const Node& tn = nodes.at(t);
+                if (!fresh(t) || !is_head_swap(tn) || consumers[t] != 1 || users[t].size() != 1) continue;
+                const uint64_t r2 = users[t][0];
+                const Node& r2n = nodes.at(r2);
+                if (!in_order.count(r2) || buffers.count(r2) || r2n.op.op.kind != MLXHIP_OP_RESHAPE ||
+                    r2n.meta.numel() != tn.meta.numel())
+                    continue;
+                head_out[id] = HeadView{r2, q[0], q[2], q[1], q[3], t, r1};
+                head_skip.insert(t);
+                head_skip.insert(r1);
+            }
         }
         for (uint64_t id : order) {
             if (buffers.count(id) || folded_transpose.count(id)) continue;
@@ -448,10 +537,109 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         }
         return best;
     };
+    // Head views (planned above). head_materialise: the split view x's
+    // permute into the Transpose's buffer, x aliasing it. head_merge: the
+    // merge of product id's buffer into the merged node's. The view's nodes
+    // count in eval_count once per stream (a split view read by the loss and
+    // again by the gradients is planned by both evaluations).
+    auto head_count = [&](std::initializer_list<uint64_t> ids) {
+        for (uint64_t h : ids)
+            if (counted_views.insert(h).second) eval_calls += 1;
+    };
+    auto head_materialise = [&](uint64_t x, const HeadView& v) -> int {
+        const Node& tn = nodes.at(v.t);
+        const Node& rn = nodes.at(v.r);
+        float* tb = nullptr;
+        MLXHIP_TRY(alloc_out(v.t, &tb));
+        const mlxhip_input_t in = {buffers.at(v.src).ptr, (size_t)rn.meta.numel(), rn.meta.shape.data(),
+                                   rn.meta.shape.size(), rn.meta.dtype};
+        const int r = eval_node_device(tn.op.c(), &in, 1, tn.meta.c(), tb, hs, scratch, nullptr);
+        if (r != MLXHIP_OK) {
+            release_later(tb);
+            buffers.erase(v.t);
+            return r;
+        }
+        buffers[x] = DevBuf{tb, (size_t)nodes.at(x).meta.numel(), false};
+        launches += 1;
+        head_count({v.t, x});
+        if (head_skip.count(v.r)) head_count({v.r});
+        return MLXHIP_OK;
+    };
+    auto head_merge = [&](uint64_t id, const HeadView& v) -> int {
+        const Node& tn = nodes.at(v.t);
+        const Node& r1n = nodes.at(v.r);
+        float* ob = nullptr;
+        MLXHIP_TRY(alloc_out(v.src, &ob));
+        const mlxhip_input_t in = {buffers.at(id).ptr, (size_t)r1n.meta.numel(), r1n.meta.shape.data(),
+                                   r1n.meta.shape.size(), r1n.meta.dtype};
+        const int r = eval_node_device(tn.op.c(), &in, 1, tn.meta.c(), ob, hs, scratch, nullptr);
+        if (r != MLXHIP_OK) {
+            release_later(ob);
+            buffers.erase(v.src);
+            return r;
+        }
+        launches += 1;
+        head_count({v.r, v.t, v.src});
+        return MLXHIP_OK;
+    };
+    // A batched product with head views on the thin kernels: operands in
+    // place, C into the merged node when it is a merge. *ran = false (and
+    // nothing done) when the thin kernels do not take it.
+    auto head_product = [&](uint64_t id, const mlxhip_input_t* ins, const int* hint, const uint64_t* msrc,
+                            const HeadView* const* hv, const HeadView* ho, bool* ran) -> int {
+        *ran = false;
+        if (ins[0].ndim != 3 || ins[1].ndim != 3) return MLXHIP_OK;
+        // Common head count and batch: every view's must agree.
+        int64_t H = 0, B = 0;
+        for (const HeadView* v : {hv[0], hv[1], ho}) {
+            if (!v) continue;
+            if (H && (v->H != H || v->B != B)) return MLXHIP_OK;
+            H = v->H, B = v->B;
+        }
+        const int64_t G = ins[0].shape[0];
+        if (ins[1].shape[0] != G || G != B * H || H > INT32_MAX) return MLXHIP_OK;
+        ThinView op[2];
+        for (int j = 0; j < 2; ++j) {
+            const int64_t R = ins[j].shape[1], C = ins[j].shape[2];
+            if (hv[j]) {
+                const HeadView& v = *hv[j];
+                op[j] = ThinView{buffers.at(v.src).ptr, v.H * v.dh, v.S * v.H * v.dh, v.dh};
+            } else {
+                op[j] = ThinView{ins[j].data, C, H * R * C, R * C};
+            }
+        }
+        const int ta = hint[0], tb = hint[1];
+        const int64_t m = ta ? ins[0].shape[2] : ins[0].shape[1], k = ta ? ins[0].shape[1] : ins[0].shape[2];
+        const int64_t n = tb ? ins[1].shape[1] : ins[1].shape[2];
+        if (ho && (m != ho->S || n != ho->dh)) return MLXHIP_OK;
+        // C's placement is known before it exists: 256-byte-aligned pool blocks.
+        const float* probe = reinterpret_cast<const float*>(uintptr_t(256));
+        ThinView cv = ho ? ThinView{probe, H * n, m * H * n, n} : ThinView{probe, n, H * m * n, m * n};
+        if (!gemm_thin_view_fits(ta, tb, m, n, k, G, (int)H, op[0], op[1], cv)) return MLXHIP_OK;
+        float* out = nullptr;
+        const uint64_t dst = ho ? ho->src : id;
+        MLXHIP_TRY(alloc_out(dst, &out));
+        cv.p = out;
+        const int r = gemm_thin_view(ta, tb, m, n, k, G, (int)H, op[0], op[1], cv, hs);
+        if (r != MLXHIP_OK) {
+            release_later(out);
+            buffers.erase(dst);
+            return r;
+        }
+        for (int j = 0; j < 2; ++j)
+            if (hv[j]) {
+                head_count({hv[j]->t, msrc[j]});
+                if (head_skip.count(hv[j]->r)) head_count({hv[j]->r});
+            }
+        if (ho) head_count({ho->r, ho->t, ho->src});
+        *ran = true;
+        return MLXHIP_OK;
+    };
     for (size_t oi = 0; oi < order.size(); ++oi) {
         const uint64_t id = order[oi];
         if (buffers.count(id) || folded_transpose.count(id) || interior.count(id) || virtual_bcast.count(id) ||
-            absorbed_matmul.count(id) || buffers.count(out_of(id)))  // a product already run with its bias term
+            absorbed_matmul.count(id) || buffers.count(out_of(id)) ||  // a product already run with its bias term
+            head_skip.count(id) || head_in.count(id))                  // head views: read or written in place
             continue;
         const Node& n = nodes.at(id);
         auto ch = chain_of.find(id);
@@ -540,6 +728,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         std::vector<mlxhip_input_t> ins;
         int hint[2] = {0, 0};
         uint64_t msrc[2] = {0, 0};  // a MatMul's resolved operand sources
+        const HeadView* hv[2] = {nullptr, nullptr};  // operands that are head-split views
         bool missing = false;
         const bool swapped = swapped_matmul.count(id) != 0;
         const Node& en = swapped ? nodes.at(n.inputs[0]) : n;  // the node whose op runs
@@ -557,10 +746,36 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             }
             if (j < 2) msrc[j] = src;
             auto b = buffers.find(src);
+            if (b == buffers.end() && en.op.op.kind == MLXHIP_OP_MATMUL && j < 2 && head_in.count(src) &&
+                ready_alias(head_in.at(src).src, 0)) {
+                hv[j] = &head_in.at(src);
+                ins.push_back(input_of(src, nullptr));  // read in place, or materialised below
+                continue;
+            }
             if (b == buffers.end()) { missing = true; break; }
             ins.push_back(input_of(src, b->second.ptr));
         }
         if (missing) { rc = fail(MLXHIP_ERR_INVALID_ARGUMENT, "input node should be evaluated before dependents"); break; }
+        auto ho = head_out.find(id);
+        if (hv[0] || hv[1] || ho != head_out.end()) {
+            bool ran = false;
+            if ((rc = head_product(id, ins.data(), hint, msrc, hv, ho == head_out.end() ? nullptr : &ho->second, &ran)) !=
+                MLXHIP_OK)
+                break;
+            if (ran) {
+                eval_calls += covered;
+                launches += 1;
+                continue;
+            }
+            // Not for the thin kernels: the split views' permutes run now, the
+            // merge's after the product (below).
+            for (int j = 0; j < 2 && rc == MLXHIP_OK; ++j)
+                if (hv[j]) {
+                    rc = head_materialise(msrc[j], *hv[j]);
+                    if (rc == MLXHIP_OK) ins[j] = input_of(msrc[j], buffers.at(msrc[j]).ptr);
+                }
+            if (rc != MLXHIP_OK) break;
+        }
         // Sibling products: later MatMuls of this evaluation with operands of
         // the same shapes and layouts, both ready, run with this one in one
         // grouped launch (the Q/K/V projections of one input; the three
@@ -723,6 +938,7 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
             buffers.erase(id);
             break;
         }
+        if (ho != head_out.end() && (rc = head_merge(id, ho->second)) != MLXHIP_OK) break;
     }
     // A product still pending (its siblings failed to come) runs alone.
     for (size_t i = 0; rc == MLXHIP_OK && i < pending.size(); ++i) {

@@ -77,6 +77,9 @@ struct mlxhip_stream_t {
     uint64_t next_id = 1;
     std::atomic<uint64_t> eval_calls{0};
     std::atomic<uint64_t> launches{0};
+    // Nodes read or written in place and never materialised (attention head
+    // views): counted in eval_calls once, however many evaluations plan them.
+    std::unordered_set<uint64_t> counted_views;
     bool fusion = true;
     // Asynchronous evaluation (mlxhip_stream_set_async): eval returns once
     // its kernels are enqueued. Blocks released while queued kernels may
@@ -235,6 +238,7 @@ struct mlxhip_stream_t {
         nodes.clear();
         cse.clear();
         consumers.clear();
+        counted_views.clear();
         return MLXHIP_OK;
     }
 

@@ -453,6 +453,34 @@ def test_hip_block_fusion_off_matches_on():
 
 @pytest.mark.gpu
 @pytest.mark.usefixtures("hip")
+@pytest.mark.parametrize("cfg", [nn.BlockConfig(), SMALL], ids=["config4", "small"])
+def test_hip_block_head_views_match_permutes(monkeypatch, cfg):
+    """The composed attention's head split and merge without permute kernels:
+    at config 4 the thin kernels read the Q, K, V and dO heads in place and
+    write O, dQ, dK and dV straight into the merged [B*S, D] layout; the
+    small block's products do not fit those kernels, so its permutes run
+    after all. Either way every gradient is bit for bit the one of the same
+    block with the permutes always run (MLXHIP_HEAD_VIEWS=0), with the same
+    eval count, and config 4 takes 8 fewer launches (4 splits, 4 merges)."""
+    from oxidizedmlx_amd.backend import HipStream
+    arrs, x, gy = block_arrays(cfg, seed=23)
+    runs = {}
+    for views in ("1", "0"):
+        monkeypatch.setenv("MLXHIP_HEAD_VIEWS", views)
+        st = HipStream()
+        loss, g = block_grads(st, cfg, arrs, x, gy)
+        runs[views] = (loss, g, st.eval_count(), st.launch_count())
+        st.close()
+    (l1, g1, e1, n1), (l0, g0, e0, n0) = runs["1"], runs["0"]
+    print(f"  head views: {n1} launches, permutes: {n0} launches; eval count {e1} / {e0}", flush=True)
+    assert l1 == l0 and e1 == e0
+    for k in g0:
+        np.testing.assert_array_equal(g1[k], g0[k], err_msg=k)
+    assert n0 - n1 == (8 if cfg is not SMALL else 0)
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("hip")
 def test_hip_block_config4_matches_torch_fp32_cpu():
     """Config 4 at full size (d_model 1024, 16 heads, seq 512, batch 4)
     against torch float32 autograd of the same block, run on the host CPU
