@@ -132,6 +132,7 @@ def test_small_f32_kernel_shapes(ta, tb, m, n, k, batch):
     (256, 256, 32, 128, 0),  # K = 32: 16 per half-wave
     (512, 256, 16, 64, 8),   # K = 16: 8 per half-wave
     (256, 256, 4, 128, 0),   # K = 4: the second half-wave reads only zeros
+    (192, 128, 32, 343, 0),  # 1029 blocks: not a multiple of 8 (no XCD ranges), 2-3 blocks per workgroup
 ])
 def test_thin_f32_kernel(m, n, k, batch, ld_pad):
     """The thin kernel for many f32 products C = A B^T with K <= 64 (64 x 128
