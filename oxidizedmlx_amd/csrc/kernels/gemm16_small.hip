@@ -16,11 +16,14 @@
 //     workgroups of 16 waves (4 per SIMD), so no second kernel.
 //   * K tiles of 64. Each thread moves two 8-element chunks of each operand
 //     per K tile: chunk = 8 consecutive elements along the operand's
-//     contiguous axis. A chunk is read as one 16-byte and one 4-byte buffer
-//     load from the dword boundary at or below its first element and shifted
-//     down by one element when that element sits at an odd position (any
-//     2-byte-aligned operand), then elements past the matrix edge are
-//     zeroed. Dwords past the descriptor's range (the slice) read as zeros.
+//     contiguous axis. A chunk is read as one 16-byte buffer load from the
+//     dword boundary at or below its first element and shifted down by one
+//     element when that element sits at an odd position (any 2-byte-aligned
+//     operand), then elements past the matrix edge are zeroed. Dwords past
+//     the descriptor's range (the slice) read as zeros. The fifth dword an
+//     odd chunk needs is the next lane's first: taken from it with a DPP
+//     row shift, and loaded (4 bytes) only by the last lane of each group of
+//     8 and where the next chunk lies outside the matrix.
 //   * Loads run DEPTH K tiles ahead in registers (20 VGPRs per tile), so the
 //     L2 / HBM latency overlaps DEPTH tiles of work per group; LDS is
 //     double-buffered per group with one barrier per K tile.
@@ -111,17 +114,21 @@ __device__ inline int lds_at(int row, int c) { return row * TILE + 8 * (c ^ (row
 // further: 64 elements along K), the funnel-shift amount (the element's
 // parity, the same in every tile since a tile step is an even number of
 // elements), and whether its rows / columns are inside the matrix.
-template <bool KC>
+template <bool KC, bool SHARE = true>
 struct Chunk {
     uint32_t off0;  // byte offset of the dword at or below the first element, tile 0
     uint32_t sh;    // 16 when that element is the upper half of its dword, else 0
     int k0;         // k of the chunk's first element in tile 0 (group-relative tile index 0)
     int lrow, lc;   // tile-local row (KC) / first row (MN), and 8-element chunk index along K
     bool ok;        // KC: its row is inside the matrix; MN: its first row is
+    bool last;      // the last of the 8 lanes that share a row (KC) or a k (MN)
+    bool nb_ok;     // MN: the next lane's first row is inside the matrix (KC: same row)
     u32x4 keep;     // MN: masks of the rows past the matrix edge (fixed)
 
     __device__ inline void init(const Operand& o, int q, int64_t r0, int64_t R, int64_t ld, int64_t kg) {
         int64_t e;
+        last = (q & 7) == 7;
+        nb_ok = true;
         if constexpr (KC) {
             lrow = q >> 3;
             lc = q & 7;
@@ -138,13 +145,28 @@ struct Chunk {
             ok = r < R;
             e = o.e0 + (int64_t)k0 * ld + (ok ? r : 0);
             keep = chunk_keep((int)max<int64_t>(0, min<int64_t>(8, R - r)));
+            nb_ok = r + 8 < R;
         }
         off0 = (uint32_t)((e >> 1) << 2);
         sh = (uint32_t)(e & 1) * 16;
     }
 
-    // One 16-byte and one 4-byte load (dword-aligned) of the chunk in K tile
-    // t (group-relative); `step` is the byte distance between two K tiles.
+    // Whether this lane loads the fifth dword of its chunk in K tile t itself
+    // (below).
+    __device__ inline bool own(int t, int K) const {
+        if constexpr (!SHARE) return true;
+        else if constexpr (KC) return last || !(k0 + 8 + t * BK < K);
+        else return last || !nb_ok;
+    }
+
+    // One 16-byte load (dword-aligned) of the chunk in K tile t
+    // (group-relative), and the fifth dword, which only a chunk starting at
+    // an odd element uses: it is the first dword of the next lane's chunk,
+    // so only the last lane of each group of 8 (its neighbour's chunk is
+    // not loaded here) and a lane whose neighbour's chunk lies outside the
+    // matrix (read as zeros) load it themselves, 4 bytes; the others take
+    // it from the neighbour in store(). `step` is the byte distance between
+    // two K tiles.
     // Out-of-range chunks read through an offset past the descriptor's
     // range: zeros. The descriptor's range check is per dword, so a chunk
     // that ends its slice keeps its in-range dwords and reads zeros past
@@ -154,7 +176,7 @@ struct Chunk {
         const bool in = ok && k0 + t * BK < K;
         const uint32_t off = in ? off0 + (uint32_t)t * step : OOB_OFF;
         r.lo = __builtin_amdgcn_raw_buffer_load_b128(o.rsrc, off, 0, 0);
-        r.hi = __builtin_amdgcn_raw_buffer_load_b32(o.rsrc, off + 16, 0, 0);
+        r.hi = __builtin_amdgcn_raw_buffer_load_b32(o.rsrc, own(t, K) && sh ? off + 16 : OOB_OFF, 0, 0);
     }
 
     // The chunk's 8 elements of K tile t, shifted down one element when the
@@ -162,10 +184,14 @@ struct Chunk {
     // the group's LDS stage. `tail`: K tile t holds the end of K (uniform
     // across the workgroup), where a K-contiguous chunk can straddle it.
     __device__ inline void store(const Raw& r, int t, int K, bool tail, SMALL16_LDS uint16_t* s) const {
+        // The fifth dword: the next lane's first (DPP row_shl:1, lanes of a
+        // group of 8 are consecutive within a row of 16), or this lane's own.
+        const uint32_t nb = (uint32_t)__builtin_amdgcn_mov_dpp((int)r.lo.x, 0x101, 0xF, 0xF, false);
+        const uint32_t hi = own(t, K) ? r.hi : nb;
         // Branch-free funnel shift by 0 or 16 bits, so the loads of later K
         // tiles stay in flight across it.
         u32x4 v{__builtin_amdgcn_alignbit(r.lo.y, r.lo.x, sh), __builtin_amdgcn_alignbit(r.lo.z, r.lo.y, sh),
-                __builtin_amdgcn_alignbit(r.lo.w, r.lo.z, sh), __builtin_amdgcn_alignbit(r.hi, r.lo.w, sh)};
+                __builtin_amdgcn_alignbit(r.lo.w, r.lo.z, sh), __builtin_amdgcn_alignbit(hi, r.lo.w, sh)};
         if constexpr (KC) {
             // Elements past K belong to the next row: zero them (only in the
             // tile holding the end of K; chunks wholly past K read zeros).
@@ -245,8 +271,11 @@ void gemm16_small_kernel(Small16Args g) {
     // along K (K-contiguous) or 64 rows of the leading dimension.
     const uint32_t step_a = KCA ? 2u * BK : (uint32_t)(2 * BK * g.lda);
     const uint32_t step_b = KCB ? 2u * BK : (uint32_t)(2 * BK * g.ldb);
-    Chunk<KCA> ca[2];
-    Chunk<KCB> cb[2];
+    // With both operands M/N-contiguous (8 transposed LDS writes per chunk
+    // each) every lane loads its own fifth dwords: sharing them spilled
+    // registers at 4 waves per SIMD.
+    Chunk<KCA, KCA || KCB> ca[2];
+    Chunk<KCB, KCA || KCB> cb[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         ca[i].init(oa, ltid + 256 * i, m0, g.m, g.lda, kg);
