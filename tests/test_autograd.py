@@ -453,7 +453,8 @@ def test_hip_block_fusion_off_matches_on():
 
 @pytest.mark.gpu
 @pytest.mark.usefixtures("hip")
-@pytest.mark.parametrize("cfg", [nn.BlockConfig(), SMALL], ids=["config4", "small"])
+@pytest.mark.parametrize("cfg", [nn.BlockConfig(), nn.BlockConfig(seq=1024, batch=2), SMALL],
+                         ids=["config4", "seq1024", "small"])
 def test_hip_block_head_views_match_permutes(monkeypatch, cfg):
     """The composed attention's head split and merge without permute kernels:
     at config 4 the thin kernels read the Q, K, V and dO heads in place and
@@ -461,7 +462,8 @@ def test_hip_block_head_views_match_permutes(monkeypatch, cfg):
     small block's products do not fit those kernels, so its permutes run
     after all. Either way every gradient is bit for bit the one of the same
     block with the permutes always run (MLXHIP_HEAD_VIEWS=0), with the same
-    eval count, and config 4 takes 8 fewer launches (4 splits, 4 merges)."""
+    eval count, and the thin-kernel blocks (config 4; 2 sequences of 1024)
+    take 8 fewer launches (4 splits, 4 merges)."""
     from oxidizedmlx_amd.backend import HipStream
     arrs, x, gy = block_arrays(cfg, seed=23)
     runs = {}
