@@ -620,6 +620,12 @@ int mlxhip_stream_t::eval(const std::vector<uint64_t>& outputs) {
         const uint64_t dst = ho ? ho->src : id;
         MLXHIP_TRY(alloc_out(dst, &out));
         cv.p = out;
+        if (!gemm_thin_view_fits(ta, tb, m, n, k, G, (int)H, op[0], op[1], cv)) {
+            // Not the placement the pool gives (256-byte blocks): run as before.
+            release_later(out);
+            buffers.erase(dst);
+            return MLXHIP_OK;
+        }
         const int r = gemm_thin_view(ta, tb, m, n, k, G, (int)H, op[0], op[1], cv, hs);
         if (r != MLXHIP_OK) {
             release_later(out);
