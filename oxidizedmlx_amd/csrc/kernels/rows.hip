@@ -139,11 +139,27 @@ __device__ inline void row_reduce_moments(float& n, float& mean, float& m2, floa
             slot[3 * wave_in_row + 2] = m2;
         }
         __syncthreads();
-        n = slot[0];
-        mean = slot[1];
-        m2 = slot[2];
+        if constexpr (EQUAL && (WPR & (WPR - 1)) == 0) {
+            // Equal counts in every wave: a pairwise tree (waves 2i and 2i+1,
+            // then the pairs) merges equal counts at every level, without
+            // the division.
+            float nn[WPR], mm[WPR], qq[WPR];
 #pragma unroll
-        for (int w = 1; w < WPR; ++w) merge_moments(n, mean, m2, slot[3 * w], slot[3 * w + 1], slot[3 * w + 2]);
+            for (int w = 0; w < WPR; ++w) nn[w] = slot[3 * w], mm[w] = slot[3 * w + 1], qq[w] = slot[3 * w + 2];
+#pragma unroll
+            for (int st = 1; st < WPR; st *= 2)
+#pragma unroll
+                for (int w = 0; w < WPR; w += 2 * st) merge_moments_equal(nn[w], mm[w], qq[w], mm[w + st], qq[w + st]);
+            n = nn[0];
+            mean = mm[0];
+            m2 = qq[0];
+        } else {
+            n = slot[0];
+            mean = slot[1];
+            m2 = slot[2];
+#pragma unroll
+            for (int w = 1; w < WPR; ++w) merge_moments(n, mean, m2, slot[3 * w], slot[3 * w + 1], slot[3 * w + 2]);
+        }
     }
 }
 
