@@ -48,7 +48,7 @@ constexpr int SPLIT_MAX = 8;  // every split plan uses at most 8 splits
 template <int CT, bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, void* c, int64_t m,
                                                             int64_t n, int64_t ldw, int64_t ldc, int64_t sc,
-                                                            int splits, const float* __restrict__ bias) {
+                                                            int splits, const float* __restrict__ bias, bool c_vec) {
     const int64_t b = blockIdx.y;
     const int64_t groups = (n + 3) / 4;
     const int gx = threadIdx.x % RED_COLS, gy = threadIdx.x / RED_COLS;
@@ -94,9 +94,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
             if (bias)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[e] += bv[e];
+            if (CT == MLXHIP_DTYPE_F32 && c_vec && col + 4 <= n) {
+                // f32 C with 16-byte aligned rows: one 16-byte store.
+                *reinterpret_cast<float4*>(static_cast<float*>(c) + b * sc + row * ldc + col) =
+                    float4{acc[0], acc[1], acc[2], acc[3]};
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (col + e < n) gemm_detail::store_c<CT>(c, b * sc + row * ldc + col + e, acc[e]);
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < n) gemm_detail::store_c<CT>(c, b * sc + row * ldc + col + e, acc[e]);
+            }
         }
     }
 }
@@ -113,12 +119,15 @@ int splitk_reduce(int c_dtype, const float* ws, void* c, int64_t m, int64_t n, i
     const int64_t row_blocks = std::max<int64_t>(
         1, std::min<int64_t>({ceil_div(m, RED_ROWS), 65535, (int64_t(1) << 22) / col_blocks}));
     const dim3 grid((unsigned)(row_blocks * col_blocks), (unsigned)batch);
+    // f32 C whose every row (and batch slice) starts 16-byte aligned.
+    const bool c_vec = c_dtype == MLXHIP_DTYPE_F32 && reinterpret_cast<uintptr_t>(c) % 16 == 0 && ldc % 4 == 0 &&
+                       (batch == 1 || sc % 4 == 0);
 #define MLXHIP_RED(CT)                                                                                       \
     do {                                                                                                    \
         if (vec) hipLaunchKernelGGL((splitk_reduce_kernel<CT, true>), grid, dim3(256), 0, s, ws, c, m, n, ldw, \
-                                    ldc, sc, splits, bias);                                                  \
+                                    ldc, sc, splits, bias, c_vec);                                           \
         else hipLaunchKernelGGL((splitk_reduce_kernel<CT, false>), grid, dim3(256), 0, s, ws, c, m, n, ldw,    \
-                                ldc, sc, splits, bias);                                                      \
+                                ldc, sc, splits, bias, c_vec);                                               \
     } while (0)
     switch (c_dtype) {
         case MLXHIP_DTYPE_F32: MLXHIP_RED(MLXHIP_DTYPE_F32); break;
